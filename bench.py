@@ -1,0 +1,211 @@
+"""Benchmark of the packed low-bit matmul path on one MI355X.
+
+A step is one FP4 E2M1 (+ E8M0 per 32 K-elements) decode GEMV, W [14336, 4096],
+x bf16 [1, 4096] -> y bf16 [1, 14336], fp32 accumulation -- one call of the C-ABI
+entry point ``tgm_gemv``.  Every step reads a different copy of the weights (18
+copies, 562 MB, more than twice the 256 MB Infinity Cache) so each launch streams
+its weights from HBM.  The K timed steps are captured once in a HIP graph and
+replayed, and timed with HIP events on the launch stream.
+
+``value`` is the achieved algorithmic bandwidth of the step (bytes of packed weights,
+scales, x and y per step / time per step).  Secondary workloads (skinny M=4/16, the
+INT4 g32 GEMV, the FP6 and FP4xFP4 GEMMs) are reported under ``workloads``.
+``cpu_baseline`` times the C restatement of the reference's CPU path
+(oracle/cpu_path.c: materialise fp32 weights, fp32 GEMV, RNE to bf16) on the host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "tinygrad-dx12_amd"))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP4_PEAK_TFLOPS = 10100.0
+N_COPIES = 18
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extras", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    return p.parse_args()
+
+
+def gemv_bytes(n: int, k: int, m: int, bits: int, scale_bytes: float, act_bytes: int, out_bytes: int) -> int:
+    return n * k * bits // 8 + int(n * (k // 32) * scale_bytes) + m * k * act_bytes + m * n * out_bytes
+
+
+class Timer:
+    """Captures ``steps`` launches of ``launch(i)`` in a HIP graph; replays and times them."""
+
+    def __init__(self, torch, launch, steps: int, warmup: int):
+        self.torch, self.launch, self.steps, self.warmup = torch, launch, steps, warmup
+
+    def run(self) -> float:
+        torch = self.torch
+        for i in range(self.warmup):
+            self.launch(i)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(self.steps):
+                    self.launch(i)
+        graph.replay()  # untimed replay: graph upload and first-touch
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            graph.replay()
+            end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / self.steps  # ms per step
+
+
+def fp4_gemv_workload(torch, K, dev, m: int, steps: int, warmup: int, copies: int = N_COPIES):
+    n, k = 14336, 4096
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    ws = [torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device=dev, generator=g) for _ in range(copies)]
+    ss = [torch.randint(123, 130, (n, k // 32), dtype=torch.uint8, device=dev, generator=g) for _ in range(copies)]
+    x = torch.randn((m, k), device=dev, generator=g).to(torch.bfloat16)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    fmt, bf16, e8m0 = K.FORMAT_IDS["fp4_e2m1"], K.DTYPE_IDS[torch.bfloat16], K.DTYPE_IDS[torch.float8_e8m0fnu]
+    lib = K.load_library()
+
+    def launch(i: int) -> None:
+        j = i % copies
+        K.check("tgm_gemv", lib.tgm_gemv(ws[j].data_ptr(), fmt, n, k, ss[j].data_ptr(), e8m0, 32, x.data_ptr(), bf16,
+                                         m, k, y.data_ptr(), bf16, n, K.stream_of(x)))
+
+    ms = Timer(torch, launch, steps, warmup).run()
+    nbytes = gemv_bytes(n, k, m, 4, 1, 2, 2)
+    return {"workload": f"fp4_e2m1 e8m0/32 GEMV N=14336 K=4096 M={m}", "ms": ms, "bytes": nbytes,
+            "GB/s": nbytes / ms / 1e6, "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS,
+            "TFLOPS": 2 * m * n * k / ms / 1e9}
+
+
+def int4_gemv_workload(torch, K, dev, steps: int, warmup: int, copies: int = 40):
+    n = k = 4096
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    ws = [torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device=dev, generator=g) for _ in range(copies)]
+    ss = [(torch.rand((n, k // 32), device=dev, generator=g) * 0.015 + 0.005).half() for _ in range(copies)]
+    x = torch.randn((1, k), device=dev, generator=g).half()
+    y = torch.empty((1, n), dtype=torch.float16, device=dev)
+    fmt, f16 = K.FORMAT_IDS["int4"], K.DTYPE_IDS[torch.float16]
+    lib = K.load_library()
+
+    def launch(i: int) -> None:
+        j = i % copies
+        K.check("tgm_gemv", lib.tgm_gemv(ws[j].data_ptr(), fmt, n, k, ss[j].data_ptr(), f16, 32, x.data_ptr(), f16,
+                                         1, k, y.data_ptr(), f16, n, K.stream_of(x)))
+
+    ms = Timer(torch, launch, steps, warmup).run()
+    nbytes = gemv_bytes(n, k, 1, 4, 2, 2, 2)
+    return {"workload": "int4 g32 fp16-scale GEMV N=K=4096 M=1 fp16", "ms": ms, "bytes": nbytes,
+            "GB/s": nbytes / ms / 1e6, "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
+
+
+def cpu_baseline(budget_s: float) -> dict:
+    """The reference CPU path restated in C (oracle/cpu_path.c), timed on the host cores."""
+    import numpy as np
+
+    lib = ctypes.CDLL(str(ROOT / "oracle" / "liboracle_cpu.so"))
+    n, k, m = 14336, 4096, 1
+    rng = np.random.default_rng(0)
+    data = rng.integers(0, 256, n * k // 2).astype(np.uint8)
+    e = (127 + rng.integers(-4, 3, (n, k // 32))).astype(np.int64)
+    scales = np.ldexp(np.float32(1.0), (e - 127)).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x = ((x.view(np.uint32) + 0x8000) & 0xFFFF0000).view(np.float32)  # bf16-valued activations
+    wdeq = np.empty(n * k, np.float32)
+    yf = np.empty(m * n, np.float32)
+    y = np.empty(m * n, np.uint16)
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    i64 = ctypes.c_int64
+
+    def once() -> float:
+        t = time.perf_counter()
+        lib.oracle_cpu_path(p(data), i64(data.size), 2, i64(n), i64(k), p(scales), i64(32), p(x), i64(m), p(wdeq),
+                            p(yf), p(y), 16)
+        return time.perf_counter() - t
+
+    once()  # warm the pages
+    times, start = [], time.perf_counter()
+    while time.perf_counter() - start < budget_s and len(times) < 200:
+        times.append(once())
+    med = statistics.median(times)
+    nbytes = gemv_bytes(n, k, m, 4, 1, 2, 2)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"full fp4 e8m0/32 GEMV 14336x4096 M=1 (dequant to fp32 + fp32 GEMV + bf16), "
+                      f"median of {len(times)} runs, {med * 1e3:.1f} ms each"}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is design-only)"}))
+        return 2
+    import torch
+
+    from tinygrad_mi355x.runtime import kernels as K
+
+    dev = torch.device("cuda:0")
+    K.load_library()
+    torch.cuda.synchronize()
+    wall = time.perf_counter()
+    primary = fp4_gemv_workload(torch, K, dev, 1, args.steps, args.warmup)
+    workloads = {}
+    if not args.no_extras:
+        for m in (4, 16):
+            workloads[f"fp4_gemv_m{m}"] = fp4_gemv_workload(torch, K, dev, m, max(args.steps // 2, 1), args.warmup)
+        workloads["int4_gemv_cfg1"] = int4_gemv_workload(torch, K, dev, max(args.steps // 2, 1), args.warmup)
+    torch.cuda.synchronize()
+    gpu_wall = time.perf_counter() - wall
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
+    gbs = primary["GB/s"]
+    line = {
+        "metric": "low-bit GEMV GB/s (% HBM peak) + FP4 GEMM TFLOPS (% MFMA peak), 1 GPU",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(primary["ms"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp4_e2m1 x bf16 -> fp32 acc -> bf16",
+        "data": "synthetic (uniform E2M1 codes, E8M0 exponents 123..129, N(0,1) bf16 activations), 18 rotating weight copies",
+        "config": {"workload": primary["workload"], "N": 14336, "K": 4096, "M": 1, "block": 32,
+                   "launch": "hip graph of the timed steps", "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "workloads": {name: {k: (round(v, 6) if isinstance(v, float) else v) for k, v in w.items()}
+                      for name, w in workloads.items()},
+        "gpu_wall_s": round(gpu_wall, 2),
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

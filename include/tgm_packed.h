@@ -1,0 +1,174 @@
+/*
+ * tgm_packed.h -- C ABI of the MI355X (gfx950) packed low-bit matmul library
+ * (libtgm_mi355x.so).
+ *
+ * Every entry point takes plain device pointers, element counts and strides, and an
+ * opaque HIP stream (hipStream_t passed as void*; NULL = the legacy default stream).
+ * Kernels are enqueued asynchronously on that stream; no entry point synchronises
+ * except where stated.  Entry points return TGM_OK (0) on success, a negative TGM_E_*
+ * code for argument errors, or a positive hipError_t for runtime failures; the text of
+ * the last failure on the calling thread is available from tgm_last_error().
+ *
+ * The packed storage contract is the reference's: a continuous little-endian bit
+ * stream over the flattened logical array (alexandreteles/tinygrad-dx12
+ * src/tinygrad_dx12/codegen/decomp/dx12.py:69-77, ARCHITECTURE.md:594-658).  Scales
+ * are numeric tensors of shape shape[:-1] + (ceil(K/block),) (dx12.py:44-47); an
+ * E8M0 scale tensor is one byte per scale holding 2^(e-127).
+ *
+ * The reference binds nothing below Python: its packed path is
+ * PackedTensor.unpack + linalg.matmul/matvec -> LinAlg HLSL kernels.  The Python
+ * package tinygrad_mi355x binds this header with ctypes (runtime/kernels.py); each
+ * declaration names the reference interface it replaces.
+ */
+#ifndef TGM_PACKED_H
+#define TGM_PACKED_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TGM_ABI_VERSION 1
+
+/* Packed formats, FORMATS of dx12.py:10. */
+enum tgm_format {
+  TGM_FMT_INT4 = 0,
+  TGM_FMT_UINT4 = 1,
+  TGM_FMT_FP4_E2M1 = 2,
+  TGM_FMT_FP6_E2M3 = 3,
+  TGM_FMT_FP6_E3M2 = 4,
+};
+
+/* Element types of ordinary (unpacked) operands, scales and results. */
+enum tgm_dtype {
+  TGM_BOOL = 0,
+  TGM_I8 = 1,
+  TGM_U8 = 2,
+  TGM_I16 = 3,
+  TGM_U16 = 4,
+  TGM_I32 = 5,
+  TGM_U32 = 6,
+  TGM_I64 = 7,
+  TGM_U64 = 8,
+  TGM_FP8E4M3 = 9, /* OCP E4M3FN */
+  TGM_FP8E5M2 = 10,
+  TGM_F16 = 11,
+  TGM_BF16 = 12,
+  TGM_F32 = 13,
+  TGM_F64 = 14,
+  TGM_E8M0 = 15, /* OCP MX shared scale: 2^(e-127), 0xFF = NaN */
+  TGM_NONE = -1,
+};
+
+enum tgm_status {
+  TGM_OK = 0,
+  TGM_E_INVALID = -1,     /* bad argument (maps to ValueError) */
+  TGM_E_UNSUPPORTED = -2, /* no kernel for this combination (caller picks another family) */
+};
+
+/* ABI version; lets the binding reject a stale library. */
+int tgm_abi_version(void);
+
+/* Message of the last failure on this thread ("" if none). */
+const char* tgm_last_error(void);
+
+/*
+ * Decode ``count`` packed elements to ``out_dtype`` (replaces PackedTensor.unpack,
+ * dx12.py:49-106).  ``k`` is the logical last dimension (scales index
+ * [i / k, (i % k) / block]).  ``scales`` may be NULL (scale_dtype ignored).
+ * Multiplication happens in f64 when scale_dtype or out_dtype is F64, else f32, then
+ * the value is cast to out_dtype (RNE for float narrowing, truncation for integers).
+ * Unscaled FP4/FP6 with an exact FP8 out_dtype (FP8_CANDIDATES, dx12.py:11) use the
+ * direct re-encode of dx12.py:78-92.
+ */
+int tgm_unpack(const void* data, int64_t nbytes, int fmt, int64_t count, int64_t k,
+               const void* scales, int scale_dtype, int64_t block_size,
+               void* out, int out_dtype, void* stream);
+
+/*
+ * Kernel family 1 -- fused unpack+dequant GEMV / skinny GEMM for decode
+ * (replaces the LinAlg thread-scope matvec thread_source, renderer/linalg.py:127-166,
+ * and the N=1 use of linalg_source through linalg.py:244-245).
+ *
+ *   Y[m, n] = sum_k X[m, k] * deq(W)[n, k]      0 <= m < M <= 16, 0 <= n < N
+ *
+ * W is packed [N, K] (K contiguous) with optional scales [N, ceil(K/block)].
+ * X element (m, k) lives at x + m*ldx + k (elements of x_dtype: BF16, F16 or F32).
+ * Y element (m, n) lives at y + m*ldy + n (y_dtype: BF16, F16 or F32).  Accumulation
+ * is fp32; the result is rounded once to y_dtype.
+ */
+int tgm_gemv(const void* w, int fmt, int64_t n, int64_t k,
+             const void* scales, int scale_dtype, int64_t block_size,
+             const void* x, int x_dtype, int64_t m, int64_t ldx,
+             void* y, int y_dtype, int64_t ldy, void* stream);
+
+/*
+ * Kernel family 2 -- prefill GEMM with packed weights and 16-bit activations
+ * (replaces the collective LinAlg GEMM linalg_source, renderer/linalg.py:38-124,
+ * for a packed weight operand; linalg.py:175-218).
+ *
+ *   C[m, n] = sum_k A[m, k] * deq(W)[n, k]
+ *
+ * A is BF16 [M, K] with row stride lda; W packed [N, K] with scales
+ * [N, ceil(K/block)]; C (c_dtype BF16, F16 or F32) with row stride ldc.  The packed
+ * weight is dequantised in registers to bf16 (exact for FP4/FP6/INT4 codes with E8M0
+ * or no scales) and fed to bf16 MFMA with fp32 accumulation.
+ */
+int tgm_gemm_w(const void* a, int a_dtype, int64_t m, int64_t lda,
+               const void* w, int fmt, int64_t n, int64_t k,
+               const void* scales, int scale_dtype, int64_t block_size,
+               void* c, int c_dtype, int64_t ldc, void* stream);
+
+/*
+ * Kernel family 2 -- block-scaled FP4/FP6 x FP4/FP6 GEMM on gfx950 scaled MFMA
+ * (replaces linalg_source for two packed operands, renderer/linalg.py:38-124;
+ * the reference decodes both to fp32 first, dx12.py:115-138).
+ *
+ *   C[m, n] = sum_k deq(A)[m, k] * deq(B)[n, k]
+ *
+ * A packed [M, K], B packed [N, K], both K contiguous with E8M0 scales per 32
+ * K-elements ([M, K/32] and [N, K/32]).  C (BF16, F16 or F32) row stride ldc.
+ */
+int tgm_gemm_mx(const void* a, int a_fmt, const void* a_scales, int64_t m,
+                const void* b, int b_fmt, const void* b_scales, int64_t n, int64_t k,
+                void* c, int c_dtype, int64_t ldc, void* stream);
+
+/*
+ * Exact-width GEMM for operands the families above do not cover (the reference's
+ * fallback lhs.matmul(rhs, dtype=...), linalg.py:169-174 and :219-223, with products
+ * formed at accumulator width as the DX12 device does, test_linalg.py:221-230).
+ *
+ *   C[m, n] = cast_c( sum_k acc(A[m, k]) * acc(B[k, n]) )
+ *
+ * Element (i, j) of A is at a + i*sa0 + j*sa1 (element strides), same for B and C.
+ * acc_dtype is one of F32, F64, I32, U32, I64, U64.
+ */
+int tgm_gemm_plain(const void* a, int a_dtype, int64_t sa0, int64_t sa1,
+                   const void* b, int b_dtype, int64_t sb0, int64_t sb1,
+                   void* c, int c_dtype, int64_t sc0, int64_t sc1,
+                   int64_t m, int64_t n, int64_t k, int acc_dtype, void* stream);
+
+/*
+ * Tensor-level pack with block scales (no reference counterpart: the reference only
+ * accepts pre-packed bytes, dx12.py:26-30; its packers are benchmark_dtypes.py:129-152).
+ * Quantises x [rows, k] (BF16, F16 or F32) along k to an MX float format with one
+ * E8M0 scale per ``block_size`` elements: shared exponent floor(log2(amax)) -
+ * emax_elem, elements rounded to nearest even and saturated.  Writes the packed
+ * bit stream (rows*k elements) to ``data`` and rows*ceil(k/block) bytes to ``scales``.
+ */
+int tgm_quantize_mx(const void* x, int x_dtype, int64_t rows, int64_t k, int fmt,
+                    int64_t block_size, void* data, void* scales, void* stream);
+
+/*
+ * Pack ``count`` payload codes (one per byte, low ``bits`` bits used) into the
+ * LSB-first bit stream (pack_payload, benchmark_dtypes.py:129-152).  ``out`` must hold
+ * ceil(count*bits/8) bytes; padding bits are zero.
+ */
+int tgm_pack_codes(const void* codes, int64_t count, int bits, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TGM_PACKED_H */

@@ -1,0 +1,225 @@
+"""GPU parity of the matrix path (gfx950 kernels through the C ABI) vs the oracle.
+
+Known-answer cases mirror the reference's test_linalg.py / test_packed.py; the random
+cases compare against the oracle's exactly dequantised weights with an fp64 product,
+max elementwise relative error <= 1e-2 (see packed_oracle.max_rel_err).
+"""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import packed_oracle as O
+from tinygrad_mi355x.codegen import linalg
+from tinygrad_mi355x.codegen.decomp.mi355x import FORMATS, PackedTensor, matmul as decomp_matmul
+from tinygrad_mi355x.codegen.linalg import matmul, matmul_nt, matvec
+
+pytestmark = pytest.mark.gpu
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
+TOL = 1e-2
+TORCH_DT = {"int8": torch.int8, "uint8": torch.uint8, "int32": torch.int32, "int64": torch.int64,
+            "uint64": torch.uint64, "float64": torch.float64, "float16": torch.float16, "float32": torch.float32}
+
+
+def bf16_np(t: torch.Tensor) -> np.ndarray:
+    return t.float().cpu().numpy()
+
+
+# ----------------------------------------------------------------------------- known answers
+def test_scales_stay_with_k_blocks(dev):
+    case = GOLDEN["scales_stay_with_k_blocks"]
+    packed = PackedTensor(torch.tensor(case["data"], dtype=torch.uint8, device=dev), case["format"], tuple(case["shape"]),
+                          torch.tensor(case["scales"], device=dev), block_size=case["block_size"])
+    rhs = torch.tensor(case["rhs"], device=dev)
+    assert decomp_matmul(packed, rhs).tolist() == case["expected"]
+    assert matmul(packed, rhs.float()).tolist() == case["expected"]
+
+
+def test_double_block_scales_matmul(dev):
+    case = GOLDEN["double_block_scales"]
+    packed = PackedTensor(torch.tensor(case["data"], dtype=torch.uint8, device=dev), case["format"], tuple(case["shape"]),
+                          torch.tensor(case["scales"], dtype=torch.float64, device=dev), block_size=case["block_size"])
+    out = decomp_matmul(packed, torch.tensor(case["rhs"], device=dev))
+    assert out.dtype is torch.float64 and out.tolist() == case["expected"]
+    assert matmul(packed, torch.tensor(case["rhs"], device=dev)).tolist() == case["expected"]
+
+
+def test_readme_uint4_matmul_and_matvec(dev):
+    case = GOLDEN["readme_uint4"]
+    packed = PackedTensor(torch.tensor(case["data"], dtype=torch.uint8, device=dev), "uint4", tuple(case["shape"]))
+    assert matmul(packed, torch.tensor(case["column"], device=dev)).tolist() == case["matmul"]
+    assert matvec(packed, torch.tensor(case["vector"], device=dev)).tolist() == case["matvec"]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.float8_e4m3fn, torch.float8_e5m2, torch.int8, torch.uint8])
+def test_matrix_tails(dev, dtype):
+    """Non-tile dimensions with exact integer arithmetic (test_linalg.py:11-20)."""
+    a = [[(i + k) % 5 for k in range(19)] for i in range(17)]
+    b = [[(k + j) % 3 for j in range(21)] for k in range(19)]
+    expected = [[sum(a[i][k] * b[k][j] for k in range(19)) for j in range(21)] for i in range(17)]
+    ta = torch.tensor(a, dtype=torch.float32).to(dtype).to(dev)
+    tb = torch.tensor(b, dtype=torch.float32).to(dtype).to(dev)
+    assert matmul(ta, tb).tolist() == expected
+
+
+def test_fp16_inputs_keep_fp32_accumulation(dev):
+    case = GOLDEN["fp16_accumulation"]
+    m = torch.tensor(case["matrix"], dtype=torch.float16, device=dev)
+    v = torch.tensor(case["vector"], dtype=torch.float16, device=dev)
+    result = matvec(m, v)
+    assert result.dtype is torch.float32 and result.tolist() == case["expected"]
+
+
+@pytest.mark.parametrize("case", GOLDEN["wide_matrix_fallback"]["cases"])
+def test_wide_matrix_fallback(dev, case):
+    dt = TORCH_DT[case["dtype"]]
+    a = torch.tensor([case["values"]], dtype=dt, device=dev)
+    b = torch.tensor([[1], [1], [1]], dtype=dt, device=dev)
+    result = matmul(a, b)
+    assert result.dtype is dt and result.tolist() == [[case["expected"]]]
+
+
+@pytest.mark.parametrize("case", GOLDEN["packed_integer_precision"]["cases"])
+def test_packed_integer_matmul_precision(dev, case):
+    dt = TORCH_DT[case["dtype"]]
+    weights = PackedTensor(torch.tensor([case["byte"]], dtype=torch.uint8, device=dev), case["format"], (1, 2))
+    output = weights.matmul(torch.tensor([[x] for x in case["values"]], dtype=dt, device=dev))
+    assert output.dtype is dt and output.tolist() == [[case["expected"]]]
+
+
+@pytest.mark.parametrize("scope", ["auto", "tiled"])
+@pytest.mark.parametrize("case", GOLDEN["accumulator_width"]["cases"])
+def test_matrix_product_uses_accumulator_width(dev, scope, case):
+    dt = TORCH_DT[case["dtype"]]
+    values = case["values"]
+    result = matmul(torch.tensor([values], dtype=dt, device=dev), torch.tensor([[x] for x in values], dtype=dt, device=dev),
+                    scope=scope)
+    assert result.dtype is {"int32": torch.int32, "uint32": torch.uint32}[case["acc"]]
+    assert result.tolist() == [[sum(x * x for x in values)]]
+
+
+def test_explicit_scope_without_native_kernel_raises(dev):
+    a = torch.ones((4, 4), dtype=torch.float64, device=dev)
+    with pytest.raises(RuntimeError, match="candidate rejected"):
+        matmul(a, a, scope="Wave")
+
+
+# ----------------------------------------------------------------------------- GEMV family
+def make_weight(dev, fmt, n, k, scale_kind, rng, bs=32):
+    bits = FORMATS[fmt][0]
+    codes = rng.integers(0, 1 << bits, (n, k)).astype(np.uint8)
+    data = torch.from_numpy(O.pack_codes(codes, bits)).to(dev)
+    nb = (k + bs - 1) // bs
+    if scale_kind == "e8m0":
+        e = (127 + rng.integers(-4, 3, (n, nb))).astype(np.uint8)
+        scales = torch.from_numpy(e).to(dev).view(torch.float8_e8m0fnu)
+        s_np = O.e8m0_decode(e)
+    elif scale_kind == "f16":
+        s_np = rng.uniform(0.005, 0.02, (n, nb)).astype(np.float16)
+        scales = torch.from_numpy(s_np).to(dev)
+    else:
+        scales, s_np = None, None
+    w = PackedTensor(data, fmt, (n, k), scales, bs)
+    deq = O.dequant_f64(O.pack_codes(codes, bits), fmt, (n, k), s_np, bs)
+    return w, deq
+
+
+@pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e2m3", "fp6_e3m2"])
+@pytest.mark.parametrize("m", [1, 4, 16])
+@pytest.mark.parametrize("nk", [(256, 512), (200, 384), (14336 // 8, 4096)])
+def test_gemv_mx_parity(dev, fmt, m, nk):
+    """Family 1 fast path: FP4/FP6 + E8M0/32, bf16 activations, bf16 out."""
+    n, k = nk
+    rng = np.random.default_rng(n * 31 + k + m)
+    w, deq = make_weight(dev, fmt, n, k, "e8m0", rng)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    y = matmul(w, x.t(), dtype=torch.bfloat16)  # [N, M] = W @ X^T
+    assert y.shape == (n, m) and y.dtype is torch.bfloat16
+    ref = O.matmul_reference(deq, bf16_np(x).T)
+    assert O.max_rel_err(bf16_np(y), ref) <= TOL
+    y2 = matmul_nt(x, w, dtype=torch.float32)  # [M, N]
+    assert O.max_rel_err(y2.cpu().numpy(), ref.T) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e2m3", "fp6_e3m2"])
+def test_gemv_one_hot_recovers_dequantised_weights_exactly(dev, fmt):
+    """x = e_j selects column j of deq(W): the fast path's in-register dequant must be exact."""
+    n, k = 64, 256
+    rng = np.random.default_rng(5)
+    w, deq = make_weight(dev, fmt, n, k, "e8m0", rng)
+    cols = [0, 1, 7, 31, 32, 100, 255]
+    x = torch.zeros((len(cols), k), dtype=torch.bfloat16, device=dev)
+    for i, j in enumerate(cols):
+        x[i, j] = 1.0
+    y = matmul_nt(x, w, dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(y, deq[:, cols].T.astype(np.float32))
+
+
+@pytest.mark.parametrize("fmt", list(FORMATS))
+@pytest.mark.parametrize("scale_kind", ["none", "f16", "e8m0"])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16, torch.float32])
+def test_gemv_general_parity(dev, fmt, scale_kind, xdt):
+    n, k, m = 96, 200, 3
+    rng = np.random.default_rng(17)
+    w, deq = make_weight(dev, fmt, n, k, scale_kind, rng)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(dev).to(xdt)
+    y = matmul_nt(x, w, dtype=torch.float32)
+    ref = O.matmul_reference(x.float().cpu().numpy(), deq.T)
+    assert O.max_rel_err(y.cpu().numpy(), ref) <= TOL
+
+
+def test_int4_config1_shape(dev):
+    """INT4 g32 fp16-scale GEMV, N=K=4096, x fp16 [1,4096] -> fp16."""
+    rng = np.random.default_rng(0)
+    x_np = rng.standard_normal((1, 4096)).astype(np.float16)
+    codes = rng.integers(-8, 8, (4096, 4096))
+    scales_np = rng.uniform(0.005, 0.02, (4096, 128)).astype(np.float16)
+    data = O.pack_codes((codes & 0xF).astype(np.uint8), 4)
+    w = PackedTensor(torch.from_numpy(data).to(dev), "int4", (4096, 4096), torch.from_numpy(scales_np).to(dev), 32)
+    x = torch.from_numpy(x_np).to(dev)
+    y = matvec(w, x[0], output_dtype=torch.float16)
+    deq = O.dequant_f64(data, "int4", (4096, 4096), scales_np, 32)
+    ref = deq @ x_np[0].astype(np.float64)
+    assert y.dtype is torch.float16 and O.max_rel_err(y.float().cpu().numpy(), ref) <= TOL
+
+
+def test_matvec_thread_true_uses_native_gemv(dev):
+    rng = np.random.default_rng(1)
+    w, deq = make_weight(dev, "fp4_e2m1", 128, 256, "e8m0", rng)
+    v = torch.from_numpy(rng.standard_normal(256).astype(np.float32)).to(dev).to(torch.bfloat16)
+    y = matvec(w, v, torch.float32, thread=True)
+    assert O.max_rel_err(y.cpu().numpy(), deq @ bf16_np(v).astype(np.float64)) <= TOL
+
+
+# ----------------------------------------------------------------------------- GEMM paths
+@pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e2m3", "fp6_e3m2"])
+def test_gemm_weight_parity(dev, fmt):
+    """Prefill-shaped (M > 16) packed-weight GEMM, C = A @ deq(W)^T."""
+    m, n, k = 96, 160, 256
+    rng = np.random.default_rng(21)
+    w, deq = make_weight(dev, fmt, n, k, "e8m0", rng)
+    a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    c = matmul_nt(a, w, dtype=torch.bfloat16)
+    assert O.max_rel_err(bf16_np(c), O.matmul_reference(bf16_np(a), deq.T)) <= TOL
+
+
+@pytest.mark.parametrize("fa,fb", [("fp4_e2m1", "fp4_e2m1"), ("fp6_e2m3", "fp4_e2m1"), ("fp6_e3m2", "fp6_e2m3")])
+def test_gemm_mx_parity(dev, fa, fb):
+    m, n, k = 64, 96, 256
+    rng = np.random.default_rng(23)
+    a, deq_a = make_weight(dev, fa, m, k, "e8m0", rng)
+    b, deq_b = make_weight(dev, fb, n, k, "e8m0", rng)
+    c = matmul_nt(a, b, dtype=torch.float32)
+    assert O.max_rel_err(c.cpu().numpy(), O.matmul_reference(deq_a, deq_b.T)) <= TOL
+
+
+def test_failures_are_cached_per_candidate(dev):
+    linalg.matrix_failures.clear()
+    rng = np.random.default_rng(2)
+    w, _ = make_weight(dev, "int4", 32, 64, "none", rng)
+    x = torch.ones((2, 64), dtype=torch.float64, device=dev)
+    out = matmul_nt(x, w)
+    assert out.dtype is torch.float64

@@ -1,0 +1,201 @@
+"""Host logic of the drop-in surface (CPU only): dtype rules, validation, registration,
+the no-CPU-fallback rule and the C-ABI library's exports."""
+
+import ctypes
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+
+import tinygrad_mi355x
+from tinygrad_mi355x import compat
+from tinygrad_mi355x import dtype as D
+from tinygrad_mi355x.codegen import linalg
+from tinygrad_mi355x.codegen.decomp.mi355x import FORMATS, FP8_CANDIDATES, PackedTensor, matrix_intermediate
+from tinygrad_mi355x.renderer.linalg import _accumulator
+from tinygrad_mi355x.runtime import kernels as K
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "tgm_packed.h"
+
+
+# ----------------------------------------------------------------------------- dtype lattice
+@pytest.mark.parametrize("a,b,expected", [
+    (torch.float32, torch.float16, torch.float32),
+    (torch.float32, torch.float64, torch.float64),
+    (torch.float16, torch.bfloat16, torch.float32),
+    (torch.float32, torch.float8_e8m0fnu, torch.float32),
+    (torch.float32, torch.int64, torch.float32),
+    (torch.int8, torch.float16, torch.float16),
+    (torch.int8, torch.int32, torch.int32),
+    (torch.uint8, torch.uint64, torch.uint64),
+    (torch.int8, torch.uint8, torch.int16),
+    (torch.float8_e4m3fn, torch.float8_e4m3fn, torch.float8_e4m3fn),
+])
+def test_least_upper_dtype(a, b, expected):
+    assert D.least_upper_dtype(a, b) is expected
+    assert D.least_upper_dtype(b, a) is expected
+
+
+@pytest.mark.parametrize("dt,expected", [
+    (torch.int8, torch.int32), (torch.uint8, torch.uint32), (torch.bool, torch.int32), (torch.float16, torch.float32),
+    (torch.bfloat16, torch.float32), (torch.float8_e4m3fn, torch.float32), (torch.float64, torch.float64),
+    (torch.int64, torch.int64), (torch.uint64, torch.uint64), (torch.float32, torch.float32),
+])
+def test_accumulator_widths(dt, expected):
+    """ARCHITECTURE.md:294-299; test_linalg.py:221-230 (int8->int32, uint8->uint32), :119-127 (fp16->fp32)."""
+    assert _accumulator(dt, dt) is expected
+
+
+# ----------------------------------------------------------------------------- PackedTensor
+def u8(values):
+    return torch.tensor(values, dtype=torch.uint8)
+
+
+@pytest.mark.parametrize("kwargs,message", [
+    (dict(data=u8([0]), format="int3", shape=(1,)), "unknown packed format"),
+    (dict(data=u8([0]), format="int4", shape=()), "nonnegative dimensions"),
+    (dict(data=u8([0]), format="int4", shape=(-1,)), "nonnegative dimensions"),
+    (dict(data=torch.zeros(2, dtype=torch.int8), format="int4", shape=(2,)), "flat uint8"),
+    (dict(data=torch.zeros((1, 2), dtype=torch.uint8), format="int4", shape=(2,)), "flat uint8"),
+    (dict(data=u8([0]), format="int4", shape=(3,)), "smaller than the declared shape"),
+    (dict(data=u8([0, 0]), format="fp6_e3m2", shape=(3,)), "smaller than the declared shape"),
+    (dict(data=u8([0]), format="int4", shape=(2,), block_size=0), "block size must be positive"),
+    (dict(data=u8([0, 0]), format="int4", shape=(1, 4), scales=torch.ones(1, 2), block_size=4), "incompatible shape"),
+    (dict(data=u8([0, 0]), format="int4", shape=(1, 4), scales=torch.ones(1, 1, device="meta"), block_size=4),
+     "incompatible shape or device"),
+])
+def test_packed_validation(kwargs, message):
+    """dx12.py:32-47: the same exception type and message for each rejected record."""
+    with pytest.raises(ValueError, match=message):
+        PackedTensor(**kwargs)
+
+
+def test_packed_accepts_exact_storage_and_scales():
+    p = PackedTensor(u8([0, 0, 0]), "fp6_e2m3", (4,))
+    assert p.shape == (4,) and p.bits == 6
+    s = PackedTensor(u8([0] * 5), "fp4_e2m1", (2, 5), torch.ones(2, 3), block_size=2)
+    assert s.default_dtype() is torch.float32
+    assert PackedTensor(u8([0]), "int4", (2,)).default_dtype() is torch.int32
+    assert PackedTensor(u8([0]), "fp4_e2m1", (1, 2), torch.ones(1, 2, dtype=torch.float64), 1).default_dtype() is torch.float64
+
+
+def test_formats_and_fp8_candidates():
+    assert FORMATS["fp6_e3m2"] == (6, 3, 2, 3) and FORMATS["fp4_e2m1"] == (4, 2, 1, 1)
+    assert FP8_CANDIDATES["fp6_e2m3"] == (torch.float8_e4m3fn,)
+
+
+def test_matrix_intermediate_preserves_activations():
+    """test_packed.py:118-124."""
+    weights = PackedTensor(u8([0]), "fp6_e2m3", (1, 1))
+    assert matrix_intermediate(torch.tensor([[1.125]], dtype=torch.float32), weights, True) is torch.float32
+    assert matrix_intermediate(weights, weights, True) is torch.float8_e4m3fn
+    fp4 = PackedTensor(u8([0]), "fp4_e2m1", (1, 1))
+    e3m2 = PackedTensor(u8([0]), "fp6_e3m2", (1, 1))
+    assert matrix_intermediate(fp4, e3m2) is torch.float8_e4m3fn
+    assert matrix_intermediate(fp4, torch.zeros(1, 1, dtype=torch.float8_e5m2)) is torch.float8_e5m2
+    assert matrix_intermediate(weights, torch.zeros(1, 1, dtype=torch.float8_e5m2)) is torch.float16
+
+
+def test_matrix_intermediate_promotion():
+    scaled = PackedTensor(u8([0]), "fp4_e2m1", (1, 2), torch.ones(1, 1, dtype=torch.float16))
+    assert matrix_intermediate(scaled, torch.zeros(2, 1, dtype=torch.bfloat16)) is torch.float32
+    wide = PackedTensor(u8([0]), "fp4_e2m1", (1, 2), torch.ones(1, 2, dtype=torch.float64), 1)
+    assert matrix_intermediate(wide, wide) is torch.float64
+    e8 = PackedTensor(u8([0]), "fp4_e2m1", (1, 2), torch.ones(1, 1).to(torch.float8_e8m0fnu))
+    assert matrix_intermediate(e8, e8) is torch.float32
+    int4 = PackedTensor(u8([0]), "int4", (1, 2))
+    assert matrix_intermediate(int4, torch.zeros(2, 1, dtype=torch.int32)) is torch.int32
+    assert matrix_intermediate(PackedTensor(u8([0]), "uint4", (1, 2)), torch.zeros(2, 1, dtype=torch.uint64)) is torch.uint64
+    assert matrix_intermediate(int4, torch.zeros(2, 1, dtype=torch.bfloat16)) is torch.bfloat16
+
+
+# ----------------------------------------------------------------------------- linalg validation
+def test_matmul_argument_errors():
+    a = torch.zeros(2, 3)
+    with pytest.raises(ValueError, match="unknown matrix scope"):
+        linalg.matmul(a, torch.zeros(3, 2), scope="Warp")
+    with pytest.raises(ValueError, match="compatible rank-two"):
+        linalg.matmul(a, torch.zeros(2, 3))
+    with pytest.raises(ValueError, match="compatible rank-two"):
+        linalg.matmul(torch.zeros(3), torch.zeros(3, 2))
+    with pytest.raises(ValueError, match="one device"):
+        linalg.matmul(a, torch.zeros(3, 2, device="meta"))
+    with pytest.raises(ValueError, match="tile dimensions"):
+        linalg.matmul(a, torch.zeros(3, 2), tile=(16, 0, 16))
+    with pytest.raises(ValueError, match="matvec expects"):
+        linalg.matvec(a, torch.zeros(2))
+    with pytest.raises(ValueError, match="compatible rank-two"):
+        linalg.matmul_nt(a, torch.zeros(3, 2))
+
+
+def test_empty_operands_need_no_kernel():
+    out = linalg.matmul(torch.zeros(2, 0), torch.zeros(0, 3))
+    assert out.shape == (2, 3) and out.dtype is torch.float32 and not out.any()
+    assert linalg.matmul(torch.zeros(0, 4), torch.zeros(4, 3)).shape == (0, 3)
+
+
+def test_no_cpu_fallback():
+    """CPU tensors never compute on the host: the product raises instead."""
+    with pytest.raises(RuntimeError, match="HIP device"):
+        PackedTensor(u8([0x21, 0x43]), "uint4", (2, 2)).unpack()
+    with pytest.raises(RuntimeError, match="HIP device"):
+        linalg.matmul(torch.ones(2, 2), torch.ones(2, 2))
+    with pytest.raises(RuntimeError, match="HIP device"):
+        linalg.matmul(PackedTensor(u8([0x21, 0x43]), "uint4", (2, 2)), torch.ones(2, 1))
+
+
+# ----------------------------------------------------------------------------- registration
+def test_register_is_idempotent_and_opens_no_hardware():
+    assert compat.registered() and compat.DEVICES[0] == "MI355X"
+    before = list(compat.DEVICES)
+    tinygrad_mi355x.register()
+    tinygrad_mi355x.register()
+    assert compat.DEVICES == before
+    code = ("import sys; sys.path.insert(0, %r); import torch, tinygrad_mi355x; "
+            "assert not torch.cuda.is_initialized(); print('ok')" % str(ROOT / "tinygrad-dx12_amd"))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert out.stdout.strip() == "ok", out.stderr
+
+
+# ----------------------------------------------------------------------------- C ABI
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(tgm_\w+)\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = K.load_library()
+    names = declared_functions()
+    assert {"tgm_unpack", "tgm_gemv", "tgm_gemm_w", "tgm_gemm_mx", "tgm_gemm_plain"} <= set(names)
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(K.EXPORTS) == set(names)
+    assert lib.tgm_abi_version() == K.ABI_VERSION
+
+
+def test_invalid_arguments_are_rejected_without_a_gpu():
+    """Argument validation runs on the host and maps to ValueError (no kernel is launched)."""
+    with pytest.raises(ValueError, match="unknown packed format"):
+        K.call("tgm_unpack", None, 0, 9, 1, 1, None, -1, 32, None, 13, None)
+    with pytest.raises(ValueError, match="smaller than the declared shape"):
+        K.call("tgm_unpack", None, 1, 0, 3, 3, None, -1, 32, None, 13, None)
+    with pytest.raises(ValueError, match="M must be <= 16"):
+        K.call("tgm_gemv", None, 2, 16, 128, None, -1, 32, None, 12, 17, 128, None, 12, 16, None)
+    with pytest.raises(ValueError, match="FP4/FP6 format"):
+        K.call("tgm_quantize_mx", None, 13, 1, 32, 0, 32, None, None, None)
+    with pytest.raises(ValueError, match="4 or 6 bits"):
+        K.call("tgm_pack_codes", None, 4, 5, None, None)
+    assert K.load_library().tgm_last_error().decode().startswith("pack width")
+
+
+def test_header_enums_match_binding():
+    text = HEADER.read_text()
+    for name, value in K.FORMAT_IDS.items():
+        enum = {"int4": "INT4", "uint4": "UINT4", "fp4_e2m1": "FP4_E2M1", "fp6_e2m3": "FP6_E2M3", "fp6_e3m2": "FP6_E3M2"}[name]
+        assert re.search(rf"TGM_FMT_{enum} = {value},", text)
+    assert "TGM_E8M0 = 15" in text and K.DTYPE_IDS[torch.float8_e8m0fnu] == 15
+    assert "TGM_BF16 = 12" in text and K.DTYPE_IDS[torch.bfloat16] == 12

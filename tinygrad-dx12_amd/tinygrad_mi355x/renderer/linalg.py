@@ -1,0 +1,47 @@
+"""Fixed gfx950 matrix-kernel table and accumulator policy.
+
+The reference asks the D3D12 runtime at run time which LinAlg operations exist
+(alexandreteles/tinygrad-dx12 src/tinygrad_dx12/codegen/linalg.py:18-34, :90-133;
+runtime/support/dx12.py:298-336) and renders HLSL for the accepted one
+(renderer/linalg.py:38-166).  On MI355X the set of kernels is known at build time,
+so selection is a static table over operand kinds; the kernels themselves are
+compiled into libtgm_mi355x.so.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from tinygrad_mi355x import dtype as D
+
+
+def _accumulator(a: torch.dtype, b: torch.dtype) -> torch.dtype:
+    """Default matrix accumulator: strong(sum_acc(strong(least_upper(a, b)))) (renderer/linalg.py:33-35)."""
+    return D.strong_dtype(D.sum_acc_dtype(D.strong_dtype(D.least_upper_dtype(a, b))))
+
+
+@dataclass(frozen=True)
+class MatrixKernel:
+    """One native kernel family: the scope name it answers to, its tile and workgroup size."""
+
+    name: str  # C-ABI entry point
+    scope: str  # reference scope it replaces
+    tile: tuple[int, int, int]  # (rows of W / C per workgroup, activation rows, K per step)
+    threads: int
+
+
+# Family 1: fused dequant GEMV / skinny GEMM (replaces thread_source and the N=1 linalg_source).
+GEMV = MatrixKernel("tgm_gemv", "Wave", (16, 16, 128), 256)
+# Family 2: dequant-to-bf16 MFMA GEMM (replaces linalg_source for one packed operand).
+GEMM_W = MatrixKernel("tgm_gemm_w", "ThreadGroup", (256, 256, 64), 256)
+# Family 2: block-scaled FP4/FP6 MFMA GEMM (two packed MX operands).
+GEMM_MX = MatrixKernel("tgm_gemm_mx", "ThreadGroup", (256, 256, 128), 256)
+# Exact-width fallback (the reference's ordinary matmul); never a "native" candidate.
+PLAIN = MatrixKernel("tgm_gemm_plain", "tiled", (16, 16, 1), 256)
+
+GEMV_MAX_ROWS = 16
+ACTIVATION_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+OUTPUT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+WEIGHT_SCALE_DTYPES = (torch.float8_e8m0fnu, torch.float16, torch.bfloat16, torch.float32)
