@@ -15,6 +15,8 @@
 //    reference's products exactly; only the summation order differs.
 //  * gemv_valu  -- every other combination: fp32 dequant (code*scale rounded in fp32,
 //    dx12.py:105) and fp32 FMA, one wave per output row.
+#include <stdlib.h>
+
 #include "tgm_common.h"
 
 namespace tgm {
@@ -60,11 +62,7 @@ __global__ void __launch_bounds__(256) gemv_valu(const uint8_t* __restrict__ w, 
 }
 
 // ------------------------------------------------------------------ MFMA GEMV
-// Work decomposition: one workgroup of 4 waves per 16 weight rows; the K axis is cut
-// into 128-element super-steps and wave w takes super-steps w, w+4, w+8, ...; the four
-// partial 16x16 tiles are summed through LDS at the end.
-//
-// Inside a super-step, lane l (row r = l & 15 of the tile, lane group q = l >> 4) owns
+// Inside a 128-element K super-step, lane l (row r = l & 15 of the tile, lane group q = l >> 4) owns
 // the 32 consecutive K elements [32q, 32q+32) of the super-step: one 16-byte load for
 // FP4 (24 bytes for FP6) and exactly one E8M0 scale (block 32).  MFMA s (s = 0..3) of
 // the super-step consumes elements [32q + 8s, 32q + 8s + 8) of every lane group, so
@@ -94,6 +92,13 @@ __device__ __forceinline__ void dequant32(const unsigned* codes, float scale, bf
   }
 }
 
+// GEMV results are bf16, f16 or f32 (checked on the host); one rounding from fp32.
+__device__ __forceinline__ void store_out(void* y, int ydt, int64_t i, float v) {
+  if (ydt == TGM_BF16) ((uint16_t*)y)[i] = f32_to_bf16(v);
+  else if (ydt == TGM_F16) ((_Float16*)y)[i] = (_Float16)v;
+  else ((float*)y)[i] = v;
+}
+
 template <int FMT>
 struct MfmaGemvTraits {
   static constexpr int kStepBytes = FMT == TGM_FMT_FP4_E2M1 ? 64 : 96;  // bytes per row per super-step
@@ -102,67 +107,147 @@ struct MfmaGemvTraits {
 };
 
 template <int FMT>
-__device__ __forceinline__ void load_codes(const uint8_t* p, bool ok, unsigned out[6]) {
+__device__ __forceinline__ void load_codes(const uint8_t* p, unsigned out[6]) {
   if constexpr (FMT == TGM_FMT_FP4_E2M1) {
-    u32x4 v = ok ? *(const u32x4*)p : u32x4{0, 0, 0, 0};
+    const u32x4 v = *(const u32x4*)p;
     out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3]; out[4] = 0; out[5] = 0;
   } else {
-    u32x2 a = ok ? *(const u32x2*)p : u32x2{0, 0};
-    u32x2 b = ok ? *(const u32x2*)(p + 8) : u32x2{0, 0};
-    u32x2 c = ok ? *(const u32x2*)(p + 16) : u32x2{0, 0};
+    const u32x2 a = *(const u32x2*)p;
+    const u32x2 b = *(const u32x2*)(p + 8);
+    const u32x2 c = *(const u32x2*)(p + 16);
     out[0] = a[0]; out[1] = a[1]; out[2] = b[0]; out[3] = b[1]; out[4] = c[0]; out[5] = c[1];
   }
 }
 
-template <int FMT>
-__global__ void __launch_bounds__(256) gemv_mfma(const uint8_t* __restrict__ w, int64_t N, int64_t K,
-                                                 const uint8_t* __restrict__ scales, int64_t nblk, int64_t bs,
-                                                 const __bf16* __restrict__ x, int M, int64_t ldx,
-                                                 void* __restrict__ y, int ydt, int64_t ldy) {
+// Work decomposition: one workgroup of NW waves per 16 weight rows; the K axis is cut
+// into 128-element super-steps and wave w owns a contiguous range of them.  Each wave
+// walks its range in chunks of PF super-steps: every weight and scale load of the next
+// chunk is issued before the MFMAs of the current chunk, so a wave keeps PF x 16 bytes
+// (FP4) per lane in flight.  Activations (M rows) are staged once per workgroup in LDS
+// when they fit (XLDS); the NW partial tiles are summed through LDS at the end.
+// Loads are unconditional: rows past N and super-steps past the wave's range read a
+// clamped (valid) address and their results are discarded, so no load sits behind a
+// branch and every load of a chunk is in flight before the first wait.
+template <int FMT, int PF>
+__device__ __forceinline__ void load_chunk(const uint8_t* wrow, const uint8_t* srow, int sshift, int q, int t0,
+                                           int t_last, unsigned codes[PF][6], uint32_t sraw[PF]) {
   using T = MfmaGemvTraits<FMT>;
-  __shared__ float partial[4][64][4];
+#pragma unroll
+  for (int j = 0; j < PF; ++j) {
+    const int t = t0 + j < t_last ? t0 + j : t_last;
+    load_codes<FMT>(wrow + (int64_t)t * T::kStepBytes, codes[j]);
+  }
+  if (srow) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int t = t0 + j < t_last ? t0 + j : t_last;
+      sraw[j] = srow[(t * 128 + q * 32) >> sshift];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < PF; ++j) sraw[j] = 127u;  // 2^0
+  }
+}
+
+template <int FMT, int NW, int PF, bool XLDS>
+__global__ void __launch_bounds__(NW * 64) gemv_mfma(const uint8_t* __restrict__ w, int64_t N, int64_t K,
+                                                     const uint8_t* __restrict__ scales, int64_t nblk, int sshift,
+                                                     const __bf16* __restrict__ x, int M, int64_t ldx,
+                                                     void* __restrict__ y, int ydt, int64_t ldy) {
+  using T = MfmaGemvTraits<FMT>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  float* partial = (float*)smem;                     // [NW][64][4]
+  __bf16* xs = (__bf16*)(smem + NW * 64 * 4 * 4);    // [M + 1][K + 8] when XLDS; row M is zero
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int64_t n0 = (int64_t)blockIdx.x * 16;
-  const int64_t row = n0 + r;
-  const bool row_ok = row < N;
+  const int64_t row = n0 + r < N ? n0 + r : N - 1;  // clamped: rows >= N are computed but not stored
   const int64_t row_bytes = K * format_info(FMT).bits / 8;
   const uint8_t* wrow = w + row * row_bytes + q * T::kLaneBytes;
   const uint8_t* srow = scales ? scales + row * nblk : nullptr;
-  const int c = lane & 15;  // activation row handled by this lane in the B operand
+  const int S = (int)(K / 128);
+  const int per = (S + NW - 1) / NW;
+  const int t_begin = wave * per < S ? wave * per : S;
+  const int t_end = t_begin + per < S ? t_begin + per : S;
+  const int c = lane & 15;  // activation row of this lane in the B operand
   const bool x_ok = c < M;
-  const __bf16* xrow = x + (int64_t)c * ldx + q * 32;
-  const int steps = (int)(K / 128);
+  const int64_t xstride = K + 8;
+  const int t_last = t_end > t_begin ? t_end - 1 : t_begin < S ? t_begin : S - 1;
 
+  unsigned cur[PF][6];
+  uint32_t s_cur[PF];
+  load_chunk<FMT, PF>(wrow, srow, sshift, q, t_begin, t_last, cur, s_cur);
+  const __bf16* xrow = x + (int64_t)(x_ok ? c : 0) * ldx;
+  if constexpr (XLDS) {
+    const int64_t total = (int64_t)M * K;
+    for (int64_t e = (int64_t)threadIdx.x * 8; e < total; e += NW * 64 * 8) {
+      const int64_t m = e / K, kk = e - m * K;
+      *(u32x4*)(xs + m * xstride + kk) = *(const u32x4*)(x + m * ldx + kk);
+    }
+    for (int64_t kk = (int64_t)threadIdx.x * 8; kk < K; kk += NW * 64 * 8)
+      *(u32x4*)(xs + (int64_t)M * xstride + kk) = u32x4{0, 0, 0, 0};
+    __syncthreads();
+  }
+  const __bf16* xl = xs + (int64_t)(x_ok ? c : M) * xstride;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int t = wave; t < steps; t += 4) {
-    unsigned codes[6];
-    load_codes<FMT>(wrow + (int64_t)t * T::kStepBytes, row_ok, codes);
-    float scale = 1.0f;
-    if (srow && row_ok) scale = e8m0_to_float(srow[(t * 128 + q * 32) / bs]);
-    bf16x8 a[4];
-    dequant32<FMT>(codes, scale, a);
-    const __bf16* xp = xrow + (int64_t)t * 128;
+  for (int t0 = t_begin; t0 < t_end; t0 += PF) {
+    unsigned nxt[PF][6];
+    uint32_t s_nxt[PF];
+    const bool more = t0 + PF < t_end;
+    if (more) load_chunk<FMT, PF>(wrow, srow, sshift, q, t0 + PF, t_last, nxt, s_nxt);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      bf16x8 b = x_ok ? *(const bf16x8*)(xp + 8 * s) : bf16x8{};
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s], b, acc, 0, 0, 0);
+    for (int j = 0; j < PF; ++j) {
+      const int t = t0 + j;
+      if (t < t_end) {
+        bf16x8 a[4];
+        dequant32<FMT>(cur[j], e8m0_to_float(s_cur[j]), a);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int64_t kk = (int64_t)t * 128 + q * 32 + 8 * s;
+          bf16x8 b;
+          if constexpr (XLDS) {
+            b = *(const bf16x8*)(xl + kk);
+          } else {
+            b = *(const bf16x8*)(xrow + kk);
+            if (!x_ok) b = bf16x8{};
+          }
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s], b, acc, 0, 0, 0);
+        }
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int j = 0; j < PF; ++j) {
+        s_cur[j] = s_nxt[j];
+#pragma unroll
+        for (int d = 0; d < 6; ++d) cur[j][d] = nxt[j][d];
+      }
     }
   }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) partial[wave][lane][i] = acc[i];
-  __syncthreads();
-  if (wave == 0) {
-    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sum[i] += partial[ww][lane][i];
+  if constexpr (NW == 1) {
     if (c < M) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t n = n0 + 4 * q + i;
-        if (n < N) store_from_f32(y, ydt, (int64_t)c * ldy + n, sum[i]);
+        if (n < N) store_out(y, ydt, (int64_t)c * ldy + n, acc[i]);
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) partial[(wave * 64 + lane) * 4 + i] = acc[i];
+  __syncthreads();
+  if (wave == 0) {
+    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sum[i] += partial[(ww * 64 + lane) * 4 + i];
+    if (c < M) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t n = n0 + 4 * q + i;
+        if (n < N) store_out(y, ydt, (int64_t)c * ldy + n, sum[i]);
       }
     }
   }
@@ -172,11 +257,50 @@ __global__ void __launch_bounds__(256) gemv_mfma(const uint8_t* __restrict__ w, 
 
 using namespace tgm;
 
+static int gemv_waves() {
+  static int cached = 0;
+  if (!cached) {
+    const char* v = getenv("TGM_GEMV_WAVES");
+    const int n = v ? atoi(v) : 4;
+    cached = (n == 1 || n == 2 || n == 4 || n == 8) ? n : 4;
+  }
+  return cached;
+}
+
+template <int FMT, int NW, bool XLDS>
+static void launch_gemv_variant(unsigned grid, size_t lds, hipStream_t s, const void* w, int64_t n, int64_t k,
+                                const void* scales, int64_t nblk, int64_t bs, const void* x, int64_t m, int64_t ldx,
+                                void* y, int ydt, int64_t ldy) {
+  constexpr int PF = 8;
+  const int sshift = __builtin_ctzll((unsigned long long)bs);
+  hipLaunchKernelGGL((gemv_mfma<FMT, NW, PF, XLDS>), dim3(grid), dim3(NW * 64), lds, s, (const uint8_t*)w, n, k,
+                     (const uint8_t*)scales, nblk, sshift, (const __bf16*)x, (int)m, ldx, y, ydt, ldy);
+}
+
+template <int FMT>
+static int launch_gemv_mfma(int nw, bool xlds, unsigned grid, size_t lds, hipStream_t s, const void* w, int64_t n,
+                            int64_t k, const void* scales, int64_t nblk, int64_t bs, const void* x, int64_t m,
+                            int64_t ldx, void* y, int ydt, int64_t ldy) {
+#define TGM_GEMV_CASE(NW)                                                                                       \
+  if (nw == NW) {                                                                                               \
+    if (xlds) launch_gemv_variant<FMT, NW, true>(grid, lds, s, w, n, k, scales, nblk, bs, x, m, ldx, y, ydt, ldy);  \
+    else launch_gemv_variant<FMT, NW, false>(grid, lds, s, w, n, k, scales, nblk, bs, x, m, ldx, y, ydt, ldy);      \
+    return TGM_OK;                                                                                              \
+  }
+  TGM_GEMV_CASE(1)
+  TGM_GEMV_CASE(2)
+  TGM_GEMV_CASE(4)
+  TGM_GEMV_CASE(8)
+#undef TGM_GEMV_CASE
+  return TGM_E_INVALID;
+}
+
 static bool mfma_gemv_ok(const void* w, int fmt, int64_t k, const void* scales, int sdt, int64_t bs, const void* x,
                          int xdt, int64_t ldx, int ydt) {
   if (fmt != TGM_FMT_FP4_E2M1 && fmt != TGM_FMT_FP6_E2M3 && fmt != TGM_FMT_FP6_E3M2) return false;
   if (xdt != TGM_BF16 || k % 128 != 0 || ldx % 8 != 0) return false;
-  if (scales && (sdt != TGM_E8M0 || bs % 32 != 0)) return false;
+  if (scales && (sdt != TGM_E8M0 || bs < 32 || (bs & (bs - 1)) != 0)) return false;
+  if (k >= (1ll << 30)) return false;
   if (ydt != TGM_BF16 && ydt != TGM_F16 && ydt != TGM_F32) return false;
   const uintptr_t align = fmt == TGM_FMT_FP4_E2M1 ? 16 : 8;
   if ((uintptr_t)w % align || (uintptr_t)x % 16) return false;
@@ -202,20 +326,17 @@ extern "C" int tgm_gemv(const void* w, int fmt, int64_t n, int64_t k, const void
   }
   if (mfma_gemv_ok(w, fmt, k, scales, scale_dtype, block_size, x, x_dtype, ldx, y_dtype)) {
     const unsigned grid = (unsigned)((n + 15) / 16);
+    const int64_t xlds_bytes = (m + 1) * (k + 8) * 2;
+    const bool xlds = xlds_bytes <= 48 * 1024;
+    const int nw = gemv_waves();
+    const size_t lds = (size_t)nw * 64 * 4 * 4 + (xlds ? (size_t)xlds_bytes : 0);
+    int st = TGM_OK;
     switch (fmt) {
-      case TGM_FMT_FP4_E2M1:
-        hipLaunchKernelGGL(gemv_mfma<TGM_FMT_FP4_E2M1>, dim3(grid), dim3(256), 0, s, (const uint8_t*)w, n, k,
-                           (const uint8_t*)scales, nblk, block_size, (const __bf16*)x, (int)m, ldx, y, y_dtype, ldy);
-        break;
-      case TGM_FMT_FP6_E2M3:
-        hipLaunchKernelGGL(gemv_mfma<TGM_FMT_FP6_E2M3>, dim3(grid), dim3(256), 0, s, (const uint8_t*)w, n, k,
-                           (const uint8_t*)scales, nblk, block_size, (const __bf16*)x, (int)m, ldx, y, y_dtype, ldy);
-        break;
-      default:
-        hipLaunchKernelGGL(gemv_mfma<TGM_FMT_FP6_E3M2>, dim3(grid), dim3(256), 0, s, (const uint8_t*)w, n, k,
-                           (const uint8_t*)scales, nblk, block_size, (const __bf16*)x, (int)m, ldx, y, y_dtype, ldy);
-        break;
+      case TGM_FMT_FP4_E2M1: st = launch_gemv_mfma<TGM_FMT_FP4_E2M1>(nw, xlds, grid, lds, s, w, n, k, scales, nblk, block_size, x, m, ldx, y, y_dtype, ldy); break;
+      case TGM_FMT_FP6_E2M3: st = launch_gemv_mfma<TGM_FMT_FP6_E2M3>(nw, xlds, grid, lds, s, w, n, k, scales, nblk, block_size, x, m, ldx, y, y_dtype, ldy); break;
+      default: st = launch_gemv_mfma<TGM_FMT_FP6_E3M2>(nw, xlds, grid, lds, s, w, n, k, scales, nblk, block_size, x, m, ldx, y, y_dtype, ldy); break;
     }
+    if (st != TGM_OK) return st;
     return launch_status("tgm_gemv(mfma)");
   }
   const int64_t wbytes = (n * k * format_info(fmt).bits + 7) / 8;
