@@ -144,6 +144,48 @@ def test_gemv_mx_parity(dev, fmt, m, nk):
     assert O.max_rel_err(y2.cpu().numpy(), ref.T) <= TOL
 
 
+@pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e3m2"])
+@pytest.mark.parametrize("nkm", [(12288, 2048, 1), (6144, 4096, 4), (4096, 14336, 1), (2048, 3584, 2),
+                                 (256, 14336, 16), (1000, 4096, 16), (64, 1536, 7)])
+def test_gemv_mx_launch_shapes(dev, fmt, nkm):
+    """Every workgroup shape of the streaming GEMV (4x2, 2x4, 1x8 tiles x K slices), exact and
+    guarded slices, activations in LDS and from global memory (M x K too large for LDS)."""
+    n, k, m = nkm
+    rng = np.random.default_rng(n + k + m)
+    w, deq = make_weight(dev, fmt, n, k, "e8m0", rng)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    y = matmul_nt(x, w, dtype=torch.bfloat16)
+    ref = bf16_np(x).astype(np.float64) @ deq.T
+    assert O.max_rel_err(bf16_np(y), ref) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e2m3"])
+def test_gemv_e8m0_extreme_scales(dev, fmt):
+    """E8M0 bytes at the ends of the range: 255 is NaN and poisons its rows; 1..3 give
+    bf16 values down to 2^-128, which the MFMA path must keep (no flush to zero)."""
+    n, k = 48, 1024
+    rng = np.random.default_rng(11)
+    bits = FORMATS[fmt][0]
+    codes = rng.integers(0, 1 << bits, (n, k)).astype(np.uint8)
+    e = (127 + rng.integers(-4, 3, (n, k // 32))).astype(np.uint8)
+    e[3, 5] = 255
+    e[10, :] = 1  # whole row at the bottom of the range
+    e[11, ::2] = 2
+    e[12, 7] = 3
+    data = O.pack_codes(codes, bits)
+    w = PackedTensor(torch.from_numpy(data).to(dev), fmt, (n, k), torch.from_numpy(e).to(dev).view(torch.float8_e8m0fnu), 32)
+    x = torch.from_numpy(rng.standard_normal((2, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    y = matmul_nt(x, w, dtype=torch.float32).cpu().numpy()  # [2, n]
+    deq = O.dequant_f64(data, fmt, (n, k), O.e8m0_decode(e), 32)
+    ref = bf16_np(x).astype(np.float64) @ deq.T
+    assert np.array_equal(np.isnan(y), np.isnan(ref)) and np.isnan(y[:, 3]).all()
+    ok = ~np.isnan(ref)
+    for row in (10, 11, 12):  # tiny rows: relative error of the row itself
+        r = ref[:, row]
+        assert np.abs(y[:, row] - r).max() <= 1e-2 * np.abs(r).max()
+    assert O.max_rel_err(np.where(ok, y, 0), np.where(ok, ref, 0)) <= TOL
+
+
 @pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e2m3", "fp6_e3m2"])
 def test_gemv_one_hot_recovers_dequantised_weights_exactly(dev, fmt):
     """x = e_j selects column j of deq(W): the fast path's in-register dequant must be exact."""
