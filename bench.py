@@ -42,6 +42,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run --steps device-to-device copies of MIB MiB (reference for HBM byte counters)")
     return p.parse_args()
 
 
@@ -122,6 +124,18 @@ def int4_gemv_workload(torch, K, dev, steps: int, warmup: int, copies: int = 40)
             "GB/s": nbytes / ms / 1e6, "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
 
 
+def measured_traffic(profile: str) -> int | None:
+    """HBM bytes per launch of the dominant kernel from its committed rocprofv3 summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by a plain copy of known size)."""
+    path = ROOT / "profiles" / profile
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch="):
+            return int(line.split("=", 1)[1])
+    return None
+
+
 def cpu_baseline(budget_s: float) -> dict:
     """The reference CPU path restated in C (oracle/cpu_path.c), timed on the host cores."""
     import numpy as np
@@ -158,6 +172,18 @@ def cpu_baseline(budget_s: float) -> dict:
                       f"median of {len(times)} runs, {med * 1e3:.1f} ms each"}
 
 
+def copy_calibration(torch, mib: int, steps: int) -> None:
+    """Plain device copies of a known size: FETCH_SIZE / WRITE_SIZE per dispatch of this copy
+    kernel calibrate the counters against bytes actually moved."""
+    n = mib << 20
+    src = torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "steps": steps}))
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -168,6 +194,9 @@ def main() -> int:
     from tinygrad_mi355x.runtime import kernels as K
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        copy_calibration(torch, args.copy_calibration, args.steps)
+        return 0
     K.load_library()
     torch.cuda.synchronize()
     wall = time.perf_counter()
@@ -197,7 +226,8 @@ def main() -> int:
         "config": {"workload": primary["workload"], "N": 14336, "K": 4096, "M": 1, "block": 32,
                    "launch": "hip graph of the timed steps", "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("gemv_fp4_e2m1_n14336_k4096_m1.txt")},
         "cpu_baseline": cpu,
         "workloads": {name: {k: (round(v, 6) if isinstance(v, float) else v) for k, v in w.items()}
                       for name, w in workloads.items()},
