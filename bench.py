@@ -136,6 +136,40 @@ def measured_traffic(profile: str) -> int | None:
     return None
 
 
+def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup: int):
+    """FP4 x FP4 + E8M0/32 GEMM C[M,N] = deq(A) deq(B)^T, bf16 out, timed with HIP events on
+    the launch stream (each launch is long enough that launch overhead is negligible)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    a = torch.randint(0, 256, (m * k // 2,), dtype=torch.uint8, device=dev, generator=g)
+    b = torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device=dev, generator=g)
+    sa = torch.randint(123, 130, (m, k // 32), dtype=torch.uint8, device=dev, generator=g)
+    sb = torch.randint(123, 130, (n, k // 32), dtype=torch.uint8, device=dev, generator=g)
+    c = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    fp4, bf16 = K.FORMAT_IDS["fp4_e2m1"], K.DTYPE_IDS[torch.bfloat16]
+    lib = K.load_library()
+    stream = torch.cuda.current_stream(dev)
+
+    def launch() -> None:
+        K.check("tgm_gemm_mx", lib.tgm_gemm_mx(a.data_ptr(), fp4, sa.data_ptr(), m, b.data_ptr(), fp4, sb.data_ptr(), n, k,
+                                               c.data_ptr(), bf16, n, stream.cuda_stream))
+
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        launch()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    tflops = 2 * m * n * k / ms / 1e9
+    nbytes = (m + n) * k // 2 + (m + n) * k // 32 + m * n * 2
+    return {"workload": f"fp4xfp4 e8m0/32 GEMM M={m} N={n} K={k} bf16 out", "ms": ms, "TFLOPS": tflops,
+            "mfma_frac": tflops / FP4_PEAK_TFLOPS, "bytes": nbytes, "GB/s": nbytes / ms / 1e6}
+
+
 def cpu_baseline(budget_s: float) -> dict:
     """The reference CPU path restated in C (oracle/cpu_path.c), timed on the host cores."""
     import numpy as np
@@ -206,6 +240,8 @@ def main() -> int:
         for m in (4, 16):
             workloads[f"fp4_gemv_m{m}"] = fp4_gemv_workload(torch, K, dev, m, max(args.steps // 2, 1), args.warmup)
         workloads["int4_gemv_cfg1"] = int4_gemv_workload(torch, K, dev, max(args.steps // 2, 1), args.warmup)
+        workloads["fp4_gemm_8192"] = fp4_gemm_workload(torch, K, dev, 8192, 8192, 8192, 10, 3)
+        workloads["fp4_gemm_4096x14336x4096"] = fp4_gemm_workload(torch, K, dev, 4096, 14336, 4096, 10, 3)
     torch.cuda.synchronize()
     gpu_wall = time.perf_counter() - wall
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)

@@ -14,7 +14,7 @@ import torch
 
 import packed_oracle as O
 from tinygrad_mi355x.codegen import linalg
-from tinygrad_mi355x.codegen.decomp.mi355x import FORMATS, PackedTensor, matmul as decomp_matmul
+from tinygrad_mi355x.codegen.decomp.mi355x import FORMATS, PackedTensor, matmul as decomp_matmul, quantize_mx
 from tinygrad_mi355x.codegen.linalg import matmul, matmul_nt, matvec
 
 pytestmark = pytest.mark.gpu
@@ -256,6 +256,52 @@ def test_gemm_mx_parity(dev, fa, fb):
     b, deq_b = make_weight(dev, fb, n, k, "e8m0", rng)
     c = matmul_nt(a, b, dtype=torch.float32)
     assert O.max_rel_err(c.cpu().numpy(), O.matmul_reference(deq_a, deq_b.T)) <= TOL
+
+
+@pytest.mark.parametrize("mnk", [(256, 256, 256), (300, 520, 512), (1000, 777, 768), (40, 1100, 1024), (513, 33, 256)])
+@pytest.mark.parametrize("cdt", [torch.bfloat16, torch.float16, torch.float32])
+def test_gemm_mx_fp4_tiles_and_tails(dev, mnk, cdt):
+    """FP4 x FP4 scaled-MFMA GEMM: whole and ragged 256 x 256 tiles, every output dtype."""
+    m, n, k = mnk
+    rng = np.random.default_rng(m * 7 + n + k)
+    a, deq_a = make_weight(dev, "fp4_e2m1", m, k, "e8m0", rng)
+    b, deq_b = make_weight(dev, "fp4_e2m1", n, k, "e8m0", rng)
+    c = matmul_nt(a, b, dtype=cdt)
+    assert c.dtype is cdt and c.shape == (m, n)
+    assert O.max_rel_err(c.float().cpu().numpy(), deq_a @ deq_b.T) <= TOL
+
+
+def test_gemm_mx_fp4_one_hot_is_exact(dev):
+    """A row of one-hot FP4 codes (1.0 at column j) recovers deq(B)[:, j] exactly: scale
+    bytes, nibble order and the MFMA's K order all line up."""
+    m, n, k = 256, 256, 512
+    rng = np.random.default_rng(8)
+    b, deq_b = make_weight(dev, "fp4_e2m1", n, k, "e8m0", rng)
+    cols = rng.choice(k, m, replace=True)
+    codes = np.zeros((m, k), np.uint8)
+    codes[np.arange(m), cols] = 2  # E2M1 code 2 = 1.0
+    data = O.pack_codes(codes, 4)
+    e = np.full((m, k // 32), 127, np.uint8)
+    a = PackedTensor(torch.from_numpy(data).to(dev), "fp4_e2m1", (m, k),
+                     torch.from_numpy(e).to(dev).view(torch.float8_e8m0fnu), 32)
+    c = matmul_nt(a, b, dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(c, deq_b[:, cols].T.astype(np.float32))
+
+
+def test_gemm_mx_fp4_full_size_sampled(dev):
+    """Config 4a at full size (M = N = K = 8192, operands MX-quantised from N(0,1)):
+    64 sampled rows of C against the exact-dequant fp64 oracle."""
+    m = n = k = 8192
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    a = quantize_mx(torch.randn((m, k), device=dev, generator=g), "fp4_e2m1")
+    b = quantize_mx(torch.randn((n, k), device=dev, generator=g), "fp4_e2m1")
+    c = matmul_nt(a, b, dtype=torch.bfloat16)
+    rows = np.random.default_rng(4).choice(m, 64, replace=False)
+    deq_b = b.unpack(torch.float32).cpu().numpy().astype(np.float64)
+    deq_a = a.unpack(torch.float32).cpu().numpy()[rows].astype(np.float64)
+    ref = deq_a @ deq_b.T
+    assert O.max_rel_err(bf16_np(c)[rows], ref) <= TOL
 
 
 def test_failures_are_cached_per_candidate(dev):
