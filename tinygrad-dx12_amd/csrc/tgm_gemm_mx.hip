@@ -140,10 +140,8 @@ __global__ void __launch_bounds__(256) gemm_mx_fp4(const uint8_t* __restrict__ a
   store_step(0);
 #pragma unroll
   for (int t = 0; t < 4; ++t) { scl_a[t] = nscl_a[t]; scl_b[t] = nscl_b[t]; }
-  if (nsteps > 1) {
-    load_step(1);
-    load_scales(1);
-  }
+  load_step(nsteps > 1 ? 1 : 0);
+  load_scales(nsteps > 1 ? 1 : 0);
   __syncthreads();
 
   const int half = lane >> 5;  // K half of the 64-element MFMA step
@@ -181,32 +179,47 @@ __global__ void __launch_bounds__(256) gemm_mx_fp4(const uint8_t* __restrict__ a
       }
   };
   // Per step: the fragments of substep u + 1 are read while substep u's MFMAs run; the
-  // next step's panels go to the other LDS buffer after substep 0 (it was last read in
-  // the previous step, before that step's barrier) and the step after next is fetched
-  // from global memory after substep 1, so its loads overlap two substeps of MFMAs.
+  // next step's panels go to the other LDS buffer during substep 1 (that buffer was last
+  // read in the previous step, before its barrier) and the step after next is fetched
+  // from global memory during substep 2, so its loads overlap two substeps of MFMAs.
+  // The body has no branches (past the last step the loads re-read step nsteps - 1 and the
+  // stores fill the buffer nobody reads again), so the instruction interleaving asked for
+  // by the scheduling barriers holds: one LDS or global instruction between MFMAs.
   Frags f0, f1;
   for (int s = 0; s < nsteps; ++s) {
     const int buf = s & 1;
-    const bool more = s + 1 < nsteps;
+    const int s2 = s + 2 < nsteps ? s + 2 : nsteps - 1;
     read_frags(f0, buf, 0);
     read_frags(f1, buf, 1);
     mfmas(f0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    if (more) store_step(buf ^ 1);
+    store_step(buf ^ 1);
     read_frags(f0, buf, 2);
     mfmas(f1, 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);  // DS write
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    }
     __builtin_amdgcn_sched_barrier(0);
-    if (s + 2 < nsteps) load_step(s + 2);
+    load_step(s2);
     read_frags(f1, buf, 3);
     mfmas(f0, 2);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
     mfmas(f1, 3);
     __builtin_amdgcn_sched_barrier(0);
-    if (more) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) { scl_a[t] = nscl_a[t]; scl_b[t] = nscl_b[t]; }
-      if (s + 2 < nsteps) load_scales(s + 2);
-    }
+    for (int t = 0; t < 4; ++t) { scl_a[t] = nscl_a[t]; scl_b[t] = nscl_b[t]; }
+    load_scales(s2);
     __syncthreads();
   }
 
