@@ -36,12 +36,34 @@ typedef __attribute__((__vector_size__(4 * sizeof(unsigned)))) unsigned u32x4;
 typedef __attribute__((__vector_size__(2 * sizeof(unsigned)))) unsigned u32x2;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+
+// Direct global -> LDS loads through a buffer resource (bounds-checked: offsets past the
+// resource's size read zeros).  The 16 (or 4) bytes of lane l land at LDS address
+// lds_addr + 16 l (4 l).  They are issued as inline assembly so that the compiler does not
+// order later LDS reads of the *other* buffer behind them; completion is awaited
+// explicitly (s_waitcnt vmcnt(0)) before the barrier that publishes a buffer.  M0 is set
+// inside each statement and nothing else in the kernel uses it.
+__device__ __forceinline__ void lds_dma16(i32x4v rsrc, unsigned lds_addr, unsigned voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" : : "s"(lds_addr), "v"(voff), "s"(rsrc) : "memory");
+}
+__device__ __forceinline__ void lds_dma4(i32x4v rsrc, unsigned lds_addr, unsigned voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" : : "s"(lds_addr), "v"(voff), "s"(rsrc) : "memory");
+}
+__device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Raw buffer resource (stride 0, num_records = bytes) for a global pointer.
+__device__ __forceinline__ i32x4v buffer_rsrc(const void* p, unsigned bytes) {
+  const unsigned long long a = (unsigned long long)p;
+  return i32x4v{(int)(unsigned)a, (int)((unsigned)(a >> 32) & 0xFFFFu), (int)bytes, 0x00020000};
+}
+
 constexpr int kBM = 256, kBN = 256;  // output tile
 constexpr int kBK = 256;             // K elements per step
 constexpr int kRowBytes = kBK / 2;   // FP4 bytes per row and step
-constexpr int kLdsRow = kRowBytes + 16;
-constexpr int kPanel = kBM * kLdsRow;            // one operand, one buffer (36 KB)
-constexpr int kLdsBytes = 2 * 2 * kPanel;        // A and B, double buffered (144 KB)
+constexpr int kPanel = kBM * kRowBytes;          // one operand, one buffer (32 KB)
+constexpr int kScalePanel = kBM * (kBK / 32);    // E8M0 bytes of one operand per step (2 KB)
+constexpr int kBuffer = 2 * kPanel + 2 * kScalePanel;  // A, B, A scales, B scales (68 KB)
 constexpr int kGroupM = 8;
 
 __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -65,7 +87,7 @@ __device__ __forceinline__ void store_c(void* c, int cdt, int64_t i, float v) {
 __global__ void __launch_bounds__(256) gemm_mx_fp4(const uint8_t* __restrict__ a, const uint8_t* __restrict__ sa,
                                                    const uint8_t* __restrict__ b, const uint8_t* __restrict__ sb,
                                                    int M, int N, int K, void* __restrict__ c, int cdt, int64_t ldc) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kBuffer];  // two buffers
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -75,56 +97,61 @@ __global__ void __launch_bounds__(256) gemm_mx_fp4(const uint8_t* __restrict__ a
   const int m0 = tm * kBM, n0 = tn * kBN;
   const int nsteps = K / kBK;
 
-  // Global -> LDS staging: chunk g = i * 256 + tid of a 256-row x 128-byte panel is row
-  // i * 32 + tid / 8, 16-byte column tid % 8 (a wave covers 8 whole 128-byte rows per
-  // load).  Offsets are 32-bit (the host keeps each operand under 4 GiB) and recomputed
-  // per step, which costs a few VALU next to the step's 64 MFMAs and keeps registers for
-  // the accumulators.  Rows past M or N re-read the last row; their results are dropped.
-  const int srow = tid >> 3, scol = (tid & 7) * 16;
-  const int lds_base = srow * kLdsRow + scol;
+  // Global -> LDS: direct loads (buffer_load_dwordx4 ... lds) write 16 bytes per lane at
+  // the LDS address of the instruction plus 16 * lane, so a wave instruction fills 64
+  // consecutive 16-byte slots of a panel (256 rows x 128 bytes).  Slot s holds row s / 8
+  // and 16-byte column (s % 8) ^ ((row >> 1) & 7): the XOR swizzle puts the 32 rows one
+  // fragment read touches (same logical column) into distinct banks, and each wave
+  // instruction still covers 8 whole 128-byte rows of global memory.  Wave w issues the
+  // 8 instructions for slots [512 w, 512 w + 512) of each operand.  The loads go through
+  // buffer resources sized to the operands: rows past M or N read zeros (their results are
+  // dropped), so no address needs clamping and every load's offset is one per-lane value
+  // plus a uniform one.  Offsets are 32-bit (the host keeps each operand under 4 GiB).
   const unsigned kb = (unsigned)(K / 2);
-  auto a_off = [&](int i, int s) __attribute__((always_inline)) {
-    const int r = m0 + i * 32 + srow;
-    return (unsigned)(r < M ? r : M - 1) * kb + (unsigned)(scol + s * kRowBytes);
-  };
-  auto b_off = [&](int i, int s) __attribute__((always_inline)) {
-    const int r = n0 + i * 32 + srow;
-    return (unsigned)(r < N ? r : N - 1) * kb + (unsigned)(scol + s * kRowBytes);
-  };
-  // Scale rows of this lane: A rows wm*128 + t*32 + l%32, B rows wn*128 + t*32 + l%32.
   const unsigned kblk = (unsigned)(K / 32);
-  auto sa_off = [&](int t, int s) __attribute__((always_inline)) {
-    const int r = m0 + wm * 128 + t * 32 + (lane & 31);
-    return (unsigned)(r < M ? r : M - 1) * kblk + (unsigned)(s * 8);
-  };
-  auto sb_off = [&](int t, int s) __attribute__((always_inline)) {
-    const int r = n0 + wn * 128 + t * 32 + (lane & 31);
-    return (unsigned)(r < N ? r : N - 1) * kblk + (unsigned)(s * 8);
-  };
-
-  u32x4 stage_a[8], stage_b[8];
-  u32x2 scl_a[4], scl_b[4], nscl_a[4], nscl_b[4];
-  auto load_step = [&](int s) __attribute__((always_inline)) {
+  const i32x4v ra = buffer_rsrc(a, (unsigned)M * kb), rb = buffer_rsrc(b, (unsigned)N * kb);
+  const i32x4v rsa = buffer_rsrc(sa, (unsigned)M * kblk), rsb = buffer_rsrc(sb, (unsigned)N * kblk);
+  // Lane l of load i covers row lrow + 8 i, whose swizzle term ((lrow + 8 i) >> 1) & 7 is
+  // ((l >> 4) + 4 i) & 7 = (l >> 4) ^ (4 (i & 1)): the 16-byte column it fetches is
+  // (l % 8) ^ (l >> 4), flipped by 4 on odd loads.
+  const int lrow = wave * 64 + (lane >> 3);  // + 8 i
+  const unsigned lcol = (unsigned)(((lane & 7) ^ (lane >> 4)) * 16);
+  const unsigned voa = (unsigned)(m0 + lrow) * kb, vob = (unsigned)(n0 + lrow) * kb;
+  // Scales take the same route: step s's 8 E8M0 bytes of row r land at byte r * 8 of the
+  // buffer's scale panel, 4 bytes per lane (two lanes per row, 32 rows per instruction;
+  // wave w loads rows [64 w, 64 w + 64) of both operands).
+  const int srow_l = wave * 64 + (lane >> 1);  // + 32 j
+  const unsigned vsa = (unsigned)(m0 + srow_l) * kblk + (unsigned)((lane & 1) * 4);
+  const unsigned vsb = (unsigned)(n0 + srow_l) * kblk + (unsigned)((lane & 1) * 4);
+  const unsigned lds_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds;
+  auto dma_step = [&](int s, int buf) __attribute__((always_inline)) {
+    const unsigned la = lds_base + (unsigned)(buf * kBuffer + wave * 512 * 16);
+    const unsigned lb = la + kPanel;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      stage_a[i] = *(const u32x4*)(a + a_off(i, s));
-      stage_b[i] = *(const u32x4*)(b + b_off(i, s));
+      const unsigned step_off = (unsigned)(8 * i) * kb + (unsigned)(s * kRowBytes);  // uniform
+      const unsigned col = lcol ^ (unsigned)((i & 1) * 64);
+      lds_dma16(ra, la + i * 1024, voa + col + step_off);
+      lds_dma16(rb, lb + i * 1024, vob + col + step_off);
+    }
+    const unsigned lsa = lds_base + (unsigned)(buf * kBuffer + 2 * kPanel + wave * 64 * 8);
+    const unsigned lsb = lsa + kScalePanel;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const unsigned step_off = (unsigned)(32 * j) * kblk + (unsigned)(s * 8);  // uniform
+      lds_dma4(rsa, lsa + j * 256, vsa + step_off);
+      lds_dma4(rsb, lsb + j * 256, vsb + step_off);
     }
   };
-  auto load_scales = [&](int s) __attribute__((always_inline)) {  // into nscl_*
+  // Scale words of this lane for one step: A rows wm*128 + t*32 + l%32, B likewise.
+  u32x2 scl_a[4], scl_b[4];
+  auto read_scales = [&](int buf) __attribute__((always_inline)) {
+    const unsigned char* lsa = lds + buf * kBuffer + 2 * kPanel;
+    const unsigned char* lsb = lsa + kScalePanel;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      nscl_a[t] = *(const u32x2*)(sa + sa_off(t, s));
-      nscl_b[t] = *(const u32x2*)(sb + sb_off(t, s));
-    }
-  };
-  auto store_step = [&](int buf) __attribute__((always_inline)) {
-    unsigned char* la = smem + buf * 2 * kPanel + lds_base;
-    unsigned char* lb = la + kPanel;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      *(u32x4*)(la + i * 32 * kLdsRow) = stage_a[i];
-      *(u32x4*)(lb + i * 32 * kLdsRow) = stage_b[i];
+      scl_a[t] = *(const u32x2*)(lsa + (wm * 128 + t * 32 + (lane & 31)) * 8);
+      scl_b[t] = *(const u32x2*)(lsb + (wn * 128 + t * 32 + (lane & 31)) * 8);
     }
   };
 
@@ -134,30 +161,23 @@ __global__ void __launch_bounds__(256) gemm_mx_fp4(const uint8_t* __restrict__ a
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  // Scales live in scl_* for the current step and nscl_* for the next one.
-  load_step(0);
-  load_scales(0);
-  store_step(0);
-#pragma unroll
-  for (int t = 0; t < 4; ++t) { scl_a[t] = nscl_a[t]; scl_b[t] = nscl_b[t]; }
-  load_step(nsteps > 1 ? 1 : 0);
-  load_scales(nsteps > 1 ? 1 : 0);
-  __syncthreads();
-
   const int half = lane >> 5;  // K half of the 64-element MFMA step
-  const int frag_off_a = (wm * 128 + (lane & 31)) * kLdsRow + half * 16;
-  const int frag_off_b = (wn * 128 + (lane & 31)) * kLdsRow + half * 16;
-  // Fragments of one 64-element K substep: rows t*32 + l%32 of the wave's A and B panels.
+  // Fragment t of substep u: row (w? * 128 + t * 32 + l % 32), logical 16-byte column
+  // 2u + half, stored at column (2u + half) ^ ((row >> 1) & 7) = (2u + half) ^ ((l >> 1) & 7).
+  const int sw = (lane >> 1) & 7;
+  const int fa_row = (wm * 128 + (lane & 31)) * kRowBytes;
+  const int fb_row = (wn * 128 + (lane & 31)) * kRowBytes;
   struct Frags {
     u32x4 a[4], b[4];
   };
   auto read_frags = [&](Frags& f, int buf, int u) __attribute__((always_inline)) {
-    const unsigned char* la = smem + buf * 2 * kPanel;
+    const unsigned char* la = lds + buf * kBuffer;
     const unsigned char* lb = la + kPanel;
+    const int col = ((2 * u + half) ^ sw) * 16;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      f.a[t] = *(const u32x4*)(la + frag_off_a + t * 32 * kLdsRow + u * 32);
-      f.b[t] = *(const u32x4*)(lb + frag_off_b + t * 32 * kLdsRow + u * 32);
+      f.a[t] = *(const u32x4*)(la + fa_row + col + t * 32 * kRowBytes);
+      f.b[t] = *(const u32x4*)(lb + fb_row + col + t * 32 * kRowBytes);
     }
   };
   auto mfmas = [&](const Frags& f, int u) __attribute__((always_inline)) {
@@ -178,55 +198,63 @@ __global__ void __launch_bounds__(256) gemm_mx_fp4(const uint8_t* __restrict__ a
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa, fb, acc[i][j], 4, 4, 0, xa[i], 0, xb[j]);
       }
   };
-  // Per step: the fragments of substep u + 1 are read while substep u's MFMAs run; the
-  // next step's panels go to the other LDS buffer during substep 1 (that buffer was last
-  // read in the previous step, before its barrier) and the step after next is fetched
-  // from global memory during substep 2, so its loads overlap two substeps of MFMAs.
-  // The body has no branches (past the last step the loads re-read step nsteps - 1 and the
-  // stores fill the buffer nobody reads again), so the instruction interleaving asked for
-  // by the scheduling barriers holds: one LDS or global instruction between MFMAs.
+
+  // Pipeline.  Step s computes from LDS buffer s & 1 in four 64-element substeps u0..u3,
+  // fragments alternating between f0 and f1:
+  //   u0: MFMAs on f0 (prefetched)
+  //   u1: read f0 <- u2, MFMAs on f1 (prefetched)
+  //   u2: read f1 <- u3, MFMAs on f0
+  //   wait for this wave's loads of step s + 1, barrier: step s + 1 is in the other buffer
+  //       and every read of this buffer has completed
+  //   loads of step s + 2 into this buffer (they have u3 and u0..u2 of the next step)
+  //   u3: MFMAs on f1, read f0, f1 <- u0, u1 of step s + 1
+  // Past the last step the loads re-read step nsteps - 1 into a buffer nobody reads again;
+  // the body has no branches, so the interleaving asked for by the scheduling barriers holds.
+  dma_step(0, 0);
+  dma_step(nsteps > 1 ? 1 : 0, 1);
+  wait_lds_dma();
+  __syncthreads();
   Frags f0, f1;
+  read_frags(f0, 0, 0);
+  read_frags(f1, 0, 1);
+  read_scales(0);
   for (int s = 0; s < nsteps; ++s) {
-    const int buf = s & 1;
+    const int cur = s & 1;
     const int s2 = s + 2 < nsteps ? s + 2 : nsteps - 1;
-    read_frags(f0, buf, 0);
-    read_frags(f1, buf, 1);
     mfmas(f0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    store_step(buf ^ 1);
-    read_frags(f0, buf, 2);
+    read_frags(f0, cur, 2);
     mfmas(f1, 1);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);  // DS write
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
     }
     __builtin_amdgcn_sched_barrier(0);
-    load_step(s2);
-    read_frags(f1, buf, 3);
+    read_frags(f1, cur, 3);
     mfmas(f0, 2);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
+    wait_lds_dma();  // this wave's loads of step s + 1
+    __syncthreads();
+    dma_step(s2, cur);
     mfmas(f1, 3);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) { scl_a[t] = nscl_a[t]; scl_b[t] = nscl_b[t]; }
-    load_scales(s2);
-    __syncthreads();
+    read_frags(f0, cur ^ 1, 0);
+    read_frags(f1, cur ^ 1, 1);
+    read_scales(cur ^ 1);
   }
+  wait_lds_dma();
+  __syncthreads();  // the epilogue reuses the operand LDS
 
   // Epilogue: each 32 x 32 accumulator tile goes through a per-wave LDS block (rows
   // padded to 36 floats) so that lane l then holds row l / 2, columns 16 * (l % 2) .. +16,
   // rounded once from fp32 and written as 16-byte row segments.
-  float* ep = (float*)smem + wave * 32 * 36;
+  float* ep = (float*)lds + wave * 32 * 36;
   const int er = lane >> 1, ec = (lane & 1) * 16;
   auto out_tile = [&](const f32x16 t, int i, int j) __attribute__((always_inline)) {
 #pragma unroll
@@ -305,17 +333,8 @@ extern "C" int tgm_gemm_mx(const void* a, int a_fmt, const void* a_scales, int64
     TGM_UNSUPPORTED("tgm_gemm_mx: operands must be under 4 GiB (32-bit offsets)");
   if ((uintptr_t)a % 16 || (uintptr_t)b % 16 || (uintptr_t)a_scales % 8 || (uintptr_t)b_scales % 8)
     TGM_UNSUPPORTED("tgm_gemm_mx: operands must be 16-byte and scales 8-byte aligned");
-  static bool raised = false;
-  if (!raised) {
-    hipError_t err = hipFuncSetAttribute((const void*)gemm_mx_fp4, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-    if (err != hipSuccess) {
-      set_error("tgm_gemm_mx: cannot raise the LDS limit: %s", hipGetErrorString(err));
-      return (int)err;
-    }
-    raised = true;
-  }
   const int64_t tiles = ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN);
-  hipLaunchKernelGGL(gemm_mx_fp4, dim3((unsigned)tiles), dim3(256), kLdsBytes, (hipStream_t)stream, (const uint8_t*)a,
+  hipLaunchKernelGGL(gemm_mx_fp4, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)a,
                      (const uint8_t*)a_scales, (const uint8_t*)b, (const uint8_t*)b_scales, (int)m, (int)n, (int)k, c,
                      c_dtype, ldc);
   return launch_status("tgm_gemm_mx");
