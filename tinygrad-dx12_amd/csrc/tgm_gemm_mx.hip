@@ -65,6 +65,7 @@ constexpr int kPanel = kBM * kRowBytes;          // one operand, one buffer (32 
 constexpr int kScalePanel = kBM * (kBK / 32);    // E8M0 bytes of one operand per step (2 KB)
 constexpr int kBuffer = 2 * kPanel + 2 * kScalePanel;  // A, B, A scales, B scales (68 KB)
 constexpr int kGroupM = 8;
+constexpr int kWavesM = 4, kWavesN = 2;  // wave grid of the launched kernel
 
 __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int ntiles = tiles_m * tiles_n;
@@ -84,13 +85,18 @@ __device__ __forceinline__ void store_c(void* c, int cdt, int64_t i, float v) {
   else ((float*)c)[i] = v;
 }
 
-__global__ void __launch_bounds__(256) gemm_mx_fp4(const uint8_t* __restrict__ a, const uint8_t* __restrict__ sa,
+// WM x WN waves per workgroup; wave tile (256 / WM) x (256 / WN) = FA x FB MFMA tiles.
+template <int WM, int WN>
+__global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __restrict__ a, const uint8_t* __restrict__ sa,
                                                    const uint8_t* __restrict__ b, const uint8_t* __restrict__ sb,
                                                    int M, int N, int K, void* __restrict__ c, int cdt, int64_t ldc) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kBuffer];  // two buffers
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  constexpr int NW = WM * WN, FA = 8 / WM, FB = 8 / WN;  // 32-row fragments per wave
+  constexpr int SW = NW < 8 ? NW : 8;                     // waves that load scales
+  constexpr int NI = 32 / NW, NJ = 8 / SW;                // panel / scale loads per wave and operand
+  const int wm = wave / WN, wn = wave % WN;
   const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
   int tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
@@ -102,9 +108,10 @@ __global__ void __launch_bounds__(256) gemm_mx_fp4(const uint8_t* __restrict__ a
   // consecutive 16-byte slots of a panel (256 rows x 128 bytes).  Slot s holds row s / 8
   // and 16-byte column (s % 8) ^ ((row >> 1) & 7): the XOR swizzle puts the 32 rows one
   // fragment read touches (same logical column) into distinct banks, and each wave
-  // instruction still covers 8 whole 128-byte rows of global memory.  Wave w issues the
-  // 8 instructions for slots [512 w, 512 w + 512) of each operand.  The loads go through
-  // buffer resources sized to the operands: rows past M or N read zeros (their results are
+  // instruction still covers 8 whole 128-byte rows of global memory.  With NW waves, wave w
+  // issues the 32 / NW instructions for slots [2048 w / NW, 2048 (w + 1) / NW) of each
+  // operand.  The loads go through buffer resources sized to the operands: rows past M or N
+  // read zeros (their results are
   // dropped), so no address needs clamping and every load's offset is one per-lane value
   // plus a uniform one.  Offsets are 32-bit (the host keeps each operand under 4 GiB).
   const unsigned kb = (unsigned)(K / 2);
@@ -114,139 +121,152 @@ __global__ void __launch_bounds__(256) gemm_mx_fp4(const uint8_t* __restrict__ a
   // Lane l of load i covers row lrow + 8 i, whose swizzle term ((lrow + 8 i) >> 1) & 7 is
   // ((l >> 4) + 4 i) & 7 = (l >> 4) ^ (4 (i & 1)): the 16-byte column it fetches is
   // (l % 8) ^ (l >> 4), flipped by 4 on odd loads.
-  const int lrow = wave * 64 + (lane >> 3);  // + 8 i
+  const int lrow = wave * (256 / NW) + (lane >> 3);  // + 8 i
   const unsigned lcol = (unsigned)(((lane & 7) ^ (lane >> 4)) * 16);
   const unsigned voa = (unsigned)(m0 + lrow) * kb, vob = (unsigned)(n0 + lrow) * kb;
   // Scales take the same route: step s's 8 E8M0 bytes of row r land at byte r * 8 of the
   // buffer's scale panel, 4 bytes per lane (two lanes per row, 32 rows per instruction;
-  // wave w loads rows [64 w, 64 w + 64) of both operands).
-  const int srow_l = wave * 64 + (lane >> 1);  // + 32 j
+  // with SW = min(NW, 8) loading waves, wave w < SW loads rows [256 w / SW, 256 (w + 1) / SW)
+  // of both operands).
+  const int srow_l = (wave % SW) * (256 / SW) + (lane >> 1);  // + 32 j
   const unsigned vsa = (unsigned)(m0 + srow_l) * kblk + (unsigned)((lane & 1) * 4);
   const unsigned vsb = (unsigned)(n0 + srow_l) * kblk + (unsigned)((lane & 1) * 4);
   const unsigned lds_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds;
-  auto dma_step = [&](int s, int buf) __attribute__((always_inline)) {
-    const unsigned la = lds_base + (unsigned)(buf * kBuffer + wave * 512 * 16);
-    const unsigned lb = la + kPanel;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
+  // One load instruction of step s into buffer buf: piece 2i / 2i + 1 is A / B load i,
+  // piece 2 NI + 2j / + 1 is A / B scale load j.
+  constexpr int NP = 2 * NI + 2 * NJ;
+  auto dma_piece = [&](int s, int buf, int p) __attribute__((always_inline)) {
+    if (p < 2 * NI) {
+      const int i = p >> 1;
       const unsigned step_off = (unsigned)(8 * i) * kb + (unsigned)(s * kRowBytes);  // uniform
       const unsigned col = lcol ^ (unsigned)((i & 1) * 64);
-      lds_dma16(ra, la + i * 1024, voa + col + step_off);
-      lds_dma16(rb, lb + i * 1024, vob + col + step_off);
-    }
-    const unsigned lsa = lds_base + (unsigned)(buf * kBuffer + 2 * kPanel + wave * 64 * 8);
-    const unsigned lsb = lsa + kScalePanel;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
+      const unsigned la = lds_base + (unsigned)(buf * kBuffer + (p & 1) * kPanel + wave * (2048 / NW) * 16 + i * 1024);
+      lds_dma16((p & 1) ? rb : ra, la, ((p & 1) ? vob : voa) + col + step_off);
+    } else {
+      if (NW > SW && wave >= SW) return;
+      const int q = p - 2 * NI, j = q >> 1;
       const unsigned step_off = (unsigned)(32 * j) * kblk + (unsigned)(s * 8);  // uniform
-      lds_dma4(rsa, lsa + j * 256, vsa + step_off);
-      lds_dma4(rsb, lsb + j * 256, vsb + step_off);
+      const unsigned ls = lds_base + (unsigned)(buf * kBuffer + 2 * kPanel + (q & 1) * kScalePanel +
+                                                (wave % SW) * (256 / SW) * 8 + j * 256);
+      lds_dma4((q & 1) ? rsb : rsa, ls, ((q & 1) ? vsb : vsa) + step_off);
     }
   };
-  // Scale words of this lane for one step: A rows wm*128 + t*32 + l%32, B likewise.
-  u32x2 scl_a[4], scl_b[4];
-  auto read_scales = [&](int buf) __attribute__((always_inline)) {
-    const unsigned char* lsa = lds + buf * kBuffer + 2 * kPanel;
-    const unsigned char* lsb = lsa + kScalePanel;
+  auto dma_pieces = [&](int s, int buf, int p0, int p1) __attribute__((always_inline)) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      scl_a[t] = *(const u32x2*)(lsa + (wm * 128 + t * 32 + (lane & 31)) * 8);
-      scl_b[t] = *(const u32x2*)(lsb + (wn * 128 + t * 32 + (lane & 31)) * 8);
-    }
+    for (int p = 0; p < NP; ++p)
+      if (p >= p0 && p < p1) dma_piece(s, buf, p);
   };
+  // Scale words of this lane for one step: A rows wm * FA * 32 + t * 32 + l % 32, B likewise.
+  u32x2 scl_a[FA], scl_b[FB];
 
-  f32x16 acc[4][4];
+  f32x16 acc[FA][FB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FA; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < FB; ++j) acc[i][j] = f32x16{};
 
   const int half = lane >> 5;  // K half of the 64-element MFMA step
   // Fragment t of substep u: row (w? * 128 + t * 32 + l % 32), logical 16-byte column
   // 2u + half, stored at column (2u + half) ^ ((row >> 1) & 7) = (2u + half) ^ ((l >> 1) & 7).
   const int sw = (lane >> 1) & 7;
-  const int fa_row = (wm * 128 + (lane & 31)) * kRowBytes;
-  const int fb_row = (wn * 128 + (lane & 31)) * kRowBytes;
+  const int fa_row = (wm * FA * 32 + (lane & 31)) * kRowBytes;
+  const int fb_row = (wn * FB * 32 + (lane & 31)) * kRowBytes;
   struct Frags {
-    u32x4 a[4], b[4];
+    u32x4 a[FA], b[FB];
   };
-  auto read_frags = [&](Frags& f, int buf, int u) __attribute__((always_inline)) {
+  // Reads placed one at a time between MFMAs: fragment t (A 0..FA-1, then B) of substep u,
+  // and scale word t (same numbering) of a buffer.
+  auto read_item = [&](Frags& f, int buf, int u, int t) __attribute__((always_inline)) {
     const unsigned char* la = lds + buf * kBuffer;
-    const unsigned char* lb = la + kPanel;
     const int col = ((2 * u + half) ^ sw) * 16;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      f.a[t] = *(const u32x4*)(la + fa_row + col + t * 32 * kRowBytes);
-      f.b[t] = *(const u32x4*)(lb + fb_row + col + t * 32 * kRowBytes);
-    }
+    if (t < FA) f.a[t < FA ? t : 0] = *(const u32x4*)(la + fa_row + col + t * 32 * kRowBytes);
+    else f.b[t < FA ? 0 : t - FA] = *(const u32x4*)(la + kPanel + fb_row + col + (t - FA) * 32 * kRowBytes);
   };
-  auto mfmas = [&](const Frags& f, int u) __attribute__((always_inline)) {
+  auto scale_item = [&](int buf, int t) __attribute__((always_inline)) {
+    const unsigned char* ls = lds + buf * kBuffer + 2 * kPanel;
+    if (t < FA) scl_a[t < FA ? t : 0] = *(const u32x2*)(ls + (wm * FA * 32 + t * 32 + (lane & 31)) * 8);
+    else scl_b[t < FA ? 0 : t - FA] = *(const u32x2*)(ls + kScalePanel + (wn * FB * 32 + (t - FA) * 32 + (lane & 31)) * 8);
+  };
+  auto mfmas = [&](const Frags& f, int u, auto&& hook) __attribute__((always_inline)) {
     // scale of block 2u + half of this step: byte (2u + half) % 4 of word (2u + half) / 4
     const int blk = 2 * u + half;
-    int xa[4], xb[4];
+    int xa[FA], xb[FB];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      xa[t] = (int)((u < 2 ? scl_a[t][0] : scl_a[t][1]) >> (8 * (blk & 3)));
-      xb[t] = (int)((u < 2 ? scl_b[t][0] : scl_b[t][1]) >> (8 * (blk & 3)));
-    }
+    for (int t = 0; t < FA; ++t) xa[t] = (int)((u < 2 ? scl_a[t][0] : scl_a[t][1]) >> (8 * (blk & 3)));
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int t = 0; t < FB; ++t) xb[t] = (int)((u < 2 ? scl_b[t][0] : scl_b[t][1]) >> (8 * (blk & 3)));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+    for (int i = 0; i < FA; ++i)
+#pragma unroll
+      for (int j = 0; j < FB; ++j) {
         const i32x8 fa = {(int)f.a[i][0], (int)f.a[i][1], (int)f.a[i][2], (int)f.a[i][3], 0, 0, 0, 0};
         const i32x8 fb = {(int)f.b[j][0], (int)f.b[j][1], (int)f.b[j][2], (int)f.b[j][3], 0, 0, 0, 0};
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa, fb, acc[i][j], 4, 4, 0, xa[i], 0, xb[j]);
+        hook(i * FB + j);
       }
   };
-
-  // Pipeline.  Step s computes from LDS buffer s & 1 in four 64-element substeps u0..u3,
-  // fragments alternating between f0 and f1:
-  //   u0: MFMAs on f0 (prefetched)
-  //   u1: read f0 <- u2, MFMAs on f1 (prefetched)
-  //   u2: read f1 <- u3, MFMAs on f0
-  //   wait for this wave's loads of step s + 1, barrier: step s + 1 is in the other buffer
-  //       and every read of this buffer has completed
-  //   loads of step s + 2 into this buffer (they have u3 and u0..u2 of the next step)
-  //   u3: MFMAs on f1, read f0, f1 <- u0, u1 of step s + 1
-  // Past the last step the loads re-read step nsteps - 1 into a buffer nobody reads again;
-  // the body has no branches, so the interleaving asked for by the scheduling barriers holds.
-  dma_step(0, 0);
-  dma_step(nsteps > 1 ? 1 : 0, 1);
+  // Pipeline.  Step s computes from LDS buffer s & 1 in four 64-element substeps u0..u3
+  // whose fragments alternate between f0 and f1.  After each of a substep's FA * FB MFMAs
+  // the wave issues an even share of the memory work placed on that substep:
+  //   u0 (f0): read f1 <- u1; second half of step s + 1's loads (into the other buffer)
+  //   u1 (f1): read f0 <- u2
+  //   u2 (f0): read f1 <- u3
+  //   wait for this wave's loads of step s + 1, barrier: step s + 1 is complete in the other
+  //       buffer and every read of this buffer has been issued and completed
+  //   u3 (f1): read the scale words and f0 <- u0 of step s + 1; first half of step s + 2's
+  //       loads (into this buffer)
+  // Each piece of memory work sits between scheduling barriers so that the order holds.  Past
+  // the last step the loads re-read step nsteps - 1 into a buffer nobody reads again; the body
+  // has no branches.
+  constexpr int kMaxItems = 2 * (FA + FB) + NP;
+  auto substep = [&](const Frags& fc, int u, Frags& fn, int rbuf, int ru, bool scales, int ds, int dbuf, int p0,
+                     int p1) __attribute__((always_inline)) {
+    const int nr = (FA + FB) * (scales ? 2 : 1);
+    const int ni = nr + (p1 - p0);
+    mfmas(fc, u, [&](int idx) __attribute__((always_inline)) {
+#pragma unroll
+      for (int it = 0; it < kMaxItems; ++it) {
+        if (it < ni && it * FA * FB / ni == idx) {
+          __builtin_amdgcn_sched_barrier(0);
+          if (it >= nr) dma_piece(ds, dbuf, p0 + it - nr);
+          else if (!scales) read_item(fn, rbuf, ru, it);
+          else if (it < FA + FB) scale_item(rbuf, it);  // scales first: the next substep starts with them
+          else read_item(fn, rbuf, ru, it - (FA + FB));
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    });
+  };
+  const int s1 = nsteps > 1 ? 1 : 0;
+  dma_pieces(0, 0, 0, NP);
+  dma_pieces(s1, 1, 0, NP / 2);
   wait_lds_dma();
   __syncthreads();
   Frags f0, f1;
-  read_frags(f0, 0, 0);
-  read_frags(f1, 0, 1);
-  read_scales(0);
+  // same order as the loop's u3 reads, so that the waits at the loop head can count
+#pragma unroll
+  for (int t = 0; t < FA + FB; ++t) {
+    __builtin_amdgcn_sched_barrier(0);
+    scale_item(0, t);
+  }
+#pragma unroll
+  for (int t = 0; t < FA + FB; ++t) {
+    __builtin_amdgcn_sched_barrier(0);
+    read_item(f0, 0, 0, t);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   for (int s = 0; s < nsteps; ++s) {
     const int cur = s & 1;
+    const int s1n = s + 1 < nsteps ? s + 1 : nsteps - 1;
     const int s2 = s + 2 < nsteps ? s + 2 : nsteps - 1;
-    mfmas(f0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(f0, cur, 2);
-    mfmas(f1, 1);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(f1, cur, 3);
-    mfmas(f0, 2);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
+    substep(f0, 0, f1, cur, 1, false, s1n, cur ^ 1, NP / 2, NP);
+    substep(f1, 1, f0, cur, 2, false, 0, 0, 0, 0);
+    substep(f0, 2, f1, cur, 3, false, 0, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     wait_lds_dma();  // this wave's loads of step s + 1
     __syncthreads();
-    dma_step(s2, cur);
-    mfmas(f1, 3);
+    substep(f1, 3, f0, cur ^ 1, 0, true, s2, cur, 0, NP / 2);
     __builtin_amdgcn_sched_barrier(0);
-    read_frags(f0, cur ^ 1, 0);
-    read_frags(f1, cur ^ 1, 1);
-    read_scales(cur ^ 1);
   }
   wait_lds_dma();
   __syncthreads();  // the epilogue reuses the operand LDS
@@ -271,8 +291,8 @@ __global__ void __launch_bounds__(256) gemm_mx_fp4(const uint8_t* __restrict__ a
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int row = m0 + wm * 128 + i * 32 + er;
-    const int col = n0 + wn * 128 + j * 32 + ec;
+    const int row = m0 + wm * FA * 32 + i * 32 + er;
+    const int col = n0 + wn * FB * 32 + j * 32 + ec;
     if (row < M) {
       const int64_t o = (int64_t)row * ldc + col;
       if (col + 15 < N && (o & 7) == 0 && cdt != TGM_F32) {
@@ -299,10 +319,11 @@ __global__ void __launch_bounds__(256) gemm_mx_fp4(const uint8_t* __restrict__ a
     }
   };
   // literal indices keep the accumulators in registers
-  out_tile(acc[0][0], 0, 0); out_tile(acc[0][1], 0, 1); out_tile(acc[0][2], 0, 2); out_tile(acc[0][3], 0, 3);
-  out_tile(acc[1][0], 1, 0); out_tile(acc[1][1], 1, 1); out_tile(acc[1][2], 1, 2); out_tile(acc[1][3], 1, 3);
-  out_tile(acc[2][0], 2, 0); out_tile(acc[2][1], 2, 1); out_tile(acc[2][2], 2, 2); out_tile(acc[2][3], 2, 3);
-  out_tile(acc[3][0], 3, 0); out_tile(acc[3][1], 3, 1); out_tile(acc[3][2], 3, 2); out_tile(acc[3][3], 3, 3);
+#define TGM_OUT(I, J) \
+  if constexpr (I < FA && J < FB) out_tile(acc[I < FA ? I : 0][J < FB ? J : 0], I, J);
+  TGM_OUT(0, 0) TGM_OUT(0, 1) TGM_OUT(0, 2) TGM_OUT(0, 3) TGM_OUT(1, 0) TGM_OUT(1, 1) TGM_OUT(1, 2) TGM_OUT(1, 3)
+  TGM_OUT(2, 0) TGM_OUT(2, 1) TGM_OUT(2, 2) TGM_OUT(2, 3) TGM_OUT(3, 0) TGM_OUT(3, 1) TGM_OUT(3, 2) TGM_OUT(3, 3)
+#undef TGM_OUT
 }
 
 }  // namespace tgm
@@ -334,7 +355,8 @@ extern "C" int tgm_gemm_mx(const void* a, int a_fmt, const void* a_scales, int64
   if ((uintptr_t)a % 16 || (uintptr_t)b % 16 || (uintptr_t)a_scales % 8 || (uintptr_t)b_scales % 8)
     TGM_UNSUPPORTED("tgm_gemm_mx: operands must be 16-byte and scales 8-byte aligned");
   const int64_t tiles = ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN);
-  hipLaunchKernelGGL(gemm_mx_fp4, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)a,
+  // 4 x 2 waves of 64 x 128: two waves per SIMD hide each other's LDS and barrier latency
+  hipLaunchKernelGGL((gemm_mx_fp4<kWavesM, kWavesN>), dim3((unsigned)tiles), dim3(kWavesM * kWavesN * 64), 0, (hipStream_t)stream, (const uint8_t*)a,
                      (const uint8_t*)a_scales, (const uint8_t*)b, (const uint8_t*)b_scales, (int)m, (int)n, (int)k, c,
                      c_dtype, ldc);
   return launch_status("tgm_gemm_mx");
