@@ -34,6 +34,9 @@ FP4_PEAK_TFLOPS = 10100.0
 N_COPIES = 18
 
 
+EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_cfg1", "fp4_gemm_8192", "fp4_gemm_4096x14336x4096")
+
+
 def parse() -> argparse.Namespace:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -42,6 +45,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    p.add_argument("--only", choices=sorted(EXTRAS), default=None,
+                   help="run only this secondary workload and print its figures (for profiling)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run --steps device-to-device copies of MIB MiB (reference for HBM byte counters)")
     return p.parse_args()
@@ -138,7 +143,8 @@ def measured_traffic(profile: str) -> int | None:
 
 def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup: int):
     """FP4 x FP4 + E8M0/32 GEMM C[M,N] = deq(A) deq(B)^T, bf16 out, timed with HIP events on
-    the launch stream (each launch is long enough that launch overhead is negligible)."""
+    the launch stream (each launch is long enough that launch overhead is negligible).  The
+    warmup launches let the clocks settle under MFMA load (the first few run ~15% slower)."""
     g = torch.Generator(device=dev)
     g.manual_seed(2)
     a = torch.randint(0, 256, (m * k // 2,), dtype=torch.uint8, device=dev, generator=g)
@@ -232,16 +238,24 @@ def main() -> int:
         copy_calibration(torch, args.copy_calibration, args.steps)
         return 0
     K.load_library()
+    half = max(args.steps // 2, 1)
+    extras = {
+        "fp4_gemv_m4": lambda: fp4_gemv_workload(torch, K, dev, 4, half, args.warmup),
+        "fp4_gemv_m16": lambda: fp4_gemv_workload(torch, K, dev, 16, half, args.warmup),
+        "int4_gemv_cfg1": lambda: int4_gemv_workload(torch, K, dev, half, args.warmup),
+        "fp4_gemm_8192": lambda: fp4_gemm_workload(torch, K, dev, 8192, 8192, 8192, 20, 20),
+        "fp4_gemm_4096x14336x4096": lambda: fp4_gemm_workload(torch, K, dev, 4096, 14336, 4096, 20, 20),
+    }
+    if args.only:
+        print(json.dumps({args.only: extras[args.only]()}))
+        return 0
     torch.cuda.synchronize()
     wall = time.perf_counter()
     primary = fp4_gemv_workload(torch, K, dev, 1, args.steps, args.warmup)
     workloads = {}
     if not args.no_extras:
-        for m in (4, 16):
-            workloads[f"fp4_gemv_m{m}"] = fp4_gemv_workload(torch, K, dev, m, max(args.steps // 2, 1), args.warmup)
-        workloads["int4_gemv_cfg1"] = int4_gemv_workload(torch, K, dev, max(args.steps // 2, 1), args.warmup)
-        workloads["fp4_gemm_8192"] = fp4_gemm_workload(torch, K, dev, 8192, 8192, 8192, 10, 3)
-        workloads["fp4_gemm_4096x14336x4096"] = fp4_gemm_workload(torch, K, dev, 4096, 14336, 4096, 10, 3)
+        for name in EXTRAS:
+            workloads[name] = extras[name]()
     torch.cuda.synchronize()
     gpu_wall = time.perf_counter() - wall
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
