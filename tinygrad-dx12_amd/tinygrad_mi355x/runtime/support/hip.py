@@ -1,0 +1,201 @@
+"""ctypes binding of the HIP runtime C API used by the MI355X device plugin.
+
+This replaces the reference's D3D12/DXGI native layer (alexandreteles/tinygrad-dx12
+src/tinygrad_dx12/runtime/support/dx12.py, runtime/autogen/*): instead of COM vtables,
+plain ``hipError_t`` functions.  Every failure becomes ``RuntimeError("<op> failed:
+<code> (<hipGetErrorString>)")``, the shape of the reference's ``check``
+(runtime/support/dx12.py:11-15).
+
+The library is the HIP runtime already loaded by torch when torch is imported first
+(its soname is libamdhip64.so.7), so device memory, streams and modules are shared with
+torch and with libtgm_mi355x.so.  Nothing here touches the GPU at import time.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+# hipMemcpyKind
+H2D, D2H, D2D = 1, 2, 3
+# hipModuleLaunchKernel "extra" markers (HIP_LAUNCH_PARAM_*)
+_PARAM_BUFFER_POINTER, _PARAM_BUFFER_SIZE, _PARAM_END = 1, 2, 3
+# hipError_t values the runtime reports for "not finished yet"
+HIP_ERROR_NOT_READY = 600
+# hipDeviceAttribute_t
+ATTR_CLOCK_RATE_KHZ = 5  # hipDeviceAttributeClockRate
+ATTR_CU_COUNT = 63  # hipDeviceAttributeMultiprocessorCount
+
+_P, _INT, _SZ, _U32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_uint
+
+_SIGNATURES = {
+    "hipInit": (_U32,),
+    "hipGetDeviceCount": (ctypes.POINTER(_INT),),
+    "hipSetDevice": (_INT,),
+    "hipGetDevice": (ctypes.POINTER(_INT),),
+    "hipDeviceGetAttribute": (ctypes.POINTER(_INT), _INT, _INT),
+    "hipDeviceGetName": (ctypes.c_char_p, _INT, _INT),
+    "hipDeviceSynchronize": (),
+    "hipMalloc": (ctypes.POINTER(_P), _SZ),
+    "hipFree": (_P,),
+    "hipHostMalloc": (ctypes.POINTER(_P), _SZ, _U32),
+    "hipHostFree": (_P,),
+    "hipMemcpyAsync": (_P, _P, _SZ, _INT, _P),
+    "hipMemcpyPeerAsync": (_P, _INT, _P, _INT, _SZ, _P),
+    "hipMemsetAsync": (_P, _INT, _SZ, _P),
+    "hipStreamCreate": (ctypes.POINTER(_P),),
+    "hipStreamDestroy": (_P,),
+    "hipStreamSynchronize": (_P,),
+    "hipStreamQuery": (_P,),
+    "hipEventCreate": (ctypes.POINTER(_P),),
+    "hipEventDestroy": (_P,),
+    "hipEventRecord": (_P, _P),
+    "hipEventSynchronize": (_P,),
+    "hipEventQuery": (_P,),
+    "hipEventElapsedTime": (ctypes.POINTER(ctypes.c_float), _P, _P),
+    "hipModuleLoadData": (ctypes.POINTER(_P), _P),
+    "hipModuleUnload": (_P,),
+    "hipModuleGetFunction": (ctypes.POINTER(_P), _P, ctypes.c_char_p),
+    "hipModuleLaunchKernel": (_P, _U32, _U32, _U32, _U32, _U32, _U32, _U32, _P, _P, _P),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+_initialised = False
+
+
+def library() -> ctypes.CDLL:
+    """Load and type the HIP runtime once (after torch, so both use the same runtime)."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            try:
+                import torch  # noqa: F401  -- binds the runtime torch ships first
+            except ImportError:
+                pass
+            name = os.environ.get("MI355X_HIP_RUNTIME", "libamdhip64.so.7")
+            try:
+                lib = ctypes.CDLL(name)
+            except OSError:
+                lib = ctypes.CDLL("/opt/rocm/lib/libamdhip64.so")
+            for fn, args in _SIGNATURES.items():
+                f = getattr(lib, fn)
+                f.argtypes = args
+                f.restype = _INT
+            lib.hipGetErrorString.argtypes = (_INT,)
+            lib.hipGetErrorString.restype = ctypes.c_char_p
+            _lib = lib
+        return _lib
+
+
+def error_string(code: int) -> str:
+    return (library().hipGetErrorString(code) or b"").decode(errors="replace")
+
+
+def check(status: int, operation: str) -> None:
+    """Raise the reference's native-failure error shape for a non-zero hipError_t."""
+    if status != 0:
+        raise RuntimeError(f"{operation} failed: {status} ({error_string(status)})")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(library(), name)(*args), name)
+
+
+def init() -> None:
+    global _initialised
+    if not _initialised:
+        call("hipInit", 0)
+        _initialised = True
+
+
+def device_count() -> int:
+    """Number of visible HIP devices (0 when none; never raises for a missing GPU)."""
+    try:
+        lib = library()
+    except OSError:
+        return 0
+    n = ctypes.c_int(0)
+    return n.value if lib.hipGetDeviceCount(ctypes.byref(n)) == 0 else 0
+
+
+def set_device(ordinal: int) -> None:
+    call("hipSetDevice", ordinal)
+
+
+def attribute(attr: int, ordinal: int) -> int:
+    v = ctypes.c_int(0)
+    call("hipDeviceGetAttribute", ctypes.byref(v), attr, ordinal)
+    return v.value
+
+
+def device_name(ordinal: int) -> str:
+    buf = ctypes.create_string_buffer(256)
+    call("hipDeviceGetName", buf, 256, ordinal)
+    return buf.value.decode(errors="replace")
+
+
+def malloc(size: int) -> int:
+    p = ctypes.c_void_p()
+    call("hipMalloc", ctypes.byref(p), max(size, 1))
+    return p.value or 0
+
+
+def host_malloc(size: int) -> int:
+    """Pinned host memory (hipHostMalloc, default flags)."""
+    p = ctypes.c_void_p()
+    call("hipHostMalloc", ctypes.byref(p), max(size, 1), 0)
+    return p.value or 0
+
+
+def stream_create() -> int:
+    """A stream at the default priority."""
+    s = ctypes.c_void_p()
+    call("hipStreamCreate", ctypes.byref(s))
+    return s.value or 0
+
+
+def event_create() -> int:
+    e = ctypes.c_void_p()
+    call("hipEventCreate", ctypes.byref(e))
+    return e.value or 0
+
+
+def query(name: str, handle: int) -> bool:
+    """True when the stream / event has completed, False while it runs; raises on failure."""
+    status = getattr(library(), name)(handle)
+    if status == HIP_ERROR_NOT_READY:
+        return False
+    check(status, name)
+    return True
+
+
+def elapsed_ms(start: int, end: int) -> float:
+    ms = ctypes.c_float(0.0)
+    call("hipEventElapsedTime", ctypes.byref(ms), start, end)
+    return float(ms.value)
+
+
+def module_load(image: bytes) -> tuple[int, ctypes.Array]:
+    """Load a code object; returns the module and the buffer that must outlive the call."""
+    buf = ctypes.create_string_buffer(image, len(image))
+    m = ctypes.c_void_p()
+    call("hipModuleLoadData", ctypes.byref(m), ctypes.cast(buf, ctypes.c_void_p))
+    return m.value or 0, buf
+
+
+def module_function(module: int, name: str) -> int:
+    f = ctypes.c_void_p()
+    call("hipModuleGetFunction", ctypes.byref(f), module, name.encode())
+    return f.value or 0
+
+
+def launch(function: int, grid: tuple[int, int, int], block: tuple[int, int, int], kernargs: bytes, stream: int,
+           shared: int = 0) -> None:
+    """hipModuleLaunchKernel with a packed kernarg buffer (HIP_LAUNCH_PARAM_BUFFER_POINTER)."""
+    args = ctypes.create_string_buffer(kernargs, max(len(kernargs), 1))
+    size = ctypes.c_size_t(len(kernargs))
+    extra = (ctypes.c_void_p * 5)(_PARAM_BUFFER_POINTER, ctypes.cast(args, ctypes.c_void_p).value,
+                                  _PARAM_BUFFER_SIZE, ctypes.cast(ctypes.byref(size), ctypes.c_void_p).value, _PARAM_END)
+    call("hipModuleLaunchKernel", function, *grid, *block, shared, stream, None, extra)
