@@ -9,7 +9,7 @@ replayed, and timed with HIP events on the launch stream.
 
 ``value`` is the achieved algorithmic bandwidth of the step (bytes of packed weights,
 scales, x and y per step / time per step).  Secondary workloads (skinny M=4/16, the
-INT4 g32 GEMV, the FP6 and FP4xFP4 GEMMs) are reported under ``workloads``.
+INT4 g32 GEMV, the FP6-weight x bf16 GEMMs and the FP4xFP4 GEMMs) are reported under ``workloads``.
 ``cpu_baseline`` times the C restatement of the reference's CPU path
 (oracle/cpu_path.c: materialise fp32 weights, fp32 GEMV, RNE to bf16) on the host.
 """
@@ -34,7 +34,8 @@ FP4_PEAK_TFLOPS = 10100.0
 N_COPIES = 18
 
 
-EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_cfg1", "fp4_gemm_8192", "fp4_gemm_4096x14336x4096")
+EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_cfg1", "fp6_e3m2_gemm_cfg3", "fp6_e2m3_gemm_cfg3", "fp4_gemm_8192",
+          "fp4_gemm_4096x14336x4096")
 
 
 def parse() -> argparse.Namespace:
@@ -176,6 +177,39 @@ def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup:
             "mfma_frac": tflops / FP4_PEAK_TFLOPS, "bytes": nbytes, "GB/s": nbytes / ms / 1e6}
 
 
+def fp6_gemm_workload(torch, K, dev, fmt: str, steps: int, warmup: int, m: int = 2048, n: int = 11008, k: int = 4096):
+    """Packed FP6 weight x bf16 activation prefill GEMM C[M,N] = A deq(W)^T (E8M0 per 32),
+    bf16 out, on the dequant-to-bf16 MFMA kernel; timed like the FP4 GEMM."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    a = torch.randn((m, k), device=dev, generator=g).to(torch.bfloat16)
+    w = torch.randint(0, 256, (n * k * 6 // 8,), dtype=torch.uint8, device=dev, generator=g)
+    s = torch.randint(123, 130, (n, k // 32), dtype=torch.uint8, device=dev, generator=g)
+    c = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    f, bf16, e8m0 = K.FORMAT_IDS[fmt], K.DTYPE_IDS[torch.bfloat16], K.DTYPE_IDS[torch.float8_e8m0fnu]
+    lib = K.load_library()
+    stream = torch.cuda.current_stream(dev)
+
+    def launch() -> None:
+        K.check("tgm_gemm_w", lib.tgm_gemm_w(a.data_ptr(), bf16, m, k, w.data_ptr(), f, n, k, s.data_ptr(), e8m0, 32,
+                                             c.data_ptr(), bf16, n, stream.cuda_stream))
+
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        launch()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    tflops = 2 * m * n * k / ms / 1e9
+    nbytes = m * k * 2 + n * k * 6 // 8 + n * (k // 32) + m * n * 2
+    return {"workload": f"{fmt} e8m0/32 weight x bf16 GEMM M={m} N={n} K={k} bf16 out", "ms": ms, "TFLOPS": tflops,
+            "bf16_mfma_frac": tflops / BF16_PEAK_TFLOPS, "bytes": nbytes, "GB/s": nbytes / ms / 1e6}
+
+
 def cpu_baseline(budget_s: float) -> dict:
     """The reference CPU path restated in C (oracle/cpu_path.c), timed on the host cores."""
     import numpy as np
@@ -243,6 +277,8 @@ def main() -> int:
         "fp4_gemv_m4": lambda: fp4_gemv_workload(torch, K, dev, 4, half, args.warmup),
         "fp4_gemv_m16": lambda: fp4_gemv_workload(torch, K, dev, 16, half, args.warmup),
         "int4_gemv_cfg1": lambda: int4_gemv_workload(torch, K, dev, half, args.warmup),
+        "fp6_e3m2_gemm_cfg3": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e3m2", 20, 20),
+        "fp6_e2m3_gemm_cfg3": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e2m3", 20, 20),
         "fp4_gemm_8192": lambda: fp4_gemm_workload(torch, K, dev, 8192, 8192, 8192, 20, 20),
         "fp4_gemm_4096x14336x4096": lambda: fp4_gemm_workload(torch, K, dev, 4096, 14336, 4096, 20, 20),
     }

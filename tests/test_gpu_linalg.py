@@ -248,6 +248,63 @@ def test_gemm_weight_parity(dev, fmt):
     assert O.max_rel_err(bf16_np(c), O.matmul_reference(bf16_np(a), deq.T)) <= TOL
 
 
+@pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e2m3", "fp6_e3m2"])
+@pytest.mark.parametrize("mnk", [(128, 256, 128), (200, 300, 256), (33, 1000, 512), (513, 257, 384)])
+@pytest.mark.parametrize("cdt", [torch.bfloat16, torch.float32])
+def test_gemm_w_tiles_and_tails(dev, fmt, mnk, cdt):
+    """Family 2 dequant-to-bf16 MFMA GEMM (the explicit scope requires the native kernel):
+    whole and ragged 128 x 256 tiles, E8M0 block scales."""
+    m, n, k = mnk
+    rng = np.random.default_rng(m + 3 * n + k)
+    w, deq = make_weight(dev, fmt, n, k, "e8m0", rng)
+    a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    c = matmul_nt(a, w, scope="ThreadGroup", dtype=cdt)
+    assert c.dtype is cdt and c.shape == (m, n)
+    assert O.max_rel_err(c.float().cpu().numpy(), bf16_np(a) @ deq.T) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e2m3", "fp6_e3m2"])
+def test_gemm_w_unscaled_and_strided_activations(dev, fmt):
+    m, n, k = 150, 270, 256
+    rng = np.random.default_rng(31)
+    w, deq = make_weight(dev, fmt, n, k, "none", rng)
+    big = torch.from_numpy(rng.standard_normal((m, k + 64)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    a = big[:, 32:32 + k]  # row stride k + 64 elements, 64-byte offset
+    c = matmul_nt(a, w, scope="ThreadGroup", dtype=torch.float32)
+    assert O.max_rel_err(c.cpu().numpy(), bf16_np(a) @ deq.T) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e2m3", "fp6_e3m2"])
+def test_gemm_w_one_hot_is_exact(dev, fmt):
+    """One-hot activation rows (1.0 at column j) recover deq(W)[:, j] exactly in fp32:
+    code order, scale bytes and the MFMA's K order all line up."""
+    m, n, k = 128, 256, 512
+    rng = np.random.default_rng(9)
+    w, deq = make_weight(dev, fmt, n, k, "e8m0", rng)
+    cols = rng.choice(k, m, replace=True)
+    a = torch.zeros((m, k), dtype=torch.bfloat16, device=dev)
+    a[torch.arange(m), torch.from_numpy(cols)] = 1.0
+    c = matmul_nt(a, w, scope="ThreadGroup", dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(c, deq[:, cols].T.astype(np.float32))
+
+
+@pytest.mark.parametrize("fmt", ["fp6_e3m2", "fp6_e2m3"])
+def test_gemm_w_config3_full_size_sampled(dev, fmt):
+    """Config 3 at full size: A bf16 [2048, 4096], W = MX-quantised N(0, 0.02) [11008, 4096]
+    (block-32 E8M0); 64 x 512 sampled outputs against the exact-dequant fp64 oracle."""
+    m, n, k = 2048, 11008, 4096
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    a = torch.randn((m, k), device=dev, generator=g).to(torch.bfloat16)
+    w = quantize_mx(torch.randn((n, k), device=dev, generator=g) * 0.02, fmt)
+    c = matmul_nt(a, w, scope="ThreadGroup", dtype=torch.bfloat16)
+    rng = np.random.default_rng(5)
+    rows, cols = rng.choice(m, 64, replace=False), rng.choice(n, 512, replace=False)
+    deq = w.unpack(torch.float32)[torch.from_numpy(cols).to(dev)].cpu().numpy().astype(np.float64)
+    ref = bf16_np(a)[rows] @ deq.T
+    assert O.max_rel_err(bf16_np(c)[np.ix_(rows, cols)], ref) <= TOL
+
+
 @pytest.mark.parametrize("fa,fb", [("fp4_e2m1", "fp4_e2m1"), ("fp6_e2m3", "fp4_e2m1"), ("fp6_e3m2", "fp6_e2m3")])
 def test_gemm_mx_parity(dev, fa, fb):
     m, n, k = 64, 96, 256

@@ -17,46 +17,16 @@
 // packed codes, i.e. one MX block, and that block's scale in byte 0 of its scale VGPR.
 // D layout: lane l holds column l % 32 and rows 8 * (v / 4) + 4 * (l / 32) + v % 4.
 //
-// Workgroup: 256 x 256 output tile, four waves in 2 x 2, each wave 128 x 128 = 4 x 4
-// MFMA tiles (256 fp32 accumulators per lane).  K advances in steps of 256 elements
-// (128 bytes per row and operand): each step's A and B panels (32 KB each) are staged
-// from global memory through registers into a double-buffered LDS tile whose rows are
-// padded to 144 bytes, so the 32 rows read by one ds_read_b128 fall in distinct banks.
-// The next step's global loads are in flight while the current step's MFMAs run.
-// Tiles are mapped XCD-aware: consecutive hardware workgroup ids go to different XCDs,
-// so the id is permuted to give each XCD a contiguous range of tiles, walked in groups
-// of 8 row-panels so that concurrently running tiles share A and B panels in its L2.
-#include "tgm_common.h"
+// Workgroup: 256 x 256 output tile, eight waves in 4 x 2, each wave 64 x 128 = 2 x 4 MFMA
+// tiles (128 fp32 accumulators per lane, two waves per SIMD).  K advances in steps of 256
+// elements (128 bytes per row and operand): each step's A and B panels (32 KB each) and
+// E8M0 scales are loaded straight from global memory into a double-buffered LDS tile
+// (buffer_load ... lds), XOR-swizzled so the 32 rows one ds_read_b128 touches fall in
+// distinct banks.  The loads of step s + 2 run while step s + 1's MFMAs do.  Tiles are
+// mapped XCD-aware (tile_of).
+#include "tgm_mfma_common.h"
 
 namespace tgm {
-
-typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8;
-typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
-typedef __attribute__((__vector_size__(4 * sizeof(unsigned)))) unsigned u32x4;
-typedef __attribute__((__vector_size__(2 * sizeof(unsigned)))) unsigned u32x2;
-typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
-
-typedef int i32x4v __attribute__((ext_vector_type(4)));
-
-// Direct global -> LDS loads through a buffer resource (bounds-checked: offsets past the
-// resource's size read zeros).  The 16 (or 4) bytes of lane l land at LDS address
-// lds_addr + 16 l (4 l).  They are issued as inline assembly so that the compiler does not
-// order later LDS reads of the *other* buffer behind them; completion is awaited
-// explicitly (s_waitcnt vmcnt(0)) before the barrier that publishes a buffer.  M0 is set
-// inside each statement and nothing else in the kernel uses it.
-__device__ __forceinline__ void lds_dma16(i32x4v rsrc, unsigned lds_addr, unsigned voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" : : "s"(lds_addr), "v"(voff), "s"(rsrc) : "memory");
-}
-__device__ __forceinline__ void lds_dma4(i32x4v rsrc, unsigned lds_addr, unsigned voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" : : "s"(lds_addr), "v"(voff), "s"(rsrc) : "memory");
-}
-__device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-// Raw buffer resource (stride 0, num_records = bytes) for a global pointer.
-__device__ __forceinline__ i32x4v buffer_rsrc(const void* p, unsigned bytes) {
-  const unsigned long long a = (unsigned long long)p;
-  return i32x4v{(int)(unsigned)a, (int)((unsigned)(a >> 32) & 0xFFFFu), (int)bytes, 0x00020000};
-}
 
 constexpr int kBM = 256, kBN = 256;  // output tile
 constexpr int kBK = 256;             // K elements per step
@@ -66,24 +36,6 @@ constexpr int kScalePanel = kBM * (kBK / 32);    // E8M0 bytes of one operand pe
 constexpr int kBuffer = 2 * kPanel + 2 * kScalePanel;  // A, B, A scales, B scales (68 KB)
 constexpr int kGroupM = 8;
 constexpr int kWavesM = 4, kWavesN = 2;  // wave grid of the launched kernel
-
-__device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int ntiles = tiles_m * tiles_n;
-  if (ntiles % 8 == 0) pid = (pid % 8) * (ntiles / 8) + pid / 8;  // contiguous range per XCD
-  const int per_group = kGroupM * tiles_n;
-  const int group = pid / per_group;
-  const int first_m = group * kGroupM;
-  const int gsize = tiles_m - first_m < kGroupM ? tiles_m - first_m : kGroupM;
-  const int in_group = pid - group * per_group;
-  tm = first_m + in_group % gsize;
-  tn = in_group / gsize;
-}
-
-__device__ __forceinline__ void store_c(void* c, int cdt, int64_t i, float v) {
-  if (cdt == TGM_BF16) ((uint16_t*)c)[i] = f32_to_bf16(v);
-  else if (cdt == TGM_F16) ((_Float16*)c)[i] = (_Float16)v;
-  else ((float*)c)[i] = v;
-}
 
 // WM x WN waves per workgroup; wave tile (256 / WM) x (256 / WN) = FA x FB MFMA tiles.
 template <int WM, int WN>
@@ -99,7 +51,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __res
   const int wm = wave / WN, wn = wave % WN;
   const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
   int tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  tile_of(blockIdx.x, tiles_m, tiles_n, kGroupM, tm, tn);
   const int m0 = tm * kBM, n0 = tn * kBN;
   const int nsteps = K / kBK;
 
@@ -329,13 +281,6 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __res
 }  // namespace tgm
 
 using namespace tgm;
-
-extern "C" int tgm_gemm_w(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n,
-                          int64_t k, const void* scales, int scale_dtype, int64_t block_size, void* c, int c_dtype,
-                          int64_t ldc, void* stream) {
-  clear_error();
-  TGM_UNSUPPORTED("tgm_gemm_w: no MFMA kernel for this combination");
-}
 
 extern "C" int tgm_gemm_mx(const void* a, int a_fmt, const void* a_scales, int64_t m, const void* b, int b_fmt,
                            const void* b_scales, int64_t n, int64_t k, void* c, int c_dtype, int64_t ldc,

@@ -1,0 +1,59 @@
+// Pieces shared by the MFMA GEMM kernels: vector typedefs, direct global -> LDS loads,
+// buffer resources, the XCD-aware tile order and the output store.
+#pragma once
+
+#include "tgm_common.h"
+
+namespace tgm {
+
+typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(unsigned)))) unsigned u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(unsigned)))) unsigned u32x2;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+
+// Direct global -> LDS loads through a buffer resource (bounds-checked: offsets past the
+// resource's size read zeros).  The 16 (or 4) bytes of lane l land at LDS address
+// lds_addr + 16 l (4 l).  They are issued as inline assembly so that the compiler does not
+// order later LDS reads of the *other* buffer behind them; completion is awaited
+// explicitly (s_waitcnt vmcnt(0)) before the barrier that publishes a buffer.  M0 is set
+// inside each statement and nothing else in the kernel uses it.
+__device__ __forceinline__ void lds_dma16(i32x4v rsrc, unsigned lds_addr, unsigned voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" : : "s"(lds_addr), "v"(voff), "s"(rsrc) : "memory");
+}
+__device__ __forceinline__ void lds_dma4(i32x4v rsrc, unsigned lds_addr, unsigned voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" : : "s"(lds_addr), "v"(voff), "s"(rsrc) : "memory");
+}
+__device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Raw buffer resource (stride 0, num_records = bytes) for a global pointer.
+__device__ __forceinline__ i32x4v buffer_rsrc(const void* p, unsigned bytes) {
+  const unsigned long long a = (unsigned long long)p;
+  return i32x4v{(int)(unsigned)a, (int)((unsigned)(a >> 32) & 0xFFFFu), (int)bytes, 0x00020000};
+}
+
+// Tile order: consecutive hardware workgroup ids go to different XCDs, so the id is permuted
+// to give each XCD a contiguous range of tiles (when the count divides by 8), walked in
+// groups of ``group_m`` row panels so that concurrently running tiles share operand panels
+// in that XCD's L2.
+__device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
+  const int ntiles = tiles_m * tiles_n;
+  if (ntiles % 8 == 0) pid = (pid % 8) * (ntiles / 8) + pid / 8;  // contiguous range per XCD
+  const int per_group = group_m * tiles_n;
+  const int group = pid / per_group;
+  const int first_m = group * group_m;
+  const int gsize = tiles_m - first_m < group_m ? tiles_m - first_m : group_m;
+  const int in_group = pid - group * per_group;
+  tm = first_m + in_group % gsize;
+  tn = in_group / gsize;
+}
+
+__device__ __forceinline__ void store_c(void* c, int cdt, int64_t i, float v) {
+  if (cdt == TGM_BF16) ((uint16_t*)c)[i] = f32_to_bf16(v);
+  else if (cdt == TGM_F16) ((_Float16*)c)[i] = (_Float16)v;
+  else ((float*)c)[i] = v;
+}
+
+}  // namespace tgm

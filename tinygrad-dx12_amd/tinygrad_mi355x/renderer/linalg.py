@@ -35,9 +35,9 @@ class MatrixKernel:
 # Family 1: fused dequant GEMV / skinny GEMM (replaces thread_source and the N=1 linalg_source).
 GEMV = MatrixKernel("tgm_gemv", "Wave", (16, 16, 128), 256)
 # Family 2: dequant-to-bf16 MFMA GEMM (replaces linalg_source for one packed operand).
-GEMM_W = MatrixKernel("tgm_gemm_w", "ThreadGroup", (256, 256, 64), 256)
+GEMM_W = MatrixKernel("tgm_gemm_w", "ThreadGroup", (256, 128, 128), 512)
 # Family 2: block-scaled FP4/FP6 MFMA GEMM (two packed MX operands).
-GEMM_MX = MatrixKernel("tgm_gemm_mx", "ThreadGroup", (256, 256, 128), 256)
+GEMM_MX = MatrixKernel("tgm_gemm_mx", "ThreadGroup", (256, 256, 256), 512)
 # Exact-width fallback (the reference's ordinary matmul); never a "native" candidate.
 PLAIN = MatrixKernel("tgm_gemm_plain", "tiled", (16, 16, 1), 256)
 
