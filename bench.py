@@ -34,7 +34,7 @@ FP4_PEAK_TFLOPS = 10100.0
 N_COPIES = 18
 
 
-EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_cfg1", "fp6_e3m2_gemm_cfg3", "fp6_e2m3_gemm_cfg3", "fp4_gemm_8192",
+EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_cfg1", "int4_gemv_n14336", "fp6_e3m2_gemm_cfg3", "fp6_e2m3_gemm_cfg3", "fp4_gemm_8192",
           "fp4_gemm_4096x14336x4096")
 
 
@@ -108,8 +108,7 @@ def fp4_gemv_workload(torch, K, dev, m: int, steps: int, warmup: int, copies: in
             "TFLOPS": 2 * m * n * k / ms / 1e9}
 
 
-def int4_gemv_workload(torch, K, dev, steps: int, warmup: int, copies: int = 40):
-    n = k = 4096
+def int4_gemv_workload(torch, K, dev, steps: int, warmup: int, copies: int = 40, n: int = 4096, k: int = 4096):
     g = torch.Generator(device=dev)
     g.manual_seed(1)
     ws = [torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device=dev, generator=g) for _ in range(copies)]
@@ -126,7 +125,7 @@ def int4_gemv_workload(torch, K, dev, steps: int, warmup: int, copies: int = 40)
 
     ms = Timer(torch, launch, steps, warmup).run()
     nbytes = gemv_bytes(n, k, 1, 4, 2, 2, 2)
-    return {"workload": "int4 g32 fp16-scale GEMV N=K=4096 M=1 fp16", "ms": ms, "bytes": nbytes,
+    return {"workload": f"int4 g32 fp16-scale GEMV N={n} K={k} M=1 fp16", "ms": ms, "bytes": nbytes,
             "GB/s": nbytes / ms / 1e6, "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
 
 
@@ -277,6 +276,7 @@ def main() -> int:
         "fp4_gemv_m4": lambda: fp4_gemv_workload(torch, K, dev, 4, half, args.warmup),
         "fp4_gemv_m16": lambda: fp4_gemv_workload(torch, K, dev, 16, half, args.warmup),
         "int4_gemv_cfg1": lambda: int4_gemv_workload(torch, K, dev, half, args.warmup),
+        "int4_gemv_n14336": lambda: int4_gemv_workload(torch, K, dev, half, args.warmup, copies=12, n=14336),
         "fp6_e3m2_gemm_cfg3": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e3m2", 20, 20),
         "fp6_e2m3_gemm_cfg3": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e2m3", 20, 20),
         "fp4_gemm_8192": lambda: fp4_gemm_workload(torch, K, dev, 8192, 8192, 8192, 20, 20),

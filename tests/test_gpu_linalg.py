@@ -228,6 +228,57 @@ def test_int4_config1_shape(dev):
     assert y.dtype is torch.float16 and O.max_rel_err(y.float().cpu().numpy(), ref) <= TOL
 
 
+def int4_weight(dev, fmt, n, k, sdt, bs, rng):
+    """Random INT4/UINT4 weight with scales of dtype ``sdt`` (None: unscaled) per ``bs``."""
+    codes = rng.integers(0, 16, (n, k)).astype(np.uint8)
+    data = O.pack_codes(codes, 4)
+    scales = s_np = None
+    if sdt is not None:
+        s_np = rng.uniform(0.005, 0.02, (n, k // bs)).astype(np.float32)
+        scales = torch.from_numpy(s_np).to(dev).to(sdt)
+        s_np = scales.float().cpu().numpy()  # the values the device holds
+    w = PackedTensor(torch.from_numpy(data).to(dev), fmt, (n, k), scales, bs)
+    return w, O.dequant_f64(data, fmt, (n, k), s_np, bs)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "uint4"])
+@pytest.mark.parametrize("sdt,bs", [(torch.float16, 32), (torch.bfloat16, 64), (torch.float32, 128), (None, 32)])
+@pytest.mark.parametrize("m", [1, 5, 16])
+def test_gemv_int4_mfma_parity(dev, fmt, sdt, bs, m):
+    """INT4/UINT4 x fp16 GEMV on the f16-MFMA kernel (K a multiple of 128), ragged N."""
+    n, k = 1000, 512
+    rng = np.random.default_rng(m * 11 + bs)
+    w, deq = int4_weight(dev, fmt, n, k, sdt, bs, rng)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float16)).to(dev)
+    y = matmul_nt(x, w, dtype=torch.float32)
+    assert O.max_rel_err(y.cpu().numpy(), x.float().cpu().numpy().astype(np.float64) @ deq.T) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["int4", "uint4"])
+def test_gemv_int4_one_hot_is_exact(dev, fmt):
+    """One-hot fp16 activation rows recover code * scale exactly (fp32 out): nibble order,
+    block K order and the per-block scale FMA line up."""
+    n, k, m = 512, 1024, 16
+    rng = np.random.default_rng(12)
+    w, deq = int4_weight(dev, fmt, n, k, torch.float16, 32, rng)
+    cols = rng.choice(k, m, replace=False)
+    x = torch.zeros((m, k), dtype=torch.float16, device=dev)
+    x[torch.arange(m), torch.from_numpy(cols)] = 1.0
+    y = matmul_nt(x, w, dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(y, deq[:, cols].T.astype(np.float32))
+
+
+def test_gemv_int4_north_star_shape(dev):
+    """INT4 g32 fp16-scale GEMV at 14336 x 4096, fp16 x [1, 4096] -> fp16."""
+    n, k = 14336, 4096
+    rng = np.random.default_rng(6)
+    w, deq = int4_weight(dev, "int4", n, k, torch.float16, 32, rng)
+    x = torch.from_numpy(rng.standard_normal((1, k)).astype(np.float16)).to(dev)
+    y = matvec(w, x[0], output_dtype=torch.float16)
+    ref = deq @ x[0].float().cpu().numpy().astype(np.float64)
+    assert O.max_rel_err(y.float().cpu().numpy(), ref) <= TOL
+
+
 def test_matvec_thread_true_uses_native_gemv(dev):
     rng = np.random.default_rng(1)
     w, deq = make_weight(dev, "fp4_e2m1", 128, 256, "e8m0", rng)

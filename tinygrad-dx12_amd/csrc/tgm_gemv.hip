@@ -8,7 +8,10 @@
 //
 //   Y[m, n] = sum_k X[m, k] * deq(W)[n, k],   M <= 16
 //
-// Two kernels:
+// Three kernels:
+//  * gemv_int4   -- INT4/UINT4 weights with fp16/bf16/f32/E8M0 group scales (groups of 32,
+//    64 or 128), fp16 activations: one f16 MFMA per 32-element block, scale applied to the
+//    block's exact partial sum (tgm_gemv_int4.hip).
 //  * gemv_stream -- FP4/FP6 weights with E8M0 (or no) scales, bf16 activations.  Each
 //    dequantised weight code*2^(e-127) is exact in bf16, every bf16*bf16 product is
 //    exact in fp32, so v_mfma_f32_16x16x32_bf16 with fp32 accumulation computes the
@@ -18,6 +21,10 @@
 #include "tgm_gemv_stream.h"
 
 namespace tgm {
+// INT4/UINT4 weights x fp16 activations on f16 MFMA (tgm_gemv_int4.hip).
+int launch_gemv_int4(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k, const void* scales, int sdt,
+                     int64_t bs, const void* x, int xdt, int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy);
+
 // ------------------------------------------------------------------ VALU GEMV
 // One wave per output row n; lanes stride over K.  Exact fp32 dequant per element.
 template <int MB>
@@ -83,6 +90,11 @@ extern "C" int tgm_gemv(const void* w, int fmt, int64_t n, int64_t k, const void
   const int64_t nblk = (k + block_size - 1) / block_size;
   if (k == 0) {
     TGM_UNSUPPORTED("K == 0 has no gemv kernel");
+  }
+  if (fmt == TGM_FMT_INT4 || fmt == TGM_FMT_UINT4) {
+    const int st = launch_gemv_int4(s, w, fmt, n, k, scales, scale_dtype, block_size, x, x_dtype, m, ldx, y, y_dtype, ldy);
+    if (st == TGM_OK) return launch_status("tgm_gemv(int4 mfma)");
+    if (st != TGM_E_UNSUPPORTED) return st;
   }
   if (mfma_gemv_ok(w, fmt, n, k, scales, scale_dtype, block_size, x, x_dtype, m, ldx, y_dtype)) {
     int st;
