@@ -8,7 +8,10 @@
 //
 //   Y[m, n] = sum_k X[m, k] * deq(W)[n, k],   M <= 16
 //
-// Three kernels:
+// Four kernels:
+//  * gemv_rows_fp4 -- M = 1, FP4 weights with E8M0 (or no) scales, bf16 activations, K a
+//    multiple of 2048: each wave streams 8 whole rows in address order and reduces on the
+//    VALU (tgm_gemv_rows.hip).
 //  * gemv_int4   -- INT4/UINT4 weights with fp16/bf16/f32/E8M0 group scales (groups of 32,
 //    64 or 128), fp16 activations: one f16 MFMA per 32-element block, scale applied to the
 //    block's exact partial sum (tgm_gemv_int4.hip).
@@ -21,6 +24,9 @@
 #include "tgm_gemv_stream.h"
 
 namespace tgm {
+// M = 1 FP4 GEMV streamed row-contiguously (tgm_gemv_rows.hip).
+int launch_gemv_rows(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k, const void* scales, int sdt,
+                     int64_t bs, const void* x, int xdt, int64_t m, void* y, int ydt);
 // INT4/UINT4 weights x fp16 activations on f16 MFMA (tgm_gemv_int4.hip).
 int launch_gemv_int4(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k, const void* scales, int sdt,
                      int64_t bs, const void* x, int xdt, int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy);
@@ -90,6 +96,11 @@ extern "C" int tgm_gemv(const void* w, int fmt, int64_t n, int64_t k, const void
   const int64_t nblk = (k + block_size - 1) / block_size;
   if (k == 0) {
     TGM_UNSUPPORTED("K == 0 has no gemv kernel");
+  }
+  if (m == 1 && n * (k / 2) < (1ll << 40)) {
+    const int st = launch_gemv_rows(s, w, fmt, n, k, scales, scale_dtype, block_size, x, x_dtype, m, y, y_dtype);
+    if (st == TGM_OK) return launch_status("tgm_gemv(rows)");
+    if (st != TGM_E_UNSUPPORTED) return st;
   }
   if (fmt == TGM_FMT_INT4 || fmt == TGM_FMT_UINT4) {
     const int st = launch_gemv_int4(s, w, fmt, n, k, scales, scale_dtype, block_size, x, x_dtype, m, ldx, y, y_dtype, ldy);

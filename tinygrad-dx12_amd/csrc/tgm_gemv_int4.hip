@@ -22,6 +22,7 @@
 // operands exactly: nibble u (p ^ 8 for int4) placed under the fp16 pattern 0x6400 is
 // 1024 + u, minus 1024 (+ 8 for int4) in a packed f16 add.
 #include "tgm_common.h"
+#include "tgm_lanes.h"
 
 namespace tgm {
 
@@ -57,12 +58,10 @@ __device__ __forceinline__ half8 int4_to_half8(unsigned d, unsigned flip, half2v
 // lane row g holds what register g of lane row r held.  A lane that loaded 16 bytes (block
 // g = its row, dwords 0..3) then holds dword g of blocks 0..3, one per MFMA.
 __device__ __forceinline__ void transpose4(unsigned& r0, unsigned& r1, unsigned& r2, unsigned& r3) {
-  const auto a = __builtin_amdgcn_permlane32_swap(r0, r2, false, false);  // rows 2,3 of r0 <-> rows 0,1 of r2
-  const auto b = __builtin_amdgcn_permlane32_swap(r1, r3, false, false);
-  r0 = a[0]; r2 = a[1]; r1 = b[0]; r3 = b[1];
-  const auto c = __builtin_amdgcn_permlane16_swap(r0, r1, false, false);  // odd rows of r0 <-> even rows of r1
-  const auto d = __builtin_amdgcn_permlane16_swap(r2, r3, false, false);
-  r0 = c[0]; r1 = c[1]; r2 = d[0]; r3 = d[1];
+  swap32(r0, r2);  // rows 2,3 of r0 <-> rows 0,1 of r2
+  swap32(r1, r3);
+  swap16(r0, r1);  // odd rows of r0 <-> even rows of r1
+  swap16(r2, r3);
 }
 
 // A workgroup holds NT x NK waves: wave (ti, ki) owns weight tile blockIdx.x * NT + ti (16

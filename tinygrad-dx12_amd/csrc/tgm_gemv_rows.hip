@@ -1,0 +1,176 @@
+// Kernel family 1, single-row decode path (M = 1): FP4 E2M1 weights with E8M0 (or no)
+// block-32 scales x bf16 activations, streamed row-contiguously and reduced on the VALU.
+//
+//   y[n] = sum_k x[k] * deq(W)[n, k]
+//
+// With one activation row an MFMA tile wastes 15 of its 16 columns, and an MFMA operand
+// layout forces every load instruction to touch 16 weight rows.  Here a wave owns R
+// consecutive rows -- R * K/2 contiguous bytes -- and reads them 1 KB per instruction in
+// address order: lane l of instruction i gets bytes [16 l, 16 l + 16) of half-row (i % IPR)
+// of row i / IPR (IPR = K / 2048 instructions per row), i.e. the 32 codes
+// K [2048 h + 32 l, + 32) -- exactly one MX block, so one E8M0 byte per lane and row.
+// Every lane therefore needs the same activations for every row: 32 bf16 per half-row,
+// loaded once into registers.  Codes become bf16 pairs with v_cvt_scalef32_pk_bf16_fp4 (the
+// E8M0 scale folded in exactly) and meet the activations in v_dot2_f32_bf16, whose bf16 x
+// bf16 products are exact in fp32.  Per-lane row partials are reduced across the wave by a
+// register-halving butterfly (each exchange moves useful data), one lane per row stores.
+//
+// Replaces the reference's thread-scope matvec / N=1 LinAlg matmul over a weight a
+// separate kernel first decoded to fp32 (alexandreteles/tinygrad-dx12
+// src/tinygrad_dx12/renderer/linalg.py:127-166, codegen/linalg.py:244-245,
+// codegen/decomp/dx12.py:49-106).
+#include "tgm_common.h"
+#include "tgm_lanes.h"
+
+namespace tgm {
+
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2r;
+typedef unsigned u32x4r __attribute__((ext_vector_type(4)));
+
+// Sum 8 per-lane partials (one per row) over the 64 lanes of a wave.  Two permlane swaps
+// fold lane halves and 16-lane rows pairwise (each swap exchanges exactly the half of two
+// registers the other side needs, so one add per register completes the stage), a DPP
+// stage halves once more, and three DPP exchanges finish the sum within groups of 8 lanes.
+// Lane l ends with row reduce_row8(l).
+__device__ __forceinline__ float reduce_rows8(float (&a)[8], int lane) {
+  float b[4], c[2];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {  // lanes 0-31 keep rows 0-3, lanes 32-63 rows 4-7
+    float lo = a[r], hi = a[r + 4];
+    swap32(lo, hi);
+    b[r] = lo + hi;
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {  // even 16-lane rows keep b[r], odd rows b[r + 2]
+    float lo = b[r], hi = b[r + 2];
+    swap16(lo, hi);
+    c[r] = lo + hi;
+  }
+  const bool up8 = lane & 8;  // lanes with bit 3 keep c[1]
+  float v = (up8 ? c[1] : c[0]) + xor8(up8 ? c[0] : c[1]);
+  v += xor4(v);
+  v += xor2(v);
+  v += xor1(v);
+  return v;
+}
+__device__ __forceinline__ int reduce_row8(int lane) {
+  return ((lane >> 5) & 1) << 2 | ((lane >> 4) & 1) << 1 | ((lane >> 3) & 1);
+}
+
+// One wave per R = 8 rows, four waves per workgroup; IPR instructions per row
+// (K = 2048 IPR); D loads in flight per wave.
+template <int R, int IPR, int D, bool SCALED>
+__global__ void __launch_bounds__(256) gemv_rows_fp4(const uint8_t* __restrict__ w, int64_t N,
+                                                   const uint8_t* __restrict__ scales, const __bf16* __restrict__ x,
+                                                   void* __restrict__ y, int ydt) {
+  constexpr int NI = R * IPR;  // load instructions per wave
+  constexpr int K = 2048 * IPR, KB = K / 32;
+  const int lane = threadIdx.x & 63;
+  const int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  // activations: lane l needs K [2048 h + 32 l, + 32) for every half-row h
+  // (loaded as pairs; the compiler merges them into 16-byte loads.  Extracting the lanes of
+  // a 4-dword vector and bit-casting each to a bf16 pair was miscompiled into one repeated
+  // pair by the ROCm 7.2 compiler.)
+  bf16x2r xr[IPR][16];
+#pragma unroll
+  for (int h = 0; h < IPR; ++h) {
+    const bf16x2r* xp = (const bf16x2r*)(x + 2048 * h + 32 * lane);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) xr[h][j] = xp[j];
+  }
+  auto row_of = [&](int i) __attribute__((always_inline)) {
+    const int64_t r = r0 + i / IPR;
+    return r < N ? r : N - 1;  // rows past N re-read the last row; they are not stored
+  };
+  // Scales: the wave's R rows own R * KB contiguous E8M0 bytes (one byte per lane and load
+  // instruction); they are fetched with 16-byte loads (addresses clamped inside the tensor,
+  // so every load is unconditional), passed through this wave's LDS slice and read back as
+  // the byte each lane needs for each instruction.
+  constexpr int SB = R * KB, SL = (SB + 1023) / 1024;  // scale bytes, 16-byte-per-lane loads
+  __shared__ __attribute__((aligned(16))) unsigned char sl[4][SCALED ? SB : 16];
+  const int wv = threadIdx.x >> 6;
+  u32x4r sraw[SL];
+  if constexpr (SCALED) {
+    const int64_t limit = N * KB - 16;  // last 16-byte chunk of the scale tensor
+#pragma unroll
+    for (int j = 0; j < SL; ++j) {
+      int64_t off = r0 * KB + 1024 * j + 16 * lane;
+      off = off < limit ? off : limit;
+      sraw[j] = *(const u32x4r*)(scales + off);
+    }
+  }
+  u32x4r codes[D];
+  auto load = [&](int i, int slot) __attribute__((always_inline)) {
+    const int64_t r = row_of(i);
+    const int h = i % IPR;
+    codes[slot] = *(const u32x4r*)(w + r * (K / 2) + 1024 * h + 16 * lane);
+  };
+#pragma unroll
+  for (int i = 0; i < D; ++i) load(i, i);
+  unsigned sbyte[NI];
+  if constexpr (SCALED) {
+#pragma unroll
+    for (int j = 0; j < SL; ++j)
+      if (1024 * j + 16 * lane < SB) *(u32x4r*)(&sl[wv][1024 * j + 16 * lane]) = sraw[j];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int i = 0; i < NI; ++i) sbyte[i] = sl[wv][(i / IPR) * KB + 64 * (i % IPR) + lane];
+  }
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int slot = i % D, h = i % IPR;
+    const float s = __builtin_bit_cast(float, (SCALED ? sbyte[i] : 127u) << 23);
+    float a[2] = {acc[i / IPR], 0.f};  // two chains halve the dependent-dot latency
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const unsigned cw = codes[slot][e];
+      const bf16x2r p[4] = {__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(cw, s, 0),
+                            __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(cw, s, 1),
+                            __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(cw, s, 2),
+                            __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(cw, s, 3)};
+#pragma unroll
+      for (int b = 0; b < 4; ++b) a[e >> 1] = __builtin_amdgcn_fdot2_f32_bf16(p[b], xr[h][4 * e + b], a[e >> 1], false);
+    }
+    acc[i / IPR] = a[0] + a[1];
+    if (i + D < NI) load(i + D, slot);
+    __builtin_amdgcn_sched_barrier(0);  // keep each refill right after the data it replaces is used
+  }
+  static_assert(R == 8, "the reduction folds 8 rows");
+  const float v = reduce_rows8(acc, lane);
+  const int64_t row = r0 + reduce_row8(lane);
+  if ((lane & 7) == 0 && row < N) store_from_f32(y, ydt, row, v);
+}
+
+constexpr int kRowsPerWave = 8;
+
+// M = 1 FP4 GEMV on the row-streaming kernel; TGM_E_UNSUPPORTED when the operands do not fit.
+int launch_gemv_rows(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k, const void* scales, int sdt,
+                     int64_t bs, const void* x, int xdt, int64_t m, void* y, int ydt) {
+  if (fmt != TGM_FMT_FP4_E2M1 || m != 1 || xdt != TGM_BF16) return TGM_E_UNSUPPORTED;
+  if (k % 2048 != 0 || k / 2048 > 4) return TGM_E_UNSUPPORTED;
+  if (scales && (sdt != TGM_E8M0 || bs != 32)) return TGM_E_UNSUPPORTED;
+  if ((uintptr_t)w % 16 || (uintptr_t)x % 16) return TGM_E_UNSUPPORTED;
+  constexpr int R = kRowsPerWave;
+  const unsigned grid = (unsigned)((n + 4 * R - 1) / (4 * R));
+  const int ipr = (int)(k / 2048);
+#define TGM_ROWS(IPR, D)                                                                                           \
+  if (ipr == IPR) {                                                                                                \
+    if (scales)                                                                                                    \
+      hipLaunchKernelGGL((gemv_rows_fp4<R, IPR, D, true>), dim3(grid), dim3(256), 0, s, (const uint8_t*)w, n,      \
+                         (const uint8_t*)scales, (const __bf16*)x, y, ydt);                                        \
+    else                                                                                                           \
+      hipLaunchKernelGGL((gemv_rows_fp4<R, IPR, D, false>), dim3(grid), dim3(256), 0, s, (const uint8_t*)w, n,     \
+                         (const uint8_t*)scales, (const __bf16*)x, y, ydt);                                        \
+    return TGM_OK;                                                                                                 \
+  }
+  TGM_ROWS(1, 8) TGM_ROWS(2, 16) TGM_ROWS(3, 16) TGM_ROWS(4, 16)
+#undef TGM_ROWS
+  return TGM_E_UNSUPPORTED;
+}
+
+}  // namespace tgm
