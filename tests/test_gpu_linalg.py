@@ -279,6 +279,41 @@ def test_gemv_int4_north_star_shape(dev):
     assert O.max_rel_err(y.float().cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("fmt", ["fp4_e2m1", "int4", "uint4"])
+@pytest.mark.parametrize("k", [2048, 4096, 8192])
+def test_gemv_rows_one_hot_is_exact(dev, fmt, k):
+    """M = 1 row-streaming kernels (K a multiple of 2048): one-hot activations recover
+    deq(W)[:, j] exactly for columns across lanes, half-rows and code positions."""
+    n = 200  # ragged: 200 rows = 6.25 workgroups of 32
+    rng = np.random.default_rng(k)
+    if fmt == "fp4_e2m1":
+        w, deq = make_weight(dev, fmt, n, k, "e8m0", rng)
+        xdt = torch.bfloat16
+    else:
+        w, deq = int4_weight(dev, fmt, n, k, torch.float16, 32, rng)
+        xdt = torch.float16
+    for j in [0, 1, 2, 3, 5, 7, 8, 31, 32, 33, 1000, 2047, 2048, k - 1]:
+        if j >= k:
+            continue
+        x = torch.zeros(k, dtype=xdt, device=dev)
+        x[j] = 1.0
+        y = matvec(w, x, torch.float32).cpu().numpy()
+        assert np.array_equal(y, deq[:, j].astype(np.float32)), f"column {j}"
+
+
+@pytest.mark.parametrize("fmt", ["int4", "uint4"])
+@pytest.mark.parametrize("sdt,bs", [(torch.float16, 32), (torch.bfloat16, 64), (torch.float32, 128), (None, 32)])
+@pytest.mark.parametrize("nk", [(1000, 4096), (300, 2048), (64, 8192)])
+def test_gemv_rows_int4_parity(dev, fmt, sdt, bs, nk):
+    """M = 1 INT4/UINT4 x fp16 on the row-streaming kernel, every scale dtype and group size."""
+    n, k = nk
+    rng = np.random.default_rng(n + k + bs)
+    w, deq = int4_weight(dev, fmt, n, k, sdt, bs, rng)
+    x = torch.from_numpy(rng.standard_normal(k).astype(np.float16)).to(dev)
+    y = matvec(w, x, torch.float32)
+    assert O.max_rel_err(y.cpu().numpy(), deq @ x.float().cpu().numpy().astype(np.float64)) <= TOL
+
+
 def test_matvec_thread_true_uses_native_gemv(dev):
     rng = np.random.default_rng(1)
     w, deq = make_weight(dev, "fp4_e2m1", 128, 256, "e8m0", rng)

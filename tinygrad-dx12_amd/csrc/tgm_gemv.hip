@@ -9,9 +9,10 @@
 //   Y[m, n] = sum_k X[m, k] * deq(W)[n, k],   M <= 16
 //
 // Four kernels:
-//  * gemv_rows_fp4 -- M = 1, FP4 weights with E8M0 (or no) scales, bf16 activations, K a
-//    multiple of 2048: each wave streams 8 whole rows in address order and reduces on the
-//    VALU (tgm_gemv_rows.hip).
+//  * gemv_rows_fp4 / gemv_rows_int4 -- M = 1 with K a multiple of 2048: FP4 weights with
+//    E8M0 (or no) scales x bf16 activations, or INT4/UINT4 weights with fp16/bf16/f32 group
+//    scales (32, 64, 128) x fp16 activations; each wave streams 8 whole rows in address
+//    order and reduces on the VALU (tgm_gemv_rows.hip).
 //  * gemv_int4   -- INT4/UINT4 weights with fp16/bf16/f32/E8M0 group scales (groups of 32,
 //    64 or 128), fp16 activations: one f16 MFMA per 32-element block, scale applied to the
 //    block's exact partial sum (tgm_gemv_int4.hip).
@@ -27,6 +28,8 @@ namespace tgm {
 // M = 1 FP4 GEMV streamed row-contiguously (tgm_gemv_rows.hip).
 int launch_gemv_rows(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k, const void* scales, int sdt,
                      int64_t bs, const void* x, int xdt, int64_t m, void* y, int ydt);
+int launch_gemv_rows_int4(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k, const void* scales, int sdt,
+                          int64_t bs, const void* x, int xdt, int64_t m, void* y, int ydt);
 // INT4/UINT4 weights x fp16 activations on f16 MFMA (tgm_gemv_int4.hip).
 int launch_gemv_int4(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k, const void* scales, int sdt,
                      int64_t bs, const void* x, int xdt, int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy);
@@ -98,7 +101,9 @@ extern "C" int tgm_gemv(const void* w, int fmt, int64_t n, int64_t k, const void
     TGM_UNSUPPORTED("K == 0 has no gemv kernel");
   }
   if (m == 1 && n * (k / 2) < (1ll << 40)) {
-    const int st = launch_gemv_rows(s, w, fmt, n, k, scales, scale_dtype, block_size, x, x_dtype, m, y, y_dtype);
+    int st = launch_gemv_rows(s, w, fmt, n, k, scales, scale_dtype, block_size, x, x_dtype, m, y, y_dtype);
+    if (st == TGM_E_UNSUPPORTED)
+      st = launch_gemv_rows_int4(s, w, fmt, n, k, scales, scale_dtype, block_size, x, x_dtype, m, y, y_dtype);
     if (st == TGM_OK) return launch_status("tgm_gemv(rows)");
     if (st != TGM_E_UNSUPPORTED) return st;
   }

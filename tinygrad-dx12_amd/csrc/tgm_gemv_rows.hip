@@ -146,6 +146,122 @@ __global__ void __launch_bounds__(256) gemv_rows_fp4(const uint8_t* __restrict__
   if ((lane & 7) == 0 && row < N) store_from_f32(y, ydt, row, v);
 }
 
+// ------------------------------------------------------------------ INT4 / UINT4
+// Same row-streaming structure for 4-bit integer codes with fp16 activations and fp16 / bf16
+// / f32 group scales (groups of 32, 64 or 128 along K).  Codes become fp16 exactly: each
+// nibble n (n ^ 8 for int4) goes under the fp16 byte 0x64 (1024 + n) and a packed f16 add
+// removes 1024 (+ 8).  One v_perm builds a pair from two nibbles of the same byte lane,
+// so a dword's codes come out as pairs (0,2) (4,6) (1,3) (5,7); the activation pairs are
+// reordered the same way once, at load time.  v_dot2_f32_f16 products (fp16 x integer) are
+// exact in fp32; each lane's 32-code partial is then scaled by its group's scale in fp32.
+typedef _Float16 half2r __attribute__((ext_vector_type(2)));
+
+template <int SDT>
+__device__ __forceinline__ float int4_scale(const unsigned char* p) {
+  if constexpr (SDT == TGM_F16) return (float)*(const _Float16*)p;
+  else if constexpr (SDT == TGM_BF16) return __builtin_bit_cast(float, (unsigned)*(const uint16_t*)p << 16);
+  else if constexpr (SDT == TGM_F32) return *(const float*)p;
+  else return 1.0f;
+}
+
+// R = 8 rows per wave; GS = log2(group size / 32); SDT = scale dtype (-1: unscaled).
+template <int R, int IPR, int D, int SDT>
+__global__ void __launch_bounds__(256) gemv_rows_int4(const uint8_t* __restrict__ w, int64_t N,
+                                                    const uint8_t* __restrict__ scales, int GS, unsigned flip,
+                                                    float bias, const _Float16* __restrict__ x, void* __restrict__ y,
+                                                    int ydt) {
+  constexpr int NI = R * IPR;
+  constexpr int K = 2048 * IPR;
+  constexpr bool SCALED = SDT >= 0;
+  constexpr int SSIZE = SDT == TGM_F32 ? 4 : 2;
+  const int lane = threadIdx.x & 63;
+  const int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  // activations K [2048 h + 32 l, + 32) as the pairs the codes come out in: dword e of
+  // the lane's 16 bytes holds codes 8e .. 8e+7, paired (0,2) (4,6) (1,3) (5,7)
+  half2r xr[IPR][16];
+#pragma unroll
+  for (int h = 0; h < IPR; ++h) {
+    const unsigned* xp = (const unsigned*)(x + 2048 * h + 32 * lane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const unsigned p0 = xp[4 * e], p1 = xp[4 * e + 1], p2 = xp[4 * e + 2], p3 = xp[4 * e + 3];  // (0,1) (2,3) (4,5) (6,7)
+      xr[h][4 * e + 0] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p1, p0, 0x05040100u));  // x0, x2
+      xr[h][4 * e + 1] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p3, p2, 0x05040100u));  // x4, x6
+      xr[h][4 * e + 2] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p1, p0, 0x07060302u));  // x1, x3
+      xr[h][4 * e + 3] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p3, p2, 0x07060302u));  // x5, x7
+    }
+  }
+  auto row_of = [&](int i) __attribute__((always_inline)) {
+    const int64_t r = r0 + i / IPR;
+    return r < N ? r : N - 1;
+  };
+  // Scales: the wave's rows own R * (K >> (5 + GS)) * SSIZE contiguous bytes; staged through
+  // LDS like the FP4 kernel's, then each lane reads its group's scale per instruction.
+  constexpr int SBMAX = R * (K / 32) * SSIZE, SL = (SBMAX + 1023) / 1024;
+  __shared__ __attribute__((aligned(16))) unsigned char sl[4][SCALED ? SBMAX : 16];
+  const int wv = threadIdx.x >> 6;
+  const int ng = (K / 32) >> GS;          // groups per row
+  const int sb = R * ng * SSIZE;          // this wave's scale bytes
+  u32x4r sraw[SL];
+  if constexpr (SCALED) {
+    const int64_t limit = N * ng * SSIZE - 16;
+#pragma unroll
+    for (int j = 0; j < SL; ++j) {
+      int64_t off = r0 * ng * SSIZE + 1024 * j + 16 * lane;
+      off = off < limit ? off : limit;
+      sraw[j] = *(const u32x4r*)(scales + off);
+    }
+  }
+  u32x4r codes[D];
+  auto load = [&](int i, int slot) __attribute__((always_inline)) {
+    const int64_t r = row_of(i);
+    codes[slot] = *(const u32x4r*)(w + r * (K / 2) + 1024 * (i % IPR) + 16 * lane);
+  };
+#pragma unroll
+  for (int i = 0; i < D; ++i) load(i, i);
+  float sv[NI];
+  if constexpr (SCALED) {
+#pragma unroll
+    for (int j = 0; j < SL; ++j)
+      if (1024 * j + 16 * lane < sb) *(u32x4r*)(&sl[wv][1024 * j + 16 * lane]) = sraw[j];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      sv[i] = int4_scale<SDT>(&sl[wv][((i / IPR) * ng + ((64 * (i % IPR) + lane) >> GS)) * SSIZE]);
+  }
+  const half2r hb = {(_Float16)bias, (_Float16)bias};
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int slot = i % D, h = i % IPR;
+    float a[2] = {0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const unsigned d = codes[slot][e] ^ flip;
+      const unsigned lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;  // codes 0,2,4,6 / 1,3,5,7
+      const half2r c0 = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(0x64646464u, lo, 0x05010400u)) - hb;  // 0, 2
+      const half2r c1 = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(0x64646464u, lo, 0x07030602u)) - hb;  // 4, 6
+      const half2r c2 = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(0x64646464u, hi, 0x05010400u)) - hb;  // 1, 3
+      const half2r c3 = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(0x64646464u, hi, 0x07030602u)) - hb;  // 5, 7
+      a[e >> 1] = __builtin_amdgcn_fdot2(c0, xr[h][4 * e + 0], a[e >> 1], false);
+      a[e >> 1] = __builtin_amdgcn_fdot2(c1, xr[h][4 * e + 1], a[e >> 1], false);
+      a[e >> 1] = __builtin_amdgcn_fdot2(c2, xr[h][4 * e + 2], a[e >> 1], false);
+      a[e >> 1] = __builtin_amdgcn_fdot2(c3, xr[h][4 * e + 3], a[e >> 1], false);
+    }
+    const float part = a[0] + a[1];
+    acc[i / IPR] = SCALED ? __builtin_fmaf(sv[i], part, acc[i / IPR]) : acc[i / IPR] + part;
+    if (i + D < NI) load(i + D, slot);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const float v = reduce_rows8(acc, lane);
+  const int64_t row = r0 + reduce_row8(lane);
+  if ((lane & 7) == 0 && row < N) store_from_f32(y, ydt, row, v);
+}
+
 constexpr int kRowsPerWave = 8;
 
 // M = 1 FP4 GEMV on the row-streaming kernel; TGM_E_UNSUPPORTED when the operands do not fit.
@@ -171,6 +287,48 @@ int launch_gemv_rows(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k
   TGM_ROWS(1, 8) TGM_ROWS(2, 16) TGM_ROWS(3, 16) TGM_ROWS(4, 16)
 #undef TGM_ROWS
   return TGM_E_UNSUPPORTED;
+}
+
+template <int IPR, int SDT>
+void launch_rows_int4(unsigned grid, hipStream_t s, const void* w, int64_t n, const void* scales, int gs, bool sgn,
+                      const void* x, void* y, int ydt) {
+  constexpr int D = IPR == 1 ? 8 : 16;
+  hipLaunchKernelGGL((gemv_rows_int4<kRowsPerWave, IPR, D, SDT>), dim3(grid), dim3(256), 0, s, (const uint8_t*)w, n,
+                     (const uint8_t*)scales, gs, sgn ? 0x88888888u : 0u, sgn ? 1032.0f : 1024.0f,
+                     (const _Float16*)x, y, ydt);
+}
+
+template <int IPR>
+void launch_rows_int4_sdt(int sdt, unsigned grid, hipStream_t s, const void* w, int64_t n, const void* scales, int gs,
+                          bool sgn, const void* x, void* y, int ydt) {
+  if (!scales) launch_rows_int4<IPR, -1>(grid, s, w, n, scales, gs, sgn, x, y, ydt);
+  else if (sdt == TGM_F16) launch_rows_int4<IPR, TGM_F16>(grid, s, w, n, scales, gs, sgn, x, y, ydt);
+  else if (sdt == TGM_BF16) launch_rows_int4<IPR, TGM_BF16>(grid, s, w, n, scales, gs, sgn, x, y, ydt);
+  else launch_rows_int4<IPR, TGM_F32>(grid, s, w, n, scales, gs, sgn, x, y, ydt);
+}
+
+// M = 1 INT4/UINT4 x fp16 GEMV on the row-streaming kernel; TGM_E_UNSUPPORTED when it does not fit.
+int launch_gemv_rows_int4(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k, const void* scales, int sdt,
+                          int64_t bs, const void* x, int xdt, int64_t m, void* y, int ydt) {
+  if ((fmt != TGM_FMT_INT4 && fmt != TGM_FMT_UINT4) || m != 1 || xdt != TGM_F16) return TGM_E_UNSUPPORTED;
+  if (k % 2048 != 0 || k / 2048 > 4) return TGM_E_UNSUPPORTED;
+  int gs = 0;
+  if (scales) {
+    if (sdt != TGM_F16 && sdt != TGM_BF16 && sdt != TGM_F32) return TGM_E_UNSUPPORTED;
+    if (bs != 32 && bs != 64 && bs != 128) return TGM_E_UNSUPPORTED;
+    gs = bs == 32 ? 0 : bs == 64 ? 1 : 2;
+    if ((uintptr_t)scales % 16 || (n * (k / bs) * dtype_size(sdt)) < 16) return TGM_E_UNSUPPORTED;
+  }
+  if ((uintptr_t)w % 16 || (uintptr_t)x % 16) return TGM_E_UNSUPPORTED;
+  const unsigned grid = (unsigned)((n + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave));
+  const bool sgn = fmt == TGM_FMT_INT4;
+  switch (k / 2048) {
+    case 1: launch_rows_int4_sdt<1>(sdt, grid, s, w, n, scales, gs, sgn, x, y, ydt); break;
+    case 2: launch_rows_int4_sdt<2>(sdt, grid, s, w, n, scales, gs, sgn, x, y, ydt); break;
+    case 3: launch_rows_int4_sdt<3>(sdt, grid, s, w, n, scales, gs, sgn, x, y, ydt); break;
+    default: launch_rows_int4_sdt<4>(sdt, grid, s, w, n, scales, gs, sgn, x, y, ydt); break;
+  }
+  return TGM_OK;
 }
 
 }  // namespace tgm
