@@ -110,10 +110,15 @@ int tgm_gemv(const void* w, int fmt, int64_t n, int64_t k,
  *
  *   C[m, n] = sum_k A[m, k] * deq(W)[n, k]
  *
- * A is BF16 [M, K] with row stride lda; W packed [N, K] with scales
- * [N, ceil(K/block)]; C (c_dtype BF16, F16 or F32) with row stride ldc.  The packed
- * weight is dequantised in registers to bf16 (exact for FP4/FP6/INT4 codes with E8M0
- * or no scales) and fed to bf16 MFMA with fp32 accumulation.
+ * W packed [N, K] with scales [N, ceil(K/block)]; C (c_dtype BF16, F16 or F32) with
+ * row stride ldc; A [M, K] with row stride lda.  K must be a multiple of 128.
+ *   - FP4 / FP6 weights: A is BF16, scales E8M0 per 32 (or none).  The codes are
+ *     dequantised in registers to bf16 (exact) and fed to bf16 MFMA.
+ *   - INT4 / UINT4 weights: A is F16, scales F16, BF16 or F32 per 32, 64 or 128 K-elements
+ *     (or none).  The codes become exact f16 values, f16 MFMA sums each scale group's
+ *     products in fp32 and the group sum is multiplied by its fp32 scale.
+ * Accumulation is fp32; the result is rounded once.  Other combinations return
+ * TGM_E_UNSUPPORTED.
  */
 int tgm_gemm_w(const void* a, int a_dtype, int64_t m, int64_t lda,
                const void* w, int fmt, int64_t n, int64_t k,

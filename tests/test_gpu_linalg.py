@@ -391,6 +391,50 @@ def test_gemm_w_config3_full_size_sampled(dev, fmt):
     assert O.max_rel_err(bf16_np(c)[np.ix_(rows, cols)], ref) <= TOL
 
 
+@pytest.mark.parametrize("fmt", ["int4", "uint4"])
+@pytest.mark.parametrize("sdt,bs", [(torch.float16, 128), (torch.float16, 32), (torch.bfloat16, 64), (torch.float32, 32),
+                                    (None, 32)])
+@pytest.mark.parametrize("mnk", [(128, 256, 128), (200, 300, 512), (513, 257, 384)])
+def test_gemm_w_int4_tiles_and_groups(dev, fmt, sdt, bs, mnk):
+    """INT4/UINT4 weights x fp16 activations on the f16-MFMA GEMM with per-group scales:
+    whole and ragged tiles, groups of 32 / 64 / 128, every scale dtype, unscaled."""
+    m, n, k = mnk
+    rng = np.random.default_rng(m + n + k + bs)
+    w, deq = int4_weight(dev, fmt, n, k, sdt, bs, rng)
+    a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float16)).to(dev)
+    c = matmul_nt(a, w, scope="ThreadGroup", dtype=torch.float32)
+    assert c.shape == (m, n)
+    assert O.max_rel_err(c.cpu().numpy(), a.float().cpu().numpy().astype(np.float64) @ deq.T) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["int4", "uint4"])
+@pytest.mark.parametrize("bs", [32, 128])
+def test_gemm_w_int4_one_hot_is_exact(dev, fmt, bs):
+    """One-hot fp16 activation rows recover code * scale exactly in fp32: nibble order, the
+    MFMA K order and the per-group scale multiply all line up."""
+    m, n, k = 256, 512, 512
+    rng = np.random.default_rng(bs)
+    w, deq = int4_weight(dev, fmt, n, k, torch.float16, bs, rng)
+    cols = rng.choice(k, m, replace=True)
+    a = torch.zeros((m, k), dtype=torch.float16, device=dev)
+    a[torch.arange(m), torch.from_numpy(cols)] = 1.0
+    c = matmul_nt(a, w, scope="ThreadGroup", dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(c, deq[:, cols].T.astype(np.float32))
+
+
+def test_gemm_w_int4_prefill_shape(dev):
+    """Attention-projection prefill shape: 512 tokens x fp16 [512, 4096] times INT4 g128
+    fp16-scale weights [6144, 4096] (q, k and v rows stacked), fp16 out."""
+    m, n, k = 512, 6144, 4096
+    rng = np.random.default_rng(17)
+    w, deq = int4_weight(dev, "int4", n, k, torch.float16, 128, rng)
+    a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float16)).to(dev)
+    c = matmul_nt(a, w, scope="ThreadGroup", dtype=torch.float16)
+    rows, cols = rng.choice(m, 64, replace=False), rng.choice(n, 512, replace=False)
+    ref = a.float().cpu().numpy().astype(np.float64)[rows] @ deq[cols].T
+    assert O.max_rel_err(c.float().cpu().numpy()[np.ix_(rows, cols)], ref) <= TOL
+
+
 @pytest.mark.parametrize("fa,fb", [("fp4_e2m1", "fp4_e2m1"), ("fp6_e2m3", "fp4_e2m1"), ("fp6_e3m2", "fp6_e2m3")])
 def test_gemm_mx_parity(dev, fa, fb):
     m, n, k = 64, 96, 256

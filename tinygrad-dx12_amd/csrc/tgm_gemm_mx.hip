@@ -223,56 +223,13 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __res
   wait_lds_dma();
   __syncthreads();  // the epilogue reuses the operand LDS
 
-  // Epilogue: each 32 x 32 accumulator tile goes through a per-wave LDS block (rows
-  // padded to 36 floats) so that lane l then holds row l / 2, columns 16 * (l % 2) .. +16,
-  // rounded once from fp32 and written as 16-byte row segments.
+  // Epilogue: each 32 x 32 accumulator tile through the wave's LDS block (store_tile32).
   float* ep = (float*)lds + wave * 32 * 36;
-  const int er = lane >> 1, ec = (lane & 1) * 16;
-  auto out_tile = [&](const f32x16 t, int i, int j) __attribute__((always_inline)) {
-#pragma unroll
-    for (int v = 0; v < 16; ++v) ep[(8 * (v >> 2) + 4 * half + (v & 3)) * 36 + (lane & 31)] = t[v];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    float vals[16];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f32x4 f = *(const f32x4*)(ep + er * 36 + ec + 4 * q);
-      vals[4 * q] = f[0]; vals[4 * q + 1] = f[1]; vals[4 * q + 2] = f[2]; vals[4 * q + 3] = f[3];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int row = m0 + wm * FA * 32 + i * 32 + er;
-    const int col = n0 + wn * FB * 32 + j * 32 + ec;
-    if (row < M) {
-      const int64_t o = (int64_t)row * ldc + col;
-      if (col + 15 < N && (o & 7) == 0 && cdt != TGM_F32) {
-        unsigned pk[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          if (cdt == TGM_BF16)
-            pk[q] = f32_to_bf16(vals[2 * q]) | ((unsigned)f32_to_bf16(vals[2 * q + 1]) << 16);
-          else
-            pk[q] = __builtin_bit_cast(unsigned short, (_Float16)vals[2 * q]) |
-                    ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)vals[2 * q + 1]) << 16);
-        }
-        *(u32x4*)((uint16_t*)c + o) = u32x4{pk[0], pk[1], pk[2], pk[3]};
-        *(u32x4*)((uint16_t*)c + o + 8) = u32x4{pk[4], pk[5], pk[6], pk[7]};
-      } else if (col + 15 < N && (o & 3) == 0 && cdt == TGM_F32) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          *(f32x4*)((float*)c + o + 4 * q) = f32x4{vals[4 * q], vals[4 * q + 1], vals[4 * q + 2], vals[4 * q + 3]};
-      } else {
-#pragma unroll
-        for (int q = 0; q < 16; ++q)
-          if (col + q < N) store_c(c, cdt, o + q, vals[q]);
-      }
-    }
-  };
   // literal indices keep the accumulators in registers
-#define TGM_OUT(I, J) \
-  if constexpr (I < FA && J < FB) out_tile(acc[I < FA ? I : 0][J < FB ? J : 0], I, J);
+#define TGM_OUT(I, J)                                                                                 \
+  if constexpr (I < FA && J < FB)                                                                     \
+    store_tile32(acc[I < FA ? I : 0][J < FB ? J : 0], ep, lane, m0 + wm * FA * 32 + I * 32, n0 + wn * FB * 32 + J * 32, \
+                 M, N, c, cdt, ldc);
   TGM_OUT(0, 0) TGM_OUT(0, 1) TGM_OUT(0, 2) TGM_OUT(0, 3) TGM_OUT(1, 0) TGM_OUT(1, 1) TGM_OUT(1, 2) TGM_OUT(1, 3)
   TGM_OUT(2, 0) TGM_OUT(2, 1) TGM_OUT(2, 2) TGM_OUT(2, 3) TGM_OUT(3, 0) TGM_OUT(3, 1) TGM_OUT(3, 2) TGM_OUT(3, 3)
 #undef TGM_OUT

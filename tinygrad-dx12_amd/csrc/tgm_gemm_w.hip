@@ -1,4 +1,5 @@
-// Kernel family 2, dequant path: packed FP4 / FP6 weights x bf16 activations on bf16 MFMA.
+// Kernel family 2, dequant path: packed FP4 / FP6 weights x bf16 activations on bf16 MFMA,
+// and INT4 / UINT4 weights with per-group scales x f16 activations on f16 MFMA (gemm_w_i4).
 //
 // Replaces the reference's collective LinAlg GEMM (alexandreteles/tinygrad-dx12
 // src/tinygrad_dx12/renderer/linalg.py:38-124) when one operand is packed: the reference
@@ -31,6 +32,8 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
 typedef __attribute__((__vector_size__(32 * sizeof(__bf16)))) __bf16 bf16x32;
 typedef __attribute__((__vector_size__(6 * sizeof(int)))) int i32x6;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 constexpr int kWM = 128, kWN = 256, kWK = 128;  // output tile and K step
 constexpr int kAPanel = kWM * kWK * 2;           // 32 KB of bf16 A per stage
@@ -210,56 +213,227 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
   wait_lds_dma();
   __syncthreads();  // the epilogue reuses the LDS
 
-  // Epilogue: each 32 x 32 tile through a per-wave LDS block (rows padded to 36 floats), then
-  // 16-element row segments per lane, rounded once.
+  // Epilogue: each 32 x 32 tile through the wave's LDS block (store_tile32).
   float* ep = (float*)lds + wave * 32 * 36;
-  const int er = lane >> 1, ec = (lane & 1) * 16;
-  auto out_tile = [&](const f32x16 t, int i, int j) __attribute__((always_inline)) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) ep[(8 * (v >> 2) + 4 * half + (v & 3)) * 36 + (lane & 31)] = t[v];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    float vals[16];
+  for (int i = 0; i < FA; ++i)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f32x4 f = *(const f32x4*)(ep + er * 36 + ec + 4 * q);
-      vals[4 * q] = f[0]; vals[4 * q + 1] = f[1]; vals[4 * q + 2] = f[2]; vals[4 * q + 3] = f[3];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int row = m0 + wm * 64 + i * 32 + er;
-    const int col = n0 + wn * 64 + j * 32 + ec;
-    if (row < M) {
-      const int64_t o = (int64_t)row * ldc + col;
-      if (col + 15 < N && (o & 7) == 0 && cdt != TGM_F32) {
-        unsigned pk[8];
+    for (int j = 0; j < FB; ++j)
+      store_tile32(acc[i][j], ep, lane, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, M, N, c, cdt, ldc);
+}
+
+// ---- INT4 / UINT4 weights x f16 activations, per-group scales (f16, bf16 or f32).
+//
+// The reference decodes int4 as (p ^ 8) - 8 and uint4 as p (dx12.py:93-94), multiplies each
+// value by its group's scale in fp32 (dx12.py:101-106) and multiplies the fp32 intermediate.
+// Here the codes become exact f16 values in registers (nibble n -- n ^ 8 for int4 -- goes
+// under the f16 byte 0x64, i.e. 1024 + n, and a packed f16 subtraction removes 1024 or 1032),
+// f16 MFMA sums code * activation products of one scale group in fp32, and the group's sum
+// is multiplied by the fp32 scale of its weight row and added to the accumulator.  The
+// products are the reference's; the summation order differs.
+//
+// Same tile, waves, A panel and W panel (64-byte rows per 128-element step, the FP4 layout)
+// as gemm_w_mx, but MFMA j of a step takes K [16 j + 8 h, + 8) for lane half h (the natural
+// order), so that one MFMA never spans two scale groups of 32 or 64.  A lane's codes for
+// MFMA j are dword 2 j + h of its weight row: two ds_read2_b32 per 16-byte chunk.  Scales
+// are read per step straight from global memory (2 rows x 128 / G values per lane), issued
+// one step ahead.
+template <bool SIGNED>
+__device__ __forceinline__ f16x8 decode_i4x8(unsigned v) {
+  if (SIGNED) v ^= 0x88888888u;
+  const unsigned lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+  const unsigned x01 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // n0 n1 n2 n3 (one per byte)
+  const unsigned x23 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // n4 n5 n6 n7
+  const half2v bias = SIGNED ? half2v{(_Float16)1032.0f, (_Float16)1032.0f} : half2v{(_Float16)1024.0f, (_Float16)1024.0f};
+  const half2v p0 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x01, 0x04010400u)) - bias;
+  const half2v p1 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x01, 0x04030402u)) - bias;
+  const half2v p2 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x23, 0x04010400u)) - bias;
+  const half2v p3 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x23, 0x04030402u)) - bias;
+  return f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+template <int SDT>
+__device__ __forceinline__ float scale_value(const void* p, int64_t i) {
+  if constexpr (SDT == TGM_F16) return (float)((const _Float16*)p)[i];
+  else if constexpr (SDT == TGM_BF16) return __builtin_bit_cast(float, (unsigned)((const uint16_t*)p)[i] << 16);
+  else return ((const float*)p)[i];
+}
+
+// G: scale group (32, 64 or 128 K-elements; 0 = unscaled), SDT: scale dtype.
+template <int G, int SDT, bool SIGNED>
+__global__ void __launch_bounds__(512) gemm_w_i4(const uint8_t* __restrict__ a, unsigned lda_bytes,
+                                                 const uint8_t* __restrict__ w, const void* __restrict__ sw,
+                                                 int M, int N, int K, void* __restrict__ c, int cdt, int64_t ldc) {
+  constexpr int FA = 2, FB = 2, kRow = 64, kPanelLoads = kWN * kRow / 1024, NWL = kPanelLoads / 8;
+  constexpr int GS = G ? kWK / G : 1;  // scale groups per step
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * (kAPanel + kWN * kRow)];
+  constexpr int kStage = kAPanel + kWN * kRow;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
+  const int tiles_m = (M + kWM - 1) / kWM, tiles_n = (N + kWN - 1) / kWN;
+  int tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, kWGroupM, tm, tn);
+  const int m0 = tm * kWM, n0 = tn * kWN;
+  const int nsteps = K / kWK;
+  const unsigned kbw = (unsigned)K / 2u;
+  const i32x4v ra = buffer_rsrc(a, (unsigned)(M - 1) * lda_bytes + (unsigned)K * 2u);
+  const i32x4v rw = buffer_rsrc(w, (unsigned)N * kbw);
+  const unsigned lds_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds;
+  // A: as gemm_w_mx (row 4 i + l / 16, logical 16-byte column (l % 16) ^ (row % 16)).
+  unsigned voa[4];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          if (cdt == TGM_BF16)
-            pk[q] = f32_to_bf16(vals[2 * q]) | ((unsigned)f32_to_bf16(vals[2 * q + 1]) << 16);
-          else
-            pk[q] = __builtin_bit_cast(unsigned short, (_Float16)vals[2 * q]) |
-                    ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)vals[2 * q + 1]) << 16);
-        }
-        *(u32x4*)((uint16_t*)c + o) = u32x4{pk[0], pk[1], pk[2], pk[3]};
-        *(u32x4*)((uint16_t*)c + o + 8) = u32x4{pk[4], pk[5], pk[6], pk[7]};
-      } else if (col + 15 < N && (o & 3) == 0 && cdt == TGM_F32) {
+  for (int q = 0; q < 4; ++q) {
+    const int row = 4 * (4 * wave + q) + (lane >> 4);
+    voa[q] = (unsigned)(m0 + row) * lda_bytes + (unsigned)((lane & 15) ^ (row & 15)) * 16u;
+  }
+  // W: 64-byte rows, 16-byte chunk (l % 4) ^ ((row / 4) % 4).
+  unsigned vow[NWL];
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          *(f32x4*)((float*)c + o + 4 * q) = f32x4{vals[4 * q], vals[4 * q + 1], vals[4 * q + 2], vals[4 * q + 3]};
-      } else {
+  for (int q = 0; q < NWL; ++q) {
+    const int row = 16 * (NWL * wave + q) + (lane >> 2);
+    vow[q] = (unsigned)(n0 + row) * kbw + (unsigned)((lane & 3) ^ ((row >> 2) & 3)) * 16u;
+  }
+  auto dma_step = [&](int s, int buf) __attribute__((always_inline)) {
+    const unsigned st = lds_base + (unsigned)(buf * kStage);
 #pragma unroll
-        for (int q = 0; q < 16; ++q)
-          if (col + q < N) store_c(c, cdt, o + q, vals[q]);
-      }
+    for (int q = 0; q < 4; ++q) lds_dma16(ra, st + (unsigned)(4 * wave + q) * 1024u, voa[q] + (unsigned)s * 256u);
+#pragma unroll
+    for (int q = 0; q < NWL; ++q)
+      lds_dma16(rw, st + kAPanel + (unsigned)(NWL * wave + q) * 1024u, vow[q] + (unsigned)s * (unsigned)kRow);
+  };
+  const int half = lane >> 5;
+  const int a_row = wm * 64 + (lane & 31);
+  const int b_row = wn * 64 + (lane & 31);
+  // Scales of this lane's two weight rows (clamped below N; those columns are not stored).
+  const int64_t ngroups = G ? K / G : 0;
+  int64_t srow[FB];
+#pragma unroll
+  for (int t = 0; t < FB; ++t) {
+    const int n = n0 + b_row + 32 * t;
+    srow[t] = (int64_t)(n < N ? n : N - 1) * ngroups;
+  }
+  float sc[FB][GS], sn[FB][GS];
+  auto load_scales = [&](int s, float (&dst)[FB][GS]) __attribute__((always_inline)) {
+    if constexpr (G != 0) {
+#pragma unroll
+      for (int t = 0; t < FB; ++t)
+#pragma unroll
+        for (int g = 0; g < GS; ++g) dst[t][g] = scale_value<SDT>(sw, srow[t] + (int64_t)s * GS + g);
     }
   };
-  out_tile(acc[0][0], 0, 0);
-  out_tile(acc[0][1], 0, 1);
-  out_tile(acc[1][0], 1, 0);
-  out_tile(acc[1][1], 1, 1);
+  f32x16 acc[FA][FB];
+#pragma unroll
+  for (int i = 0; i < FA; ++i)
+#pragma unroll
+    for (int j = 0; j < FB; ++j) acc[i][j] = f32x16{};
+
+  const int s1 = nsteps > 1 ? 1 : 0;
+  load_scales(0, sc);
+  dma_step(0, 0);
+  dma_step(s1, 1);
+  wait_lds_dma();
+  __syncthreads();
+  for (int s = 0; s < nsteps; ++s) {
+    const int cur = s & 1;
+    const int s2 = s + 2 < nsteps ? s + 2 : nsteps - 1;
+    load_scales(s + 1 < nsteps ? s + 1 : s, sn);
+    const unsigned char* pa = lds + cur * kStage;
+    const unsigned char* pw = pa + kAPanel;
+    // codes: dwords 2 j + h of both weight rows (chunk j / 2, dword 2 (j % 2) + h)
+    unsigned cw[FB][8];
+#pragma unroll
+    for (int t = 0; t < FB; ++t) {
+      const int row = b_row + 32 * t;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const unsigned* p = (const unsigned*)(pw + row * kRow + ((q ^ ((row >> 2) & 3)) * 16) + 4 * half);
+        cw[t][2 * q] = p[0];
+        cw[t][2 * q + 1] = p[2];
+      }
+    }
+    f32x16 part[FA][FB];
+    f16x8 af[2][FA];
+    auto read_a = [&](int j, f16x8 (&dst)[FA]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int t = 0; t < FA; ++t) {
+        const int row = a_row + 32 * t;
+        dst[t] = *(const f16x8*)(pa + row * 256 + (((2 * j + half) ^ (row & 15)) * 16));
+      }
+    };
+    read_a(0, af[0]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      // one MFMA group at a time: A of MFMA j + 1 is read while MFMA j runs
+      __builtin_amdgcn_sched_barrier(0);
+      if (j < 7) read_a(j + 1, af[(j + 1) & 1]);
+      f16x8 bf[FB];
+#pragma unroll
+      for (int t = 0; t < FB; ++t) bf[t] = decode_i4x8<SIGNED>(cw[t][j]);
+      constexpr int JPG = G ? G / 16 : 8;  // MFMAs per scale group
+#pragma unroll
+      for (int ta = 0; ta < FA; ++ta)
+#pragma unroll
+        for (int tb = 0; tb < FB; ++tb) {
+          if constexpr (G == 0) {
+            acc[ta][tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j & 1][ta], bf[tb], acc[ta][tb], 0, 0, 0);
+          } else {
+            part[ta][tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j & 1][ta], bf[tb], j % JPG ? part[ta][tb] : f32x16{},
+                                                                   0, 0, 0);
+            if (j % JPG == JPG - 1) {
+              const float sv = sc[tb][j / JPG];
+#pragma unroll
+              for (int v = 0; v < 16; ++v) acc[ta][tb][v] += part[ta][tb][v] * sv;
+            }
+          }
+        }
+    }
+    wait_lds_dma();  // this wave's loads of step s + 1 (and its scale loads)
+    if constexpr (G != 0) {
+      // the scale loads are complete; make the compiler's wait for them happen here, before
+      // the next step's loads are issued
+#pragma unroll
+      for (int t = 0; t < FB; ++t)
+#pragma unroll
+        for (int g = 0; g < GS; ++g) asm volatile("" : "+v"(sn[t][g]));
+    }
+    __syncthreads();
+    dma_step(s2, cur);
+#pragma unroll
+    for (int t = 0; t < FB; ++t)
+#pragma unroll
+      for (int g = 0; g < GS; ++g) sc[t][g] = sn[t][g];
+  }
+  wait_lds_dma();
+  __syncthreads();
+  float* ep = (float*)lds + wave * 32 * 36;
+#pragma unroll
+  for (int i = 0; i < FA; ++i)
+#pragma unroll
+    for (int j = 0; j < FB; ++j)
+      store_tile32(acc[i][j], ep, lane, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, M, N, c, cdt, ldc);
+}
+
+template <int G, int SDT, bool SIGNED>
+int launch_gemm_w_i4(const void* a, int64_t lda, const void* w, const void* scales, int64_t m, int64_t n, int64_t k,
+                     void* c, int cdt, int64_t ldc, hipStream_t stream) {
+  const int64_t tiles = ((m + kWM - 1) / kWM) * ((n + kWN - 1) / kWN);
+  hipLaunchKernelGGL((gemm_w_i4<G, SDT, SIGNED>), dim3((unsigned)tiles), dim3(512), 0, stream, (const uint8_t*)a,
+                     (unsigned)(lda * 2), (const uint8_t*)w, scales, (int)m, (int)n, (int)k, c, cdt, ldc);
+  return launch_status("tgm_gemm_w");
+}
+
+template <bool SIGNED>
+int dispatch_gemm_w_i4(const void* a, int64_t lda, const void* w, const void* scales, int sdt, int64_t bs, int64_t m,
+                       int64_t n, int64_t k, void* c, int cdt, int64_t ldc, hipStream_t st) {
+  if (!scales) return launch_gemm_w_i4<0, TGM_F32, SIGNED>(a, lda, w, scales, m, n, k, c, cdt, ldc, st);
+#define TGM_I4_CASE(G, SDT) \
+  if (bs == G && sdt == SDT) return launch_gemm_w_i4<G, SDT, SIGNED>(a, lda, w, scales, m, n, k, c, cdt, ldc, st);
+  TGM_I4_CASE(32, TGM_F16) TGM_I4_CASE(64, TGM_F16) TGM_I4_CASE(128, TGM_F16)
+  TGM_I4_CASE(32, TGM_BF16) TGM_I4_CASE(64, TGM_BF16) TGM_I4_CASE(128, TGM_BF16)
+  TGM_I4_CASE(32, TGM_F32) TGM_I4_CASE(64, TGM_F32) TGM_I4_CASE(128, TGM_F32)
+#undef TGM_I4_CASE
+  TGM_UNSUPPORTED("tgm_gemm_w: int4 scales must be f16, bf16 or f32 per 32, 64 or 128 K-elements");
 }
 
 template <int FMT, bool SCALED>
@@ -287,21 +461,25 @@ extern "C" int tgm_gemm_w(const void* a, int a_dtype, int64_t m, int64_t lda, co
   TGM_CHECK_ARG(c_dtype == TGM_BF16 || c_dtype == TGM_F16 || c_dtype == TGM_F32, "output must be bf16, f16 or f32");
   TGM_CHECK_ARG(m <= 1 || ldc >= n, "ldc smaller than N");
   if (m == 0 || n == 0) return TGM_OK;
-  if (a_dtype != TGM_BF16) TGM_UNSUPPORTED("tgm_gemm_w: activations must be bf16");
-  if (fmt != TGM_FMT_FP4_E2M1 && fmt != TGM_FMT_FP6_E2M3 && fmt != TGM_FMT_FP6_E3M2)
-    TGM_UNSUPPORTED("tgm_gemm_w: only FP4 / FP6 weights have a bf16-MFMA kernel");
+  const bool int4 = fmt == TGM_FMT_INT4 || fmt == TGM_FMT_UINT4;
+  if (int4 && a_dtype != TGM_F16) TGM_UNSUPPORTED("tgm_gemm_w: int4 / uint4 weights take f16 activations");
+  if (!int4 && a_dtype != TGM_BF16) TGM_UNSUPPORTED("tgm_gemm_w: FP4 / FP6 weights take bf16 activations");
   const bool scaled = scales != nullptr;
-  if (scaled && (scale_dtype != TGM_E8M0 || block_size != 32))
-    TGM_UNSUPPORTED("tgm_gemm_w: scales must be E8M0 per 32 K-elements");
+  if (!int4 && scaled && (scale_dtype != TGM_E8M0 || block_size != 32))
+    TGM_UNSUPPORTED("tgm_gemm_w: FP4 / FP6 scales must be E8M0 per 32 K-elements");
   if (k == 0 || k % kWK != 0) TGM_UNSUPPORTED("tgm_gemm_w: K must be a positive multiple of %d", kWK);
   if (m > 1 && (lda * 2) % 16 != 0) TGM_UNSUPPORTED("tgm_gemm_w: activation rows must be 16-byte aligned");
-  const int64_t kbw = k / 8 * (fmt == TGM_FMT_FP4_E2M1 ? 4 : 6);
+  const int64_t kbw = k / 8 * (fmt == TGM_FMT_FP6_E2M3 || fmt == TGM_FMT_FP6_E3M2 ? 6 : 4);
   if (m >= (1ll << 31) || n >= (1ll << 31) || (m - 1) * lda * 2 + k * 2 >= (1ll << 32) || n * kbw >= (1ll << 32))
     TGM_UNSUPPORTED("tgm_gemm_w: operands must be under 4 GiB (32-bit offsets)");
   if ((uintptr_t)a % 16 || (uintptr_t)w % 16 || (scaled && (uintptr_t)scales % 4))
     TGM_UNSUPPORTED("tgm_gemm_w: operands must be 16-byte and scales 4-byte aligned");
   const hipStream_t st = (hipStream_t)stream;
   const int64_t lda_eff = m > 1 ? lda : k;
+  if (int4)
+    return fmt == TGM_FMT_INT4
+               ? dispatch_gemm_w_i4<true>(a, lda_eff, w, scales, scale_dtype, block_size, m, n, k, c, c_dtype, ldc, st)
+               : dispatch_gemm_w_i4<false>(a, lda_eff, w, scales, scale_dtype, block_size, m, n, k, c, c_dtype, ldc, st);
   switch (fmt * 2 + (scaled ? 1 : 0)) {
     case TGM_FMT_FP4_E2M1 * 2 + 1: return launch_gemm_w<TGM_FMT_FP4_E2M1, true>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st);
     case TGM_FMT_FP4_E2M1 * 2: return launch_gemm_w<TGM_FMT_FP4_E2M1, false>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st);

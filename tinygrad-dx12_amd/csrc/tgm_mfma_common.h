@@ -56,4 +56,52 @@ __device__ __forceinline__ void store_c(void* c, int cdt, int64_t i, float v) {
   else ((float*)c)[i] = v;
 }
 
+// Store one 32 x 32 fp32 accumulator tile in the 32x32 MFMA D layout (lane l holds column
+// l % 32, rows 8 (v / 4) + 4 (l / 32) + v % 4) to C rows r0 .. r0 + 31, columns c0 .. c0 + 31.
+// The tile goes through the wave's own LDS block ``ep`` (32 rows padded to 36 floats) so
+// that lane l then holds row l / 2, columns 16 (l % 2) .. + 16, rounded once from fp32 and
+// written as 16-byte row segments; rows past M and columns past N are not written.
+__device__ __forceinline__ void store_tile32(const f32x16& t, float* ep, int lane, int r0, int c0, int M, int N,
+                                             void* c, int cdt, int64_t ldc) {
+  const int half = lane >> 5, er = lane >> 1, ec = (lane & 1) * 16;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) ep[(8 * (v >> 2) + 4 * half + (v & 3)) * 36 + (lane & 31)] = t[v];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float vals[16];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const f32x4 f = *(const f32x4*)(ep + er * 36 + ec + 4 * q);
+    vals[4 * q] = f[0]; vals[4 * q + 1] = f[1]; vals[4 * q + 2] = f[2]; vals[4 * q + 3] = f[3];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int row = r0 + er, col = c0 + ec;
+  if (row >= M) return;
+  const int64_t o = (int64_t)row * ldc + col;
+  if (col + 15 < N && (o & 7) == 0 && cdt != TGM_F32) {
+    unsigned pk[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      if (cdt == TGM_BF16)
+        pk[q] = f32_to_bf16(vals[2 * q]) | ((unsigned)f32_to_bf16(vals[2 * q + 1]) << 16);
+      else
+        pk[q] = __builtin_bit_cast(unsigned short, (_Float16)vals[2 * q]) |
+                ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)vals[2 * q + 1]) << 16);
+    }
+    *(u32x4*)((uint16_t*)c + o) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+    *(u32x4*)((uint16_t*)c + o + 8) = u32x4{pk[4], pk[5], pk[6], pk[7]};
+  } else if (col + 15 < N && (o & 3) == 0 && cdt == TGM_F32) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *(f32x4*)((float*)c + o + 4 * q) = f32x4{vals[4 * q], vals[4 * q + 1], vals[4 * q + 2], vals[4 * q + 3]};
+  } else {
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+      if (col + q < N) store_c(c, cdt, o + q, vals[q]);
+  }
+}
+
 }  // namespace tgm
