@@ -1,0 +1,85 @@
+/*
+ * Decoder-step kernels around the packed matmul path (libtgm_mi355x.so).
+ *
+ * The reference has no model code: a decoder built on it would be ordinary tinygrad ops
+ * plus PackedTensor.matmul (alexandreteles/tinygrad-dx12 src/tinygrad_dx12/codegen/decomp/
+ * dx12.py:108-112, with block_size=128 allowed by dx12.py:30 and :44-47).  These entry
+ * points are the non-matmul operations of a Llama-style decoder layer, written for gfx950
+ * so that a whole decode step runs on the device:
+ *
+ *   embed -> [add + RMSNorm -> QKV (INT4 GEMV/GEMM) -> RoPE + KV store -> attention
+ *             -> O (INT4) -> add + RMSNorm -> gate|up (FP4) -> SwiGLU -> down (FP4)] x L
+ *         -> add + RMSNorm -> output head (bf16 GEMV) -> greedy argmax
+ *
+ * Sequence positions live in device memory (``pos``, int32 per sequence) and the argmax
+ * advances them, so the launches of one decode step do not change from step to step and can
+ * be captured once and replayed as a HIP graph.  None of these entry points allocates memory
+ * or issues a memset.
+ *
+ * Layouts (row-major, element strides):
+ *   rows         = batch * seq_rows tokens; row r is token r % seq_rows of sequence r / seq_rows
+ *   h            = float32 [rows, d] residual stream
+ *   qkv          = float32 [rows, (heads + 2 * kv_heads) * head_dim]: q heads, k heads, v heads
+ *   k/v caches   = bfloat16 [batch, kv_heads, max_seq, head_dim]
+ * Token r of sequence b has position pos[b] + r % seq_rows.
+ *
+ * Every function returns TGM_OK or a negative tgm_status (message in tgm_last_error()).
+ */
+#ifndef TGM_DECODER_H
+#define TGM_DECODER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* h[r, :] = float(table[tokens[r], :]); table is BF16 [vocab, d].  Tokens outside
+ * [0, vocab) read row 0 (the host validates prompts; generated tokens are in range). */
+int tgm_dec_embed(const void* table, int64_t vocab, int64_t d, const int32_t* tokens, int64_t rows, float* h,
+                  void* stream);
+
+/* h[r] += delta[r] (delta may be NULL); out[r, i] = h[r, i] / sqrt(mean_i(h[r, i]^2) + eps) * weight[i],
+ * computed in fp32 and rounded once to out_dtype (F16, BF16 or F32).  weight is BF16 [d]. */
+int tgm_dec_add_rmsnorm(float* h, const float* delta, int64_t rows, int64_t d, const void* weight, float eps,
+                        void* out, int out_dtype, void* stream);
+
+/* Rotary position embedding (pairs (i, i + head_dim / 2), angle p * base^(-2 i / head_dim),
+ * evaluated in double) applied in place to the q and k heads of qkv; the rotated k heads and
+ * the v heads are stored as bf16 into the caches at each token's position. */
+int tgm_dec_rope_kv(float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                    const int32_t* pos, double rope_base, void* k_cache, void* v_cache, int64_t max_seq, void* stream);
+
+/* Causal grouped-query attention of every q head over its kv head's cache, positions
+ * 0 .. pos(token) (softmax of q.k / sqrt(head_dim) in fp32).  head_dim is 64 or 128; heads /
+ * kv_heads is 1, 2, 4 or 8.  ``splits`` > 1 divides each token's positions over that many
+ * workgroups (split-K over the sequence, merged by a second kernel) and needs
+ * ``workspace`` of at least rows * heads * splits * (head_dim + 2) floats;
+ * tgm_dec_attention_workspace gives the byte count.  out is [rows, heads * head_dim]. */
+int64_t tgm_dec_attention_workspace(int64_t rows, int64_t heads, int64_t head_dim, int64_t splits);
+int tgm_dec_attention(const float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, int64_t kv_heads,
+                      int64_t head_dim, const int32_t* pos, const void* k_cache, const void* v_cache,
+                      int64_t max_seq, int64_t splits, float* workspace, int64_t workspace_bytes, void* out,
+                      int out_dtype, void* stream);
+
+/* SwiGLU: out[r, i] = silu(g) * u with g = gate_up[r, i], u = gate_up[r, ffn + i] (float32
+ * [rows, 2 * ffn]); out is [rows, ffn] of out_dtype. */
+int tgm_dec_silu_mul(const float* gate_up, int64_t rows, int64_t ffn, void* out, int out_dtype, void* stream);
+
+/* Dense bf16 GEMV for the output head: y[m, n] = sum_k x[m, k] * w[n, k] in fp32.  w is BF16
+ * [n, k], x BF16 (row stride ldx), y F32 (row stride ldy); m <= 8, k a multiple of 8 and
+ * m * k <= 32768. */
+int tgm_dec_gemv_bf16(const void* w, int64_t n, int64_t k, const void* x, int64_t m, int64_t ldx, float* y,
+                      int64_t ldy, void* stream);
+
+/* Greedy decode: tokens[r] = argmax_n logits[r, n] (row stride ld; the first maximum wins).
+ * When pos is given, also history[r * hist_stride + pos[r] + 1 - hist_base] = tokens[r]
+ * (when that index lies in [0, hist_stride) and history is given) and pos[r] += 1. */
+int tgm_dec_argmax(const float* logits, int64_t rows, int64_t n, int64_t ld, int32_t* tokens, int32_t* pos,
+                   int32_t* history, int64_t hist_stride, int64_t hist_base, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TGM_DECODER_H */

@@ -1,0 +1,223 @@
+"""Decoder-step kernels and the Llama-style decoder on gfx950 against the decoder oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+import decoder_oracle as D
+import packed_oracle as O
+from tinygrad_mi355x.codegen.decomp.mi355x import PackedTensor
+from tinygrad_mi355x.decoder import Decoder, DecoderConfig, DecoderWeights, random_weights
+from tinygrad_mi355x.runtime import kernels as K
+
+pytestmark = pytest.mark.gpu
+F16, BF16, F32 = 11, 12, 13
+SMALL = DecoderConfig(hidden=256, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000, layers=2)
+
+
+def np64(t: torch.Tensor) -> np.ndarray:
+    return t.float().cpu().numpy().astype(np.float64)
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def deq(p: PackedTensor) -> np.ndarray:
+    if p.scales.dtype == torch.float8_e8m0fnu:
+        s = O.e8m0_decode(p.scales.view(torch.uint8).cpu().numpy())
+    else:
+        s = p.scales.float().cpu().numpy()
+    return O.dequant_f64(p.data.cpu().numpy(), p.format, p.shape, s, p.block_size)
+
+
+def oracle_weights(w: DecoderWeights) -> D.OracleWeights:
+    layers = [D.OracleLayer(np64(L.attn_norm), deq(L.wqkv), deq(L.wo), np64(L.ffn_norm), deq(L.w_gate_up),
+                            deq(L.w_down)) for L in w.layers]
+    return D.OracleWeights(np64(w.embed), layers, np64(w.final_norm), np64(w.lm_head))
+
+
+def oracle_for(w: DecoderWeights, cfg: DecoderConfig, batch: int, max_seq: int) -> D.OracleDecoder:
+    return D.OracleDecoder(oracle_weights(w), cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.ffn, cfg.eps, cfg.rope_base,
+                           batch, max_seq)
+
+
+# ----------------------------------------------------------------------------- single kernels
+def test_add_rmsnorm(dev):
+    rng = np.random.default_rng(0)
+    rows, d = 5, 4096
+    h = torch.from_numpy(rng.standard_normal((rows, d)).astype(np.float32)).to(dev)
+    delta = torch.from_numpy(rng.standard_normal((rows, d)).astype(np.float32)).to(dev)
+    w = torch.from_numpy(1 + 0.1 * rng.standard_normal(d)).to(dev).to(torch.bfloat16)
+    ref_h = np64(h) + np64(delta)
+    for dt, cast in ((F32, lambda x: x), (F16, D.f16), (BF16, D.bf16)):
+        hh = h.clone()
+        out = torch.empty((rows, d), dtype={F32: torch.float32, F16: torch.float16, BF16: torch.bfloat16}[dt], device=dev)
+        K.call("tgm_dec_add_rmsnorm", hh.data_ptr(), delta.data_ptr(), rows, d, w.data_ptr(), 1e-5, out.data_ptr(), dt,
+               stream())
+        assert np.allclose(np64(hh), ref_h, rtol=0, atol=1e-6)
+        ref = D.rmsnorm(ref_h, np64(w), 1e-5)
+        assert O.max_rel_err(np64(out), cast(ref)) <= (1e-5 if dt == F32 else 1e-2)
+
+
+def test_rope_kv_rotates_and_stores_at_each_position(dev):
+    rng = np.random.default_rng(1)
+    B, T, H, HK, hd, max_seq = 2, 3, 4, 2, 64, 40
+    width = (H + 2 * HK) * hd
+    qkv = torch.from_numpy(rng.standard_normal((B * T, width)).astype(np.float32)).to(dev)
+    pos = torch.tensor([5, 17], dtype=torch.int32, device=dev)
+    kc = torch.zeros((B, HK, max_seq, hd), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    src = np64(qkv).reshape(B, T, H + 2 * HK, hd)
+    K.call("tgm_dec_rope_kv", qkv.data_ptr(), B * T, T, H, HK, hd, pos.data_ptr(), 10000.0, kc.data_ptr(),
+           vc.data_ptr(), max_seq, stream())
+    got = np64(qkv).reshape(B, T, H + 2 * HK, hd)
+    kcn, vcn = np64(kc), np64(vc)
+    for b, p0 in enumerate((5, 17)):
+        positions = np.arange(p0, p0 + T)
+        rq = D.rope(src[b, :, :H + HK].transpose(1, 0, 2), positions, 10000.0).transpose(1, 0, 2)
+        assert np.allclose(got[b, :, :H + HK], rq, rtol=0, atol=2e-6)
+        assert np.array_equal(got[b, :, H + HK:], src[b, :, H + HK:])  # v untouched
+        want_k = D.bf16(got[b, :, H:H + HK]).transpose(1, 0, 2)
+        assert np.array_equal(kcn[b, :, p0:p0 + T], want_k)
+        assert np.array_equal(vcn[b, :, p0:p0 + T], D.bf16(src[b, :, H + HK:]).transpose(1, 0, 2))
+        others = np.ones(max_seq, bool)
+        others[p0:p0 + T] = False
+        assert not kcn[b][:, others].any() and not vcn[b][:, others].any()
+
+
+@pytest.mark.parametrize("hd,H,HK", [(128, 32, 8), (64, 4, 2), (128, 8, 8), (64, 16, 2)])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_attention_matches_oracle(dev, hd, H, HK, splits):
+    """Causal GQA over the cache: query t of sequence b at position pos[b] + t sees 0 .. pos."""
+    rng = np.random.default_rng(hd + H + splits)
+    B, T, max_seq = 2, 3, 300
+    width = (H + 2 * HK) * hd
+    qkv = torch.from_numpy(rng.standard_normal((B * T, width)).astype(np.float32)).to(dev)
+    kc = torch.from_numpy(rng.standard_normal((B, HK, max_seq, hd)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    vc = torch.from_numpy(rng.standard_normal((B, HK, max_seq, hd)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    p0 = [130, 297]  # sequence 1 reaches max_seq - 1 at its last token
+    pos = torch.tensor(p0, dtype=torch.int32, device=dev)
+    out = torch.empty((B * T, H * hd), dtype=torch.float32, device=dev)
+    ws_bytes = K.load_library().tgm_dec_attention_workspace(B * T, H, hd, splits)
+    ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=dev)
+    K.call("tgm_dec_attention", qkv.data_ptr(), B * T, T, H, HK, hd, pos.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+           max_seq, splits, ws.data_ptr() if splits > 1 else None, ws_bytes, out.data_ptr(), F32, stream())
+    q = np64(qkv).reshape(B, T, H + 2 * HK, hd)[:, :, :H]
+    got = np64(out).reshape(B, T, H, hd)
+    for b in range(B):
+        positions = np.arange(p0[b], p0[b] + T)
+        ref = D.attention(q[b].transpose(1, 0, 2), np64(kc[b]), np64(vc[b]), positions).transpose(1, 0, 2)
+        err = O.max_rel_err(got[b], ref)  # fp32 scores, exp and sums over up to 300 positions
+        assert err <= 1e-3, err
+
+
+def test_silu_mul(dev):
+    rng = np.random.default_rng(2)
+    rows, F = 3, 14336
+    gu = torch.from_numpy((rng.standard_normal((rows, 2 * F)) * 4).astype(np.float32)).to(dev)
+    out = torch.empty((rows, F), dtype=torch.bfloat16, device=dev)
+    K.call("tgm_dec_silu_mul", gu.data_ptr(), rows, F, out.data_ptr(), BF16, stream())
+    g = np64(gu)
+    ref = D.silu(g[:, :F]) * g[:, F:]
+    assert O.max_rel_err(np64(out), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("m", [1, 2, 5, 8])
+def test_gemv_bf16(dev, m):
+    rng = np.random.default_rng(m)
+    n, k = 32000, 4096
+    w = torch.from_numpy((rng.standard_normal((n, k)) * 0.02).astype(np.float32)).to(dev).to(torch.bfloat16)
+    big = torch.from_numpy(rng.standard_normal((m, k + 512)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    x = big[:, 256:256 + k]  # strided rows
+    y = torch.full((m, n + 8), float("nan"), dtype=torch.float32, device=dev)
+    K.call("tgm_dec_gemv_bf16", w.data_ptr(), n, k, x.data_ptr(), m, x.stride(0), y.data_ptr(), n + 8, stream())
+    ref = np64(x) @ np64(w).T
+    assert O.max_rel_err(np64(y)[:, :n], ref) <= 1e-3
+    assert torch.isnan(y[:, n:]).all()
+
+
+def test_argmax_first_maximum_and_step_bookkeeping(dev):
+    n = 5000
+    logits = torch.randn((3, n), device=dev)
+    logits[0, 17] = logits[0, 4000] = 50.0            # tie: the first wins
+    logits[1] = float("-inf")
+    logits[1, n - 1] = -1e30                           # only finite value, last index
+    logits[2, :10] = float("nan")
+    logits[2, 2222] = 60.0                             # NaN never wins
+    tokens = torch.zeros(3, dtype=torch.int32, device=dev)
+    pos = torch.tensor([10, 11, 12], dtype=torch.int32, device=dev)
+    hist = torch.full((3, 4), -1, dtype=torch.int32, device=dev)
+    K.call("tgm_dec_argmax", logits.data_ptr(), 3, n, n, tokens.data_ptr(), pos.data_ptr(), hist.data_ptr(), 4, 9,
+           stream())
+    assert tokens.tolist() == [17, n - 1, 2222]
+    assert pos.tolist() == [11, 12, 13]
+    # history index pos + 1 - base: 2, 3 and 4 (out of range: not written)
+    assert hist.tolist() == [[-1, -1, 17, -1], [-1, -1, -1, n - 1], [-1, -1, -1, -1]]
+
+
+# ----------------------------------------------------------------------------- whole decoder
+def _compare_logits(dec: Decoder, ref_logits: np.ndarray, tol: float = 1e-2) -> None:
+    err = O.max_rel_err(np64(dec.logits), ref_logits)
+    assert err <= tol, err
+
+
+@pytest.mark.parametrize("batch,prompt", [(2, 12), (1, 8)])
+def test_decoder_matches_oracle(dev, batch, prompt):
+    """Reduced config: prefill (GEMM path for 24 rows, GEMV path for 8) and six cached decode
+    steps; logits within 1e-2 of the oracle fed the same tokens, and the device's greedy
+    token is the oracle's wherever the oracle's top-2 margin exceeds the tolerance."""
+    cfg, max_seq, steps = SMALL, 160, 6
+    w = random_weights(cfg, dev, seed=batch)
+    rng = np.random.default_rng(prompt)
+    prompts = rng.integers(0, cfg.vocab, (batch, prompt))
+    dec = Decoder(w, cfg, batch, max_seq, prompt)
+    oracle = oracle_for(w, cfg, batch, max_seq)
+    dec.history = None
+    first = dec.prefill(torch.from_numpy(prompts).to(dev))
+    ref = oracle.forward(prompts, 0)[:, -1]
+    _compare_logits(dec, ref)
+    toks = first.cpu().numpy()
+    checked = 0
+    for i in range(steps):
+        top2 = np.sort(ref, axis=-1)[:, -2:]
+        clear = (top2[:, 1] - top2[:, 0]) > 2e-2 * np.abs(ref).max()
+        assert np.array_equal(toks[clear], ref.argmax(-1)[clear])
+        checked += int(clear.sum())
+        dec.step()
+        ref = oracle.forward(toks[:, None], prompt + i)[:, -1]
+        _compare_logits(dec, ref)
+        toks = dec.tokens[:batch].cpu().numpy()
+    assert dec.pos.tolist() == [prompt + steps] * batch
+    assert checked >= steps * batch // 2
+
+
+def test_graph_replay_matches_eager_decode(dev):
+    cfg = SMALL
+    w = random_weights(cfg, dev, seed=7)
+    prompts = torch.from_numpy(np.random.default_rng(3).integers(0, cfg.vocab, (2, 10))).to(dev)
+    dec = Decoder(w, cfg, 2, 128, 10)
+    eager = dec.generate(prompts, 12, graph=False)
+    eager_logits = dec.logits.clone()
+    graphed = dec.generate(prompts, 12, graph=True)
+    torch.cuda.synchronize()
+    assert torch.equal(eager, graphed)
+    assert torch.equal(eager_logits, dec.logits)
+    # a second graphed run (new prompts, the graph is captured again) is still exact
+    eager2 = dec.generate(prompts.flip(1), 5, graph=False)
+    assert torch.equal(eager2, dec.generate(prompts.flip(1), 5, graph=True))
+
+
+def test_config5_full_size_prefill_and_graph_decode(dev):
+    """8 layers, hidden 4096, 32/8 heads, SwiGLU 14336, vocab 32000: 512-token prefill at batch
+    1 and graph-replayed decode agree with eager decode bit for bit; logits are finite."""
+    cfg = DecoderConfig()
+    w = random_weights(cfg, dev, seed=0)
+    prompts = torch.randint(0, cfg.vocab, (1, 512), device=dev)
+    dec = Decoder(w, cfg, 1, 640, 512)
+    eager = dec.generate(prompts, 4, graph=False)
+    graphed = dec.generate(prompts, 4, graph=True)
+    torch.cuda.synchronize()
+    assert torch.equal(eager, graphed)
+    assert torch.isfinite(dec.logits).all()
+    assert dec.pos.tolist() == [512 + 3]

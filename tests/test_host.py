@@ -163,14 +163,14 @@ def test_register_is_idempotent_and_opens_no_hardware():
 
 # ----------------------------------------------------------------------------- C ABI
 def declared_functions() -> list[str]:
-    text = HEADER.read_text()
-    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(tgm_\w+)\(", text, flags=re.M)))
+    text = "\n".join(h.read_text() for h in sorted((ROOT / "include").glob("*.h")))
+    return sorted(set(re.findall(r"^(?:int|int64_t|const char\*)\s+(tgm_\w+)\(", text, flags=re.M)))
 
 
 def test_library_exports_every_declared_symbol():
     lib = K.load_library()
     names = declared_functions()
-    assert {"tgm_unpack", "tgm_gemv", "tgm_gemm_w", "tgm_gemm_mx", "tgm_gemm_plain"} <= set(names)
+    assert {"tgm_unpack", "tgm_gemv", "tgm_gemm_w", "tgm_gemm_mx", "tgm_gemm_plain", "tgm_dec_attention"} <= set(names)
     for name in names:
         assert hasattr(lib, name), name
     assert set(K.EXPORTS) == set(names)

@@ -1,0 +1,497 @@
+// Decoder-step kernels for a Llama-style model on the packed matmul path (tgm_decoder.h).
+//
+// The reference has no model code; a decoder on it would be tinygrad ops around
+// PackedTensor.matmul (alexandreteles/tinygrad-dx12 src/tinygrad_dx12/codegen/decomp/
+// dx12.py:108-112).  These kernels are the layer's non-matmul work on gfx950: embedding
+// gather, residual add fused with RMSNorm, RoPE fused with the KV-cache store, split-K
+// grouped-query attention, SwiGLU, a bf16 GEMV for the output head and a greedy argmax
+// that advances the sequence positions on the device.  Everything a step launches reads its
+// position from device memory, so a decode step is the same launch sequence every time and
+// can be replayed as a HIP graph.  Nothing here allocates or issues a memset.
+#include <math.h>
+
+#include "../../include/tgm_decoder.h"
+#include "tgm_common.h"
+
+namespace tgm {
+
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 dec_bf16x2;
+typedef unsigned dec_u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float lo_bf16(unsigned w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float hi_bf16(unsigned w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
+
+// ------------------------------------------------------------------ embedding
+__global__ void __launch_bounds__(256) dec_embed(const uint16_t* __restrict__ table, int64_t vocab, int d,
+                                                 const int32_t* __restrict__ tokens, float* __restrict__ h) {
+  const int64_t r = blockIdx.x;
+  int64_t tok = tokens[r];
+  if (tok < 0 || tok >= vocab) tok = 0;
+  const uint16_t* src = table + tok * d;
+  float* dst = h + r * d;
+  for (int i = threadIdx.x; i < d; i += 256) dst[i] = bf16_to_f32(src[i]);
+}
+
+// ------------------------------------------------------------------ residual add + RMSNorm
+// One workgroup per row; the row's sum of squares is reduced over four waves.
+__global__ void __launch_bounds__(256) dec_add_rmsnorm(float* __restrict__ h, const float* __restrict__ delta, int d,
+                                                       const uint16_t* __restrict__ w, float eps, void* __restrict__ out,
+                                                       int odt) {
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float* hr = h + r * d;
+  float ss = 0.f;
+  for (int i = tid; i < d; i += 256) {
+    float v = hr[i];
+    if (delta) {
+      v += delta[r * d + i];
+      hr[i] = v;
+    }
+    ss += v * v;
+  }
+  __shared__ float part[4];
+  ss = wave_sum(ss);
+  if (lane == 0) part[wave] = ss;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / (float)d + eps);
+  for (int i = tid; i < d; i += 256) store_from_f32(out, odt, r * d + i, hr[i] * inv * bf16_to_f32(w[i]));
+}
+
+// ------------------------------------------------------------------ RoPE + KV store
+// Grid (rows, heads + kv_heads), head_dim / 2 threads: thread i rotates the pair
+// (i, i + head_dim / 2) of one q or k head; k heads also store k (rotated) and v as bf16.
+__global__ void dec_rope_kv(float* __restrict__ qkv, int T, int H, int HK, int hd, const int32_t* __restrict__ pos,
+                            double base, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int max_seq) {
+  const int64_t r = blockIdx.x;
+  const int hh = blockIdx.y, i = threadIdx.x, half = hd / 2;
+  const int b = (int)(r / T), t = (int)(r % T);
+  const int p = pos[b] + t;
+  const int64_t ld = (int64_t)(H + 2 * HK) * hd;
+  float* x = qkv + r * ld + (int64_t)hh * hd;
+  double s, c;
+  sincos((double)p * pow(base, -2.0 * i / hd), &s, &c);
+  const double x1 = x[i], x2 = x[i + half];
+  const float y1 = (float)(x1 * c - x2 * s), y2 = (float)(x2 * c + x1 * s);
+  x[i] = y1;
+  x[i + half] = y2;
+  if (hh >= H && p >= 0 && p < max_seq) {
+    const int j = hh - H;
+    const int64_t o = (((int64_t)b * HK + j) * max_seq + p) * hd;
+    kc[o + i] = f32_to_bf16(y1);
+    kc[o + i + half] = f32_to_bf16(y2);
+    const float* v = qkv + r * ld + (int64_t)(H + HK + j) * hd;
+    vc[o + i] = f32_to_bf16(v[i]);
+    vc[o + i + half] = f32_to_bf16(v[i + half]);
+  }
+}
+
+// ------------------------------------------------------------------ attention
+// Grid (rows, kv_heads, splits), 256 threads.  A workgroup takes the G = heads / kv_heads q
+// heads that share kv head j, and the chunks of 64 cache positions [z * cps * 64, +cps * 64)
+// of its split, clipped to the token's causal length.  Per chunk:
+//   1. scores: 4 lanes per position, each a quarter of head_dim, dot with the G scaled q's
+//      (q kept in LDS), combined by two lane swaps;
+//   2. wave g (g, g + 4) folds the chunk into the running max / sum of head g (online
+//      softmax) and turns the chunk's scores into probabilities;
+//   3. lane l accumulates dims (2 l, 2 l + 1) of p . v over the positions of its wave
+//      (positions w, w + 4, ...), rescaled by exp(m_old - m_new).
+// One split writes the normalised output; several write (o, m, l) partials per (row, head,
+// split) that dec_attention_merge combines.  Loads use positions clamped into the valid range
+// (their probabilities are zero), so every load in a chunk is unconditional.
+template <int G, int HD>
+__global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ qkv, int T, int H, int HK,
+                                                     const int32_t* __restrict__ pos, const uint16_t* __restrict__ kc,
+                                                     const uint16_t* __restrict__ vc, int max_seq, int cps, float scale,
+                                                     float* __restrict__ part, void* __restrict__ out, int odt) {
+  constexpr int CH = 64, NP = HD / 2, QD = HD / 4;
+  const int r = blockIdx.x, j = blockIdx.y, z = blockIdx.z, S = gridDim.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = r / T, t = r % T;
+  const int p = pos[b] + t;
+  const int len = p + 1 < max_seq ? p + 1 : max_seq;
+  const int c_begin = z * cps * CH;
+  const int c_end = len < c_begin + cps * CH ? len : c_begin + cps * CH;
+  const int64_t ld = (int64_t)(H + 2 * HK) * HD;
+  __shared__ float qs[G][HD];
+  __shared__ float sc[G][CH];
+  __shared__ float m_sh[G], l_sh[G], a_sh[G];
+  __shared__ float red[4][G][HD];
+  for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = qkv[(int64_t)r * ld + (int64_t)j * G * HD + i] * scale;
+  if (tid < G) {
+    m_sh[tid] = -INFINITY;
+    l_sh[tid] = 0.f;
+  }
+  float oa[G][2];
+#pragma unroll
+  for (int g = 0; g < G; ++g) oa[g][0] = oa[g][1] = 0.f;
+  const int64_t kvbase = ((int64_t)b * HK + j) * max_seq;
+  __syncthreads();
+  for (int c0 = c_begin; c0 < c_end; c0 += CH) {
+    const int last = c_end - 1;
+    {
+      const int pi = tid >> 2, qd = tid & 3;
+      const int tt = c0 + pi;
+      const uint16_t* kr = kc + (kvbase + (tt < last ? tt : last)) * HD + qd * QD;
+      float s[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) s[g] = 0.f;
+#pragma unroll
+      for (int e = 0; e < QD; e += 8) {
+        const dec_u32x4 kv = *(const dec_u32x4*)(kr + e);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float k0 = lo_bf16(kv[q]), k1 = hi_bf16(kv[q]);
+#pragma unroll
+          for (int g = 0; g < G; ++g) s[g] += qs[g][qd * QD + e + 2 * q] * k0 + qs[g][qd * QD + e + 2 * q + 1] * k1;
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        s[g] += __shfl_xor(s[g], 1, 64);
+        s[g] += __shfl_xor(s[g], 2, 64);
+      }
+      if (qd == 0)
+#pragma unroll
+        for (int g = 0; g < G; ++g) sc[g][pi] = tt < c_end ? s[g] : -INFINITY;
+    }
+    __syncthreads();
+    for (int g = wave; g < G; g += 4) {
+      const float v = sc[g][lane];
+      const float m_old = m_sh[g];
+      const float m_new = fmaxf(m_old, wave_max(v));  // the chunk has a valid position
+      const float pv = v == -INFINITY ? 0.f : expf(v - m_new);
+      const float sum = wave_sum(pv);
+      sc[g][lane] = pv;
+      if (lane == 0) {
+        const float alpha = m_old == -INFINITY ? 0.f : expf(m_old - m_new);
+        a_sh[g] = alpha;
+        l_sh[g] = l_sh[g] * alpha + sum;
+        m_sh[g] = m_new;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float al = a_sh[g];
+      oa[g][0] *= al;
+      oa[g][1] *= al;
+    }
+    if (lane < NP) {
+#pragma unroll
+      for (int i = 0; i < CH / 4; ++i) {
+        const int pi = wave + 4 * i, tt = c0 + pi;
+        const unsigned vv = *(const unsigned*)(vc + (kvbase + (tt < last ? tt : last)) * HD + 2 * lane);
+        const float v0 = lo_bf16(vv), v1 = hi_bf16(vv);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float pg = sc[g][pi];
+          oa[g][0] += pg * v0;
+          oa[g][1] += pg * v1;
+        }
+      }
+    }
+    __syncthreads();  // the next chunk rewrites sc and a_sh
+  }
+  if (lane < NP)
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      red[wave][g][2 * lane] = oa[g][0];
+      red[wave][g][2 * lane + 1] = oa[g][1];
+    }
+  __syncthreads();
+  for (int i = tid; i < G * HD; i += 256) {
+    const int g = i / HD, d = i % HD, h = j * G + g;
+    const float o = red[0][g][d] + red[1][g][d] + red[2][g][d] + red[3][g][d];
+    if (part == nullptr) {
+      const float l = l_sh[g];
+      store_from_f32(out, odt, (int64_t)r * H * HD + (int64_t)h * HD + d, l > 0.f ? o / l : 0.f);
+    } else {
+      float* pp = part + (((int64_t)r * H + h) * S + z) * (HD + 2);
+      pp[d] = o;
+      if (d == 0) {
+        pp[HD] = m_sh[g];
+        pp[HD + 1] = l_sh[g];
+      }
+    }
+  }
+}
+
+// Grid (rows, heads), head_dim threads: combine the splits' (o, m, l) partials.
+template <int HD>
+__global__ void dec_attention_merge(const float* __restrict__ part, int S, int H, void* __restrict__ out, int odt) {
+  const int r = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+  const float* pp = part + ((int64_t)r * H + h) * S * (HD + 2);
+  float M = -INFINITY;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, pp[s * (HD + 2) + HD]);
+  float L = 0.f, o = 0.f;
+  for (int s = 0; s < S; ++s) {
+    const float m = pp[s * (HD + 2) + HD];
+    if (m == -INFINITY) continue;
+    const float w = expf(m - M);
+    L += pp[s * (HD + 2) + HD + 1] * w;
+    o += pp[s * (HD + 2) + d] * w;
+  }
+  store_from_f32(out, odt, (int64_t)r * H * HD + (int64_t)h * HD + d, L > 0.f ? o / L : 0.f);
+}
+
+// ------------------------------------------------------------------ SwiGLU
+__global__ void __launch_bounds__(256) dec_silu_mul(const float* __restrict__ gu, int64_t rows, int64_t F,
+                                                    void* __restrict__ out, int odt) {
+  const int64_t n = rows * F;
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / F, c = i - r * F;
+    const float g = gu[r * 2 * F + c], u = gu[r * 2 * F + F + c];
+    store_from_f32(out, odt, i, g / (1.0f + expf(-g)) * u);
+  }
+}
+
+// ------------------------------------------------------------------ bf16 GEMV (output head)
+// x (M rows) is staged in LDS once per workgroup; each wave then streams whole weight rows
+// (lane l reads 16-byte chunks l, l + 64, ...) and reduces its M dot products over the wave.
+template <int M>
+__global__ void __launch_bounds__(256) dec_gemv_bf16(const uint16_t* __restrict__ w, int N, int K,
+                                                     const uint16_t* __restrict__ x, int64_t ldx, float* __restrict__ y,
+                                                     int64_t ldy) {
+  __shared__ dec_u32x4 xs[32768 / 8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kc = K / 8;  // 16-byte chunks per row
+  for (int i = tid; i < M * kc; i += 256) xs[i] = *(const dec_u32x4*)(x + (int64_t)(i / kc) * ldx + (int64_t)(i % kc) * 8);
+  __syncthreads();
+  const int nw = gridDim.x * 4;
+  for (int n = blockIdx.x * 4 + wave; n < N; n += nw) {
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = 0.f;
+    // bf16 pairs are loaded as pairs: bit-casting the dwords of a loaded 4-dword vector to
+    // bf16 pairs has been compiled into one repeated pair
+    const dec_bf16x2* wr = (const dec_bf16x2*)(w + (int64_t)n * K);
+    const dec_bf16x2* xp = (const dec_bf16x2*)xs;
+#pragma unroll 8
+    for (int c = lane; c < kc; c += 64) {  // 16-byte chunk c: pairs 4 c .. 4 c + 3
+      dec_bf16x2 wv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wv[e] = wr[4 * c + e];
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          acc[m] = __builtin_amdgcn_fdot2_f32_bf16(wv[e], xp[4 * (m * kc + c) + e], acc[m], false);
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = wave_sum(acc[m]);
+    if (lane == 0)
+#pragma unroll
+      for (int m = 0; m < M; ++m) y[m * ldy + n] = acc[m];
+  }
+}
+
+// ------------------------------------------------------------------ greedy argmax
+__global__ void __launch_bounds__(1024) dec_argmax(const float* __restrict__ logits, int n, int64_t ld,
+                                                   int32_t* __restrict__ tokens, int32_t* __restrict__ pos,
+                                                   int32_t* __restrict__ hist, int64_t hstride, int64_t hbase) {
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* row = logits + r * ld;
+  float best = -INFINITY;
+  int bi = n;  // none yet (NaN and -inf never win)
+  for (int i = tid; i < n; i += 1024) {
+    const float v = row[i];
+    if (v > best) {
+      best = v;
+      bi = i;
+    }
+  }
+  auto better = [](float v, int i, float bv, int bidx) { return v > bv || (v == bv && i < bidx); };
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (better(ov, oi, best, bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  __shared__ float bv[16];
+  __shared__ int bx[16];
+  if (lane == 0) {
+    bv[wave] = best;
+    bx[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 16; ++w)
+      if (better(bv[w], bx[w], best, bi)) {
+        best = bv[w];
+        bi = bx[w];
+      }
+    if (bi >= n) bi = 0;
+    tokens[r] = bi;
+    if (pos) {
+      const int p = pos[r];
+      const int64_t k = (int64_t)p + 1 - hbase;
+      if (hist && k >= 0 && k < hstride) hist[r * hstride + k] = bi;
+      pos[r] = p + 1;
+    }
+  }
+}
+
+}  // namespace tgm
+
+using namespace tgm;
+
+static bool out_dtype_ok(int dt) { return dt == TGM_F16 || dt == TGM_BF16 || dt == TGM_F32; }
+
+extern "C" int tgm_dec_embed(const void* table, int64_t vocab, int64_t d, const int32_t* tokens, int64_t rows,
+                             float* h, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(table && tokens && h, "null operand");
+  TGM_CHECK_ARG(vocab > 0 && d > 0 && rows >= 0 && d < (1ll << 31) && rows < (1ll << 31), "invalid embedding sizes");
+  if (rows == 0) return TGM_OK;
+  hipLaunchKernelGGL(dec_embed, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)table, vocab,
+                     (int)d, tokens, h);
+  return launch_status("tgm_dec_embed");
+}
+
+extern "C" int tgm_dec_add_rmsnorm(float* h, const float* delta, int64_t rows, int64_t d, const void* weight, float eps,
+                                   void* out, int out_dtype, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(h && weight && out, "null operand");
+  TGM_CHECK_ARG(rows >= 0 && d > 0 && d < (1ll << 31) && rows < (1ll << 31), "invalid norm sizes");
+  TGM_CHECK_ARG(out_dtype_ok(out_dtype), "output must be f16, bf16 or f32");
+  TGM_CHECK_ARG(eps >= 0.f, "eps must be non-negative");
+  if (rows == 0) return TGM_OK;
+  hipLaunchKernelGGL(dec_add_rmsnorm, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, h, delta, (int)d,
+                     (const uint16_t*)weight, eps, out, out_dtype);
+  return launch_status("tgm_dec_add_rmsnorm");
+}
+
+extern "C" int tgm_dec_rope_kv(float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, int64_t kv_heads,
+                               int64_t head_dim, const int32_t* pos, double rope_base, void* k_cache, void* v_cache,
+                               int64_t max_seq, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(qkv && pos && k_cache && v_cache, "null operand");
+  TGM_CHECK_ARG(rows >= 0 && seq_rows > 0 && rows % seq_rows == 0, "rows must be a multiple of seq_rows");
+  TGM_CHECK_ARG(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "heads must be a multiple of kv_heads");
+  TGM_CHECK_ARG(head_dim > 0 && head_dim % 2 == 0 && head_dim <= 1024, "head_dim must be even and at most 1024");
+  TGM_CHECK_ARG(max_seq > 0 && max_seq < (1ll << 31) && rows < (1ll << 31), "invalid cache sizes");
+  TGM_CHECK_ARG(rope_base > 0.0, "rope base must be positive");
+  if (rows == 0) return TGM_OK;
+  hipLaunchKernelGGL(dec_rope_kv, dim3((unsigned)rows, (unsigned)(heads + kv_heads)), dim3((unsigned)(head_dim / 2)), 0,
+                     (hipStream_t)stream, qkv, (int)seq_rows, (int)heads, (int)kv_heads, (int)head_dim, pos, rope_base,
+                     (uint16_t*)k_cache, (uint16_t*)v_cache, (int)max_seq);
+  return launch_status("tgm_dec_rope_kv");
+}
+
+extern "C" int64_t tgm_dec_attention_workspace(int64_t rows, int64_t heads, int64_t head_dim, int64_t splits) {
+  return splits > 1 ? rows * heads * splits * (head_dim + 2) * (int64_t)sizeof(float) : 0;
+}
+
+template <int G, int HD>
+static void launch_attention(dim3 grid, hipStream_t st, const float* qkv, int T, int H, int HK, const int32_t* pos,
+                             const void* kc, const void* vc, int max_seq, int cps, float scale, float* part, void* out,
+                             int odt) {
+  hipLaunchKernelGGL((dec_attention<G, HD>), grid, dim3(256), 0, st, qkv, T, H, HK, pos, (const uint16_t*)kc,
+                     (const uint16_t*)vc, max_seq, cps, scale, part, out, odt);
+}
+
+extern "C" int tgm_dec_attention(const float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, int64_t kv_heads,
+                                 int64_t head_dim, const int32_t* pos, const void* k_cache, const void* v_cache,
+                                 int64_t max_seq, int64_t splits, float* workspace, int64_t workspace_bytes, void* out,
+                                 int out_dtype, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(qkv && pos && k_cache && v_cache && out, "null operand");
+  TGM_CHECK_ARG(rows >= 0 && seq_rows > 0 && rows % seq_rows == 0, "rows must be a multiple of seq_rows");
+  TGM_CHECK_ARG(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "heads must be a multiple of kv_heads");
+  TGM_CHECK_ARG(out_dtype_ok(out_dtype), "output must be f16, bf16 or f32");
+  TGM_CHECK_ARG(max_seq > 0 && max_seq < (1 << 30) && rows < (1ll << 31) && kv_heads <= 65535, "invalid sizes");
+  const int64_t chunks = (max_seq + 63) / 64;
+  TGM_CHECK_ARG(splits >= 1 && splits <= chunks, "splits must be in [1, ceil(max_seq / 64)]");
+  TGM_CHECK_ARG(splits == 1 || (workspace && workspace_bytes >= tgm_dec_attention_workspace(rows, heads, head_dim, splits)),
+                "split attention needs a workspace of tgm_dec_attention_workspace() bytes");
+  const int64_t G = heads / kv_heads;
+  if (head_dim != 64 && head_dim != 128) TGM_UNSUPPORTED("tgm_dec_attention: head_dim must be 64 or 128");
+  if (G != 1 && G != 2 && G != 4 && G != 8) TGM_UNSUPPORTED("tgm_dec_attention: heads / kv_heads must be 1, 2, 4 or 8");
+  if ((uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 4) TGM_UNSUPPORTED("tgm_dec_attention: caches must be 16-byte aligned");
+  if (rows == 0) return TGM_OK;
+  const int cps = (int)((chunks + splits - 1) / splits);
+  const dim3 grid((unsigned)rows, (unsigned)kv_heads, (unsigned)splits);
+  const hipStream_t st = (hipStream_t)stream;
+  float* part = splits > 1 ? workspace : nullptr;
+  const float scale = (float)(1.0 / sqrt((double)head_dim));
+#define TGM_ATT(GG, HDD)                                                                                            \
+  if (G == GG && head_dim == HDD)                                                                                   \
+    launch_attention<GG, HDD>(grid, st, qkv, (int)seq_rows, (int)heads, (int)kv_heads, pos, k_cache, v_cache,        \
+                              (int)max_seq, cps, scale, part, out, out_dtype);
+  TGM_ATT(1, 64) TGM_ATT(2, 64) TGM_ATT(4, 64) TGM_ATT(8, 64)
+  TGM_ATT(1, 128) TGM_ATT(2, 128) TGM_ATT(4, 128) TGM_ATT(8, 128)
+#undef TGM_ATT
+  int status = launch_status("tgm_dec_attention");
+  if (status != TGM_OK || splits == 1) return status;
+  const dim3 mgrid((unsigned)rows, (unsigned)heads);
+  if (head_dim == 64)
+    hipLaunchKernelGGL(dec_attention_merge<64>, mgrid, dim3(64), 0, st, part, (int)splits, (int)heads, out, out_dtype);
+  else
+    hipLaunchKernelGGL(dec_attention_merge<128>, mgrid, dim3(128), 0, st, part, (int)splits, (int)heads, out, out_dtype);
+  return launch_status("tgm_dec_attention");
+}
+
+extern "C" int tgm_dec_silu_mul(const float* gate_up, int64_t rows, int64_t ffn, void* out, int out_dtype,
+                                void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(gate_up && out, "null operand");
+  TGM_CHECK_ARG(rows >= 0 && ffn > 0, "invalid sizes");
+  TGM_CHECK_ARG(out_dtype_ok(out_dtype), "output must be f16, bf16 or f32");
+  if (rows == 0) return TGM_OK;
+  const int64_t n = rows * ffn;
+  const int64_t blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
+  hipLaunchKernelGGL(dec_silu_mul, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, gate_up, rows, ffn, out,
+                     out_dtype);
+  return launch_status("tgm_dec_silu_mul");
+}
+
+extern "C" int tgm_dec_gemv_bf16(const void* w, int64_t n, int64_t k, const void* x, int64_t m, int64_t ldx, float* y,
+                                 int64_t ldy, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(w && x && y, "null operand");
+  TGM_CHECK_ARG(n >= 0 && k > 0 && m >= 0 && m <= 8, "m must be at most 8");
+  TGM_CHECK_ARG(m <= 1 || (ldx >= k && ldy >= n), "row strides smaller than the rows");
+  if (n == 0 || m == 0) return TGM_OK;
+  if (k % 8 != 0 || m * k > 32768 || n >= (1ll << 31))
+    TGM_UNSUPPORTED("tgm_dec_gemv_bf16: k must be a multiple of 8 with m * k <= 32768");
+  if ((uintptr_t)w % 16 || (uintptr_t)x % 16 || (m > 1 && (ldx * 2) % 16))
+    TGM_UNSUPPORTED("tgm_dec_gemv_bf16: operands and x rows must be 16-byte aligned");
+  const int64_t waves = (n + 3) / 4;
+  const unsigned blocks = (unsigned)(waves < 512 ? waves : 512);
+  const hipStream_t st = (hipStream_t)stream;
+  const uint16_t* wp = (const uint16_t*)w;
+  const uint16_t* xp = (const uint16_t*)x;
+  switch (m) {
+#define TGM_GV(MM) \
+  case MM: hipLaunchKernelGGL(dec_gemv_bf16<MM>, dim3(blocks), dim3(256), 0, st, wp, (int)n, (int)k, xp, ldx, y, ldy); break;
+    TGM_GV(1) TGM_GV(2) TGM_GV(3) TGM_GV(4) TGM_GV(5) TGM_GV(6) TGM_GV(7) TGM_GV(8)
+#undef TGM_GV
+  }
+  return launch_status("tgm_dec_gemv_bf16");
+}
+
+extern "C" int tgm_dec_argmax(const float* logits, int64_t rows, int64_t n, int64_t ld, int32_t* tokens, int32_t* pos,
+                              int32_t* history, int64_t hist_stride, int64_t hist_base, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(logits && tokens, "null operand");
+  TGM_CHECK_ARG(rows >= 0 && n > 0 && n < (1ll << 31) && (rows <= 1 || ld >= n), "invalid logits shape");
+  TGM_CHECK_ARG(!history || (pos && hist_stride > 0), "history needs positions and a positive stride");
+  if (rows == 0) return TGM_OK;
+  hipLaunchKernelGGL(dec_argmax, dim3((unsigned)rows), dim3(1024), 0, (hipStream_t)stream, logits, (int)n, ld, tokens, pos,
+                     history, hist_stride, hist_base);
+  return launch_status("tgm_dec_argmax");
+}

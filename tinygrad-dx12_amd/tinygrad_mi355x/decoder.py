@@ -1,0 +1,269 @@
+"""Llama-style decoder on the packed matmul path: prefill and greedy decode on gfx950.
+
+The reference has no model code.  A decoder on it would be ordinary tinygrad ops around
+``PackedTensor.matmul`` (alexandreteles/tinygrad-dx12 src/tinygrad_dx12/codegen/decomp/
+dx12.py:108-112), with INT4 ``block_size=128`` accepted by dx12.py:30, :44-47.  This module is
+that consumer, the one that turns the packed kernels into tokens per second:
+
+* attention projections: INT4 weights with fp16 scales per 128 K-elements; q, k and v rows
+  are stacked into one weight so that a token needs one QKV product;
+* feed-forward: FP4 E2M1 weights with E8M0 scales per 32; gate and up rows stacked;
+* embeddings and output head: bf16; RMSNorm weights bf16; residual stream fp32;
+* RoPE (rotate-half pairs, base 10000) and grouped-query attention over a bf16 KV cache.
+
+Every operation is a gfx950 kernel of ``libtgm_mi355x.so``: the packed GEMV (decode, up to
+16 rows) and GEMM (prefill), plus the decoder-step kernels (include/tgm_decoder.h).  torch
+supplies device memory and the stream.  Activations feeding INT4 weights are fp16 and those
+feeding FP4 weights bf16, the activation types of the two kernel families.
+
+A decode step reads sequence positions and the previous tokens from device memory and its
+argmax writes the next tokens and advances the positions, so its launch sequence never
+changes: ``Decoder.generate`` captures one step as a HIP graph and replays it.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from tinygrad_mi355x.codegen.decomp.mi355x import PackedTensor, quantize_mx
+from tinygrad_mi355x.runtime import kernels as K
+from tinygrad_mi355x.runtime.graph import StreamGraph
+
+F16, BF16, F32 = K.DTYPE_IDS[torch.float16], K.DTYPE_IDS[torch.bfloat16], K.DTYPE_IDS[torch.float32]
+GEMV_MAX_ROWS = 16
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    hidden: int = 4096
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    ffn: int = 14336
+    vocab: int = 32000
+    layers: int = 8
+    eps: float = 1e-5
+    rope_base: float = 10000.0
+    attn_group: int = 128  # INT4 scale group along K
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+    def weight_bytes_per_token(self) -> int:
+        """Weight bytes one decode step streams: packed layers plus the bf16 output head."""
+        d, f = self.hidden, self.ffn
+        attn = (self.qkv_rows + d) * d // 2 + (self.qkv_rows + d) * (d // self.attn_group) * 2
+        ffn = 3 * d * f // 2 + 3 * d * f // 32
+        norms = 2 * d * 2
+        return self.layers * (attn + ffn + norms) + self.vocab * d * 2 + d * 2
+
+
+@dataclass
+class LayerWeights:
+    attn_norm: torch.Tensor      # bf16 [D]
+    wqkv: PackedTensor           # int4 [(H + 2 HK) hd, D], fp16 scales per attn_group
+    wo: PackedTensor             # int4 [D, H hd]
+    ffn_norm: torch.Tensor       # bf16 [D]
+    w_gate_up: PackedTensor      # fp4 [2 F, D], E8M0 per 32 (gate rows, then up rows)
+    w_down: PackedTensor         # fp4 [D, F]
+
+
+@dataclass
+class DecoderWeights:
+    embed: torch.Tensor          # bf16 [V, D]
+    layers: list[LayerWeights]
+    final_norm: torch.Tensor     # bf16 [D]
+    lm_head: torch.Tensor        # bf16 [V, D]
+
+
+def random_weights(cfg: DecoderConfig, device: str | torch.device = "cuda", seed: int = 0) -> DecoderWeights:
+    """Synthetic random-init weights of the configured shape, generated on the device.
+
+    INT4 codes are uniform over all 16 nibbles with scales in [0.002, 0.005]; FP4 weights are
+    N(0, 0.02) MX-quantised along K; norms 1 + 0.1 N(0, 1); embeddings N(0, 1); head N(0, 0.02).
+    """
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    d = cfg.hidden
+
+    def int4(n: int, k: int) -> PackedTensor:
+        data = torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device=device, generator=g)
+        scales = (torch.rand((n, k // cfg.attn_group), device=device, generator=g) * 0.003 + 0.002).to(torch.float16)
+        return PackedTensor(data, "int4", (n, k), scales, cfg.attn_group)
+
+    def fp4(n: int, k: int) -> PackedTensor:
+        return quantize_mx(torch.randn((n, k), device=device, generator=g) * 0.02, "fp4_e2m1")
+
+    def norm() -> torch.Tensor:
+        return (1.0 + 0.1 * torch.randn(d, device=device, generator=g)).to(torch.bfloat16)
+
+    layers = []
+    for _ in range(cfg.layers):
+        layers.append(LayerWeights(norm(), int4(cfg.qkv_rows, d), int4(d, cfg.heads * cfg.head_dim), norm(),
+                                   fp4(2 * cfg.ffn, d), fp4(d, cfg.ffn)))
+    embed = torch.randn((cfg.vocab, d), device=device, generator=g).to(torch.bfloat16)
+    final_norm = norm()
+    lm_head = (torch.randn((cfg.vocab, d), device=device, generator=g) * 0.02).to(torch.bfloat16)
+    return DecoderWeights(embed, layers, final_norm, lm_head)
+
+
+def _packed_product(x: torch.Tensor, m: int, ldx: int, w: PackedTensor, y: torch.Tensor, ldy: int, stream: int) -> None:
+    """y[:m] = x[:m] @ deq(w)^T: packed GEMV for m <= 16 rows, packed GEMM above."""
+    n, k = w.shape
+    sdt = K.dtype_id(w.scales.dtype) if w.scales is not None else -1
+    if m <= GEMV_MAX_ROWS:
+        K.call("tgm_gemv", w.data.data_ptr(), K.FORMAT_IDS[w.format], n, k, K.ptr(w.scales), sdt, w.block_size,
+               x.data_ptr(), K.dtype_id(x.dtype), m, ldx, y.data_ptr(), K.dtype_id(y.dtype), ldy, stream)
+    else:
+        K.call("tgm_gemm_w", x.data_ptr(), K.dtype_id(x.dtype), m, ldx, w.data.data_ptr(), K.FORMAT_IDS[w.format], n,
+               k, K.ptr(w.scales), sdt, w.block_size, y.data_ptr(), K.dtype_id(y.dtype), ldy, stream)
+
+
+class Decoder:
+    """Prefill + greedy decode for ``batch`` sequences of up to ``max_seq`` tokens.
+
+    All activations, the KV caches and the attention workspace are allocated once here;
+    ``prefill`` and ``step`` launch kernels only.
+    """
+
+    def __init__(self, weights: DecoderWeights, cfg: DecoderConfig, batch: int, max_seq: int, max_prompt: int) -> None:
+        if cfg.heads % cfg.kv_heads or cfg.head_dim not in (64, 128):
+            raise ValueError("heads must be a multiple of kv_heads and head_dim 64 or 128")
+        if not 1 <= batch <= 8:
+            raise ValueError("batch must be in [1, 8] (the output-head GEMV takes up to 8 rows)")
+        if not 1 <= max_prompt <= max_seq:
+            raise ValueError("max_prompt must be in [1, max_seq]")
+        self.w, self.cfg, self.batch, self.max_seq, self.max_prompt = weights, cfg, batch, max_seq, max_prompt
+        dev = weights.embed.device
+        K.require_device(weights.embed)
+        self.device = dev
+        d, rows = cfg.hidden, batch * max_prompt
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.h = torch.empty((rows, d), **f32)
+        self.delta = torch.empty((rows, d), **f32)
+        self.xn16 = torch.empty((rows, d), dtype=torch.float16, device=dev)
+        self.xnb = torch.empty((rows, d), dtype=torch.bfloat16, device=dev)
+        self.qkv = torch.empty((rows, cfg.qkv_rows), **f32)
+        self.attn = torch.empty((rows, cfg.heads * cfg.head_dim), dtype=torch.float16, device=dev)
+        self.gu = torch.empty((rows, 2 * cfg.ffn), **f32)
+        self.act = torch.empty((rows, cfg.ffn), dtype=torch.bfloat16, device=dev)
+        self.logits = torch.empty((batch, cfg.vocab), **f32)
+        cache = (cfg.layers, batch, cfg.kv_heads, max_seq, cfg.head_dim)
+        self.k_cache = torch.zeros(cache, dtype=torch.bfloat16, device=dev)
+        self.v_cache = torch.zeros(cache, dtype=torch.bfloat16, device=dev)
+        self.splits = max(1, math.ceil(max_seq / 64))
+        ws = K.load_library().tgm_dec_attention_workspace(batch, cfg.heads, cfg.head_dim, self.splits)
+        self.workspace = torch.empty(max(ws // 4, 1), **f32)
+        self.workspace_bytes = ws
+        self.tokens = torch.zeros(rows, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.history: torch.Tensor | None = None
+        self._graph: StreamGraph | None = None
+
+    # ---------------------------------------------------------------- building blocks
+    def _layers(self, rows: int, seq_rows: int, splits: int, stream: int) -> None:
+        cfg = self.cfg
+        d = cfg.hidden
+        for li, L in enumerate(self.w.layers):
+            K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr() if li else None, rows, d,
+                   L.attn_norm.data_ptr(), cfg.eps, self.xn16.data_ptr(), F16, stream)
+            _packed_product(self.xn16, rows, d, L.wqkv, self.qkv, cfg.qkv_rows, stream)
+            kc, vc = self.k_cache[li], self.v_cache[li]
+            K.call("tgm_dec_rope_kv", self.qkv.data_ptr(), rows, seq_rows, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                   self.pos.data_ptr(), cfg.rope_base, kc.data_ptr(), vc.data_ptr(), self.max_seq, stream)
+            K.call("tgm_dec_attention", self.qkv.data_ptr(), rows, seq_rows, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                   self.pos.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.max_seq, splits,
+                   self.workspace.data_ptr() if splits > 1 else None, self.workspace_bytes if splits > 1 else 0,
+                   self.attn.data_ptr(), F16, stream)
+            _packed_product(self.attn, rows, cfg.heads * cfg.head_dim, L.wo, self.delta, d, stream)
+            K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr(), rows, d, L.ffn_norm.data_ptr(),
+                   cfg.eps, self.xnb.data_ptr(), BF16, stream)
+            _packed_product(self.xnb, rows, d, L.w_gate_up, self.gu, 2 * cfg.ffn, stream)
+            K.call("tgm_dec_silu_mul", self.gu.data_ptr(), rows, cfg.ffn, self.act.data_ptr(), BF16, stream)
+            _packed_product(self.act, rows, cfg.ffn, L.w_down, self.delta, d, stream)
+        K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr(), rows, d, self.w.final_norm.data_ptr(),
+               cfg.eps, self.xnb.data_ptr(), BF16, stream)
+
+    def _head(self, first_row: int, row_stride: int, stream: int, advance: bool) -> None:
+        """Output head over one normed row per sequence (rows first_row + b * row_stride of the
+        normed activations) and the greedy argmax."""
+        cfg = self.cfg
+        x = self.xnb[first_row]
+        K.call("tgm_dec_gemv_bf16", self.w.lm_head.data_ptr(), cfg.vocab, cfg.hidden, x.data_ptr(), self.batch,
+               row_stride * cfg.hidden, self.logits.data_ptr(), cfg.vocab, stream)
+        hist = self.history
+        K.call("tgm_dec_argmax", self.logits.data_ptr(), self.batch, cfg.vocab, cfg.vocab, self.tokens.data_ptr(),
+               self.pos.data_ptr() if advance else None, hist.data_ptr() if (advance and hist is not None) else None,
+               hist.shape[1] if hist is not None else 0, self.prompt_len, stream)
+
+    # ---------------------------------------------------------------- public API
+    def prefill(self, prompts: torch.Tensor) -> torch.Tensor:
+        """Run the prompts (int [batch, T], T <= max_prompt) and return the first greedy tokens."""
+        if prompts.dim() != 2 or prompts.shape[0] != self.batch or not 1 <= prompts.shape[1] <= self.max_prompt:
+            raise ValueError(f"prompts must be [{self.batch}, 1..{self.max_prompt}]")
+        if int(prompts.min()) < 0 or int(prompts.max()) >= self.cfg.vocab:
+            raise ValueError("prompt tokens out of range")
+        t = prompts.shape[1]
+        rows = self.batch * t
+        stream = K.stream_of(self.h)
+        self.prompt_len = t
+        self.tokens[:rows].copy_(prompts.reshape(-1).to(torch.int32))
+        self.pos.zero_()
+        K.call("tgm_dec_embed", self.w.embed.data_ptr(), self.cfg.vocab, self.cfg.hidden, self.tokens.data_ptr(), rows,
+               self.h.data_ptr(), stream)
+        self._layers(rows, t, 1, stream)
+        self._head(t - 1, t, stream, advance=False)  # the last prompt row of each sequence
+        self.pos.fill_(t)
+        self._graph = None
+        return self.tokens[:self.batch].clone()
+
+    def _decode_step(self) -> None:
+        stream = K.stream_of(self.h)
+        K.call("tgm_dec_embed", self.w.embed.data_ptr(), self.cfg.vocab, self.cfg.hidden, self.tokens.data_ptr(),
+               self.batch, self.h.data_ptr(), stream)
+        self._layers(self.batch, 1, self.splits, stream)
+        self._head(0, 1, stream, advance=True)
+
+    def step(self) -> None:
+        """One eager decode step: consumes ``tokens[:batch]`` at ``pos``, writes the next tokens."""
+        self._decode_step()
+
+    def capture(self) -> StreamGraph:
+        """Capture one decode step on a side stream as a HIP graph (replayed by ``generate``)."""
+        if self._graph is None:
+            stream = torch.cuda.Stream(device=self.device)
+            stream.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(stream):
+                self._graph = StreamGraph(self._decode_step, stream.cuda_stream)
+            self._graph_stream = stream
+        return self._graph
+
+    def generate(self, prompts: torch.Tensor, new_tokens: int, graph: bool = True) -> torch.Tensor:
+        """Greedy generation: [batch, new_tokens] token ids (the first comes from the prefill)."""
+        if new_tokens < 1 or prompts.shape[1] + new_tokens - 1 > self.max_seq:
+            raise ValueError("prompt + generated tokens exceed max_seq")
+        self.history = torch.zeros((self.batch, new_tokens), dtype=torch.int32, device=self.device)
+        self.prompt_len = prompts.shape[1]
+        self._graph = None
+        first = self.prefill(prompts)
+        self.history[:, 0] = first
+        if new_tokens > 1:
+            # the first step runs eagerly: it also performs every kernel's one-time set-up, which
+            # must not happen inside a capture
+            self._decode_step()
+        remaining = new_tokens - 2
+        if graph and remaining > 0:
+            g = self.capture()
+            cur = torch.cuda.current_stream(self.device)
+            self._graph_stream.wait_stream(cur)
+            for _ in range(remaining):
+                g.launch()
+            cur.wait_stream(self._graph_stream)
+        else:
+            for _ in range(max(remaining, 0)):
+                self._decode_step()
+        return self.history.clone()

@@ -1,4 +1,5 @@
-"""ctypes binding of the gfx950 kernel library ``libtgm_mi355x.so`` (include/tgm_packed.h).
+"""ctypes binding of the gfx950 kernel library ``libtgm_mi355x.so`` (include/tgm_packed.h,
+include/tgm_decoder.h).
 
 This is the only route from Python into the packed kernels.  There is no CPU
 implementation behind it: when the library is missing or no MI355X is visible,
@@ -45,8 +46,16 @@ _SIGNATURES = {
     "tgm_gemm_plain": (_P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _I64, _I64, _I64, _INT, _P),
     "tgm_quantize_mx": (_P, _INT, _I64, _I64, _INT, _I64, _P, _P, _P),
     "tgm_pack_codes": (_P, _I64, _INT, _P, _P),
+    # decoder-step kernels (include/tgm_decoder.h)
+    "tgm_dec_embed": (_P, _I64, _I64, _P, _I64, _P, _P),
+    "tgm_dec_add_rmsnorm": (_P, _P, _I64, _I64, _P, ctypes.c_float, _P, _INT, _P),
+    "tgm_dec_rope_kv": (_P, _I64, _I64, _I64, _I64, _I64, _P, ctypes.c_double, _P, _P, _I64, _P),
+    "tgm_dec_attention": (_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _P, _I64, _P, _INT, _P),
+    "tgm_dec_silu_mul": (_P, _I64, _I64, _P, _INT, _P),
+    "tgm_dec_gemv_bf16": (_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P),
+    "tgm_dec_argmax": (_P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _P),
 }
-EXPORTS = ("tgm_abi_version", "tgm_last_error", *_SIGNATURES)
+EXPORTS = ("tgm_abi_version", "tgm_last_error", "tgm_dec_attention_workspace", *_SIGNATURES)
 
 
 def library_path() -> Path:
@@ -77,6 +86,8 @@ def load_library() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = ctypes.c_int
+        lib.tgm_dec_attention_workspace.argtypes = (_I64, _I64, _I64, _I64)
+        lib.tgm_dec_attention_workspace.restype = _I64
         _lib = lib
         return lib
 

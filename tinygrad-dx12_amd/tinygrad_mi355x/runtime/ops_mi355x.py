@@ -245,10 +245,8 @@ class MI355XProgram:
             out += data
         return bytes(out)
 
-    def __call__(self, *bufs: MI355XBuffer, global_size: tuple[int, int, int] = (1, 1, 1),
-                 local_size: tuple[int, int, int] = (1, 1, 1), vals: tuple[int | float, ...] = (), wait: bool = False,
-                 timeout: int | None = None) -> float | None:
-        """Launch ``global_size`` workgroups of ``local_size`` work-items; seconds when ``wait``."""
+    def validate(self, bufs, global_size, local_size, vals) -> tuple[tuple[int, int, int], tuple[int, int, int]]:
+        """Check a launch's arguments (ValueError on any mismatch); returns the launch sizes."""
         global_size = tuple(global_size or (1, 1, 1))
         local_size = tuple(local_size or (1, 1, 1))
         limits = MI355XRenderer.global_max
@@ -259,11 +257,23 @@ class MI355XProgram:
         if len(bufs) != self.signature.buffers or any(not isinstance(b, MI355XBuffer) or b.dev is not self.dev
                                                       for b in bufs):
             raise ValueError("MI355X buffer device/signature mismatch")
+        if 0 not in global_size and len(vals) != self.signature.scalars:
+            raise ValueError("MI355X scalar argument count mismatch")
+        return global_size, local_size
+
+    def enqueue(self, bufs, global_size, local_size, vals) -> None:
+        """Launch validated arguments on the device stream (the caller holds the device lock)."""
+        if 0 in global_size:
+            return
+        hip.launch(self.function, tuple(global_size), tuple(local_size), self._kernargs(bufs, vals), self.dev.stream)
+
+    def __call__(self, *bufs: MI355XBuffer, global_size: tuple[int, int, int] = (1, 1, 1),
+                 local_size: tuple[int, int, int] = (1, 1, 1), vals: tuple[int | float, ...] = (), wait: bool = False,
+                 timeout: int | None = None) -> float | None:
+        """Launch ``global_size`` workgroups of ``local_size`` work-items; seconds when ``wait``."""
+        global_size, local_size = self.validate(bufs, global_size, local_size, vals)
         if 0 in global_size:
             return 0.0 if wait else None
-        if len(vals) != self.signature.scalars:
-            raise ValueError("MI355X scalar argument count mismatch")
-        kernargs = self._kernargs(bufs, vals)
         with self.dev.lock:
             self.dev.check_failure()
             self.dev.select()
@@ -272,7 +282,7 @@ class MI355XProgram:
             try:
                 if wait:
                     hip.call("hipEventRecord", start, self.dev.stream)
-                hip.launch(self.function, global_size, local_size, kernargs, self.dev.stream)
+                self.enqueue(bufs, global_size, local_size, vals)
                 if wait:
                     hip.call("hipEventRecord", stop, self.dev.stream)
                 self.dev.submitted(tuple(b.owner for b in bufs))

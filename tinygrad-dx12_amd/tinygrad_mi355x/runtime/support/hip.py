@@ -58,7 +58,15 @@ _SIGNATURES = {
     "hipModuleUnload": (_P,),
     "hipModuleGetFunction": (ctypes.POINTER(_P), _P, ctypes.c_char_p),
     "hipModuleLaunchKernel": (_P, _U32, _U32, _U32, _U32, _U32, _U32, _U32, _P, _P, _P),
+    "hipStreamBeginCapture": (_P, _INT),
+    "hipStreamEndCapture": (_P, ctypes.POINTER(_P)),
+    "hipGraphInstantiate": (ctypes.POINTER(_P), _P, _P, ctypes.c_char_p, _SZ),
+    "hipGraphLaunch": (_P, _P),
+    "hipGraphExecDestroy": (_P,),
+    "hipGraphDestroy": (_P,),
 }
+# hipStreamCaptureMode: only this thread's HIP calls are checked against the capture
+CAPTURE_THREAD_LOCAL = 1
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -199,3 +207,25 @@ def launch(function: int, grid: tuple[int, int, int], block: tuple[int, int, int
     extra = (ctypes.c_void_p * 5)(_PARAM_BUFFER_POINTER, ctypes.cast(args, ctypes.c_void_p).value,
                                   _PARAM_BUFFER_SIZE, ctypes.cast(ctypes.byref(size), ctypes.c_void_p).value, _PARAM_END)
     call("hipModuleLaunchKernel", function, *grid, *block, shared, stream, None, extra)
+
+
+def capture_begin(stream: int) -> None:
+    """Start recording the work issued to ``stream`` (hipStreamBeginCapture, thread-local mode)."""
+    call("hipStreamBeginCapture", stream, CAPTURE_THREAD_LOCAL)
+
+
+def capture_end(stream: int) -> int:
+    """Stop recording; returns the captured hipGraph_t."""
+    g = ctypes.c_void_p()
+    call("hipStreamEndCapture", stream, ctypes.byref(g))
+    return g.value or 0
+
+
+def graph_instantiate(graph: int) -> int:
+    """hipGraphInstantiate; returns the executable graph."""
+    e = ctypes.c_void_p()
+    log = ctypes.create_string_buffer(512)
+    status = library().hipGraphInstantiate(ctypes.byref(e), graph, None, log, 512)
+    if status != 0:
+        raise RuntimeError(f"hipGraphInstantiate failed: {status} ({error_string(status)}) {log.value.decode(errors='replace')}")
+    return e.value or 0
