@@ -35,7 +35,7 @@ N_COPIES = 18
 
 
 EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_cfg1", "int4_gemv_n14336", "fp6_e3m2_gemm_cfg3", "fp6_e2m3_gemm_cfg3", "fp4_gemm_8192",
-          "fp4_gemm_4096x14336x4096")
+          "fp4_gemm_4096x14336x4096", "decoder_cfg5_b1", "decoder_cfg5_b8")
 
 
 def parse() -> argparse.Namespace:
@@ -209,6 +209,52 @@ def fp6_gemm_workload(torch, K, dev, fmt: str, steps: int, warmup: int, m: int =
             "bf16_mfma_frac": tflops / BF16_PEAK_TFLOPS, "bytes": nbytes, "GB/s": nbytes / ms / 1e6}
 
 
+def decoder_workload(torch, dev, batch: int, prompt: int = 512, new_tokens: int = 128):
+    """Config-5 decoder (8 layers, hidden 4096, 32 / 8 heads x 128, SwiGLU 14336, vocab 32000;
+    INT4 g128 attention, FP4 + E8M0 FFN, bf16 head): a 512-token prefill, then greedy decode of
+    128 tokens, the decode steps replayed as a HIP graph and timed with HIP events on the
+    graph's stream.  Random-init weights and prompts."""
+    from tinygrad_mi355x.decoder import Decoder, DecoderConfig, random_weights
+
+    cfg = DecoderConfig()
+    w = random_weights(cfg, dev, seed=0)
+    dec = Decoder(w, cfg, batch, prompt + new_tokens, prompt)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    prompts = torch.randint(0, cfg.vocab, (batch, prompt), device=dev, generator=g)
+    cur = torch.cuda.current_stream(dev)
+    dec.history = torch.zeros((batch, new_tokens), dtype=torch.int32, device=dev)
+    dec.prefill(prompts)  # warm-up
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(cur)
+    dec.prefill(prompts)
+    e1.record(cur)
+    torch.cuda.synchronize()
+    prefill_ms = e0.elapsed_time(e1)
+    dec.step()  # first decode step eagerly (kernel set-up), then the graph
+    graph = dec.capture()
+    s = dec.graph_stream
+    s.wait_stream(cur)
+    steps = new_tokens - 2
+    e0.record(s)
+    for _ in range(steps):
+        graph.launch()
+    e1.record(s)
+    torch.cuda.synchronize()
+    step_ms = e0.elapsed_time(e1) / steps
+    mean_ctx = prompt + 1 + (steps + 1) / 2
+    kv_bytes = int(cfg.layers * batch * cfg.kv_heads * mean_ctx * cfg.head_dim * 2 * 2)
+    step_bytes = cfg.weight_bytes_per_token() + kv_bytes
+    return {"workload": f"config-5 decoder batch {batch}: {prompt}-token prefill + greedy decode of {new_tokens} tokens "
+                        "(decode steps replayed as a HIP graph)",
+            "decode_ms_per_step": step_ms, "tokens_per_s": batch / step_ms * 1e3,
+            "bytes_per_step": step_bytes, "GB/s": step_bytes / step_ms / 1e6,
+            "hbm_frac": step_bytes / step_ms / 1e6 / HBM_PEAK_GBS,
+            "prefill_ms": prefill_ms, "prefill_tokens_per_s": batch * prompt / prefill_ms * 1e3,
+            "final_pos": int(dec.pos[0])}
+
+
 def cpu_baseline(budget_s: float) -> dict:
     """The reference CPU path restated in C (oracle/cpu_path.c), timed on the host cores."""
     import numpy as np
@@ -281,6 +327,8 @@ def main() -> int:
         "fp6_e2m3_gemm_cfg3": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e2m3", 20, 20),
         "fp4_gemm_8192": lambda: fp4_gemm_workload(torch, K, dev, 8192, 8192, 8192, 20, 20),
         "fp4_gemm_4096x14336x4096": lambda: fp4_gemm_workload(torch, K, dev, 4096, 14336, 4096, 20, 20),
+        "decoder_cfg5_b1": lambda: decoder_workload(torch, dev, 1),
+        "decoder_cfg5_b8": lambda: decoder_workload(torch, dev, 8),
     }
     if args.only:
         print(json.dumps({args.only: extras[args.only]()}))

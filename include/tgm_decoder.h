@@ -34,13 +34,15 @@
 extern "C" {
 #endif
 
-/* h[r, :] = float(table[tokens[r], :]); table is BF16 [vocab, d].  Tokens outside
- * [0, vocab) read row 0 (the host validates prompts; generated tokens are in range). */
+/* h[r, :] = float(table[tokens[r], :]); table is BF16 [vocab, d] with d a multiple of 8, table
+ * and h 16-byte aligned.  Tokens outside [0, vocab) read row 0 (the host validates prompts;
+ * generated tokens are in range). */
 int tgm_dec_embed(const void* table, int64_t vocab, int64_t d, const int32_t* tokens, int64_t rows, float* h,
                   void* stream);
 
 /* h[r] += delta[r] (delta may be NULL); out[r, i] = h[r, i] / sqrt(mean_i(h[r, i]^2) + eps) * weight[i],
- * computed in fp32 and rounded once to out_dtype (F16, BF16 or F32).  weight is BF16 [d]. */
+ * computed in fp32 and rounded once to out_dtype (F16, BF16 or F32).  weight is BF16 [d]; d is a
+ * multiple of 4 and at most 16384; h, delta and out are 16-byte and weight 8-byte aligned. */
 int tgm_dec_add_rmsnorm(float* h, const float* delta, int64_t rows, int64_t d, const void* weight, float eps,
                         void* out, int out_dtype, void* stream);
 
@@ -52,14 +54,17 @@ int tgm_dec_rope_kv(float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, i
 
 /* Causal grouped-query attention of every q head over its kv head's cache, positions
  * 0 .. pos(token) (softmax of q.k / sqrt(head_dim) in fp32).  head_dim is 64 or 128; heads /
- * kv_heads is 1, 2, 4 or 8.  ``splits`` > 1 divides each token's positions over that many
- * workgroups (split-K over the sequence, merged by a second kernel) and needs
- * ``workspace`` of at least rows * heads * splits * (head_dim + 2) floats;
- * tgm_dec_attention_workspace gives the byte count.  out is [rows, heads * head_dim]. */
+ * kv_heads is 1, 2, 4 or 8.  ``splits`` > 1 (at most 32) divides each token's positions over
+ * that many workgroups (split-K over the sequence, merged by a second kernel) and needs
+ * ``workspace`` of tgm_dec_attention_workspace() bytes.  out is [rows, heads * head_dim].
+ * rope_base > 0 (seq_rows == 1 only) also does tgm_dec_rope_kv's work for each token in the
+ * same arithmetic: q and k of qkv are read unrotated, and the token's k (rotated) and v are
+ * stored into the caches.  rope_base <= 0: qkv holds rotated q and the caches already hold
+ * every position the tokens attend to. */
 int64_t tgm_dec_attention_workspace(int64_t rows, int64_t heads, int64_t head_dim, int64_t splits);
 int tgm_dec_attention(const float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, int64_t kv_heads,
-                      int64_t head_dim, const int32_t* pos, const void* k_cache, const void* v_cache,
-                      int64_t max_seq, int64_t splits, float* workspace, int64_t workspace_bytes, void* out,
+                      int64_t head_dim, const int32_t* pos, void* k_cache, void* v_cache, int64_t max_seq,
+                      double rope_base, int64_t splits, float* workspace, int64_t workspace_bytes, void* out,
                       int out_dtype, void* stream);
 
 /* SwiGLU: out[r, i] = silu(g) * u with g = gate_up[r, i], u = gate_up[r, ffn + i] (float32

@@ -100,9 +100,11 @@ def test_attention_matches_oracle(dev, hd, H, HK, splits):
     pos = torch.tensor(p0, dtype=torch.int32, device=dev)
     out = torch.empty((B * T, H * hd), dtype=torch.float32, device=dev)
     ws_bytes = K.load_library().tgm_dec_attention_workspace(B * T, H, hd, splits)
-    ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=dev)
-    K.call("tgm_dec_attention", qkv.data_ptr(), B * T, T, H, HK, hd, pos.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-           max_seq, splits, ws.data_ptr() if splits > 1 else None, ws_bytes, out.data_ptr(), F32, stream())
+    ws = torch.zeros(max(ws_bytes // 4, 1), dtype=torch.float32, device=dev)
+    for _ in range(2):  # the second call reuses the workspace
+        out.fill_(float("nan"))
+        K.call("tgm_dec_attention", qkv.data_ptr(), B * T, T, H, HK, hd, pos.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+               max_seq, 0.0, splits, ws.data_ptr() if splits > 1 else None, ws_bytes, out.data_ptr(), F32, stream())
     q = np64(qkv).reshape(B, T, H + 2 * HK, hd)[:, :, :H]
     got = np64(out).reshape(B, T, H, hd)
     for b in range(B):
@@ -110,6 +112,35 @@ def test_attention_matches_oracle(dev, hd, H, HK, splits):
         ref = D.attention(q[b].transpose(1, 0, 2), np64(kc[b]), np64(vc[b]), positions).transpose(1, 0, 2)
         err = O.max_rel_err(got[b], ref)  # fp32 scores, exp and sums over up to 300 positions
         assert err <= 1e-3, err
+
+
+@pytest.mark.parametrize("hd,H,HK,max_seq", [(128, 32, 8, 320), (64, 16, 2, 2000), (128, 8, 8, 1100), (64, 4, 4, 300)])
+@pytest.mark.parametrize("splits", [1, 5])
+def test_attention_fused_rope_equals_separate_kernels(dev, hd, H, HK, max_seq, splits):
+    """One token per sequence: attention with the fused RoPE + cache store gives the same output
+    and cache entries, bit for bit, as tgm_dec_rope_kv followed by attention."""
+    rng = np.random.default_rng(splits + hd + max_seq)
+    B = 3
+    width = (H + 2 * HK) * hd
+    qkv = torch.from_numpy(rng.standard_normal((B, width)).astype(np.float32)).to(dev)
+    kc = torch.from_numpy(rng.standard_normal((B, HK, max_seq, hd)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    vc = torch.from_numpy(rng.standard_normal((B, HK, max_seq, hd)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    pos = torch.tensor([0, 63, max_seq - 1], dtype=torch.int32, device=dev)  # first, chunk-last and last positions
+    ws_bytes = K.load_library().tgm_dec_attention_workspace(B, H, hd, splits)
+    ws = torch.zeros(max(ws_bytes // 4, 1), dtype=torch.float32, device=dev)
+    wsp = ws.data_ptr() if splits > 1 else None
+    outs = []
+    for fused in (False, True):
+        q, k, v = qkv.clone(), kc.clone(), vc.clone()
+        out = torch.empty((B, H * hd), dtype=torch.float16, device=dev)
+        if not fused:
+            K.call("tgm_dec_rope_kv", q.data_ptr(), B, 1, H, HK, hd, pos.data_ptr(), 10000.0, k.data_ptr(), v.data_ptr(),
+                   max_seq, stream())
+        K.call("tgm_dec_attention", q.data_ptr(), B, 1, H, HK, hd, pos.data_ptr(), k.data_ptr(), v.data_ptr(), max_seq,
+               10000.0 if fused else 0.0, splits, wsp, ws_bytes, out.data_ptr(), F16, stream())
+        outs.append((out, k, v))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1]) and torch.equal(outs[0][2], outs[1][2])
 
 
 def test_silu_mul(dev):

@@ -17,6 +17,7 @@ namespace tgm {
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 dec_bf16x2;
 typedef unsigned dec_u32x4 __attribute__((ext_vector_type(4)));
+typedef float dec_f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -32,56 +33,116 @@ __device__ __forceinline__ float lo_bf16(unsigned w) { return __builtin_bit_cast
 __device__ __forceinline__ float hi_bf16(unsigned w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
 
 // ------------------------------------------------------------------ embedding
-__global__ void __launch_bounds__(256) dec_embed(const uint16_t* __restrict__ table, int64_t vocab, int d,
+// 16 bytes (8 bf16) of the table row per thread and pass, written as two float4.
+__global__ void __launch_bounds__(512) dec_embed(const uint16_t* __restrict__ table, int64_t vocab, int d,
                                                  const int32_t* __restrict__ tokens, float* __restrict__ h) {
   const int64_t r = blockIdx.x;
   int64_t tok = tokens[r];
   if (tok < 0 || tok >= vocab) tok = 0;
   const uint16_t* src = table + tok * d;
   float* dst = h + r * d;
-  for (int i = threadIdx.x; i < d; i += 256) dst[i] = bf16_to_f32(src[i]);
+  for (int c = threadIdx.x; c < d / 8; c += 512) {
+    const dec_u32x4 v = *(const dec_u32x4*)(src + 8 * c);
+    *(dec_f32x4*)(dst + 8 * c) = dec_f32x4{lo_bf16(v[0]), hi_bf16(v[0]), lo_bf16(v[1]), hi_bf16(v[1])};
+    *(dec_f32x4*)(dst + 8 * c + 4) = dec_f32x4{lo_bf16(v[2]), hi_bf16(v[2]), lo_bf16(v[3]), hi_bf16(v[3])};
+  }
 }
 
 // ------------------------------------------------------------------ residual add + RMSNorm
-// One workgroup per row; the row's sum of squares is reduced over four waves.
-__global__ void __launch_bounds__(256) dec_add_rmsnorm(float* __restrict__ h, const float* __restrict__ delta, int d,
-                                                       const uint16_t* __restrict__ w, float eps, void* __restrict__ out,
-                                                       int odt) {
+// One workgroup of 1024 threads per row.  A row of up to 16384 floats stays in registers (four
+// float4 per thread) between the sum of squares and the scaled store, so every element is
+// loaded once; the loads of a thread are independent and issued together.
+constexpr int kNormThreads = 1024, kNormMaxD = 4 * 4 * kNormThreads;
+
+__device__ __forceinline__ void store4(void* out, int odt, int64_t i, dec_f32x4 y) {
+  if (odt == TGM_F32) {
+    *(dec_f32x4*)((float*)out + i) = y;
+  } else if (odt == TGM_BF16) {
+    *(uint2*)((uint16_t*)out + i) = uint2{f32_to_bf16(y[0]) | ((unsigned)f32_to_bf16(y[1]) << 16),
+                                          f32_to_bf16(y[2]) | ((unsigned)f32_to_bf16(y[3]) << 16)};
+  } else {
+    *(uint2*)((uint16_t*)out + i) =
+        uint2{__builtin_bit_cast(unsigned short, (_Float16)y[0]) | ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)y[1]) << 16),
+              __builtin_bit_cast(unsigned short, (_Float16)y[2]) | ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)y[3]) << 16)};
+  }
+}
+
+__global__ void __launch_bounds__(kNormThreads) dec_add_rmsnorm(float* __restrict__ h, const float* __restrict__ delta,
+                                                                int d, const uint16_t* __restrict__ w, float eps,
+                                                                void* __restrict__ out, int odt) {
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float* hr = h + r * d;
+  const int d4 = d >> 2;
+  dec_f32x4* hr = (dec_f32x4*)(h + r * d);
+  const dec_f32x4* dr = delta ? (const dec_f32x4*)(delta + r * d) : nullptr;
+  dec_f32x4 v[4];
   float ss = 0.f;
-  for (int i = tid; i < d; i += 256) {
-    float v = hr[i];
-    if (delta) {
-      v += delta[r * d + i];
-      hr[i] = v;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int i = tid + q * kNormThreads;
+    if (i < d4) {
+      dec_f32x4 x = hr[i];
+      if (dr) {
+        const dec_f32x4 y = dr[i];
+        x = dec_f32x4{x[0] + y[0], x[1] + y[1], x[2] + y[2], x[3] + y[3]};
+        hr[i] = x;
+      }
+      v[q] = x;
+      ss += x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
     }
-    ss += v * v;
   }
-  __shared__ float part[4];
+  __shared__ float part[kNormThreads / 64];
   ss = wave_sum(ss);
   if (lane == 0) part[wave] = ss;
   __syncthreads();
-  const float inv = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / (float)d + eps);
-  for (int i = tid; i < d; i += 256) store_from_f32(out, odt, r * d + i, hr[i] * inv * bf16_to_f32(w[i]));
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) tot += part[i];
+  const float inv = 1.0f / sqrtf(tot / (float)d + eps);
+  const uint2* w4 = (const uint2*)w;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int i = tid + q * kNormThreads;
+    if (i < d4) {
+      const uint2 ww = w4[i];
+      const dec_f32x4 x = v[q];
+      store4(out, odt, r * d + 4 * i,
+             dec_f32x4{x[0] * inv * lo_bf16(ww.x), x[1] * inv * hi_bf16(ww.x), x[2] * inv * lo_bf16(ww.y),
+                       x[3] * inv * hi_bf16(ww.y)});
+    }
+  }
 }
 
 // ------------------------------------------------------------------ RoPE + KV store
+// Rotate the pair (x1, x2) = (x[i], x[i + hd / 2]) of one head at position p: rotate-half RoPE
+// with angle p * base^(-2 i / hd).  The frequency exp2(-(2 i / hd) log2(base)) and the angle
+// are formed in double and reduced to [-pi, pi] by a two-term Cody-Waite subtraction of 2 pi,
+// so that the float sine and cosine need no large-argument reduction.
+__device__ __forceinline__ void rope_pair(float x1, float x2, int p, int i, int hd, double log2_base, float& y1,
+                                          float& y2) {
+  constexpr double kTwoPiHi = 6.28318530717958623200e+00;  // 2 pi rounded to double
+  constexpr double kTwoPiLo = 2.44929359829470641e-16;     // 2 pi - kTwoPiHi
+  const double a = (double)p * exp2(-(2.0 * i / hd) * log2_base);
+  const double n = rint(a * (1.0 / kTwoPiHi));
+  const float r = (float)fma(-n, kTwoPiLo, fma(-n, kTwoPiHi, a));
+  float sn, cs;
+  sincosf(r, &sn, &cs);
+  y1 = x1 * cs - x2 * sn;
+  y2 = x2 * cs + x1 * sn;
+}
+
 // Grid (rows, heads + kv_heads), head_dim / 2 threads: thread i rotates the pair
 // (i, i + head_dim / 2) of one q or k head; k heads also store k (rotated) and v as bf16.
 __global__ void dec_rope_kv(float* __restrict__ qkv, int T, int H, int HK, int hd, const int32_t* __restrict__ pos,
-                            double base, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int max_seq) {
+                            double log2_base, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int max_seq) {
   const int64_t r = blockIdx.x;
   const int hh = blockIdx.y, i = threadIdx.x, half = hd / 2;
   const int b = (int)(r / T), t = (int)(r % T);
   const int p = pos[b] + t;
   const int64_t ld = (int64_t)(H + 2 * HK) * hd;
   float* x = qkv + r * ld + (int64_t)hh * hd;
-  double s, c;
-  sincos((double)p * pow(base, -2.0 * i / hd), &s, &c);
-  const double x1 = x[i], x2 = x[i + half];
-  const float y1 = (float)(x1 * c - x2 * s), y2 = (float)(x2 * c + x1 * s);
+  float y1, y2;
+  rope_pair(x[i], x[i + half], p, i, hd, log2_base, y1, y2);
   x[i] = y1;
   x[i + half] = y2;
   if (hh >= H && p >= 0 && p < max_seq) {
@@ -96,6 +157,8 @@ __global__ void dec_rope_kv(float* __restrict__ qkv, int T, int H, int HK, int h
 }
 
 // ------------------------------------------------------------------ attention
+constexpr int kMaxSplits = 32;
+
 // Grid (rows, kv_heads, splits), 256 threads.  A workgroup takes the G = heads / kv_heads q
 // heads that share kv head j, and the chunks of 64 cache positions [z * cps * 64, +cps * 64)
 // of its split, clipped to the token's causal length.  Per chunk:
@@ -108,11 +171,18 @@ __global__ void dec_rope_kv(float* __restrict__ qkv, int T, int H, int HK, int h
 // One split writes the normalised output; several write (o, m, l) partials per (row, head,
 // split) that dec_attention_merge combines.  Loads use positions clamped into the valid range
 // (their probabilities are zero), so every load in a chunk is unconditional.
+//
+// With ``base`` > 0 (one token per sequence) the kernel also does tgm_dec_rope_kv's work for
+// its token in the same arithmetic: q is rotated as it is staged, and the workgroup whose split
+// holds the token's own position rotates k, stores k and v into the cache and uses those bf16
+// values for that position from LDS.
 template <int G, int HD>
 __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ qkv, int T, int H, int HK,
-                                                     const int32_t* __restrict__ pos, const uint16_t* __restrict__ kc,
-                                                     const uint16_t* __restrict__ vc, int max_seq, int cps, float scale,
-                                                     float* __restrict__ part, void* __restrict__ out, int odt) {
+                                                     const int32_t* __restrict__ pos, uint16_t* __restrict__ kc,
+                                                     uint16_t* __restrict__ vc, int max_seq, int cps, float scale,
+                                                     int own, double log2_base, float* __restrict__ part,
+                                                     void* __restrict__ out,
+                                                     int odt) {
   constexpr int CH = 64, NP = HD / 2, QD = HD / 4;
   const int r = blockIdx.x, j = blockIdx.y, z = blockIdx.z, S = gridDim.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -126,7 +196,39 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
   __shared__ float sc[G][CH];
   __shared__ float m_sh[G], l_sh[G], a_sh[G];
   __shared__ float red[4][G][HD];
-  for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = qkv[(int64_t)r * ld + (int64_t)j * G * HD + i] * scale;
+  const int64_t kvbase = ((int64_t)b * HK + j) * max_seq;
+  // own: rotate q, k and store this token's k, v
+  const bool mine = own && p >= c_begin && p < c_end;   // this split holds the token's position
+  __shared__ float kp[HD], vp[HD];
+  const float* qrow = qkv + (int64_t)r * ld + (int64_t)j * G * HD;
+  if (own) {
+    for (int i = tid; i < G * NP; i += 256) {
+      const int g = i / NP, e = i % NP;
+      float y1, y2;
+      rope_pair(qrow[g * HD + e], qrow[g * HD + e + NP], p, e, HD, log2_base, y1, y2);
+      qs[g][e] = y1 * scale;
+      qs[g][e + NP] = y2 * scale;
+    }
+    if (mine && tid < NP) {
+      const float* kx = qkv + (int64_t)r * ld + (int64_t)(H + j) * HD;
+      const float* vx = qkv + (int64_t)r * ld + (int64_t)(H + HK + j) * HD;
+      float y1, y2;
+      rope_pair(kx[tid], kx[tid + NP], p, tid, HD, log2_base, y1, y2);
+      const uint16_t k1 = f32_to_bf16(y1), k2 = f32_to_bf16(y2);
+      const uint16_t v1 = f32_to_bf16(vx[tid]), v2 = f32_to_bf16(vx[tid + NP]);
+      const int64_t o = (kvbase + p) * HD;
+      kc[o + tid] = k1;
+      kc[o + tid + NP] = k2;
+      vc[o + tid] = v1;
+      vc[o + tid + NP] = v2;
+      kp[tid] = bf16_to_f32(k1);
+      kp[tid + NP] = bf16_to_f32(k2);
+      vp[tid] = bf16_to_f32(v1);
+      vp[tid + NP] = bf16_to_f32(v2);
+    }
+  } else {
+    for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = qrow[i] * scale;
+  }
   if (tid < G) {
     m_sh[tid] = -INFINITY;
     l_sh[tid] = 0.f;
@@ -134,7 +236,6 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
   float oa[G][2];
 #pragma unroll
   for (int g = 0; g < G; ++g) oa[g][0] = oa[g][1] = 0.f;
-  const int64_t kvbase = ((int64_t)b * HK + j) * max_seq;
   __syncthreads();
   for (int c0 = c_begin; c0 < c_end; c0 += CH) {
     const int last = c_end - 1;
@@ -150,7 +251,11 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
         const dec_u32x4 kv = *(const dec_u32x4*)(kr + e);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const float k0 = lo_bf16(kv[q]), k1 = hi_bf16(kv[q]);
+          float k0 = lo_bf16(kv[q]), k1 = hi_bf16(kv[q]);
+          if (mine && tt == p) {
+            k0 = kp[qd * QD + e + 2 * q];
+            k1 = kp[qd * QD + e + 2 * q + 1];
+          }
 #pragma unroll
           for (int g = 0; g < G; ++g) s[g] += qs[g][qd * QD + e + 2 * q] * k0 + qs[g][qd * QD + e + 2 * q + 1] * k1;
         }
@@ -191,7 +296,11 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
       for (int i = 0; i < CH / 4; ++i) {
         const int pi = wave + 4 * i, tt = c0 + pi;
         const unsigned vv = *(const unsigned*)(vc + (kvbase + (tt < last ? tt : last)) * HD + 2 * lane);
-        const float v0 = lo_bf16(vv), v1 = hi_bf16(vv);
+        float v0 = lo_bf16(vv), v1 = hi_bf16(vv);
+        if (mine && tt == p) {
+          v0 = vp[2 * lane];
+          v1 = vp[2 * lane + 1];
+        }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           const float pg = sc[g][pi];
@@ -226,22 +335,41 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
   }
 }
 
-// Grid (rows, heads), head_dim threads: combine the splits' (o, m, l) partials.
+// Grid (rows, heads), head_dim threads: combine the splits' (o, m, l) partials.  The (m, l) of
+// every split go to LDS and become merge weights exp(m_s - M); each thread issues the loads of
+// its S partial sums at once.  (The kernel boundary publishes the partials; merging in the last
+// attention workgroup instead needs agent-scope fences, which on gfx950 write back and
+// invalidate the per-XCD L2 and cost more than this launch.)
 template <int HD>
-__global__ void dec_attention_merge(const float* __restrict__ part, int S, int H, void* __restrict__ out, int odt) {
+__global__ void __launch_bounds__(HD) dec_attention_merge(const float* __restrict__ part, int S, int H,
+                                                          void* __restrict__ out, int odt) {
   const int r = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
   const float* pp = part + ((int64_t)r * H + h) * S * (HD + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, pp[s * (HD + 2) + HD]);
-  float L = 0.f, o = 0.f;
-  for (int s = 0; s < S; ++s) {
-    const float m = pp[s * (HD + 2) + HD];
-    if (m == -INFINITY) continue;
-    const float w = expf(m - M);
-    L += pp[s * (HD + 2) + HD + 1] * w;
-    o += pp[s * (HD + 2) + d] * w;
+  __shared__ float mw[kMaxSplits], lw[kMaxSplits], inv_l;
+  if (d < kMaxSplits) {
+    mw[d] = d < S ? pp[d * (HD + 2) + HD] : -INFINITY;
+    lw[d] = d < S ? pp[d * (HD + 2) + HD + 1] : 0.f;
   }
-  store_from_f32(out, odt, (int64_t)r * H * HD + (int64_t)h * HD + d, L > 0.f ? o / L : 0.f);
+  float ov[kMaxSplits];
+#pragma unroll
+  for (int s2 = 0; s2 < kMaxSplits; ++s2) ov[s2] = s2 < S ? pp[s2 * (HD + 2) + d] : 0.f;
+  __syncthreads();
+  if (d == 0) {
+    float M = -INFINITY;
+    for (int s2 = 0; s2 < kMaxSplits; ++s2) M = fmaxf(M, mw[s2]);
+    float L = 0.f;
+    for (int s2 = 0; s2 < kMaxSplits; ++s2) {
+      const float wgt = mw[s2] == -INFINITY ? 0.f : expf(mw[s2] - M);
+      mw[s2] = wgt;
+      L += lw[s2] * wgt;
+    }
+    inv_l = L > 0.f ? 1.0f / L : 0.f;
+  }
+  __syncthreads();
+  float o = 0.f;
+#pragma unroll
+  for (int s2 = 0; s2 < kMaxSplits; ++s2) o += mw[s2] * ov[s2];
+  store_from_f32(out, odt, (int64_t)r * H * HD + (int64_t)h * HD + d, o * inv_l);
 }
 
 // ------------------------------------------------------------------ SwiGLU
@@ -304,7 +432,21 @@ __global__ void __launch_bounds__(1024) dec_argmax(const float* __restrict__ log
   const float* row = logits + r * ld;
   float best = -INFINITY;
   int bi = n;  // none yet (NaN and -inf never win)
-  for (int i = tid; i < n; i += 1024) {
+  // float4 loads where the row is 16-byte aligned; a thread visits its indices in increasing
+  // order, so the strict comparison keeps its first maximum
+  const int n4 = ((uintptr_t)row & 15) == 0 ? n / 4 : 0;
+  const dec_f32x4* row4 = (const dec_f32x4*)row;
+#pragma unroll 4
+  for (int i = tid; i < n4; i += 1024) {
+    const dec_f32x4 v = row4[i];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (v[c] > best) {
+        best = v[c];
+        bi = 4 * i + c;
+      }
+  }
+  for (int i = 4 * n4 + tid; i < n; i += 1024) {
     const float v = row[i];
     if (v > best) {
       best = v;
@@ -356,8 +498,10 @@ extern "C" int tgm_dec_embed(const void* table, int64_t vocab, int64_t d, const 
   clear_error();
   TGM_CHECK_ARG(table && tokens && h, "null operand");
   TGM_CHECK_ARG(vocab > 0 && d > 0 && rows >= 0 && d < (1ll << 31) && rows < (1ll << 31), "invalid embedding sizes");
+  if (d % 8 || (uintptr_t)table % 16 || (uintptr_t)h % 16)
+    TGM_UNSUPPORTED("tgm_dec_embed: d must be a multiple of 8 and the table and h 16-byte aligned");
   if (rows == 0) return TGM_OK;
-  hipLaunchKernelGGL(dec_embed, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)table, vocab,
+  hipLaunchKernelGGL(dec_embed, dim3((unsigned)rows), dim3(512), 0, (hipStream_t)stream, (const uint16_t*)table, vocab,
                      (int)d, tokens, h);
   return launch_status("tgm_dec_embed");
 }
@@ -369,8 +513,11 @@ extern "C" int tgm_dec_add_rmsnorm(float* h, const float* delta, int64_t rows, i
   TGM_CHECK_ARG(rows >= 0 && d > 0 && d < (1ll << 31) && rows < (1ll << 31), "invalid norm sizes");
   TGM_CHECK_ARG(out_dtype_ok(out_dtype), "output must be f16, bf16 or f32");
   TGM_CHECK_ARG(eps >= 0.f, "eps must be non-negative");
+  if (d % 4 || d > kNormMaxD || (uintptr_t)h % 16 || (uintptr_t)out % 16 || (delta && (uintptr_t)delta % 16) ||
+      (uintptr_t)weight % 8)
+    TGM_UNSUPPORTED("tgm_dec_add_rmsnorm: d must be a multiple of 4 and at most %d, rows 16-byte aligned", kNormMaxD);
   if (rows == 0) return TGM_OK;
-  hipLaunchKernelGGL(dec_add_rmsnorm, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, h, delta, (int)d,
+  hipLaunchKernelGGL(dec_add_rmsnorm, dim3((unsigned)rows), dim3(kNormThreads), 0, (hipStream_t)stream, h, delta, (int)d,
                      (const uint16_t*)weight, eps, out, out_dtype);
   return launch_status("tgm_dec_add_rmsnorm");
 }
@@ -387,7 +534,7 @@ extern "C" int tgm_dec_rope_kv(float* qkv, int64_t rows, int64_t seq_rows, int64
   TGM_CHECK_ARG(rope_base > 0.0, "rope base must be positive");
   if (rows == 0) return TGM_OK;
   hipLaunchKernelGGL(dec_rope_kv, dim3((unsigned)rows, (unsigned)(heads + kv_heads)), dim3((unsigned)(head_dim / 2)), 0,
-                     (hipStream_t)stream, qkv, (int)seq_rows, (int)heads, (int)kv_heads, (int)head_dim, pos, rope_base,
+                     (hipStream_t)stream, qkv, (int)seq_rows, (int)heads, (int)kv_heads, (int)head_dim, pos, log2(rope_base),
                      (uint16_t*)k_cache, (uint16_t*)v_cache, (int)max_seq);
   return launch_status("tgm_dec_rope_kv");
 }
@@ -398,16 +545,16 @@ extern "C" int64_t tgm_dec_attention_workspace(int64_t rows, int64_t heads, int6
 
 template <int G, int HD>
 static void launch_attention(dim3 grid, hipStream_t st, const float* qkv, int T, int H, int HK, const int32_t* pos,
-                             const void* kc, const void* vc, int max_seq, int cps, float scale, float* part, void* out,
-                             int odt) {
-  hipLaunchKernelGGL((dec_attention<G, HD>), grid, dim3(256), 0, st, qkv, T, H, HK, pos, (const uint16_t*)kc,
-                     (const uint16_t*)vc, max_seq, cps, scale, part, out, odt);
+                             void* kc, void* vc, int max_seq, int cps, float scale, int own, double log2_base,
+                             float* part, void* out, int odt) {
+  hipLaunchKernelGGL((dec_attention<G, HD>), grid, dim3(256), 0, st, qkv, T, H, HK, pos, (uint16_t*)kc, (uint16_t*)vc,
+                     max_seq, cps, scale, own, log2_base, part, out, odt);
 }
 
 extern "C" int tgm_dec_attention(const float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, int64_t kv_heads,
-                                 int64_t head_dim, const int32_t* pos, const void* k_cache, const void* v_cache,
-                                 int64_t max_seq, int64_t splits, float* workspace, int64_t workspace_bytes, void* out,
-                                 int out_dtype, void* stream) {
+                                 int64_t head_dim, const int32_t* pos, void* k_cache, void* v_cache, int64_t max_seq,
+                                 double rope_base, int64_t splits, float* workspace, int64_t workspace_bytes,
+                                 void* out, int out_dtype, void* stream) {
   clear_error();
   TGM_CHECK_ARG(qkv && pos && k_cache && v_cache && out, "null operand");
   TGM_CHECK_ARG(rows >= 0 && seq_rows > 0 && rows % seq_rows == 0, "rows must be a multiple of seq_rows");
@@ -415,7 +562,9 @@ extern "C" int tgm_dec_attention(const float* qkv, int64_t rows, int64_t seq_row
   TGM_CHECK_ARG(out_dtype_ok(out_dtype), "output must be f16, bf16 or f32");
   TGM_CHECK_ARG(max_seq > 0 && max_seq < (1 << 30) && rows < (1ll << 31) && kv_heads <= 65535, "invalid sizes");
   const int64_t chunks = (max_seq + 63) / 64;
-  TGM_CHECK_ARG(splits >= 1 && splits <= chunks, "splits must be in [1, ceil(max_seq / 64)]");
+  TGM_CHECK_ARG(splits >= 1 && splits <= chunks && splits <= kMaxSplits, "splits must be in [1, min(ceil(max_seq / 64), %d)]",
+                kMaxSplits);
+  TGM_CHECK_ARG(rope_base <= 0.0 || seq_rows == 1, "the fused RoPE + cache store takes one token per sequence");
   TGM_CHECK_ARG(splits == 1 || (workspace && workspace_bytes >= tgm_dec_attention_workspace(rows, heads, head_dim, splits)),
                 "split attention needs a workspace of tgm_dec_attention_workspace() bytes");
   const int64_t G = heads / kv_heads;
@@ -427,11 +576,12 @@ extern "C" int tgm_dec_attention(const float* qkv, int64_t rows, int64_t seq_row
   const dim3 grid((unsigned)rows, (unsigned)kv_heads, (unsigned)splits);
   const hipStream_t st = (hipStream_t)stream;
   float* part = splits > 1 ? workspace : nullptr;
+  const int own = rope_base > 0.0;
   const float scale = (float)(1.0 / sqrt((double)head_dim));
 #define TGM_ATT(GG, HDD)                                                                                            \
   if (G == GG && head_dim == HDD)                                                                                   \
     launch_attention<GG, HDD>(grid, st, qkv, (int)seq_rows, (int)heads, (int)kv_heads, pos, k_cache, v_cache,        \
-                              (int)max_seq, cps, scale, part, out, out_dtype);
+                              (int)max_seq, cps, scale, own, own ? log2(rope_base) : 0.0, part, out, out_dtype);
   TGM_ATT(1, 64) TGM_ATT(2, 64) TGM_ATT(4, 64) TGM_ATT(8, 64)
   TGM_ATT(1, 128) TGM_ATT(2, 128) TGM_ATT(4, 128) TGM_ATT(8, 128)
 #undef TGM_ATT

@@ -155,14 +155,17 @@ class Decoder:
         cache = (cfg.layers, batch, cfg.kv_heads, max_seq, cfg.head_dim)
         self.k_cache = torch.zeros(cache, dtype=torch.bfloat16, device=dev)
         self.v_cache = torch.zeros(cache, dtype=torch.bfloat16, device=dev)
-        self.splits = max(1, math.ceil(max_seq / 64))
+        self.splits = min(max(1, math.ceil(max_seq / 64)), 32)
+        self.fuse_rope = True
         ws = K.load_library().tgm_dec_attention_workspace(batch, cfg.heads, cfg.head_dim, self.splits)
         self.workspace = torch.empty(max(ws // 4, 1), **f32)
         self.workspace_bytes = ws
         self.tokens = torch.zeros(rows, dtype=torch.int32, device=dev)
         self.pos = torch.zeros(batch, dtype=torch.int32, device=dev)
         self.history: torch.Tensor | None = None
+        self.prompt_len = 0
         self._graph: StreamGraph | None = None
+        self.graph_stream: torch.cuda.Stream | None = None
 
     # ---------------------------------------------------------------- building blocks
     def _layers(self, rows: int, seq_rows: int, splits: int, stream: int) -> None:
@@ -173,12 +176,14 @@ class Decoder:
                    L.attn_norm.data_ptr(), cfg.eps, self.xn16.data_ptr(), F16, stream)
             _packed_product(self.xn16, rows, d, L.wqkv, self.qkv, cfg.qkv_rows, stream)
             kc, vc = self.k_cache[li], self.v_cache[li]
-            K.call("tgm_dec_rope_kv", self.qkv.data_ptr(), rows, seq_rows, cfg.heads, cfg.kv_heads, cfg.head_dim,
-                   self.pos.data_ptr(), cfg.rope_base, kc.data_ptr(), vc.data_ptr(), self.max_seq, stream)
+            fused = seq_rows == 1 and self.fuse_rope  # one new token per sequence: RoPE + cache store in attention
+            if not fused:
+                K.call("tgm_dec_rope_kv", self.qkv.data_ptr(), rows, seq_rows, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                       self.pos.data_ptr(), cfg.rope_base, kc.data_ptr(), vc.data_ptr(), self.max_seq, stream)
             K.call("tgm_dec_attention", self.qkv.data_ptr(), rows, seq_rows, cfg.heads, cfg.kv_heads, cfg.head_dim,
-                   self.pos.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.max_seq, splits,
-                   self.workspace.data_ptr() if splits > 1 else None, self.workspace_bytes if splits > 1 else 0,
-                   self.attn.data_ptr(), F16, stream)
+                   self.pos.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.max_seq, cfg.rope_base if fused else 0.0,
+                   splits, self.workspace.data_ptr() if splits > 1 else None,
+                   self.workspace_bytes if splits > 1 else 0, self.attn.data_ptr(), F16, stream)
             _packed_product(self.attn, rows, cfg.heads * cfg.head_dim, L.wo, self.delta, d, stream)
             K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr(), rows, d, L.ffn_norm.data_ptr(),
                    cfg.eps, self.xnb.data_ptr(), BF16, stream)
@@ -239,7 +244,7 @@ class Decoder:
             stream.wait_stream(torch.cuda.current_stream(self.device))
             with torch.cuda.stream(stream):
                 self._graph = StreamGraph(self._decode_step, stream.cuda_stream)
-            self._graph_stream = stream
+            self.graph_stream = stream
         return self._graph
 
     def generate(self, prompts: torch.Tensor, new_tokens: int, graph: bool = True) -> torch.Tensor:
@@ -259,10 +264,10 @@ class Decoder:
         if graph and remaining > 0:
             g = self.capture()
             cur = torch.cuda.current_stream(self.device)
-            self._graph_stream.wait_stream(cur)
+            self.graph_stream.wait_stream(cur)
             for _ in range(remaining):
                 g.launch()
-            cur.wait_stream(self._graph_stream)
+            cur.wait_stream(self.graph_stream)
         else:
             for _ in range(max(remaining, 0)):
                 self._decode_step()

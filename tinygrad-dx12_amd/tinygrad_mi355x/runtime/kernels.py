@@ -50,7 +50,8 @@ _SIGNATURES = {
     "tgm_dec_embed": (_P, _I64, _I64, _P, _I64, _P, _P),
     "tgm_dec_add_rmsnorm": (_P, _P, _I64, _I64, _P, ctypes.c_float, _P, _INT, _P),
     "tgm_dec_rope_kv": (_P, _I64, _I64, _I64, _I64, _I64, _P, ctypes.c_double, _P, _P, _I64, _P),
-    "tgm_dec_attention": (_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _P, _I64, _P, _INT, _P),
+    "tgm_dec_attention": (_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, ctypes.c_double, _I64, _P, _I64, _P, _INT,
+                          _P),
     "tgm_dec_silu_mul": (_P, _I64, _I64, _P, _INT, _P),
     "tgm_dec_gemv_bf16": (_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P),
     "tgm_dec_argmax": (_P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _P),
