@@ -280,7 +280,7 @@ def test_gemv_int4_north_star_shape(dev):
 
 
 @pytest.mark.parametrize("fmt", ["fp4_e2m1", "int4", "uint4"])
-@pytest.mark.parametrize("k", [2048, 4096, 8192])
+@pytest.mark.parametrize("k", [2048, 4096, 8192, 14336, 16384])
 def test_gemv_rows_one_hot_is_exact(dev, fmt, k):
     """M = 1 row-streaming kernels (K a multiple of 2048): one-hot activations recover
     deq(W)[:, j] exactly for columns across lanes, half-rows and code positions."""
@@ -292,7 +292,7 @@ def test_gemv_rows_one_hot_is_exact(dev, fmt, k):
     else:
         w, deq = int4_weight(dev, fmt, n, k, torch.float16, 32, rng)
         xdt = torch.float16
-    for j in [0, 1, 2, 3, 5, 7, 8, 31, 32, 33, 1000, 2047, 2048, k - 1]:
+    for j in [0, 1, 2, 3, 5, 7, 8, 31, 32, 33, 1000, 2047, 2048, 10241, k - 1]:
         if j >= k:
             continue
         x = torch.zeros(k, dtype=xdt, device=dev)
@@ -312,6 +312,18 @@ def test_gemv_rows_int4_parity(dev, fmt, sdt, bs, nk):
     x = torch.from_numpy(rng.standard_normal(k).astype(np.float16)).to(dev)
     y = matvec(w, x, torch.float32)
     assert O.max_rel_err(y.cpu().numpy(), deq @ x.float().cpu().numpy().astype(np.float64)) <= TOL
+
+
+@pytest.mark.parametrize("nk", [(4096, 14336), (200, 10240), (333, 16384)])
+def test_gemv_rows_fp4_long_rows_parity(dev, nk):
+    """M = 1 FP4 rows kernel with 4 rows per wave (K of 10240 .. 16384, e.g. the SwiGLU down
+    projection 4096 x 14336), ragged N."""
+    n, k = nk
+    rng = np.random.default_rng(n + k)
+    w, deq = make_weight(dev, "fp4_e2m1", n, k, "e8m0", rng)
+    x = torch.from_numpy(rng.standard_normal(k).astype(np.float32)).to(dev).to(torch.bfloat16)
+    y = matvec(w, x, torch.float32)
+    assert O.max_rel_err(y.cpu().numpy(), deq @ bf16_np(x).astype(np.float64)) <= TOL
 
 
 def test_matvec_thread_true_uses_native_gemv(dev):

@@ -87,7 +87,7 @@ __device__ __forceinline__ int reduce_row(int lane) {
   return R == 8 ? reduce_row8(lane) : reduce_row4(lane);
 }
 
-// One wave per R = 8 rows, four waves per workgroup; IPR instructions per row
+// One wave per R (8 or 4) rows, four waves per workgroup; IPR instructions per row
 // (K = 2048 IPR); D loads in flight per wave.
 template <int R, int IPR, int D, bool SCALED>
 __global__ void __launch_bounds__(256) gemv_rows_fp4(const uint8_t* __restrict__ w, int64_t N,
@@ -298,14 +298,15 @@ constexpr int kRowsPerWave = 8;
 int launch_gemv_rows(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k, const void* scales, int sdt,
                      int64_t bs, const void* x, int xdt, int64_t m, void* y, int ydt) {
   if (fmt != TGM_FMT_FP4_E2M1 || m != 1 || xdt != TGM_BF16) return TGM_E_UNSUPPORTED;
-  if (k % 2048 != 0 || k / 2048 > 4) return TGM_E_UNSUPPORTED;
+  if (k % 2048 != 0 || k / 2048 > 8) return TGM_E_UNSUPPORTED;
   if (scales && (sdt != TGM_E8M0 || bs != 32)) return TGM_E_UNSUPPORTED;
   if ((uintptr_t)w % 16 || (uintptr_t)x % 16) return TGM_E_UNSUPPORTED;
-  constexpr int R = kRowsPerWave;
-  const unsigned grid = (unsigned)((n + 4 * R - 1) / (4 * R));
   const int ipr = (int)(k / 2048);
-#define TGM_ROWS(IPR, D)                                                                                           \
+  // up to K = 8192 a wave takes 8 rows; longer rows (their activations fill IPR * 16 registers)
+  // take 4 rows per wave
+#define TGM_ROWS(R, IPR, D)                                                                                        \
   if (ipr == IPR) {                                                                                                \
+    const unsigned grid = (unsigned)((n + 4 * R - 1) / (4 * R));                                                   \
     if (scales)                                                                                                    \
       hipLaunchKernelGGL((gemv_rows_fp4<R, IPR, D, true>), dim3(grid), dim3(256), 0, s, (const uint8_t*)w, n,      \
                          (const uint8_t*)scales, (const __bf16*)x, y, ydt);                                        \
@@ -314,7 +315,8 @@ int launch_gemv_rows(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k
                          (const uint8_t*)scales, (const __bf16*)x, y, ydt);                                        \
     return TGM_OK;                                                                                                 \
   }
-  TGM_ROWS(1, 8) TGM_ROWS(2, 16) TGM_ROWS(3, 16) TGM_ROWS(4, 16)
+  TGM_ROWS(kRowsPerWave, 1, 8) TGM_ROWS(kRowsPerWave, 2, 16) TGM_ROWS(kRowsPerWave, 3, 16)
+  TGM_ROWS(kRowsPerWave, 4, 16) TGM_ROWS(4, 5, 16) TGM_ROWS(4, 6, 16) TGM_ROWS(4, 7, 16) TGM_ROWS(4, 8, 16)
 #undef TGM_ROWS
   return TGM_E_UNSUPPORTED;
 }
