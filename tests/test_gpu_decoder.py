@@ -252,3 +252,21 @@ def test_config5_full_size_prefill_and_graph_decode(dev):
     assert torch.equal(eager, graphed)
     assert torch.isfinite(dec.logits).all()
     assert dec.pos.tolist() == [512 + 3]
+
+
+def test_decoder_weights_file_round_trip(dev, tmp_path):
+    """Weights saved to a packed-weights file and loaded back generate the same tokens."""
+    from tinygrad_mi355x.decoder import load_weights, save_weights
+
+    cfg = SMALL
+    w = random_weights(cfg, dev, seed=11)
+    path = tmp_path / "decoder.safetensors"
+    save_weights(path, w, cfg)
+    w2, cfg2 = load_weights(path, dev)
+    assert cfg2 == cfg
+    assert torch.equal(w2.layers[1].w_gate_up.data, w.layers[1].w_gate_up.data)
+    assert torch.equal(w2.layers[0].wqkv.scales, w.layers[0].wqkv.scales)
+    prompts = torch.from_numpy(np.random.default_rng(4).integers(0, cfg.vocab, (2, 8))).to(dev)
+    a = Decoder(w, cfg, 2, 64, 8).generate(prompts, 6)
+    b = Decoder(w2, cfg2, 2, 64, 8).generate(prompts, 6)
+    assert torch.equal(a, b)

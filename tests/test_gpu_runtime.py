@@ -130,3 +130,37 @@ def test_packed_gemv_through_plugin_buffers(device):
     deq = O.dequant_f64(data, "fp4_e2m1", (n, k), O.e8m0_decode(e), 32)
     want = deq @ x.astype(np.float64)
     assert O.max_rel_err(got, want) <= 1e-4  # fp32 output: only the summation order differs
+
+
+def test_graph_replays_program_sequence(device):
+    """MI355XGraph (the reference's graph runner, runtime/graph/dx12.py:49-253): a sequence of
+    program calls replayed as one HIP graph equals the eager sequence, replay after replay with
+    eager work in between; changed scalars re-record; wait=True returns GPU seconds."""
+    from tinygrad_mi355x.runtime.graph import MI355XGraph
+
+    src = device.renderer.render(SAXPY)
+    prog = device.runtime("saxpy", device.compiler.compile(src))
+    n = 100_003
+    rng = np.random.default_rng(3)
+    x, y0 = rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32)
+    bx, by = upload(device, x), upload(device, y0)
+    groups = ((n + 255) // 256, 1, 1)
+    calls = [(prog, (by, bx), groups, (256, 1, 1), (0.5, n)), (prog, (by, bx), groups, (256, 1, 1), (-2.0, n))]
+    graph = MI355XGraph(calls)
+    want = y0.astype(np.float64)
+    for replay in range(4):
+        seconds = graph(wait=(replay == 3))
+        want = want + 0.5 * x - 2.0 * x
+        if replay == 1:  # eager work between replays, ordered on the same stream
+            prog(by, bx, global_size=groups, local_size=(256, 1, 1), vals=(1.0, n))
+            want = want + x
+        device.synchronize()
+        np.testing.assert_allclose(download(device, by, np.float32, n), want, rtol=1e-5, atol=1e-5)
+    assert isinstance(seconds, float) and 0 < seconds < 1
+    graph({1: ((by, bx), groups, (256, 1, 1), (3.0, n))})  # new scalar: the graph is recorded again
+    device.synchronize()
+    want = want + 0.5 * x + 3.0 * x
+    np.testing.assert_allclose(download(device, by, np.float32, n), want, rtol=1e-5, atol=1e-5)
+    with pytest.raises(ValueError):
+        graph({0: ((by,), groups, (256, 1, 1), (1.0, n))})  # wrong buffer count, rejected before capture
+    graph.close()

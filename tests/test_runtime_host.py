@@ -139,3 +139,18 @@ def test_allocator_checks_need_no_gpu():
 def test_opening_a_device_without_a_gpu_raises():
     with pytest.raises(RuntimeError):
         R.MI355XDevice("MI355X")
+
+
+def test_graph_validation_without_a_gpu():
+    """MI355XGraph rejects empty sequences and programs of several devices before touching HIP."""
+    from types import SimpleNamespace
+
+    from tinygrad_mi355x.runtime.graph import MI355XGraph, StreamGraph
+
+    with pytest.raises(ValueError, match="at least one"):
+        MI355XGraph([])
+    a, b = SimpleNamespace(dev=object()), SimpleNamespace(dev=object())
+    with pytest.raises(ValueError, match="one device"):
+        MI355XGraph([(a, (), (1, 1, 1), (1, 1, 1), ()), (b, (), (1, 1, 1), (1, 1, 1), ())])
+    with pytest.raises(ValueError, match="non-null"):
+        StreamGraph(lambda: None, 0)

@@ -111,6 +111,38 @@ def random_weights(cfg: DecoderConfig, device: str | torch.device = "cuda", seed
     return DecoderWeights(embed, layers, final_norm, lm_head)
 
 
+_LAYER_FIELDS = ("attn_norm", "wqkv", "wo", "ffn_norm", "w_gate_up", "w_down")
+
+
+def save_weights(path, w: DecoderWeights, cfg: DecoderConfig) -> None:
+    """Write the weights and configuration as a packed-weights file (tinygrad_mi355x.checkpoint)."""
+    from dataclasses import asdict
+
+    from tinygrad_mi355x import checkpoint
+
+    tensors = {"embed": w.embed, "final_norm": w.final_norm, "lm_head": w.lm_head}
+    for i, layer in enumerate(w.layers):
+        for field in _LAYER_FIELDS:
+            tensors[f"layers.{i}.{field}"] = getattr(layer, field)
+    checkpoint.save(path, tensors, {"decoder": asdict(cfg)})
+
+
+def load_weights(path, device: str | torch.device = "cuda") -> tuple[DecoderWeights, DecoderConfig]:
+    """Read weights written by ``save_weights`` onto ``device``."""
+    from tinygrad_mi355x import checkpoint
+
+    tensors, meta = checkpoint.load(path, device)
+    if "decoder" not in meta:
+        raise ValueError(f"{path} holds no decoder configuration")
+    cfg = DecoderConfig(**meta["decoder"])
+    try:
+        layers = [LayerWeights(*(tensors[f"layers.{i}.{field}"] for field in _LAYER_FIELDS)) for i in range(cfg.layers)]
+        weights = DecoderWeights(tensors["embed"], layers, tensors["final_norm"], tensors["lm_head"])
+    except KeyError as error:
+        raise ValueError(f"{path} lacks decoder tensor {error}") from error
+    return weights, cfg
+
+
 def _packed_product(x: torch.Tensor, m: int, ldx: int, w: PackedTensor, y: torch.Tensor, ldy: int, stream: int) -> None:
     """y[:m] = x[:m] @ deq(w)^T: packed GEMV for m <= 16 rows, packed GEMM above."""
     n, k = w.shape
