@@ -140,6 +140,28 @@ int tgm_gemm_mx(const void* a, int a_fmt, const void* a_scales, int64_t m,
                 void* c, int c_dtype, int64_t ldc, void* stream);
 
 /*
+ * Kernel family 2 -- ordinary bf16 x bf16 or f16 x f16 GEMM on MFMA (the reference's LinAlg
+ * lowering of a scheduled ordinary matrix product, codegen/matmul.py:156-246 with
+ * renderer/linalg.py:38-124).
+ *
+ *   C[m, n] = sum_k A[m, k] * B[n, k]
+ *
+ * A [M, K] (row stride lda) and B [N, K] (row stride ldb) of one dtype, both K-contiguous;
+ * C (BF16, F16 or F32) with row stride ldc.  Products are exact in fp32, accumulation fp32.
+ * K must be a multiple of 64 and rows 16-byte aligned; otherwise TGM_E_UNSUPPORTED.
+ */
+int tgm_gemm_dense(const void* a, int a_dtype, int64_t m, int64_t lda, const void* b, int b_dtype, int64_t n,
+                   int64_t ldb, int64_t k, void* c, int c_dtype, int64_t ldc, void* stream);
+
+/*
+ * out[j, i] = in[i, j] for 16-bit elements: in is [rows, cols] (row stride ld_in), out is
+ * [cols, rows] (row stride ld_out).  Stages a row-major [K, N] operand as [N, K] for
+ * tgm_gemm_dense (the reference stages operands it cannot bind directly, matmul.py:218-226).
+ */
+int tgm_transpose16(const void* in, int64_t rows, int64_t cols, int64_t ld_in, void* out, int64_t ld_out,
+                    void* stream);
+
+/*
  * Exact-width GEMM for operands the families above do not cover (the reference's
  * fallback lhs.matmul(rhs, dtype=...), linalg.py:169-174 and :219-223, with products
  * formed at accumulator width as the DX12 device does, test_linalg.py:221-230).

@@ -1,0 +1,194 @@
+// Kernel family 2, ordinary operands: bf16 x bf16 or f16 x f16 GEMM on 32x32x16 MFMA.
+//
+// The reference lowers an ordinary scheduled matrix product to its collective LinAlg GEMM
+// (alexandreteles/tinygrad-dx12 src/tinygrad_dx12/codegen/matmul.py:156-246, source from
+// renderer/linalg.py:38-124).  This is that product on gfx950:
+//
+//   C[m, n] = sum_k A[m, k] * B[n, k]      A [M, K] (row stride lda), B [N, K] (row stride ldb)
+//
+// i.e. A @ B^T with both operands K-contiguous; a row-major B [K, N] is first transposed by
+// tgm_transpose16 (the caller's staging copy, as the reference stages operands it cannot
+// bind directly, matmul.py:218-226).  Products of two bf16 or two f16 values are exact in
+// fp32; accumulation is fp32 and the output is rounded once.
+//
+// Workgroup: 128 (M) x 256 (N) output tile, eight waves in 2 x 4 (64 x 64 each, 2 x 2 MFMA
+// tiles).  K advances 64 elements per step: the A panel (128 rows x 128 B) and B panel (256 rows
+// x 128 B) go straight from global memory into a double-buffered LDS stage (buffer_load ... lds,
+// zero-filled past M and N), 16-byte columns XOR-swizzled by (row / 2) % 8 so that the 32 rows a
+// fragment read touches fall in distinct banks.  MFMA j of a step takes K [16 j + 8 h, + 8) for
+// lane half h.  Loads of step s + 2 run while step s + 1 computes.
+#include <type_traits>
+
+#include "tgm_mfma_common.h"
+
+namespace tgm {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 dn_bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 dn_f16x8;
+
+constexpr int kDM = 128, kDN = 256, kDK = 64;        // tile and K step
+constexpr int kDRow = kDK * 2;                        // bytes per panel row and step
+constexpr int kDStage = (kDM + kDN) * kDRow;          // 48 KB
+constexpr int kDGroupM = 8;
+
+template <bool BF16>
+__global__ void __launch_bounds__(512) gemm_dense(const uint8_t* __restrict__ a, unsigned lda_bytes,
+                                                  const uint8_t* __restrict__ b, unsigned ldb_bytes, int M, int N,
+                                                  int K, void* __restrict__ c, int cdt, int64_t ldc) {
+  constexpr int FA = 2, FB = 2;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kDStage];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
+  const int tiles_m = (M + kDM - 1) / kDM, tiles_n = (N + kDN - 1) / kDN;
+  int tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, kDGroupM, tm, tn);
+  const int m0 = tm * kDM, n0 = tn * kDN;
+  const int nsteps = K / kDK;
+  const i32x4v ra = buffer_rsrc(a, (unsigned)(M - 1) * lda_bytes + (unsigned)K * 2u);
+  const i32x4v rb = buffer_rsrc(b, (unsigned)(N - 1) * ldb_bytes + (unsigned)K * 2u);
+  const unsigned lds_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds;
+  // Load instruction i fills rows 8 i .. 8 i + 7 of a panel: lane l writes slot l % 8 of row
+  // 8 i + l / 8, which holds logical column (l % 8) ^ ((row / 2) % 8).  A: instructions
+  // 2 wave, 2 wave + 1; B: 4 wave .. 4 wave + 3.
+  unsigned voa[2], vob[4];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int row = 8 * (2 * wave + q) + (lane >> 3);
+    voa[q] = (unsigned)(m0 + row) * lda_bytes + (unsigned)((lane & 7) ^ ((row >> 1) & 7)) * 16u;
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int row = 8 * (4 * wave + q) + (lane >> 3);
+    vob[q] = (unsigned)(n0 + row) * ldb_bytes + (unsigned)((lane & 7) ^ ((row >> 1) & 7)) * 16u;
+  }
+  auto dma_step = [&](int s, int buf) __attribute__((always_inline)) {
+    const unsigned st = lds_base + (unsigned)(buf * kDStage);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) lds_dma16(ra, st + (unsigned)(2 * wave + q) * 1024u, voa[q] + (unsigned)s * kDRow);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      lds_dma16(rb, st + (unsigned)(kDM * kDRow) + (unsigned)(4 * wave + q) * 1024u, vob[q] + (unsigned)s * kDRow);
+  };
+  const int half = lane >> 5;
+  const int a_row = wm * 64 + (lane & 31), b_row = wn * 64 + (lane & 31);
+  using V = typename std::conditional<BF16, dn_bf16x8, dn_f16x8>::type;  // read as the MFMA operand type
+  auto frag = [&](const unsigned char* panel, int row, int j) __attribute__((always_inline)) {
+    return *(const V*)(panel + row * kDRow + (((2 * j + half) ^ ((row >> 1) & 7)) * 16));
+  };
+  f32x16 acc[FA][FB];
+#pragma unroll
+  for (int i = 0; i < FA; ++i)
+#pragma unroll
+    for (int j = 0; j < FB; ++j) acc[i][j] = f32x16{};
+
+  const int s1 = nsteps > 1 ? 1 : 0;
+  dma_step(0, 0);
+  dma_step(s1, 1);
+  wait_lds_dma();
+  __syncthreads();
+  for (int s = 0; s < nsteps; ++s) {
+    const int cur = s & 1;
+    const int s2 = s + 2 < nsteps ? s + 2 : nsteps - 1;
+    const unsigned char* pa = lds + cur * kDStage;
+    const unsigned char* pb = pa + kDM * kDRow;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      V fa[FA], fb[FB];
+#pragma unroll
+      for (int t = 0; t < FA; ++t) fa[t] = frag(pa, a_row + 32 * t, j);
+#pragma unroll
+      for (int t = 0; t < FB; ++t) fb[t] = frag(pb, b_row + 32 * t, j);
+#pragma unroll
+      for (int ta = 0; ta < FA; ++ta)
+#pragma unroll
+        for (int tb = 0; tb < FB; ++tb) {
+          if constexpr (BF16)
+            acc[ta][tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ta], fb[tb], acc[ta][tb], 0, 0, 0);
+          else
+            acc[ta][tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[ta], fb[tb], acc[ta][tb], 0, 0, 0);
+        }
+    }
+    wait_lds_dma();   // this wave's loads of step s + 1
+    __syncthreads();  // every wave is done with this buffer; step s + 1 is complete in the other
+    dma_step(s2, cur);
+  }
+  wait_lds_dma();
+  __syncthreads();  // the epilogue reuses the LDS
+  float* ep = (float*)lds + wave * 32 * 36;
+#pragma unroll
+  for (int i = 0; i < FA; ++i)
+#pragma unroll
+    for (int j = 0; j < FB; ++j)
+      store_tile32(acc[i][j], ep, lane, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, M, N, c, cdt, ldc);
+}
+
+// out[j, i] = in[i, j] for 16-bit elements, through 64 x 64 LDS tiles (padded rows).
+__global__ void __launch_bounds__(256) transpose16(const uint16_t* __restrict__ in, int rows, int cols, int64_t ld_in,
+                                                   uint16_t* __restrict__ out, int64_t ld_out) {
+  __shared__ uint16_t t[64][65];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = ty; i < 64; i += 4) {
+    const int r = r0 + i, cc = c0 + tx;
+    if (r < rows && cc < cols) t[i][tx] = in[(int64_t)r * ld_in + cc];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = ty; i < 64; i += 4) {
+    const int cc = c0 + i, r = r0 + tx;
+    if (cc < cols && r < rows) out[(int64_t)cc * ld_out + r] = t[tx][i];
+  }
+}
+
+}  // namespace tgm
+
+using namespace tgm;
+
+extern "C" int tgm_gemm_dense(const void* a, int a_dtype, int64_t m, int64_t lda, const void* b, int b_dtype, int64_t n,
+                              int64_t ldb, int64_t k, void* c, int c_dtype, int64_t ldc, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(a && b && c, "null operand");
+  TGM_CHECK_ARG(m >= 0 && n >= 0 && k >= 0, "invalid gemm sizes");
+  TGM_CHECK_ARG(m <= 1 || lda >= k, "lda smaller than K");
+  TGM_CHECK_ARG(n <= 1 || ldb >= k, "ldb smaller than K");
+  TGM_CHECK_ARG(m <= 1 || ldc >= n, "ldc smaller than N");
+  TGM_CHECK_ARG(c_dtype == TGM_BF16 || c_dtype == TGM_F16 || c_dtype == TGM_F32, "output must be bf16, f16 or f32");
+  if (m == 0 || n == 0) return TGM_OK;
+  if (a_dtype != b_dtype || (a_dtype != TGM_BF16 && a_dtype != TGM_F16))
+    TGM_UNSUPPORTED("tgm_gemm_dense: operands must both be bf16 or both f16");
+  if (k == 0 || k % kDK != 0) TGM_UNSUPPORTED("tgm_gemm_dense: K must be a positive multiple of %d", kDK);
+  const int64_t lda_eff = m > 1 ? lda : k, ldb_eff = n > 1 ? ldb : k;
+  if ((lda_eff * 2) % 16 || (ldb_eff * 2) % 16 || (uintptr_t)a % 16 || (uintptr_t)b % 16)
+    TGM_UNSUPPORTED("tgm_gemm_dense: operands and their rows must be 16-byte aligned");
+  if (m >= (1ll << 31) || n >= (1ll << 31) || (m - 1) * lda_eff * 2 + k * 2 >= (1ll << 32) ||
+      (n - 1) * ldb_eff * 2 + k * 2 >= (1ll << 32))
+    TGM_UNSUPPORTED("tgm_gemm_dense: operands must be under 4 GiB (32-bit offsets)");
+  const int64_t tiles = ((m + kDM - 1) / kDM) * ((n + kDN - 1) / kDN);
+  const hipStream_t st = (hipStream_t)stream;
+  if (a_dtype == TGM_BF16)
+    hipLaunchKernelGGL(gemm_dense<true>, dim3((unsigned)tiles), dim3(512), 0, st, (const uint8_t*)a,
+                       (unsigned)(lda_eff * 2), (const uint8_t*)b, (unsigned)(ldb_eff * 2), (int)m, (int)n, (int)k, c,
+                       c_dtype, ldc);
+  else
+    hipLaunchKernelGGL(gemm_dense<false>, dim3((unsigned)tiles), dim3(512), 0, st, (const uint8_t*)a,
+                       (unsigned)(lda_eff * 2), (const uint8_t*)b, (unsigned)(ldb_eff * 2), (int)m, (int)n, (int)k, c,
+                       c_dtype, ldc);
+  return launch_status("tgm_gemm_dense");
+}
+
+extern "C" int tgm_transpose16(const void* in, int64_t rows, int64_t cols, int64_t ld_in, void* out, int64_t ld_out,
+                               void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(in && out, "null operand");
+  TGM_CHECK_ARG(rows >= 0 && cols >= 0 && rows < (1ll << 31) && cols < (1ll << 31), "invalid sizes");
+  TGM_CHECK_ARG(rows <= 1 || ld_in >= cols, "ld_in smaller than cols");
+  TGM_CHECK_ARG(cols <= 1 || ld_out >= rows, "ld_out smaller than rows");
+  if (rows == 0 || cols == 0) return TGM_OK;
+  const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+  if (grid.y > 65535) TGM_UNSUPPORTED("tgm_transpose16: too many rows");
+  hipLaunchKernelGGL(transpose16, grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t*)in, (int)rows, (int)cols,
+                     ld_in, (uint16_t*)out, ld_out);
+  return launch_status("tgm_transpose16");
+}

@@ -142,6 +142,12 @@ def pack(codes: torch.Tensor, format: str, shape: tuple[int, ...] | None = None,
     return PackedTensor(out, format, shape, scales, block_size)
 
 
+def unpack(packed: PackedTensor, dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Functional form of ``PackedTensor.unpack``: the node a traced program records for a decode
+    (tinygrad_mi355x.codegen.matmul rewrites products whose operand it is)."""
+    return packed.unpack(dtype)
+
+
 def quantize_mx(x: torch.Tensor, format: str, block_size: int = 32) -> PackedTensor:
     """MX-quantise ``x`` [..., K] along its last axis into ``format`` with E8M0 block scales.
 

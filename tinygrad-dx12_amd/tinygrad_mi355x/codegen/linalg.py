@@ -8,6 +8,7 @@ scopes raise" behaviour.  What changes is what runs:
 * a packed K-blocked weight times activations goes to kernel family 1 (fused
   dequant GEMV, M <= 16) or family 2 (dequant-to-bf16 MFMA GEMM);
 * two packed MX operands (``matmul_nt``) go to the block-scaled FP4/FP6 MFMA GEMM;
+* two ordinary bf16 or f16 operands go to the ordinary MFMA GEMM (``tgm_gemm_dense``);
 * everything else runs the exact-width device GEMM ``tgm_gemm_plain`` -- the
   analogue of the reference's ordinary-matmul fallback.
 
@@ -26,8 +27,9 @@ import torch
 
 from tinygrad_mi355x import dtype as D
 from tinygrad_mi355x.codegen.decomp.mi355x import MX_FORMATS, PackedTensor, matrix_intermediate
-from tinygrad_mi355x.renderer.linalg import (ACTIVATION_DTYPES, GEMM_MX, GEMM_W, GEMV, GEMV_MAX_ROWS, OUTPUT_DTYPES,
-                                             WEIGHT_SCALE_DTYPES, MatrixKernel, _accumulator)
+from tinygrad_mi355x.renderer.linalg import (ACTIVATION_DTYPES, DENSE_DTYPES, GEMM_DENSE, GEMM_MX, GEMM_W, GEMV,
+                                             GEMV_MAX_ROWS, OUTPUT_DTYPES, WEIGHT_SCALE_DTYPES, MatrixKernel,
+                                             _accumulator)
 from tinygrad_mi355x.runtime import kernels as K
 
 SCOPES = ("auto", "Wave", "ThreadGroup", "tiled")
@@ -70,6 +72,44 @@ def plain_matmul(lhs: torch.Tensor, rhs: torch.Tensor, out_dtype: torch.dtype, a
            out.data_ptr(), K.dtype_id(out_dtype), out.stride(0), out.stride(1), m, n, k, _ACC_IDS[acc],
            K.stream_of(lhs))
     return out
+
+
+def transpose16(x: torch.Tensor) -> torch.Tensor:
+    """Contiguous transpose of a 2-D 16-bit tensor on the device (the staging copy of a
+    row-major right operand for the NT GEMM)."""
+    K.require_device(x)
+    rows, cols = x.shape
+    out = torch.empty((cols, rows), dtype=x.dtype, device=x.device)
+    if x.stride(1) != 1 and rows > 1 and cols > 1:
+        x = x.contiguous()
+    K.call("tgm_transpose16", x.data_ptr(), rows, cols, x.stride(0) if rows > 1 else cols, out.data_ptr(), rows,
+           K.stream_of(x))
+    return out
+
+
+def _k_rows(x: torch.Tensor) -> torch.Tensor:
+    """``x`` with contiguous rows (unit stride along the last axis)."""
+    return x if x.stride(1) == 1 or x.shape[1] == 1 else x.contiguous()
+
+
+def dense_matmul_nt(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+    """C[M, N] = a[M, K] @ b[N, K]^T on the ordinary MFMA GEMM (bf16 or f16 operands)."""
+    a, b = _k_rows(a), _k_rows(b)
+    m, k = a.shape
+    n = b.shape[0]
+    c = torch.empty((m, n), dtype=out_dtype, device=a.device)
+    K.call("tgm_gemm_dense", a.data_ptr(), K.dtype_id(a.dtype), m, a.stride(0) if m > 1 else k, b.data_ptr(),
+           K.dtype_id(b.dtype), n, b.stride(0) if n > 1 else k, k, c.data_ptr(), K.dtype_id(out_dtype), n,
+           K.stream_of(a))
+    return c
+
+
+def _dense_kernel(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype, tile, scope: str) -> MatrixKernel | None:
+    if scope == "tiled" or not MI355X_LINALG or a.dtype not in DENSE_DTYPES or b.dtype is not a.dtype:
+        return None
+    if out_dtype not in OUTPUT_DTYPES or (tile is not None and tuple(tile) != GEMM_DENSE.tile):
+        return None
+    return GEMM_DENSE
 
 
 def _decoded(x: torch.Tensor | PackedTensor, intermediate: torch.dtype) -> torch.Tensor:
@@ -221,6 +261,12 @@ def matmul(a: torch.Tensor | PackedTensor, b: torch.Tensor | PackedTensor, scope
         kernel = choose_matrix(a, b, intermediate, out_dtype, n, tile, scope)
         key = _key(kernel, a, b, out_dtype=out_dtype, m=n)
         return _dispatch(lambda: _weight_left(kernel, a, b.t(), out_dtype).t(), generic, kernel, scope, key)
+    if not packed:
+        kernel = _dense_kernel(a, b, out_dtype, tile, scope)
+        key = _key(kernel, a, b, out_dtype=out_dtype, m=m)
+        # b [K, N]: a transposed view of a K-last tensor binds directly, a row-major one is staged
+        native = lambda: dense_matmul_nt(a, b.t() if b.stride(0) == 1 else transpose16(b), out_dtype)  # noqa: E731
+        return _dispatch(native, generic, kernel, scope, key)
     return _dispatch(None, generic, None, scope, ())
 
 
@@ -261,7 +307,9 @@ def matmul_nt(a: torch.Tensor | PackedTensor, b: torch.Tensor | PackedTensor, sc
         kernel = choose_matrix(a, b, intermediate, out_dtype, n, tile, scope)
         key = _key(kernel, a, b, out_dtype=out_dtype, m=n)
         return _dispatch(lambda: _weight_left(kernel, a, b, out_dtype).t(), generic, kernel, scope, key)
-    return _dispatch(None, generic, None, scope, ())
+    kernel = _dense_kernel(a, b, out_dtype, tile, scope)
+    key = _key(kernel, a, b, out_dtype=out_dtype, m=m)
+    return _dispatch(lambda: dense_matmul_nt(a, b, out_dtype), generic, kernel, scope, key)
 
 
 def linear(x: torch.Tensor, weight: PackedTensor | torch.Tensor, dtype: torch.dtype | None = None) -> torch.Tensor:

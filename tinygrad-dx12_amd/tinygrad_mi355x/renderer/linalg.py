@@ -38,6 +38,10 @@ GEMV = MatrixKernel("tgm_gemv", "Wave", (16, 16, 128), 256)
 GEMM_W = MatrixKernel("tgm_gemm_w", "ThreadGroup", (256, 128, 128), 512)
 # Family 2: block-scaled FP4/FP6 MFMA GEMM (two packed MX operands).
 GEMM_MX = MatrixKernel("tgm_gemm_mx", "ThreadGroup", (256, 256, 256), 512)
+# Family 2: ordinary bf16 x bf16 / f16 x f16 MFMA GEMM (the reference's LinAlg lowering of an
+# ordinary matrix product, codegen/matmul.py:156-246).
+GEMM_DENSE = MatrixKernel("tgm_gemm_dense", "ThreadGroup", (256, 128, 64), 512)
+DENSE_DTYPES = (torch.bfloat16, torch.float16)
 # Exact-width fallback (the reference's ordinary matmul); never a "native" candidate.
 PLAIN = MatrixKernel("tgm_gemm_plain", "tiled", (16, 16, 1), 256)
 
