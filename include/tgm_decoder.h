@@ -67,8 +67,9 @@ int tgm_dec_attention(const float* qkv, int64_t rows, int64_t seq_rows, int64_t 
                       double rope_base, int64_t splits, float* workspace, int64_t workspace_bytes, void* out,
                       int out_dtype, void* stream);
 
-/* SwiGLU: out[r, i] = silu(g) * u with g = gate_up[r, i], u = gate_up[r, ffn + i] (float32
- * [rows, 2 * ffn]); out is [rows, ffn] of out_dtype. */
+/* SwiGLU: out[r, i] = silu(g) * u with g = gate_up[r, 2 i], u = gate_up[r, 2 i + 1] (float32
+ * [rows, 2 * ffn], gate and up interleaved as the rows of the gate|up weight are, so that the
+ * M = 1 projection can apply it in its epilogue, tgm_gemv_swiglu); out is [rows, ffn]. */
 int tgm_dec_silu_mul(const float* gate_up, int64_t rows, int64_t ffn, void* out, int out_dtype, void* stream);
 
 /* Dense bf16 GEMV for the output head: y[m, n] = sum_k x[m, k] * w[n, k] in fp32.  w is BF16

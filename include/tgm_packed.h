@@ -104,6 +104,19 @@ int tgm_gemv(const void* w, int fmt, int64_t n, int64_t k,
              void* y, int y_dtype, int64_t ldy, void* stream);
 
 /*
+ * Family 1 with a SwiGLU epilogue (the gate / up projection of a decoder's feed-forward
+ * block; no reference counterpart, where the activation would be a separate tinygrad op):
+ *
+ *   y[i] = silu(g) * u,  g = sum_k x[k] * deq(W)[2 i, k],  u = sum_k x[k] * deq(W)[2 i + 1, k]
+ *
+ * W packed [n, k] with gate and up rows interleaved, n even; one activation row x (BF16);
+ * y has n / 2 elements.  Only the M = 1 FP4 + E8M0/32 row-streaming kernel has this epilogue
+ * (K a multiple of 2048, at most 16384); otherwise TGM_E_UNSUPPORTED.
+ */
+int tgm_gemv_swiglu(const void* w, int fmt, int64_t n, int64_t k, const void* scales, int scale_dtype,
+                    int64_t block_size, const void* x, int x_dtype, void* y, int y_dtype, void* stream);
+
+/*
  * Kernel family 2 -- prefill GEMM with packed weights and 16-bit activations
  * (replaces the collective LinAlg GEMM linalg_source, renderer/linalg.py:38-124,
  * for a packed weight operand; linalg.py:175-218).

@@ -14,7 +14,7 @@ follows a reference file line by line.  The math is the standard Llama decoder l
     0 .. p (GQA: q head h reads kv head h // (heads / kv_heads))      -> f16
     h  += attn @ deq(Wo)^T
     x   = RMSNorm(h) * w_ffn             -> bf16          (input of the FP4 projections)
-    g|u = x @ deq(Wgu)^T; a = silu(g) * u -> bf16
+    g|u = x @ deq(Wgu)^T (gate and up rows interleaved); a = silu(g) * u -> bf16
     h  += a @ deq(Wdown)^T
     logits = bf16(RMSNorm(h) * w_final) @ lm_head^T; next token = first argmax
 
@@ -62,7 +62,8 @@ def rope(x: np.ndarray, positions: np.ndarray, base: float) -> np.ndarray:
 
 
 def silu(g: np.ndarray) -> np.ndarray:
-    return g / (1.0 + np.exp(-g))
+    with np.errstate(over="ignore"):  # exp(-g) = inf for very negative g gives the limit -0
+        return g / (1.0 + np.exp(-g))
 
 
 def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, q_pos: np.ndarray) -> np.ndarray:
@@ -134,7 +135,7 @@ class OracleDecoder:
             h = h + att @ L.wo.T
             x = bf16(rmsnorm(h, L.ffn_norm, self.eps))
             gu = x @ L.w_gate_up.T
-            a = bf16(silu(gu[..., :self.F]) * gu[..., self.F:])
+            a = bf16(silu(gu[..., 0::2]) * gu[..., 1::2])  # gate and up rows interleaved
             h = h + a @ L.w_down.T
         x = bf16(rmsnorm(h, self.w.final_norm, self.eps))
         return x @ self.w.lm_head.T

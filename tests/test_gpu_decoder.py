@@ -150,7 +150,7 @@ def test_silu_mul(dev):
     out = torch.empty((rows, F), dtype=torch.bfloat16, device=dev)
     K.call("tgm_dec_silu_mul", gu.data_ptr(), rows, F, out.data_ptr(), BF16, stream())
     g = np64(gu)
-    ref = D.silu(g[:, :F]) * g[:, F:]
+    ref = D.silu(g[:, 0::2]) * g[:, 1::2]
     assert O.max_rel_err(np64(out), ref) <= 1e-2
 
 
@@ -270,3 +270,28 @@ def test_decoder_weights_file_round_trip(dev, tmp_path):
     a = Decoder(w, cfg, 2, 64, 8).generate(prompts, 6)
     b = Decoder(w2, cfg2, 2, 64, 8).generate(prompts, 6)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("nk", [(28672, 4096), (200, 2048), (8192, 14336)])
+def test_gemv_swiglu_epilogue(dev, nk):
+    """The gate|up GEMV with the SwiGLU epilogue equals the plain GEMV followed by
+    tgm_dec_silu_mul bit for bit (same row kernel, same fp32 values), and the oracle within 1e-2."""
+    n, k = nk
+    rng = np.random.default_rng(n + k)
+    codes = rng.integers(0, 16, (n, k)).astype(np.uint8)
+    e = (127 + rng.integers(-4, 3, (n, k // 32))).astype(np.uint8)
+    w = PackedTensor(torch.from_numpy(O.pack_codes(codes, 4)).to(dev), "fp4_e2m1", (n, k),
+                     torch.from_numpy(e).to(dev).view(torch.float8_e8m0fnu), 32)
+    x = torch.from_numpy(rng.standard_normal(k).astype(np.float32)).to(dev).to(torch.bfloat16)
+    fused = torch.empty(n // 2, dtype=torch.bfloat16, device=dev)
+    K.call("tgm_gemv_swiglu", w.data.data_ptr(), 2, n, k, w.scales.data_ptr(), 15, 32, x.data_ptr(), BF16,
+           fused.data_ptr(), BF16, stream())
+    gu = torch.empty(n, dtype=torch.float32, device=dev)
+    K.call("tgm_gemv", w.data.data_ptr(), 2, n, k, w.scales.data_ptr(), 15, 32, x.data_ptr(), BF16, 1, k,
+           gu.data_ptr(), F32, n, stream())
+    sep = torch.empty(n // 2, dtype=torch.bfloat16, device=dev)
+    K.call("tgm_dec_silu_mul", gu.data_ptr(), 1, n // 2, sep.data_ptr(), BF16, stream())
+    assert torch.equal(fused, sep)
+    g = O.dequant_f64(O.pack_codes(codes, 4), "fp4_e2m1", (n, k), O.e8m0_decode(e), 32) @ np64(x)
+    err = O.max_rel_err(np64(fused), D.silu(g[0::2]) * g[1::2])
+    assert err <= 1e-2, err

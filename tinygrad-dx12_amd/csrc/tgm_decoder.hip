@@ -377,8 +377,7 @@ __global__ void __launch_bounds__(256) dec_silu_mul(const float* __restrict__ gu
                                                     void* __restrict__ out, int odt) {
   const int64_t n = rows * F;
   for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const int64_t r = i / F, c = i - r * F;
-    const float g = gu[r * 2 * F + c], u = gu[r * 2 * F + F + c];
+    const float g = gu[2 * i], u = gu[2 * i + 1];  // gate and up rows interleaved
     store_from_f32(out, odt, i, g / (1.0f + expf(-g)) * u);
   }
 }

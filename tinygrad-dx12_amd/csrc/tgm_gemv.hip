@@ -27,7 +27,7 @@
 namespace tgm {
 // M = 1 FP4 GEMV streamed row-contiguously (tgm_gemv_rows.hip).
 int launch_gemv_rows(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k, const void* scales, int sdt,
-                     int64_t bs, const void* x, int xdt, int64_t m, void* y, int ydt);
+                     int64_t bs, const void* x, int xdt, int64_t m, void* y, int ydt, bool swiglu = false);
 int launch_gemv_rows_int4(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k, const void* scales, int sdt,
                           int64_t bs, const void* x, int xdt, int64_t m, void* y, int ydt);
 // INT4/UINT4 weights x fp16 activations on f16 MFMA (tgm_gemv_int4.hip).
@@ -81,6 +81,21 @@ static bool mfma_gemv_ok(const void* w, int fmt, int64_t n, int64_t k, const voi
   const uintptr_t align = fmt == TGM_FMT_FP4_E2M1 ? 16 : 8;
   if ((uintptr_t)w % align || (uintptr_t)x % 16) return false;
   return true;
+}
+
+extern "C" int tgm_gemv_swiglu(const void* w, int fmt, int64_t n, int64_t k, const void* scales, int scale_dtype,
+                               int64_t block_size, const void* x, int x_dtype, void* y, int y_dtype, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(valid_format(fmt), "unknown packed format %d", fmt);
+  TGM_CHECK_ARG(n >= 0 && n % 2 == 0 && k >= 0 && block_size >= 1, "n must be even (gate and up rows interleaved)");
+  TGM_CHECK_ARG(y_dtype == TGM_BF16 || y_dtype == TGM_F16 || y_dtype == TGM_F32, "output must be bf16, f16 or f32");
+  if (n == 0) return TGM_OK;
+  if (k == 0 || n * (k / 2) >= (1ll << 40)) TGM_UNSUPPORTED("tgm_gemv_swiglu: no kernel for this size");
+  const int st = launch_gemv_rows((hipStream_t)stream, w, fmt, n, k, scales, scale_dtype, block_size, x, x_dtype, 1, y,
+                                  y_dtype, true);
+  if (st == TGM_E_UNSUPPORTED)
+    TGM_UNSUPPORTED("tgm_gemv_swiglu: needs FP4 weights with E8M0/32 scales, bf16 x, K a multiple of 2048 up to 16384");
+  return st == TGM_OK ? launch_status("tgm_gemv_swiglu") : st;
 }
 
 extern "C" int tgm_gemv(const void* w, int fmt, int64_t n, int64_t k, const void* scales, int scale_dtype,

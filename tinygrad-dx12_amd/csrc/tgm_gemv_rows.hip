@@ -89,7 +89,9 @@ __device__ __forceinline__ int reduce_row(int lane) {
 
 // One wave per R (8 or 4) rows, four waves per workgroup; IPR instructions per row
 // (K = 2048 IPR); D loads in flight per wave.
-template <int R, int IPR, int D, bool SCALED>
+// SWIGLU: rows 2 i and 2 i + 1 are the gate and up rows of output i, which becomes
+// silu(gate) * up (the two rows are reduced in lanes l and l ^ 8 for R = 8, l ^ 16 for R = 4).
+template <int R, int IPR, int D, bool SCALED, bool SWIGLU = false>
 __global__ void __launch_bounds__(256) gemv_rows_fp4(const uint8_t* __restrict__ w, int64_t N,
                                                    const uint8_t* __restrict__ scales, const __bf16* __restrict__ x,
                                                    void* __restrict__ y, int ydt) {
@@ -173,7 +175,13 @@ __global__ void __launch_bounds__(256) gemv_rows_fp4(const uint8_t* __restrict__
   static_assert(R == 8 || R == 4, "the reduction folds 4 or 8 rows");
   const float v = reduce_rows<R>(acc, lane);
   const int64_t row = r0 + reduce_row<R>(lane);
-  if ((lane & (64 / R - 1)) == 0 && row < N) store_from_f32(y, ydt, row, v);
+  if constexpr (SWIGLU) {
+    const float partner = R == 8 ? xor8(v) : __shfl_xor(v, 16, 64);  // row ^ 1
+    if ((lane & (64 / R - 1)) == 0 && (row & 1) == 0 && row < N)
+      store_from_f32(y, ydt, row >> 1, v / (1.0f + expf(-v)) * partner);
+  } else {
+    if ((lane & (64 / R - 1)) == 0 && row < N) store_from_f32(y, ydt, row, v);
+  }
 }
 
 // ------------------------------------------------------------------ INT4 / UINT4
@@ -296,18 +304,22 @@ constexpr int kRowsPerWave = 8;
 
 // M = 1 FP4 GEMV on the row-streaming kernel; TGM_E_UNSUPPORTED when the operands do not fit.
 int launch_gemv_rows(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k, const void* scales, int sdt,
-                     int64_t bs, const void* x, int xdt, int64_t m, void* y, int ydt) {
+                     int64_t bs, const void* x, int xdt, int64_t m, void* y, int ydt, bool swiglu) {
   if (fmt != TGM_FMT_FP4_E2M1 || m != 1 || xdt != TGM_BF16) return TGM_E_UNSUPPORTED;
   if (k % 2048 != 0 || k / 2048 > 8) return TGM_E_UNSUPPORTED;
   if (scales && (sdt != TGM_E8M0 || bs != 32)) return TGM_E_UNSUPPORTED;
   if ((uintptr_t)w % 16 || (uintptr_t)x % 16) return TGM_E_UNSUPPORTED;
+  if (swiglu && (!scales || n % 2)) return TGM_E_UNSUPPORTED;
   const int ipr = (int)(k / 2048);
   // up to K = 8192 a wave takes 8 rows; longer rows (their activations fill IPR * 16 registers)
   // take 4 rows per wave
 #define TGM_ROWS(R, IPR, D)                                                                                        \
   if (ipr == IPR) {                                                                                                \
     const unsigned grid = (unsigned)((n + 4 * R - 1) / (4 * R));                                                   \
-    if (scales)                                                                                                    \
+    if (swiglu)                                                                                                    \
+      hipLaunchKernelGGL((gemv_rows_fp4<R, IPR, D, true, true>), dim3(grid), dim3(256), 0, s, (const uint8_t*)w,   \
+                         n, (const uint8_t*)scales, (const __bf16*)x, y, ydt);                                     \
+    else if (scales)                                                                                               \
       hipLaunchKernelGGL((gemv_rows_fp4<R, IPR, D, true>), dim3(grid), dim3(256), 0, s, (const uint8_t*)w, n,      \
                          (const uint8_t*)scales, (const __bf16*)x, y, ydt);                                        \
     else                                                                                                           \

@@ -7,7 +7,8 @@ that consumer, the one that turns the packed kernels into tokens per second:
 
 * attention projections: INT4 weights with fp16 scales per 128 K-elements; q, k and v rows
   are stacked into one weight so that a token needs one QKV product;
-* feed-forward: FP4 E2M1 weights with E8M0 scales per 32; gate and up rows stacked;
+* feed-forward: FP4 E2M1 weights with E8M0 scales per 32; gate and up rows interleaved in one
+  weight, so that the one-token GEMV applies SwiGLU in its epilogue;
 * embeddings and output head: bf16; RMSNorm weights bf16; residual stream fp32;
 * RoPE (rotate-half pairs, base 10000) and grouped-query attention over a bf16 KV cache.
 
@@ -68,7 +69,7 @@ class LayerWeights:
     wqkv: PackedTensor           # int4 [(H + 2 HK) hd, D], fp16 scales per attn_group
     wo: PackedTensor             # int4 [D, H hd]
     ffn_norm: torch.Tensor       # bf16 [D]
-    w_gate_up: PackedTensor      # fp4 [2 F, D], E8M0 per 32 (gate rows, then up rows)
+    w_gate_up: PackedTensor      # fp4 [2 F, D], E8M0 per 32; row 2 i is gate i, row 2 i + 1 is up i
     w_down: PackedTensor         # fp4 [D, F]
 
 
@@ -189,6 +190,8 @@ class Decoder:
         self.v_cache = torch.zeros(cache, dtype=torch.bfloat16, device=dev)
         self.splits = min(max(1, math.ceil(max_seq / 64)), 32)
         self.fuse_rope = True
+        # one token: the gate|up GEMV applies SwiGLU itself when its row-streaming kernel covers the shape
+        self.fuse_swiglu = (cfg.hidden % 2048 == 0 and cfg.hidden <= 16384)
         ws = K.load_library().tgm_dec_attention_workspace(batch, cfg.heads, cfg.head_dim, self.splits)
         self.workspace = torch.empty(max(ws // 4, 1), **f32)
         self.workspace_bytes = ws
@@ -219,8 +222,14 @@ class Decoder:
             _packed_product(self.attn, rows, cfg.heads * cfg.head_dim, L.wo, self.delta, d, stream)
             K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr(), rows, d, L.ffn_norm.data_ptr(),
                    cfg.eps, self.xnb.data_ptr(), BF16, stream)
-            _packed_product(self.xnb, rows, d, L.w_gate_up, self.gu, 2 * cfg.ffn, stream)
-            K.call("tgm_dec_silu_mul", self.gu.data_ptr(), rows, cfg.ffn, self.act.data_ptr(), BF16, stream)
+            if rows == 1 and self.fuse_swiglu:  # gate|up GEMV with the SwiGLU epilogue
+                w = L.w_gate_up
+                K.call("tgm_gemv_swiglu", w.data.data_ptr(), K.FORMAT_IDS[w.format], 2 * cfg.ffn, d, K.ptr(w.scales),
+                       K.dtype_id(w.scales.dtype), w.block_size, self.xnb.data_ptr(), BF16, self.act.data_ptr(), BF16,
+                       stream)
+            else:
+                _packed_product(self.xnb, rows, d, L.w_gate_up, self.gu, 2 * cfg.ffn, stream)
+                K.call("tgm_dec_silu_mul", self.gu.data_ptr(), rows, cfg.ffn, self.act.data_ptr(), BF16, stream)
             _packed_product(self.act, rows, cfg.ffn, L.w_down, self.delta, d, stream)
         K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr(), rows, d, self.w.final_norm.data_ptr(),
                cfg.eps, self.xnb.data_ptr(), BF16, stream)
