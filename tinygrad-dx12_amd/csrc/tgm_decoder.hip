@@ -384,8 +384,10 @@ __global__ void __launch_bounds__(256) dec_silu_mul(const float* __restrict__ gu
 
 // ------------------------------------------------------------------ bf16 GEMV (output head)
 // x (M rows) is staged in LDS once per workgroup; each wave then streams whole weight rows
-// (lane l reads 16-byte chunks l, l + 64, ...) and reduces its M dot products over the wave.
-template <int M>
+// (lane l reads 16-byte chunks l, l + 64, ...) and reduces its dot products over the wave.
+// R weight rows per wave at a time: each x chunk read from LDS serves R rows (for M > 1 the
+// LDS reads of x, M per weight chunk, would otherwise bound the kernel).
+template <int M, int R>
 __global__ void __launch_bounds__(256) dec_gemv_bf16(const uint16_t* __restrict__ w, int N, int K,
                                                      const uint16_t* __restrict__ x, int64_t ldx, float* __restrict__ y,
                                                      int64_t ldy) {
@@ -395,30 +397,46 @@ __global__ void __launch_bounds__(256) dec_gemv_bf16(const uint16_t* __restrict_
   for (int i = tid; i < M * kc; i += 256) xs[i] = *(const dec_u32x4*)(x + (int64_t)(i / kc) * ldx + (int64_t)(i % kc) * 8);
   __syncthreads();
   const int nw = gridDim.x * 4;
-  for (int n = blockIdx.x * 4 + wave; n < N; n += nw) {
-    float acc[M];
+  // bf16 pairs are loaded as pairs: bit-casting the dwords of a loaded 4-dword vector to
+  // bf16 pairs has been compiled into one repeated pair
+  const dec_bf16x2* xp = (const dec_bf16x2*)xs;
+  for (int n = (blockIdx.x * 4 + wave) * R; n < N; n += nw * R) {
+    float acc[R][M];
+    const dec_bf16x2* wr[R];
 #pragma unroll
-    for (int m = 0; m < M; ++m) acc[m] = 0.f;
-    // bf16 pairs are loaded as pairs: bit-casting the dwords of a loaded 4-dword vector to
-    // bf16 pairs has been compiled into one repeated pair
-    const dec_bf16x2* wr = (const dec_bf16x2*)(w + (int64_t)n * K);
-    const dec_bf16x2* xp = (const dec_bf16x2*)xs;
-#pragma unroll 8
+    for (int r = 0; r < R; ++r) {
+      wr[r] = (const dec_bf16x2*)(w + (int64_t)(n + r < N ? n + r : N - 1) * K);  // rows past N are not stored
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
+    }
+#pragma unroll (R == 1 ? 8 : 2)
     for (int c = lane; c < kc; c += 64) {  // 16-byte chunk c: pairs 4 c .. 4 c + 3
-      dec_bf16x2 wv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) wv[e] = wr[4 * c + e];
+      dec_bf16x2 xv[M][4];
 #pragma unroll
       for (int m = 0; m < M; ++m)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          acc[m] = __builtin_amdgcn_fdot2_f32_bf16(wv[e], xp[4 * (m * kc + c) + e], acc[m], false);
+        for (int e = 0; e < 4; ++e) xv[m][e] = xp[4 * (m * kc + c) + e];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        dec_bf16x2 wv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wv[e] = wr[r][4 * c + e];
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[r][m] = __builtin_amdgcn_fdot2_f32_bf16(wv[e], xv[m][e], acc[r][m], false);
+      }
     }
 #pragma unroll
-    for (int m = 0; m < M; ++m) acc[m] = wave_sum(acc[m]);
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[r][m] = wave_sum(acc[r][m]);
     if (lane == 0)
 #pragma unroll
-      for (int m = 0; m < M; ++m) y[m * ldy + n] = acc[m];
+      for (int r = 0; r < R; ++r)
+        if (n + r < N)
+#pragma unroll
+          for (int m = 0; m < M; ++m) y[m * ldy + n + r] = acc[r][m];
   }
 }
 
@@ -619,14 +637,18 @@ extern "C" int tgm_dec_gemv_bf16(const void* w, int64_t n, int64_t k, const void
     TGM_UNSUPPORTED("tgm_dec_gemv_bf16: k must be a multiple of 8 with m * k <= 32768");
   if ((uintptr_t)w % 16 || (uintptr_t)x % 16 || (m > 1 && (ldx * 2) % 16))
     TGM_UNSUPPORTED("tgm_dec_gemv_bf16: operands and x rows must be 16-byte aligned");
-  const int64_t waves = (n + 3) / 4;
-  const unsigned blocks = (unsigned)(waves < 512 ? waves : 512);
+  const int rows_per_wave = m == 1 ? 1 : 4;
+  const int64_t waves = (n + rows_per_wave - 1) / rows_per_wave;
+  const unsigned blocks = (unsigned)((waves + 3) / 4 < 512 ? (waves + 3) / 4 : 512);
   const hipStream_t st = (hipStream_t)stream;
   const uint16_t* wp = (const uint16_t*)w;
   const uint16_t* xp = (const uint16_t*)x;
   switch (m) {
-#define TGM_GV(MM) \
-  case MM: hipLaunchKernelGGL(dec_gemv_bf16<MM>, dim3(blocks), dim3(256), 0, st, wp, (int)n, (int)k, xp, ldx, y, ldy); break;
+#define TGM_GV(MM)                                                                                                \
+  case MM:                                                                                                        \
+    hipLaunchKernelGGL((dec_gemv_bf16<MM, MM == 1 ? 1 : 4>), dim3(blocks), dim3(256), 0, st, wp, (int)n, (int)k, xp, \
+                       ldx, y, ldy);                                                                              \
+    break;
     TGM_GV(1) TGM_GV(2) TGM_GV(3) TGM_GV(4) TGM_GV(5) TGM_GV(6) TGM_GV(7) TGM_GV(8)
 #undef TGM_GV
   }
