@@ -46,11 +46,29 @@ int tgm_dec_embed(const void* table, int64_t vocab, int64_t d, const int32_t* to
 int tgm_dec_add_rmsnorm(float* h, const float* delta, int64_t rows, int64_t d, const void* weight, float eps,
                         void* out, int out_dtype, void* stream);
 
-/* Rotary position embedding (pairs (i, i + head_dim / 2), angle p * base^(-2 i / head_dim),
- * evaluated in double) applied in place to the q and k heads of qkv; the rotated k heads and
- * the v heads are stored as bf16 into the caches at each token's position. */
+/* Rotary position embedding (rotate-half pairs (i, i + head_dim / 2), angle p * base^(-2 i /
+ * head_dim)) applied in place to the q and k heads of qkv; the rotated k heads and the v heads
+ * are stored as bf16 into the caches at each token's position.  For the prefill GEMMs it can
+ * also write (each may be NULL) bf16 operands split into `parts` (1 to 3) terms, x = t_0 +
+ * t_1 + ... with t_0 = bf16(x) and t_s = bf16 of what the earlier terms leave (three terms hold
+ * all 24 bits of an fp32 value):
+ *   q_out  [batch, heads, seq_rows, parts * head_dim]: the terms of the rotated q side by side;
+ *   k_out  [batch, kv_heads, seq_rows, parts * head_dim]: the cached k, `parts` times;
+ *   vt_out [batch, kv_heads, head_dim, ld_vt]: the cached v transposed, token t at columns
+ *          s * ld_vt / parts + t for each term s (ld_vt a multiple of parts, ld_vt / parts >=
+ *          seq_rows);
+ * so that one bf16 MFMA GEMM of q_out against k_out gives q . k^T with fp32-like accuracy. */
 int tgm_dec_rope_kv(float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, int64_t kv_heads, int64_t head_dim,
-                    const int32_t* pos, double rope_base, void* k_cache, void* v_cache, int64_t max_seq, void* stream);
+                    const int32_t* pos, double rope_base, void* k_cache, void* v_cache, int64_t max_seq, void* q_out,
+                    void* k_out, void* vt_out, int64_t ld_vt, int64_t parts, void* stream);
+
+/* Causal softmax of prefill scores: for row = z * seq_rows + t (float32, row stride ld_scores),
+ * p[j] = softmax over j <= t of scale * scores[row, j] is split into `parts` (1 to 3) bf16 terms
+ * as in tgm_dec_rope_kv, term s at probs[row, s * ld_probs / parts + j], all 0 for
+ * t < j < ld_probs / parts (ld_probs a multiple of parts, ld_probs / parts >= seq_rows), so that
+ * one GEMM of probs against the vt_out of tgm_dec_rope_kv (K = ld_probs) gives P . V. */
+int tgm_dec_causal_softmax(const float* scores, int64_t rows, int64_t seq_rows, int64_t ld_scores, float scale,
+                           void* probs, int64_t ld_probs, int64_t parts, void* stream);
 
 /* Causal grouped-query attention of every q head over its kv head's cache, positions
  * 0 .. pos(token) (softmax of q.k / sqrt(head_dim) in fp32).  head_dim is 64 or 128; heads /

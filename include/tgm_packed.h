@@ -167,6 +167,20 @@ int tgm_gemm_dense(const void* a, int a_dtype, int64_t m, int64_t lda, const voi
                    int64_t ldb, int64_t k, void* c, int c_dtype, int64_t ldc, void* stream);
 
 /*
+ * The same product for ``batch`` independent matrices (the reference's tinygrad lowering
+ * handles one scheduled matrix reduction per kernel; a batch here is one launch): batch z uses
+ * A + z * stride_a, B + (z / b_group) * stride_b and
+ * C + (z / c_group) * stride_c_group + (z % c_group) * stride_c (element offsets), so b_group
+ * consecutive batches can share one B (grouped-query attention's shared keys) and the outputs
+ * of c_group consecutive batches can interleave (heads side by side in one token row).
+ * c_group = batch with stride_c_group = 0 gives plain C + z * stride_c.  At most 65535 batches.
+ */
+int tgm_gemm_dense_batched(const void* a, int a_dtype, int64_t m, int64_t lda, int64_t stride_a, const void* b,
+                           int b_dtype, int64_t n, int64_t ldb, int64_t stride_b, int64_t b_group, int64_t k, void* c,
+                           int c_dtype, int64_t ldc, int64_t stride_c, int64_t c_group, int64_t stride_c_group,
+                           int64_t batch, void* stream);
+
+/*
  * out[j, i] = in[i, j] for 16-bit elements: in is [rows, cols] (row stride ld_in), out is
  * [cols, rows] (row stride ld_out).  Stages a row-major [K, N] operand as [N, K] for
  * tgm_gemm_dense (the reference stages operands it cannot bind directly, matmul.py:218-226).

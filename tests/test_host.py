@@ -177,6 +177,42 @@ def test_library_exports_every_declared_symbol():
     assert lib.tgm_abi_version() == K.ABI_VERSION
 
 
+def declared_arities() -> dict[str, int]:
+    """Parameter count of every function declared in include/*.h."""
+    text = "\n".join(h.read_text() for h in sorted((ROOT / "include").glob("*.h")))
+    found = {}
+    for m in re.finditer(r"^(?:int|int64_t|const char\*)\s+(tgm_\w+)\(([^)]*)\);", text, flags=re.M):
+        params = m.group(2).strip()
+        found[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return found
+
+
+def test_binding_arities_match_the_headers():
+    """The ctypes argument lists have one entry per declared parameter, and every
+    ``K.call("tgm_...", ...)`` in the package, the tests and the bench passes that many."""
+    import ast
+
+    arity = declared_arities()
+    assert set(arity) == set(declared_functions())
+    lib = K.load_library()
+    for name, n in arity.items():
+        argtypes = getattr(lib, name).argtypes
+        assert argtypes is not None and len(argtypes) == n, name
+    sources = [*(ROOT / "tinygrad-dx12_amd").rglob("*.py"), *(ROOT / "tests").glob("*.py"), ROOT / "bench.py",
+               ROOT / "__graft_entry__.py"]
+    calls = 0
+    for path in sources:
+        for node in ast.walk(ast.parse(path.read_text())):
+            if (isinstance(node, ast.Call) and isinstance(node.func, ast.Attribute) and node.func.attr == "call"
+                    and node.args and isinstance(node.args[0], ast.Constant) and isinstance(node.args[0].value, str)
+                    and node.args[0].value.startswith("tgm_")
+                    and not any(isinstance(a, ast.Starred) for a in node.args)):
+                name = node.args[0].value
+                assert len(node.args) - 1 == arity[name], f"{path.name}:{node.lineno} {name}"
+                calls += 1
+    assert calls > 40
+
+
 def test_invalid_arguments_are_rejected_without_a_gpu():
     """Argument validation runs on the host and maps to ValueError (no kernel is launched)."""
     with pytest.raises(ValueError, match="unknown packed format"):

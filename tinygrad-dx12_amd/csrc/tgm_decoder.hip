@@ -30,6 +30,7 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 __device__ __forceinline__ float lo_bf16(unsigned w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) { return __builtin_bit_cast(float, (unsigned)h << 16); }
 __device__ __forceinline__ float hi_bf16(unsigned w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
 
 // ------------------------------------------------------------------ embedding
@@ -134,7 +135,9 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, int p, int i, int 
 // Grid (rows, heads + kv_heads), head_dim / 2 threads: thread i rotates the pair
 // (i, i + head_dim / 2) of one q or k head; k heads also store k (rotated) and v as bf16.
 __global__ void dec_rope_kv(float* __restrict__ qkv, int T, int H, int HK, int hd, const int32_t* __restrict__ pos,
-                            double log2_base, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int max_seq) {
+                            double log2_base, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int max_seq,
+                            uint16_t* __restrict__ qs, uint16_t* __restrict__ ks, uint16_t* __restrict__ vt,
+                            int64_t ldvt, int parts) {
   const int64_t r = blockIdx.x;
   const int hh = blockIdx.y, i = threadIdx.x, half = hd / 2;
   const int b = (int)(r / T), t = (int)(r % T);
@@ -145,14 +148,73 @@ __global__ void dec_rope_kv(float* __restrict__ qkv, int T, int H, int HK, int h
   rope_pair(x[i], x[i + half], p, i, hd, log2_base, y1, y2);
   x[i] = y1;
   x[i + half] = y2;
+  if (hh < H && qs) {  // rotated q split into `parts` bf16 terms, [b, head, t, parts * hd]
+    const int64_t o = (((int64_t)b * H + hh) * T + t) * parts * hd;
+    float r1 = y1, r2 = y2;
+    for (int s = 0; s < parts; ++s) {
+      const uint16_t a1 = f32_to_bf16(r1), a2 = f32_to_bf16(r2);
+      qs[o + s * hd + i] = a1;
+      qs[o + s * hd + i + half] = a2;
+      r1 -= bf16_bits_to_f32(a1);  // exact in fp32: the residual has at most 16 significant bits
+      r2 -= bf16_bits_to_f32(a2);
+    }
+  }
   if (hh >= H && p >= 0 && p < max_seq) {
     const int j = hh - H;
     const int64_t o = (((int64_t)b * HK + j) * max_seq + p) * hd;
-    kc[o + i] = f32_to_bf16(y1);
-    kc[o + i + half] = f32_to_bf16(y2);
+    const uint16_t k1 = f32_to_bf16(y1), kk2 = f32_to_bf16(y2);
+    kc[o + i] = k1;
+    kc[o + i + half] = kk2;
     const float* v = qkv + r * ld + (int64_t)(H + HK + j) * hd;
-    vc[o + i] = f32_to_bf16(v[i]);
-    vc[o + i + half] = f32_to_bf16(v[i + half]);
+    const uint16_t v1 = f32_to_bf16(v[i]), v2 = f32_to_bf16(v[i + half]);
+    vc[o + i] = v1;
+    vc[o + i + half] = v2;
+    if (ks) {  // the cached k `parts` times, [b, kv head, t, parts * hd], against q's terms
+      const int64_t o2 = (((int64_t)b * HK + j) * T + t) * parts * hd;
+      for (int s = 0; s < parts; ++s) {
+        ks[o2 + s * hd + i] = k1;
+        ks[o2 + s * hd + i + half] = kk2;
+      }
+    }
+    if (vt) {  // v transposed `parts` times, [b, kv head, hd, ldvt] at columns s * ldvt / parts + t
+      const int64_t ot = ((int64_t)b * HK + j) * hd, w = ldvt / parts;
+      for (int s = 0; s < parts; ++s) {
+        vt[(ot + i) * ldvt + s * w + t] = v1;
+        vt[(ot + i + half) * ldvt + s * w + t] = v2;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ prefill softmax
+// p[j] = softmax over j <= t of scale * S[row, j] for row = z * T + t (causal, the prompt
+// starting at position 0), split into `parts` bf16 terms: term s of p[j] at P[row, s * w + j]
+// (w = ldp / parts; term 0 = bf16(p), term s = bf16 of what the earlier terms leave), all 0 for
+// t < j < w.  One wave per row.
+__global__ void __launch_bounds__(256) dec_causal_softmax(const float* __restrict__ S, int64_t rows, int T,
+                                                          int64_t lds_, float scale, uint16_t* __restrict__ P,
+                                                          int64_t ldp, int parts) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;  // whole waves leave together
+  const int len = (int)(row % T) + 1;
+  const float* s = S + row * lds_;
+  uint16_t* pr = P + row * ldp;
+  float mx = -INFINITY;
+  for (int j = lane; j < len; j += 64) mx = fmaxf(mx, s[j]);
+  mx = wave_max(mx);
+  float sum = 0.f;
+  for (int j = lane; j < len; j += 64) sum += expf((s[j] - mx) * scale);
+  sum = wave_sum(sum);
+  const float inv = 1.0f / sum;
+  const int64_t w = ldp / parts;
+  for (int j = lane; j < w; j += 64) {
+    float r = j < len ? expf((s[j] - mx) * scale) * inv : 0.f;
+    for (int q = 0; q < parts; ++q) {
+      const uint16_t a = f32_to_bf16(r);
+      pr[q * w + j] = a;
+      r -= bf16_bits_to_f32(a);
+    }
   }
 }
 
@@ -541,7 +603,8 @@ extern "C" int tgm_dec_add_rmsnorm(float* h, const float* delta, int64_t rows, i
 
 extern "C" int tgm_dec_rope_kv(float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, int64_t kv_heads,
                                int64_t head_dim, const int32_t* pos, double rope_base, void* k_cache, void* v_cache,
-                               int64_t max_seq, void* stream) {
+                               int64_t max_seq, void* q_out, void* k_out, void* vt_out, int64_t ld_vt,
+                               int64_t parts, void* stream) {
   clear_error();
   TGM_CHECK_ARG(qkv && pos && k_cache && v_cache, "null operand");
   TGM_CHECK_ARG(rows >= 0 && seq_rows > 0 && rows % seq_rows == 0, "rows must be a multiple of seq_rows");
@@ -549,10 +612,14 @@ extern "C" int tgm_dec_rope_kv(float* qkv, int64_t rows, int64_t seq_rows, int64
   TGM_CHECK_ARG(head_dim > 0 && head_dim % 2 == 0 && head_dim <= 1024, "head_dim must be even and at most 1024");
   TGM_CHECK_ARG(max_seq > 0 && max_seq < (1ll << 31) && rows < (1ll << 31), "invalid cache sizes");
   TGM_CHECK_ARG(rope_base > 0.0, "rope base must be positive");
+  TGM_CHECK_ARG(!(q_out || k_out || vt_out) || (parts >= 1 && parts <= 3), "parts must be 1, 2 or 3");
+  TGM_CHECK_ARG(!vt_out || (ld_vt % parts == 0 && ld_vt / parts >= seq_rows),
+                "ld_vt must be a multiple of parts and at least parts * seq_rows");
   if (rows == 0) return TGM_OK;
   hipLaunchKernelGGL(dec_rope_kv, dim3((unsigned)rows, (unsigned)(heads + kv_heads)), dim3((unsigned)(head_dim / 2)), 0,
                      (hipStream_t)stream, qkv, (int)seq_rows, (int)heads, (int)kv_heads, (int)head_dim, pos, log2(rope_base),
-                     (uint16_t*)k_cache, (uint16_t*)v_cache, (int)max_seq);
+                     (uint16_t*)k_cache, (uint16_t*)v_cache, (int)max_seq, (uint16_t*)q_out, (uint16_t*)k_out, (uint16_t*)vt_out,
+                     ld_vt, (int)parts);
   return launch_status("tgm_dec_rope_kv");
 }
 
@@ -610,6 +677,20 @@ extern "C" int tgm_dec_attention(const float* qkv, int64_t rows, int64_t seq_row
   else
     hipLaunchKernelGGL(dec_attention_merge<128>, mgrid, dim3(128), 0, st, part, (int)splits, (int)heads, out, out_dtype);
   return launch_status("tgm_dec_attention");
+}
+
+extern "C" int tgm_dec_causal_softmax(const float* scores, int64_t rows, int64_t seq_rows, int64_t ld_scores,
+                                      float scale, void* probs, int64_t ld_probs, int64_t parts, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(scores && probs, "null operand");
+  TGM_CHECK_ARG(rows >= 0 && seq_rows > 0 && rows % seq_rows == 0, "rows must be a multiple of seq_rows");
+  TGM_CHECK_ARG(parts >= 1 && parts <= 3, "parts must be 1, 2 or 3");
+  TGM_CHECK_ARG(ld_scores >= seq_rows && ld_probs % parts == 0 && ld_probs / parts >= seq_rows,
+                "ld_scores must be at least seq_rows, ld_probs a multiple of parts and at least parts * seq_rows");
+  if (rows == 0) return TGM_OK;
+  hipLaunchKernelGGL(dec_causal_softmax, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, scores,
+                     rows, (int)seq_rows, ld_scores, scale, (uint16_t*)probs, ld_probs, (int)parts);
+  return launch_status("tgm_dec_causal_softmax");
 }
 
 extern "C" int tgm_dec_silu_mul(const float* gate_up, int64_t rows, int64_t ffn, void* out, int out_dtype,

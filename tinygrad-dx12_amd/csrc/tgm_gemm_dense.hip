@@ -6,7 +6,8 @@
 //
 //   C[m, n] = sum_k A[m, k] * B[n, k]      A [M, K] (row stride lda), B [N, K] (row stride ldb)
 //
-// i.e. A @ B^T with both operands K-contiguous; a row-major B [K, N] is first transposed by
+// i.e. A @ B^T with both operands K-contiguous (batched over blockIdx.y with per-operand
+// strides; consecutive batches may share B); a row-major B [K, N] is first transposed by
 // tgm_transpose16 (the caller's staging copy, as the reference stages operands it cannot
 // bind directly, matmul.py:218-226).  Products of two bf16 or two f16 values are exact in
 // fp32; accumulation is fp32 and the output is rounded once.
@@ -31,11 +32,18 @@ constexpr int kDRow = kDK * 2;                        // bytes per panel row and
 constexpr int kDStage = (kDM + kDN) * kDRow;          // 48 KB
 constexpr int kDGroupM = 8;
 
+// Batched: blockIdx.y = z selects A + z * sa, B + (z / b_group) * sb and
+// C + (z / c_group) * scg + (z % c_group) * sc (elements).
 template <bool BF16>
 __global__ void __launch_bounds__(512) gemm_dense(const uint8_t* __restrict__ a, unsigned lda_bytes,
                                                   const uint8_t* __restrict__ b, unsigned ldb_bytes, int M, int N,
-                                                  int K, void* __restrict__ c, int cdt, int64_t ldc) {
+                                                  int K, void* __restrict__ c, int cdt, int64_t ldc, int64_t sa,
+                                                  int64_t sb, int64_t sc, int b_group, int c_group, int64_t scg) {
   constexpr int FA = 2, FB = 2;
+  const int z = blockIdx.y;
+  a += z * sa * 2;
+  b += (z / b_group) * sb * 2;
+  c = (uint8_t*)c + ((int64_t)(z / c_group) * scg + (int64_t)(z % c_group) * sc) * dtype_size(cdt);
   __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kDStage];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -129,13 +137,11 @@ __global__ void __launch_bounds__(256) transpose16(const uint16_t* __restrict__ 
   __shared__ uint16_t t[64][65];
   const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-#pragma unroll
   for (int i = ty; i < 64; i += 4) {
     const int r = r0 + i, cc = c0 + tx;
     if (r < rows && cc < cols) t[i][tx] = in[(int64_t)r * ld_in + cc];
   }
   __syncthreads();
-#pragma unroll
   for (int i = ty; i < 64; i += 4) {
     const int cc = c0 + i, r = r0 + tx;
     if (cc < cols && r < rows) out[(int64_t)cc * ld_out + r] = t[tx][i];
@@ -146,36 +152,48 @@ __global__ void __launch_bounds__(256) transpose16(const uint16_t* __restrict__ 
 
 using namespace tgm;
 
-extern "C" int tgm_gemm_dense(const void* a, int a_dtype, int64_t m, int64_t lda, const void* b, int b_dtype, int64_t n,
-                              int64_t ldb, int64_t k, void* c, int c_dtype, int64_t ldc, void* stream) {
+extern "C" int tgm_gemm_dense_batched(const void* a, int a_dtype, int64_t m, int64_t lda, int64_t stride_a,
+                                      const void* b, int b_dtype, int64_t n, int64_t ldb, int64_t stride_b,
+                                      int64_t b_group, int64_t k, void* c, int c_dtype, int64_t ldc, int64_t stride_c,
+                                      int64_t c_group, int64_t stride_c_group,
+                                      int64_t batch, void* stream) {
   clear_error();
   TGM_CHECK_ARG(a && b && c, "null operand");
-  TGM_CHECK_ARG(m >= 0 && n >= 0 && k >= 0, "invalid gemm sizes");
+  TGM_CHECK_ARG(m >= 0 && n >= 0 && k >= 0 && batch >= 0 && b_group >= 1 && c_group >= 1,
+                "invalid gemm sizes");
   TGM_CHECK_ARG(m <= 1 || lda >= k, "lda smaller than K");
   TGM_CHECK_ARG(n <= 1 || ldb >= k, "ldb smaller than K");
   TGM_CHECK_ARG(m <= 1 || ldc >= n, "ldc smaller than N");
+  TGM_CHECK_ARG(stride_a >= 0 && stride_b >= 0 && stride_c >= 0 && stride_c_group >= 0, "negative batch stride");
   TGM_CHECK_ARG(c_dtype == TGM_BF16 || c_dtype == TGM_F16 || c_dtype == TGM_F32, "output must be bf16, f16 or f32");
-  if (m == 0 || n == 0) return TGM_OK;
+  if (m == 0 || n == 0 || batch == 0) return TGM_OK;
   if (a_dtype != b_dtype || (a_dtype != TGM_BF16 && a_dtype != TGM_F16))
     TGM_UNSUPPORTED("tgm_gemm_dense: operands must both be bf16 or both f16");
   if (k == 0 || k % kDK != 0) TGM_UNSUPPORTED("tgm_gemm_dense: K must be a positive multiple of %d", kDK);
   const int64_t lda_eff = m > 1 ? lda : k, ldb_eff = n > 1 ? ldb : k;
-  if ((lda_eff * 2) % 16 || (ldb_eff * 2) % 16 || (uintptr_t)a % 16 || (uintptr_t)b % 16)
+  if ((lda_eff * 2) % 16 || (ldb_eff * 2) % 16 || (uintptr_t)a % 16 || (uintptr_t)b % 16 ||
+      (batch > 1 && ((stride_a * 2) % 16 || (stride_b * 2) % 16)))
     TGM_UNSUPPORTED("tgm_gemm_dense: operands and their rows must be 16-byte aligned");
   if (m >= (1ll << 31) || n >= (1ll << 31) || (m - 1) * lda_eff * 2 + k * 2 >= (1ll << 32) ||
-      (n - 1) * ldb_eff * 2 + k * 2 >= (1ll << 32))
-    TGM_UNSUPPORTED("tgm_gemm_dense: operands must be under 4 GiB (32-bit offsets)");
+      (n - 1) * ldb_eff * 2 + k * 2 >= (1ll << 32) || batch > 65535)
+    TGM_UNSUPPORTED("tgm_gemm_dense: operands must be under 4 GiB (32-bit offsets), at most 65535 batches");
   const int64_t tiles = ((m + kDM - 1) / kDM) * ((n + kDN - 1) / kDN);
   const hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)tiles, (unsigned)batch);
   if (a_dtype == TGM_BF16)
-    hipLaunchKernelGGL(gemm_dense<true>, dim3((unsigned)tiles), dim3(512), 0, st, (const uint8_t*)a,
-                       (unsigned)(lda_eff * 2), (const uint8_t*)b, (unsigned)(ldb_eff * 2), (int)m, (int)n, (int)k, c,
-                       c_dtype, ldc);
+    hipLaunchKernelGGL(gemm_dense<true>, grid, dim3(512), 0, st, (const uint8_t*)a, (unsigned)(lda_eff * 2),
+                       (const uint8_t*)b, (unsigned)(ldb_eff * 2), (int)m, (int)n, (int)k, c, c_dtype, ldc, stride_a,
+                       stride_b, stride_c, (int)b_group, (int)c_group, stride_c_group);
   else
-    hipLaunchKernelGGL(gemm_dense<false>, dim3((unsigned)tiles), dim3(512), 0, st, (const uint8_t*)a,
-                       (unsigned)(lda_eff * 2), (const uint8_t*)b, (unsigned)(ldb_eff * 2), (int)m, (int)n, (int)k, c,
-                       c_dtype, ldc);
+    hipLaunchKernelGGL(gemm_dense<false>, grid, dim3(512), 0, st, (const uint8_t*)a, (unsigned)(lda_eff * 2),
+                       (const uint8_t*)b, (unsigned)(ldb_eff * 2), (int)m, (int)n, (int)k, c, c_dtype, ldc, stride_a,
+                       stride_b, stride_c, (int)b_group, (int)c_group, stride_c_group);
   return launch_status("tgm_gemm_dense");
+}
+
+extern "C" int tgm_gemm_dense(const void* a, int a_dtype, int64_t m, int64_t lda, const void* b, int b_dtype, int64_t n,
+                              int64_t ldb, int64_t k, void* c, int c_dtype, int64_t ldc, void* stream) {
+  return tgm_gemm_dense_batched(a, a_dtype, m, lda, 0, b, b_dtype, n, ldb, 0, 1, k, c, c_dtype, ldc, 0, 1, 0, 1, stream);
 }
 
 extern "C" int tgm_transpose16(const void* in, int64_t rows, int64_t cols, int64_t ld_in, void* out, int64_t ld_out,

@@ -190,6 +190,19 @@ class Decoder:
         self.v_cache = torch.zeros(cache, dtype=torch.bfloat16, device=dev)
         self.splits = min(max(1, math.ceil(max_seq / 64)), 32)
         self.fuse_rope = True
+        # prompts of several tokens: attention as two batched MFMA GEMMs around a causal softmax
+        # (scores for every (sequence, head) pair at once) instead of the per-token split kernel
+        # (3 bf16 terms per operand value: the accuracy of fp32; 1 or 2 trade it for GEMM work)
+        self.mfma_prefill = max_prompt > 1
+        self.prefill_parts = 3
+        if self.mfma_prefill:
+            hd, tp, n = cfg.head_dim, -(-max_prompt // 64) * 64, 3
+            b16 = dict(dtype=torch.bfloat16, device=dev)
+            self.q_terms = torch.empty((batch * cfg.heads * max_prompt * n * hd,), **b16)
+            self.k_terms = torch.empty((batch * cfg.kv_heads * max_prompt * n * hd,), **b16)
+            self.vt = torch.zeros((batch * cfg.kv_heads * hd * n * tp,), **b16)
+            self.scores = torch.empty((batch * cfg.heads * max_prompt * tp,), **f32)
+            self.probs = torch.empty((batch * cfg.heads * max_prompt * n * tp,), **b16)
         # one token: the gate|up GEMV applies SwiGLU itself when its row-streaming kernel covers the shape
         self.fuse_swiglu = (cfg.hidden % 2048 == 0 and cfg.hidden <= 16384)
         ws = K.load_library().tgm_dec_attention_workspace(batch, cfg.heads, cfg.head_dim, self.splits)
@@ -212,13 +225,17 @@ class Decoder:
             _packed_product(self.xn16, rows, d, L.wqkv, self.qkv, cfg.qkv_rows, stream)
             kc, vc = self.k_cache[li], self.v_cache[li]
             fused = seq_rows == 1 and self.fuse_rope  # one new token per sequence: RoPE + cache store in attention
-            if not fused:
-                K.call("tgm_dec_rope_kv", self.qkv.data_ptr(), rows, seq_rows, cfg.heads, cfg.kv_heads, cfg.head_dim,
-                       self.pos.data_ptr(), cfg.rope_base, kc.data_ptr(), vc.data_ptr(), self.max_seq, stream)
-            K.call("tgm_dec_attention", self.qkv.data_ptr(), rows, seq_rows, cfg.heads, cfg.kv_heads, cfg.head_dim,
-                   self.pos.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.max_seq, cfg.rope_base if fused else 0.0,
-                   splits, self.workspace.data_ptr() if splits > 1 else None,
-                   self.workspace_bytes if splits > 1 else 0, self.attn.data_ptr(), F16, stream)
+            if seq_rows > 1 and self.mfma_prefill:
+                self._prefill_attention(rows, seq_rows, kc, vc, stream)
+            else:
+                if not fused:
+                    K.call("tgm_dec_rope_kv", self.qkv.data_ptr(), rows, seq_rows, cfg.heads, cfg.kv_heads,
+                           cfg.head_dim, self.pos.data_ptr(), cfg.rope_base, kc.data_ptr(), vc.data_ptr(),
+                           self.max_seq, None, None, None, 0, 1, stream)
+                K.call("tgm_dec_attention", self.qkv.data_ptr(), rows, seq_rows, cfg.heads, cfg.kv_heads,
+                       cfg.head_dim, self.pos.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.max_seq,
+                       cfg.rope_base if fused else 0.0, splits, self.workspace.data_ptr() if splits > 1 else None,
+                       self.workspace_bytes if splits > 1 else 0, self.attn.data_ptr(), F16, stream)
             _packed_product(self.attn, rows, cfg.heads * cfg.head_dim, L.wo, self.delta, d, stream)
             K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr(), rows, d, L.ffn_norm.data_ptr(),
                    cfg.eps, self.xnb.data_ptr(), BF16, stream)
@@ -233,6 +250,38 @@ class Decoder:
             _packed_product(self.act, rows, cfg.ffn, L.w_down, self.delta, d, stream)
         K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr(), rows, d, self.w.final_norm.data_ptr(),
                cfg.eps, self.xnb.data_ptr(), BF16, stream)
+
+    def _prefill_attention(self, rows: int, t: int, kc: torch.Tensor, vc: torch.Tensor, stream: int) -> None:
+        """Causal attention of a whole prompt (positions 0 .. t - 1 of every sequence) as two
+        batched bf16 MFMA GEMMs around a softmax.  The first operand of each product is split
+        into n = ``prefill_parts`` bf16 terms (x = bf16(x) + bf16(rest) + ..., three terms
+        hold an fp32 value) side by side along K, against n copies of the second operand, so
+        the products keep fp32 accuracy for n times the (small) GEMM work:
+
+        1. RoPE; k and v go to the caches; the q terms [seq, head, t, n hd], k n times [seq,
+           kv head, t, n hd] and v transposed n times [seq, kv head, hd, n tp] (tp = t rounded
+           up to 64) for the GEMMs;
+        2. S = q k^T for every (sequence, head) pair in fp32, the heads / kv_heads q heads of a
+           group sharing their kv head's keys;
+        3. P = causal softmax(S / sqrt(hd)) as n terms, zero beyond each row's position;
+        4. O = P v over the padded key count, written as f16 straight into the [token,
+           head * hd] rows of the attention output.
+        """
+        cfg = self.cfg
+        H, HK, hd, n = cfg.heads, cfg.kv_heads, cfg.head_dim, self.prefill_parts
+        if not 1 <= n <= 3:
+            raise ValueError("prefill_parts must be 1, 2 or 3")
+        tp = -(-t // 64) * 64
+        z, g = self.batch * H, H // HK
+        K.call("tgm_dec_rope_kv", self.qkv.data_ptr(), rows, t, H, HK, hd, self.pos.data_ptr(), cfg.rope_base,
+               kc.data_ptr(), vc.data_ptr(), self.max_seq, self.q_terms.data_ptr(), self.k_terms.data_ptr(),
+               self.vt.data_ptr(), n * tp, n, stream)
+        K.call("tgm_gemm_dense_batched", self.q_terms.data_ptr(), BF16, t, n * hd, t * n * hd, self.k_terms.data_ptr(),
+               BF16, t, n * hd, t * n * hd, g, n * hd, self.scores.data_ptr(), F32, tp, t * tp, z, 0, z, stream)
+        K.call("tgm_dec_causal_softmax", self.scores.data_ptr(), z * t, t, tp, 1.0 / math.sqrt(hd),
+               self.probs.data_ptr(), n * tp, n, stream)
+        K.call("tgm_gemm_dense_batched", self.probs.data_ptr(), BF16, t, n * tp, t * n * tp, self.vt.data_ptr(), BF16,
+               hd, n * tp, hd * n * tp, g, n * tp, self.attn.data_ptr(), F16, H * hd, hd, H, t * H * hd, z, stream)
 
     def _head(self, first_row: int, row_stride: int, stream: int, advance: bool) -> None:
         """Output head over one normed row per sequence (rows first_row + b * row_stride of the

@@ -47,12 +47,16 @@ _SIGNATURES = {
     "tgm_quantize_mx": (_P, _INT, _I64, _I64, _INT, _I64, _P, _P, _P),
     "tgm_pack_codes": (_P, _I64, _INT, _P, _P),
     "tgm_gemm_dense": (_P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _I64, _P, _INT, _I64, _P),
+    "tgm_gemm_dense_batched": (_P, _INT, _I64, _I64, _I64, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P, _INT, _I64, _I64,
+                               _I64, _I64, _I64, _P),
     "tgm_gemv_swiglu": (_P, _INT, _I64, _I64, _P, _INT, _I64, _P, _INT, _P, _INT, _P),
     "tgm_transpose16": (_P, _I64, _I64, _I64, _P, _I64, _P),
     # decoder-step kernels (include/tgm_decoder.h)
     "tgm_dec_embed": (_P, _I64, _I64, _P, _I64, _P, _P),
     "tgm_dec_add_rmsnorm": (_P, _P, _I64, _I64, _P, ctypes.c_float, _P, _INT, _P),
-    "tgm_dec_rope_kv": (_P, _I64, _I64, _I64, _I64, _I64, _P, ctypes.c_double, _P, _P, _I64, _P),
+    "tgm_dec_rope_kv": (_P, _I64, _I64, _I64, _I64, _I64, _P, ctypes.c_double, _P, _P, _I64, _P, _P, _P, _I64, _I64,
+                        _P),
+    "tgm_dec_causal_softmax": (_P, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _I64, _P),
     "tgm_dec_attention": (_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, ctypes.c_double, _I64, _P, _I64, _P, _INT,
                           _P),
     "tgm_dec_silu_mul": (_P, _I64, _I64, _P, _INT, _P),
