@@ -55,8 +55,8 @@ int tgm_dec_add_rmsnorm(float* h, const float* delta, int64_t rows, int64_t d, c
  *   q_out  [batch, heads, seq_rows, parts * head_dim]: the terms of the rotated q side by side;
  *   k_out  [batch, kv_heads, seq_rows, parts * head_dim]: the cached k, `parts` times;
  *   vt_out [batch, kv_heads, head_dim, ld_vt]: the cached v transposed, token t at columns
- *          s * ld_vt / parts + t for each term s (ld_vt a multiple of parts, ld_vt / parts >=
- *          seq_rows);
+ *          s * ld_vt / parts + t for each term s (ld_vt / parts >= seq_rows and a multiple of
+ *          8, head_dim % 8 == 0, 16-byte aligned; tokens past max_seq are not written);
  * so that one bf16 MFMA GEMM of q_out against k_out gives q . k^T with fp32-like accuracy. */
 int tgm_dec_rope_kv(float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, int64_t kv_heads, int64_t head_dim,
                     const int32_t* pos, double rope_base, void* k_cache, void* v_cache, int64_t max_seq, void* q_out,
@@ -66,7 +66,8 @@ int tgm_dec_rope_kv(float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, i
  * p[j] = softmax over j <= t of scale * scores[row, j] is split into `parts` (1 to 3) bf16 terms
  * as in tgm_dec_rope_kv, term s at probs[row, s * ld_probs / parts + j], all 0 for
  * t < j < ld_probs / parts (ld_probs a multiple of parts, ld_probs / parts >= seq_rows), so that
- * one GEMM of probs against the vt_out of tgm_dec_rope_kv (K = ld_probs) gives P . V. */
+ * one GEMM of probs against the vt_out of tgm_dec_rope_kv (K = ld_probs) gives P . V.
+ * ld_scores must be a multiple of 4, ld_probs / parts of 8, and both buffers 16-byte aligned. */
 int tgm_dec_causal_softmax(const float* scores, int64_t rows, int64_t seq_rows, int64_t ld_scores, float scale,
                            void* probs, int64_t ld_probs, int64_t parts, void* stream);
 

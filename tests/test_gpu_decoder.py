@@ -98,14 +98,16 @@ def _terms(x: torch.Tensor, parts: int) -> list[torch.Tensor]:
 @pytest.mark.parametrize("parts", [1, 2, 3])
 def test_rope_kv_prefill_outputs(dev, parts):
     """The GEMM operands of prompt attention: the bf16 terms of the rotated q side by side, the
-    cached k `parts` times and the cached v transposed `parts` times; three terms add up to the
-    fp32 q exactly; columns of the transposed v outside the prompt stay untouched."""
+    cached k `parts` times and the cached v transposed `parts` times (from the positions the
+    tokens were cached at); three terms add up to the fp32 q exactly; columns of the transposed
+    v outside the prompt stay untouched."""
     rng = np.random.default_rng(4)
     B, T, H, HK, hd, max_seq = 2, 37, 8, 2, 128, 64
     w = 64
     ld = parts * w
     qkv = torch.from_numpy(rng.standard_normal((B * T, (H + 2 * HK) * hd)).astype(np.float32)).to(dev)
-    pos = torch.zeros(B, dtype=torch.int32, device=dev)
+    starts = (0, 3)
+    pos = torch.tensor(starts, dtype=torch.int32, device=dev)
     kc = torch.zeros((B, HK, max_seq, hd), dtype=torch.bfloat16, device=dev)
     vc = torch.zeros_like(kc)
     qs = torch.zeros((B, H, T, parts * hd), dtype=torch.bfloat16, device=dev)
@@ -119,10 +121,11 @@ def test_rope_kv_prefill_outputs(dev, parts):
     assert ((total - q.double()).abs() <= 2.0 ** (-8 * parts) * q.double().abs()).all()
     if parts == 3:
         assert torch.equal(total.float(), q)
-    vtt = vc[:, :, :T].transpose(2, 3)
-    for s in range(parts):
-        assert torch.equal(ks[..., s * hd:(s + 1) * hd], kc[:, :, :T])
-        assert torch.equal(vt[..., s * w:s * w + T], vtt) and (vt[..., s * w + T:(s + 1) * w] == 7.0).all()
+    for b, p0 in enumerate(starts):  # the terms follow the cache entries at positions p0 .. p0 + T - 1
+        vtt = vc[b, :, p0:p0 + T].transpose(1, 2)
+        for s in range(parts):
+            assert torch.equal(ks[b, ..., s * hd:(s + 1) * hd], kc[b, :, p0:p0 + T])
+            assert torch.equal(vt[b, ..., s * w:s * w + T], vtt) and (vt[b, ..., s * w + T:(s + 1) * w] == 7.0).all()
 
 
 @pytest.mark.parametrize("parts", [1, 2, 3])

@@ -136,8 +136,7 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, int p, int i, int 
 // (i, i + head_dim / 2) of one q or k head; k heads also store k (rotated) and v as bf16.
 __global__ void dec_rope_kv(float* __restrict__ qkv, int T, int H, int HK, int hd, const int32_t* __restrict__ pos,
                             double log2_base, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int max_seq,
-                            uint16_t* __restrict__ qs, uint16_t* __restrict__ ks, uint16_t* __restrict__ vt,
-                            int64_t ldvt, int parts) {
+                            uint16_t* __restrict__ qs, uint16_t* __restrict__ ks, int parts) {
   const int64_t r = blockIdx.x;
   const int hh = blockIdx.y, i = threadIdx.x, half = hd / 2;
   const int b = (int)(r / T), t = (int)(r % T);
@@ -176,13 +175,52 @@ __global__ void dec_rope_kv(float* __restrict__ qkv, int T, int H, int HK, int h
         ks[o2 + s * hd + i + half] = kk2;
       }
     }
-    if (vt) {  // v transposed `parts` times, [b, kv head, hd, ldvt] at columns s * ldvt / parts + t
-      const int64_t ot = ((int64_t)b * HK + j) * hd, w = ldvt / parts;
-      for (int s = 0; s < parts; ++s) {
-        vt[(ot + i) * ldvt + s * w + t] = v1;
-        vt[(ot + i + half) * ldvt + s * w + t] = v2;
+  }
+}
+
+// Grid (ceil(T / 64), batch * kv_heads), 256 threads: the cached v of 64 tokens of one kv head
+// (bf16 [64, hd] at positions pos[b] + t, as tgm_dec_rope_kv stored them; tokens past the cache
+// are skipped) transposed through LDS, 128 columns at a time, into `parts` copies of vt [hd,
+// ldvt] at columns s * ldvt / parts + t; each thread stores 8 tokens (16 bytes) of one row.
+// Needs hd % 8 == 0 and ldvt / parts % 8 == 0.
+__global__ void __launch_bounds__(256) dec_vt_terms(const uint16_t* __restrict__ vc, const int32_t* __restrict__ pos,
+                                                    int T, int HK, int hd, int max_seq, uint16_t* __restrict__ vt,
+                                                    int64_t ldvt, int parts) {
+  __shared__ uint16_t tile[64][130];
+  const int t0 = blockIdx.x * 64, tid = threadIdx.x;
+  const int p0 = pos[blockIdx.y / HK];
+  const int rows = min(min(64, T - t0), max_seq - p0 - t0);
+  if (p0 < 0 || rows <= 0) return;  // uniform over the workgroup, before any barrier
+  const uint16_t* src = vc + ((int64_t)blockIdx.y * max_seq + p0 + t0) * hd;
+  uint16_t* dst = vt + (int64_t)blockIdx.y * hd * ldvt + t0;
+  const int64_t w = ldvt / parts;
+  for (int c0 = 0; c0 < hd; c0 += 128) {
+    const int cw = min(128, hd - c0);
+    for (int idx = tid; idx < 64 * 16; idx += 256) {
+      const int r = idx >> 4, c = (idx & 15) * 8;
+      if (r < rows && c < cw) {
+        const dec_u32x4 v = *(const dec_u32x4*)(src + (int64_t)r * hd + c0 + c);
+        unsigned* tp = (unsigned*)&tile[r][c];  // 4-byte aligned: c is even, rows are 260 bytes
+        tp[0] = v[0]; tp[1] = v[1]; tp[2] = v[2]; tp[3] = v[3];
       }
     }
+    __syncthreads();
+    for (int idx = tid; idx < 128 * 8; idx += 256) {
+      const int c = idx >> 3, r = (idx & 7) * 8;
+      if (c < cw && r < rows) {
+        uint16_t* o = dst + (int64_t)(c0 + c) * ldvt + r;
+        if (r + 8 <= rows) {
+          dec_u32x4 pk;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) pk[q] = (unsigned)tile[r + 2 * q][c] | ((unsigned)tile[r + 2 * q + 1][c] << 16);
+          for (int s = 0; s < parts; ++s) *(dec_u32x4*)(o + s * w) = pk;
+        } else {
+          for (int s = 0; s < parts; ++s)
+            for (int e = 0; e < rows - r; ++e) o[s * w + e] = tile[r + e][c];
+        }
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -190,7 +228,8 @@ __global__ void dec_rope_kv(float* __restrict__ qkv, int T, int H, int HK, int h
 // p[j] = softmax over j <= t of scale * S[row, j] for row = z * T + t (causal, the prompt
 // starting at position 0), split into `parts` bf16 terms: term s of p[j] at P[row, s * w + j]
 // (w = ldp / parts; term 0 = bf16(p), term s = bf16 of what the earlier terms leave), all 0 for
-// t < j < w.  One wave per row.
+// t < j < w.  One wave per row; scores are read as float4 (ld_scores % 4 == 0) and each term is
+// written with 16-byte stores (w % 8 == 0).
 __global__ void __launch_bounds__(256) dec_causal_softmax(const float* __restrict__ S, int64_t rows, int T,
                                                           int64_t lds_, float scale, uint16_t* __restrict__ P,
                                                           int64_t ldp, int parts) {
@@ -200,20 +239,54 @@ __global__ void __launch_bounds__(256) dec_causal_softmax(const float* __restric
   const int len = (int)(row % T) + 1;
   const float* s = S + row * lds_;
   uint16_t* pr = P + row * ldp;
-  float mx = -INFINITY;
-  for (int j = lane; j < len; j += 64) mx = fmaxf(mx, s[j]);
-  mx = wave_max(mx);
-  float sum = 0.f;
-  for (int j = lane; j < len; j += 64) sum += expf((s[j] - mx) * scale);
-  sum = wave_sum(sum);
-  const float inv = 1.0f / sum;
+  // pass 1: running (max, sum of exp) per lane over 4-float groups, then across the wave
+  float m = -INFINITY, l = 0.f;
+  for (int j0 = lane * 4; j0 < len; j0 += 256) {
+    dec_f32x4 v;
+    if (j0 + 4 <= len) {
+      v = *(const dec_f32x4*)(s + j0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = j0 + e < len ? s[j0 + e] : -INFINITY;
+    }
+    const float mn = fmaxf(m, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+    l = (m == -INFINITY ? 0.f : l * expf((m - mn) * scale)) + expf((v[0] - mn) * scale) +
+        expf((v[1] - mn) * scale) + expf((v[2] - mn) * scale) + expf((v[3] - mn) * scale);
+    m = mn;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float m2 = __shfl_xor(m, off, 64), l2 = __shfl_xor(l, off, 64);
+    const float mn = fmaxf(m, m2);
+    l = (m == -INFINITY ? 0.f : l * expf((m - mn) * scale)) + (m2 == -INFINITY ? 0.f : l2 * expf((m2 - mn) * scale));
+    m = mn;
+  }
+  const float inv = 1.0f / l;
+  // pass 2: 8 consecutive probabilities per lane, split into terms, 16-byte stores per term
   const int64_t w = ldp / parts;
-  for (int j = lane; j < w; j += 64) {
-    float r = j < len ? expf((s[j] - mx) * scale) * inv : 0.f;
+  for (int j0 = lane * 8; j0 < w; j0 += 512) {
+    float r[8];
+    if (j0 + 8 <= len) {
+      const dec_f32x4 a = *(const dec_f32x4*)(s + j0), b = *(const dec_f32x4*)(s + j0 + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        r[e] = expf((a[e] - m) * scale) * inv;
+        r[e + 4] = expf((b[e] - m) * scale) * inv;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = j0 + e < len ? expf((s[j0 + e] - m) * scale) * inv : 0.f;
+    }
     for (int q = 0; q < parts; ++q) {
-      const uint16_t a = f32_to_bf16(r);
-      pr[q * w + j] = a;
-      r -= bf16_bits_to_f32(a);
+      dec_u32x4 pk;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint16_t lo = f32_to_bf16(r[2 * e]), hi = f32_to_bf16(r[2 * e + 1]);
+        pk[e] = (unsigned)lo | ((unsigned)hi << 16);
+        r[2 * e] -= bf16_bits_to_f32(lo);
+        r[2 * e + 1] -= bf16_bits_to_f32(hi);
+      }
+      *(dec_u32x4*)(pr + q * w + j0) = pk;
     }
   }
 }
@@ -613,13 +686,19 @@ extern "C" int tgm_dec_rope_kv(float* qkv, int64_t rows, int64_t seq_rows, int64
   TGM_CHECK_ARG(max_seq > 0 && max_seq < (1ll << 31) && rows < (1ll << 31), "invalid cache sizes");
   TGM_CHECK_ARG(rope_base > 0.0, "rope base must be positive");
   TGM_CHECK_ARG(!(q_out || k_out || vt_out) || (parts >= 1 && parts <= 3), "parts must be 1, 2 or 3");
-  TGM_CHECK_ARG(!vt_out || (ld_vt % parts == 0 && ld_vt / parts >= seq_rows),
-                "ld_vt must be a multiple of parts and at least parts * seq_rows");
+  TGM_CHECK_ARG(!vt_out || (ld_vt % parts == 0 && ld_vt / parts >= seq_rows && (ld_vt / parts) % 8 == 0 &&
+                             head_dim % 8 == 0 && (uintptr_t)vt_out % 16 == 0 && (uintptr_t)v_cache % 16 == 0),
+                "vt_out needs ld_vt / parts >= seq_rows and a multiple of 8, head_dim % 8 == 0, 16-byte alignment");
+  TGM_CHECK_ARG(!vt_out || rows / seq_rows * kv_heads <= 65535, "too many sequences for vt_out");
   if (rows == 0) return TGM_OK;
   hipLaunchKernelGGL(dec_rope_kv, dim3((unsigned)rows, (unsigned)(heads + kv_heads)), dim3((unsigned)(head_dim / 2)), 0,
                      (hipStream_t)stream, qkv, (int)seq_rows, (int)heads, (int)kv_heads, (int)head_dim, pos, log2(rope_base),
-                     (uint16_t*)k_cache, (uint16_t*)v_cache, (int)max_seq, (uint16_t*)q_out, (uint16_t*)k_out, (uint16_t*)vt_out,
-                     ld_vt, (int)parts);
+                     (uint16_t*)k_cache, (uint16_t*)v_cache, (int)max_seq, (uint16_t*)q_out, (uint16_t*)k_out, (int)parts);
+  if (vt_out) {  // after the cache store on the same stream
+    hipLaunchKernelGGL(dec_vt_terms, dim3((unsigned)((seq_rows + 63) / 64), (unsigned)(rows / seq_rows * kv_heads)),
+                       dim3(256), 0, (hipStream_t)stream, (const uint16_t*)v_cache, pos, (int)seq_rows,
+                       (int)kv_heads, (int)head_dim, (int)max_seq, (uint16_t*)vt_out, ld_vt, (int)parts);
+  }
   return launch_status("tgm_dec_rope_kv");
 }
 
@@ -687,6 +766,9 @@ extern "C" int tgm_dec_causal_softmax(const float* scores, int64_t rows, int64_t
   TGM_CHECK_ARG(parts >= 1 && parts <= 3, "parts must be 1, 2 or 3");
   TGM_CHECK_ARG(ld_scores >= seq_rows && ld_probs % parts == 0 && ld_probs / parts >= seq_rows,
                 "ld_scores must be at least seq_rows, ld_probs a multiple of parts and at least parts * seq_rows");
+  TGM_CHECK_ARG(ld_scores % 4 == 0 && (ld_probs / parts) % 8 == 0 && (uintptr_t)scores % 16 == 0 &&
+                    (uintptr_t)probs % 16 == 0,
+                "ld_scores must be a multiple of 4, ld_probs / parts of 8, both operands 16-byte aligned");
   if (rows == 0) return TGM_OK;
   hipLaunchKernelGGL(dec_causal_softmax, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, scores,
                      rows, (int)seq_rows, ld_scores, scale, (uint16_t*)probs, ld_probs, (int)parts);
