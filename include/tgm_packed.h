@@ -139,6 +139,20 @@ int tgm_gemm_w(const void* a, int a_dtype, int64_t m, int64_t lda,
                void* c, int c_dtype, int64_t ldc, void* stream);
 
 /*
+ * tgm_gemm_w for FP4 weights whose rows interleave the gate (row 2 i) and up (row 2 i + 1)
+ * projections of a SwiGLU block, with the activation in the epilogue:
+ *
+ *   C[m, i] = silu(G[m, 2 i]) * G[m, 2 i + 1],  G = A . deq(W)^T,  silu(g) = g / (1 + exp(-g))
+ *
+ * in fp32, rounded once to c_dtype; C has N / 2 columns (row stride ldc).  The gate and up
+ * products never reach memory.  The reference has no fused activation (a tinygrad caller
+ * applies silu to the matmul's output); tgm_gemv_swiglu is the one-token form.
+ */
+int tgm_gemm_w_swiglu(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n, int64_t k,
+                      const void* scales, int scale_dtype, int64_t block_size, void* c, int c_dtype, int64_t ldc,
+                      void* stream);
+
+/*
  * Kernel family 2 -- block-scaled FP4/FP6 x FP4/FP6 GEMM on gfx950 scaled MFMA
  * (replaces linalg_source for two packed operands, renderer/linalg.py:38-124;
  * the reference decodes both to fp32 first, dx12.py:115-138).

@@ -414,3 +414,33 @@ def test_gemv_swiglu_epilogue(dev, nk):
     g = O.dequant_f64(O.pack_codes(codes, 4), "fp4_e2m1", (n, k), O.e8m0_decode(e), 32) @ np64(x)
     err = O.max_rel_err(np64(fused), D.silu(g[0::2]) * g[1::2])
     assert err <= 1e-2, err
+
+
+@pytest.mark.parametrize("m,n,k,pad", [(300, 1000, 512, 0), (17, 28672 // 8, 4096, 3), (256, 512, 128, 8)])
+@pytest.mark.parametrize("scaled", [True, False])
+def test_gemm_swiglu_epilogue(dev, m, n, k, pad, scaled):
+    """The FP4 GEMM with the SwiGLU epilogue equals the plain GEMM (fp32 out) followed by
+    tgm_dec_silu_mul bit for bit (same accumulators, same fp32 formula), for ragged tiles and
+    output row strides that break the 16-byte stores, and the oracle within 1e-2."""
+    rng = np.random.default_rng(m + n + k)
+    codes = rng.integers(0, 16, (n, k)).astype(np.uint8)
+    e = (127 + rng.integers(-4, 3, (n, k // 32))).astype(np.uint8)
+    sc = torch.from_numpy(e).to(dev).view(torch.float8_e8m0fnu) if scaled else None
+    w = PackedTensor(torch.from_numpy(O.pack_codes(codes, 4)).to(dev), "fp4_e2m1", (n, k), sc, 32)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    ld = n // 2 + pad
+    fused = torch.full((m, ld), 7.0, dtype=torch.bfloat16, device=dev)
+    K.call("tgm_gemm_w_swiglu", x.data_ptr(), BF16, m, k, w.data.data_ptr(), 2, n, k, K.ptr(sc), 15 if scaled else -1,
+           32, fused.data_ptr(), BF16, ld, stream())
+    gu = torch.empty((m, n), dtype=torch.float32, device=dev)
+    K.call("tgm_gemm_w", x.data_ptr(), BF16, m, k, w.data.data_ptr(), 2, n, k, K.ptr(sc), 15 if scaled else -1, 32,
+           gu.data_ptr(), F32, n, stream())
+    sep = torch.empty((m, n // 2), dtype=torch.bfloat16, device=dev)
+    K.call("tgm_dec_silu_mul", gu.data_ptr(), m, n // 2, sep.data_ptr(), BF16, stream())
+    assert torch.equal(fused[:, :n // 2], sep)
+    assert (fused[:, n // 2:] == 7.0).all()
+    scales = O.e8m0_decode(e) if scaled else None
+    g = np64(x) @ O.dequant_f64(O.pack_codes(codes, 4), "fp4_e2m1", (n, k), scales, 32).T
+    err = O.max_rel_err(np64(fused[:, :n // 2]), D.silu(g[:, 0::2]) * g[:, 1::2])
+    assert err <= 1e-2, err
+

@@ -83,7 +83,7 @@ __device__ __forceinline__ void decode64(const u32x4* raw, unsigned sbits, bf16x
   }
 }
 
-template <int FMT, bool SCALED>
+template <int FMT, bool SCALED, bool SWIGLU = false>
 __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, unsigned lda_bytes,
                                                  const uint8_t* __restrict__ w, const uint8_t* __restrict__ sw,
                                                  int M, int N, int K, void* __restrict__ c, int cdt, int64_t ldc) {
@@ -219,7 +219,10 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
   for (int i = 0; i < FA; ++i)
 #pragma unroll
     for (int j = 0; j < FB; ++j)
-      store_tile32(acc[i][j], ep, lane, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, M, N, c, cdt, ldc);
+      if constexpr (SWIGLU)
+        store_tile32_swiglu(acc[i][j], ep, lane, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, M, N, c, cdt, ldc);
+      else
+        store_tile32(acc[i][j], ep, lane, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, M, N, c, cdt, ldc);
 }
 
 // ---- INT4 / UINT4 weights x f16 activations, per-group scales (f16, bf16 or f32).
@@ -436,14 +439,14 @@ int dispatch_gemm_w_i4(const void* a, int64_t lda, const void* w, const void* sc
   TGM_UNSUPPORTED("tgm_gemm_w: int4 scales must be f16, bf16 or f32 per 32, 64 or 128 K-elements");
 }
 
-template <int FMT, bool SCALED>
+template <int FMT, bool SCALED, bool SWIGLU = false>
 int launch_gemm_w(const void* a, int64_t lda, const void* w, const void* scales, int64_t m, int64_t n, int64_t k,
                   void* c, int cdt, int64_t ldc, hipStream_t stream) {
   const int64_t tiles = ((m + kWM - 1) / kWM) * ((n + kWN - 1) / kWN);
-  hipLaunchKernelGGL((gemm_w_mx<FMT, SCALED>), dim3((unsigned)tiles), dim3(512), 0, stream, (const uint8_t*)a,
-                     (unsigned)(lda * 2), (const uint8_t*)w, (const uint8_t*)scales, (int)m, (int)n, (int)k, c, cdt,
-                     ldc);
-  return launch_status("tgm_gemm_w");
+  hipLaunchKernelGGL((gemm_w_mx<FMT, SCALED, SWIGLU>), dim3((unsigned)tiles), dim3(512), 0, stream,
+                     (const uint8_t*)a, (unsigned)(lda * 2), (const uint8_t*)w, (const uint8_t*)scales, (int)m, (int)n,
+                     (int)k, c, cdt, ldc);
+  return launch_status(SWIGLU ? "tgm_gemm_w_swiglu" : "tgm_gemm_w");
 }
 
 }  // namespace tgm
@@ -488,4 +491,33 @@ extern "C" int tgm_gemm_w(const void* a, int a_dtype, int64_t m, int64_t lda, co
     case TGM_FMT_FP6_E3M2 * 2 + 1: return launch_gemm_w<TGM_FMT_FP6_E3M2, true>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st);
     default: return launch_gemm_w<TGM_FMT_FP6_E3M2, false>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st);
   }
+}
+
+extern "C" int tgm_gemm_w_swiglu(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n,
+                                 int64_t k, const void* scales, int scale_dtype, int64_t block_size, void* c,
+                                 int c_dtype, int64_t ldc, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(a && w && c, "null operand");
+  TGM_CHECK_ARG(valid_format(fmt), "unknown packed format %d", fmt);
+  TGM_CHECK_ARG(m >= 0 && n >= 0 && k >= 0 && n % 2 == 0, "invalid gemm sizes (N must be even)");
+  TGM_CHECK_ARG(m <= 1 || lda >= k, "lda smaller than K");
+  TGM_CHECK_ARG(c_dtype == TGM_BF16 || c_dtype == TGM_F16 || c_dtype == TGM_F32, "output must be bf16, f16 or f32");
+  TGM_CHECK_ARG(m <= 1 || ldc >= n / 2, "ldc smaller than N / 2");
+  if (m == 0 || n == 0) return TGM_OK;
+  if (fmt != TGM_FMT_FP4_E2M1 || a_dtype != TGM_BF16)
+    TGM_UNSUPPORTED("tgm_gemm_w_swiglu: FP4 weights with bf16 activations only");
+  const bool scaled = scales != nullptr;
+  if (scaled && (scale_dtype != TGM_E8M0 || block_size != 32))
+    TGM_UNSUPPORTED("tgm_gemm_w_swiglu: scales must be E8M0 per 32 K-elements");
+  if (k == 0 || k % kWK != 0) TGM_UNSUPPORTED("tgm_gemm_w_swiglu: K must be a positive multiple of %d", kWK);
+  if (m > 1 && (lda * 2) % 16 != 0) TGM_UNSUPPORTED("tgm_gemm_w_swiglu: activation rows must be 16-byte aligned");
+  if (m >= (1ll << 31) || n >= (1ll << 31) || (m - 1) * lda * 2 + k * 2 >= (1ll << 32) || n * (k / 2) >= (1ll << 32))
+    TGM_UNSUPPORTED("tgm_gemm_w_swiglu: operands must be under 4 GiB (32-bit offsets)");
+  if ((uintptr_t)a % 16 || (uintptr_t)w % 16 || (scaled && (uintptr_t)scales % 4))
+    TGM_UNSUPPORTED("tgm_gemm_w_swiglu: operands must be 16-byte and scales 4-byte aligned");
+  const int64_t lda_eff = m > 1 ? lda : k;
+  return scaled ? launch_gemm_w<TGM_FMT_FP4_E2M1, true, true>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc,
+                                                              (hipStream_t)stream)
+                : launch_gemm_w<TGM_FMT_FP4_E2M1, false, true>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc,
+                                                               (hipStream_t)stream);
 }

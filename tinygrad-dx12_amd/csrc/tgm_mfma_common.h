@@ -2,6 +2,8 @@
 // buffer resources, the XCD-aware tile order and the output store.
 #pragma once
 
+#include <math.h>
+
 #include "tgm_common.h"
 
 namespace tgm {
@@ -61,15 +63,14 @@ __device__ __forceinline__ void store_c(void* c, int cdt, int64_t i, float v) {
 // The tile goes through the wave's own LDS block ``ep`` (32 rows padded to 36 floats) so
 // that lane l then holds row l / 2, columns 16 (l % 2) .. + 16, rounded once from fp32 and
 // written as 16-byte row segments; rows past M and columns past N are not written.
-__device__ __forceinline__ void store_tile32(const f32x16& t, float* ep, int lane, int r0, int c0, int M, int N,
-                                             void* c, int cdt, int64_t ldc) {
+// Lane l gets row l / 2, columns 16 (l % 2) .. + 16 of a 32 x 32 accumulator tile.
+__device__ __forceinline__ void tile32_row_values(const f32x16& t, float* ep, int lane, float (&vals)[16]) {
   const int half = lane >> 5, er = lane >> 1, ec = (lane & 1) * 16;
 #pragma unroll
   for (int v = 0; v < 16; ++v) ep[(8 * (v >> 2) + 4 * half + (v & 3)) * 36 + (lane & 31)] = t[v];
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  float vals[16];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const f32x4 f = *(const f32x4*)(ep + er * 36 + ec + 4 * q);
@@ -78,6 +79,13 @@ __device__ __forceinline__ void store_tile32(const f32x16& t, float* ep, int lan
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ void store_tile32(const f32x16& t, float* ep, int lane, int r0, int c0, int M, int N,
+                                             void* c, int cdt, int64_t ldc) {
+  const int er = lane >> 1, ec = (lane & 1) * 16;
+  float vals[16];
+  tile32_row_values(t, ep, lane, vals);
   const int row = r0 + er, col = c0 + ec;
   if (row >= M) return;
   const int64_t o = (int64_t)row * ldc + col;
@@ -101,6 +109,42 @@ __device__ __forceinline__ void store_tile32(const f32x16& t, float* ep, int lan
 #pragma unroll
     for (int q = 0; q < 16; ++q)
       if (col + q < N) store_c(c, cdt, o + q, vals[q]);
+  }
+}
+
+// SwiGLU epilogue of a product whose columns interleave gate (even) and up (odd) rows: column
+// pair (2 i, 2 i + 1) of a row becomes output column i, silu(gate) * up = gate / (1 +
+// exp(-gate)) * up in fp32, rounded once.  N is the product's (even) column count and ldc
+// counts output elements; a lane's 16 columns are 8 whole pairs.
+__device__ __forceinline__ void store_tile32_swiglu(const f32x16& t, float* ep, int lane, int r0, int c0, int M,
+                                                    int N, void* c, int cdt, int64_t ldc) {
+  const int er = lane >> 1, ec = (lane & 1) * 16;
+  float vals[16];
+  tile32_row_values(t, ep, lane, vals);
+  const int row = r0 + er, col = c0 + ec;
+  if (row >= M) return;
+  float y[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const float g = vals[2 * q], u = vals[2 * q + 1];
+    y[q] = g / (1.0f + expf(-g)) * u;
+  }
+  const int64_t o = (int64_t)row * ldc + col / 2;
+  if (col + 15 < N && (o & 7) == 0 && cdt != TGM_F32) {
+    unsigned pk[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (cdt == TGM_BF16)
+        pk[q] = f32_to_bf16(y[2 * q]) | ((unsigned)f32_to_bf16(y[2 * q + 1]) << 16);
+      else
+        pk[q] = __builtin_bit_cast(unsigned short, (_Float16)y[2 * q]) |
+                ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)y[2 * q + 1]) << 16);
+    }
+    *(u32x4*)((uint16_t*)c + o) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+  } else {
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (col + 2 * q + 1 < N) store_c(c, cdt, o + q, y[q]);
   }
 }
 

@@ -244,6 +244,12 @@ class Decoder:
                 K.call("tgm_gemv_swiglu", w.data.data_ptr(), K.FORMAT_IDS[w.format], 2 * cfg.ffn, d, K.ptr(w.scales),
                        K.dtype_id(w.scales.dtype), w.block_size, self.xnb.data_ptr(), BF16, self.act.data_ptr(), BF16,
                        stream)
+            elif rows > GEMV_MAX_ROWS and L.w_gate_up.format == "fp4_e2m1":  # GEMM with the SwiGLU epilogue
+                w = L.w_gate_up
+                K.call("tgm_gemm_w_swiglu", self.xnb.data_ptr(), BF16, rows, d, w.data.data_ptr(),
+                       K.FORMAT_IDS[w.format], 2 * cfg.ffn, d, K.ptr(w.scales),
+                       K.dtype_id(w.scales.dtype) if w.scales is not None else -1, w.block_size,
+                       self.act.data_ptr(), BF16, cfg.ffn, stream)
             else:
                 _packed_product(self.xnb, rows, d, L.w_gate_up, self.gu, 2 * cfg.ffn, stream)
                 K.call("tgm_dec_silu_mul", self.gu.data_ptr(), rows, cfg.ffn, self.act.data_ptr(), BF16, stream)
