@@ -302,7 +302,8 @@ constexpr int kMaxSplits = 32;
 //   2. wave g (g, g + 4) folds the chunk into the running max / sum of head g (online
 //      softmax) and turns the chunk's scores into probabilities;
 //   3. lane l accumulates dims (2 l, 2 l + 1) of p . v over the positions of its wave
-//      (positions w, w + 4, ...), rescaled by exp(m_old - m_new).
+//      (positions w, w + 4, ...), rescaled by exp(m_old - m_new); those v values are loaded
+//      at the start of the chunk, together with k.
 // One split writes the normalised output; several write (o, m, l) partials per (row, head,
 // split) that dec_attention_merge combines.  Loads use positions clamped into the valid range
 // (their probabilities are zero), so every load in a chunk is unconditional.
@@ -374,6 +375,15 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
   __syncthreads();
   for (int c0 = c_begin; c0 < c_end; c0 += CH) {
     const int last = c_end - 1;
+    // v of this wave's positions, issued with the k loads so both latencies overlap
+    unsigned vpre[CH / 4];
+    if (lane < NP) {
+#pragma unroll
+      for (int i = 0; i < CH / 4; ++i) {
+        const int tt = c0 + wave + 4 * i;
+        vpre[i] = *(const unsigned*)(vc + (kvbase + (tt < last ? tt : last)) * HD + 2 * lane);
+      }
+    }
     {
       const int pi = tid >> 2, qd = tid & 3;
       const int tt = c0 + pi;
@@ -430,7 +440,7 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
 #pragma unroll
       for (int i = 0; i < CH / 4; ++i) {
         const int pi = wave + 4 * i, tt = c0 + pi;
-        const unsigned vv = *(const unsigned*)(vc + (kvbase + (tt < last ? tt : last)) * HD + 2 * lane);
+        const unsigned vv = vpre[i];
         float v0 = lo_bf16(vv), v1 = hi_bf16(vv);
         if (mine && tt == p) {
           v0 = vp[2 * lane];
