@@ -302,8 +302,8 @@ constexpr int kMaxSplits = 32;
 //   2. wave g (g, g + 4) folds the chunk into the running max / sum of head g (online
 //      softmax) and turns the chunk's scores into probabilities;
 //   3. lane l accumulates dims (2 l, 2 l + 1) of p . v over the positions of its wave
-//      (positions w, w + 4, ...), rescaled by exp(m_old - m_new); those v values are loaded
-//      at the start of the chunk, together with k.
+//      (positions w, w + 4, ...), rescaled by exp(m_old - m_new).
+// A chunk's k and v are loaded together into registers; the first chunk's before q is staged.
 // One split writes the normalised output; several write (o, m, l) partials per (row, head,
 // split) that dec_attention_merge combines.  Loads use positions clamped into the valid range
 // (their probabilities are zero), so every load in a chunk is unconditional.
@@ -337,6 +337,29 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
   const bool mine = own && p >= c_begin && p < c_end;   // this split holds the token's position
   __shared__ float kp[HD], vp[HD];
   const float* qrow = qkv + (int64_t)r * ld + (int64_t)j * G * HD;
+  // k (4 lanes per position, a quarter of head_dim each) and v (lane l: dims 2 l, 2 l + 1 of
+  // the wave's positions w, w + 4, ...) of a chunk; the first chunk's loads are issued before
+  // q is staged, later chunks' at the top of their iteration
+  const int pi = tid >> 2, qd = tid & 3;
+  dec_u32x4 kreg[QD / 8];
+  unsigned vreg[CH / 4];
+  auto load_chunk = [&](int c0) __attribute__((always_inline)) {
+    const int last = c_end - 1;
+    const int tk = c0 + pi;
+    const uint16_t* kr = kc + (kvbase + (tk < last ? tk : last)) * HD + qd * QD;
+#pragma unroll
+    for (int e = 0; e < QD / 8; ++e) kreg[e] = *(const dec_u32x4*)(kr + 8 * e);
+    if (lane < NP) {
+#pragma unroll
+      for (int i = 0; i < CH / 4; ++i) {
+        const int tt = c0 + wave + 4 * i;
+        vreg[i] = *(const unsigned*)(vc + (kvbase + (tt < last ? tt : last)) * HD + 2 * lane);
+      }
+    }
+  };
+  // (the split holding the token's own position may read that position's k, v before this
+  // workgroup stores them: those two values are taken from LDS instead)
+  if (c_begin < c_end) load_chunk(c_begin);
   if (own) {
     for (int i = tid; i < G * NP; i += 256) {
       const int g = i / NP, e = i % NP;
@@ -374,26 +397,15 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
   for (int g = 0; g < G; ++g) oa[g][0] = oa[g][1] = 0.f;
   __syncthreads();
   for (int c0 = c_begin; c0 < c_end; c0 += CH) {
-    const int last = c_end - 1;
-    // v of this wave's positions, issued with the k loads so both latencies overlap
-    unsigned vpre[CH / 4];
-    if (lane < NP) {
-#pragma unroll
-      for (int i = 0; i < CH / 4; ++i) {
-        const int tt = c0 + wave + 4 * i;
-        vpre[i] = *(const unsigned*)(vc + (kvbase + (tt < last ? tt : last)) * HD + 2 * lane);
-      }
-    }
+    if (c0 != c_begin) load_chunk(c0);
     {
-      const int pi = tid >> 2, qd = tid & 3;
       const int tt = c0 + pi;
-      const uint16_t* kr = kc + (kvbase + (tt < last ? tt : last)) * HD + qd * QD;
       float s[G];
 #pragma unroll
       for (int g = 0; g < G; ++g) s[g] = 0.f;
 #pragma unroll
       for (int e = 0; e < QD; e += 8) {
-        const dec_u32x4 kv = *(const dec_u32x4*)(kr + e);
+        const dec_u32x4 kv = kreg[e / 8];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           float k0 = lo_bf16(kv[q]), k1 = hi_bf16(kv[q]);
@@ -439,8 +451,8 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
     if (lane < NP) {
 #pragma unroll
       for (int i = 0; i < CH / 4; ++i) {
-        const int pi = wave + 4 * i, tt = c0 + pi;
-        const unsigned vv = vpre[i];
+        const int pv_i = wave + 4 * i, tt = c0 + pv_i;
+        const unsigned vv = vreg[i];
         float v0 = lo_bf16(vv), v1 = hi_bf16(vv);
         if (mine && tt == p) {
           v0 = vp[2 * lane];
@@ -448,7 +460,7 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          const float pg = sc[g][pi];
+          const float pg = sc[g][pv_i];
           oa[g][0] += pg * v0;
           oa[g][1] += pg * v1;
         }
