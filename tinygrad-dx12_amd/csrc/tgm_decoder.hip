@@ -318,9 +318,12 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
                                                      uint16_t* __restrict__ vc, int max_seq, int cps, float scale,
                                                      int own, double log2_base, float* __restrict__ part,
                                                      void* __restrict__ out,
-                                                     int odt) {
+                                                     int odt, int hs) {
   constexpr int CH = 64, NP = HD / 2, QD = HD / 4;
-  const int r = blockIdx.x, j = blockIdx.y, z = blockIdx.z, S = gridDim.z;
+  // blockIdx.y = kv head * hs + sub-group: the workgroup takes q heads [blockIdx.y * G, + G)
+  // of the G * hs heads that share kv head j
+  const int r = blockIdx.x, j = blockIdx.y / hs, z = blockIdx.z, S = gridDim.z;
+  const int hq0 = blockIdx.y * G;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = r / T, t = r % T;
   const int p = pos[b] + t;
@@ -336,7 +339,7 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
   // own: rotate q, k and store this token's k, v
   const bool mine = own && p >= c_begin && p < c_end;   // this split holds the token's position
   __shared__ float kp[HD], vp[HD];
-  const float* qrow = qkv + (int64_t)r * ld + (int64_t)j * G * HD;
+  const float* qrow = qkv + (int64_t)r * ld + (int64_t)hq0 * HD;
   // k (4 lanes per position, a quarter of head_dim each) and v (lane l: dims 2 l, 2 l + 1 of
   // the wave's positions w, w + 4, ...) of a chunk; the first chunk's loads are issued before
   // q is staged, later chunks' at the top of their iteration
@@ -376,10 +379,12 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
       const uint16_t k1 = f32_to_bf16(y1), k2 = f32_to_bf16(y2);
       const uint16_t v1 = f32_to_bf16(vx[tid]), v2 = f32_to_bf16(vx[tid + NP]);
       const int64_t o = (kvbase + p) * HD;
-      kc[o + tid] = k1;
-      kc[o + tid + NP] = k2;
-      vc[o + tid] = v1;
-      vc[o + tid + NP] = v2;
+      if (blockIdx.y % hs == 0) {  // one sub-group stores; every sub-group uses the values from LDS
+        kc[o + tid] = k1;
+        kc[o + tid + NP] = k2;
+        vc[o + tid] = v1;
+        vc[o + tid + NP] = v2;
+      }
       kp[tid] = bf16_to_f32(k1);
       kp[tid + NP] = bf16_to_f32(k2);
       vp[tid] = bf16_to_f32(v1);
@@ -476,7 +481,7 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
     }
   __syncthreads();
   for (int i = tid; i < G * HD; i += 256) {
-    const int g = i / HD, d = i % HD, h = j * G + g;
+    const int g = i / HD, d = i % HD, h = hq0 + g;
     const float o = red[0][g][d] + red[1][g][d] + red[2][g][d] + red[3][g][d];
     if (part == nullptr) {
       const float l = l_sh[g];
@@ -731,9 +736,9 @@ extern "C" int64_t tgm_dec_attention_workspace(int64_t rows, int64_t heads, int6
 template <int G, int HD>
 static void launch_attention(dim3 grid, hipStream_t st, const float* qkv, int T, int H, int HK, const int32_t* pos,
                              void* kc, void* vc, int max_seq, int cps, float scale, int own, double log2_base,
-                             float* part, void* out, int odt) {
+                             float* part, void* out, int odt, int hs) {
   hipLaunchKernelGGL((dec_attention<G, HD>), grid, dim3(256), 0, st, qkv, T, H, HK, pos, (uint16_t*)kc, (uint16_t*)vc,
-                     max_seq, cps, scale, own, log2_base, part, out, odt);
+                     max_seq, cps, scale, own, log2_base, part, out, odt, hs);
 }
 
 extern "C" int tgm_dec_attention(const float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, int64_t kv_heads,
@@ -758,15 +763,20 @@ extern "C" int tgm_dec_attention(const float* qkv, int64_t rows, int64_t seq_row
   if ((uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 4) TGM_UNSUPPORTED("tgm_dec_attention: caches must be 16-byte aligned");
   if (rows == 0) return TGM_OK;
   const int cps = (int)((chunks + splits - 1) / splits);
-  const dim3 grid((unsigned)rows, (unsigned)kv_heads, (unsigned)splits);
+  // few (token, kv head, split) workgroups leave most CUs idle: then the q heads of a kv head
+  // are spread over hs workgroups (each re-reads the kv head's chunk, mostly from cache)
+  int hs = 1;
+  while (hs < G && rows * kv_heads * splits * hs * 2 <= 512) hs *= 2;
+  const int64_t Gw = G / hs;
+  const dim3 grid((unsigned)rows, (unsigned)(kv_heads * hs), (unsigned)splits);
   const hipStream_t st = (hipStream_t)stream;
   float* part = splits > 1 ? workspace : nullptr;
   const int own = rope_base > 0.0;
   const float scale = (float)(1.0 / sqrt((double)head_dim));
 #define TGM_ATT(GG, HDD)                                                                                            \
-  if (G == GG && head_dim == HDD)                                                                                   \
+  if (Gw == GG && head_dim == HDD)                                                                                  \
     launch_attention<GG, HDD>(grid, st, qkv, (int)seq_rows, (int)heads, (int)kv_heads, pos, k_cache, v_cache,        \
-                              (int)max_seq, cps, scale, own, own ? log2(rope_base) : 0.0, part, out, out_dtype);
+                              (int)max_seq, cps, scale, own, own ? log2(rope_base) : 0.0, part, out, out_dtype, hs);
   TGM_ATT(1, 64) TGM_ATT(2, 64) TGM_ATT(4, 64) TGM_ATT(8, 64)
   TGM_ATT(1, 128) TGM_ATT(2, 128) TGM_ATT(4, 128) TGM_ATT(8, 128)
 #undef TGM_ATT
