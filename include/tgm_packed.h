@@ -107,14 +107,17 @@ int tgm_gemv(const void* w, int fmt, int64_t n, int64_t k,
  * Family 1 with a SwiGLU epilogue (the gate / up projection of a decoder's feed-forward
  * block; no reference counterpart, where the activation would be a separate tinygrad op):
  *
- *   y[i] = silu(g) * u,  g = sum_k x[k] * deq(W)[2 i, k],  u = sum_k x[k] * deq(W)[2 i + 1, k]
+ *   y[m, i] = silu(g) * u,  g = sum_k x[m, k] deq(W)[2 i, k],  u = sum_k x[m, k] deq(W)[2 i + 1, k]
  *
- * W packed [n, k] with gate and up rows interleaved, n even; one activation row x (BF16);
- * y has n / 2 elements.  Only the M = 1 FP4 + E8M0/32 row-streaming kernel has this epilogue
- * (K a multiple of 2048, at most 16384); otherwise TGM_E_UNSUPPORTED.
+ * W packed [n, k] with gate and up rows interleaved, n even; m <= 16 activation rows x (BF16,
+ * row stride ldx); y has n / 2 columns (row stride ldy).  silu(g) = g / (1 + exp(-g)) in
+ * fp32, rounded once.  M = 1 runs the FP4 + E8M0/32 row-streaming kernel (K a multiple of
+ * 2048, at most 16384); 2 <= M <= 16 the streaming MFMA GEMV (FP4 / FP6, E8M0/32 or no
+ * scales, K a multiple of 128); otherwise TGM_E_UNSUPPORTED.
  */
 int tgm_gemv_swiglu(const void* w, int fmt, int64_t n, int64_t k, const void* scales, int scale_dtype,
-                    int64_t block_size, const void* x, int x_dtype, void* y, int y_dtype, void* stream);
+                    int64_t block_size, const void* x, int x_dtype, int64_t m, int64_t ldx, void* y, int y_dtype,
+                    int64_t ldy, void* stream);
 
 /*
  * Kernel family 2 -- prefill GEMM with packed weights and 16-bit activations

@@ -403,8 +403,8 @@ def test_gemv_swiglu_epilogue(dev, nk):
                      torch.from_numpy(e).to(dev).view(torch.float8_e8m0fnu), 32)
     x = torch.from_numpy(rng.standard_normal(k).astype(np.float32)).to(dev).to(torch.bfloat16)
     fused = torch.empty(n // 2, dtype=torch.bfloat16, device=dev)
-    K.call("tgm_gemv_swiglu", w.data.data_ptr(), 2, n, k, w.scales.data_ptr(), 15, 32, x.data_ptr(), BF16,
-           fused.data_ptr(), BF16, stream())
+    K.call("tgm_gemv_swiglu", w.data.data_ptr(), 2, n, k, w.scales.data_ptr(), 15, 32, x.data_ptr(), BF16, 1, k,
+           fused.data_ptr(), BF16, n // 2, stream())
     gu = torch.empty(n, dtype=torch.float32, device=dev)
     K.call("tgm_gemv", w.data.data_ptr(), 2, n, k, w.scales.data_ptr(), 15, 32, x.data_ptr(), BF16, 1, k,
            gu.data_ptr(), F32, n, stream())
@@ -441,6 +441,31 @@ def test_gemm_swiglu_epilogue(dev, m, n, k, pad, scaled):
     assert (fused[:, n // 2:] == 7.0).all()
     scales = O.e8m0_decode(e) if scaled else None
     g = np64(x) @ O.dequant_f64(O.pack_codes(codes, 4), "fp4_e2m1", (n, k), scales, 32).T
+    err = O.max_rel_err(np64(fused[:, :n // 2]), D.silu(g[:, 0::2]) * g[:, 1::2])
+    assert err <= 1e-2, err
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 28672 // 4, 4096), (2, 1000, 512), (16, 4096, 14336 // 4)])
+def test_gemv_swiglu_epilogue_rows(dev, m, n, k):
+    """2 to 16 activation rows: the streaming MFMA GEMV with the SwiGLU epilogue equals the plain
+    GEMV (fp32 out) followed by tgm_dec_silu_mul bit for bit, and the oracle within 1e-2."""
+    rng = np.random.default_rng(m + n + k)
+    codes = rng.integers(0, 16, (n, k)).astype(np.uint8)
+    e = (127 + rng.integers(-4, 3, (n, k // 32))).astype(np.uint8)
+    w = PackedTensor(torch.from_numpy(O.pack_codes(codes, 4)).to(dev), "fp4_e2m1", (n, k),
+                     torch.from_numpy(e).to(dev).view(torch.float8_e8m0fnu), 32)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    fused = torch.full((m, n // 2 + 3), 7.0, dtype=torch.bfloat16, device=dev)
+    K.call("tgm_gemv_swiglu", w.data.data_ptr(), 2, n, k, w.scales.data_ptr(), 15, 32, x.data_ptr(), BF16, m, k,
+           fused.data_ptr(), BF16, n // 2 + 3, stream())
+    gu = torch.empty((m, n), dtype=torch.float32, device=dev)
+    K.call("tgm_gemv", w.data.data_ptr(), 2, n, k, w.scales.data_ptr(), 15, 32, x.data_ptr(), BF16, m, k,
+           gu.data_ptr(), F32, n, stream())
+    sep = torch.empty((m, n // 2), dtype=torch.bfloat16, device=dev)
+    K.call("tgm_dec_silu_mul", gu.data_ptr(), m, n // 2, sep.data_ptr(), BF16, stream())
+    assert torch.equal(fused[:, :n // 2], sep)
+    assert (fused[:, n // 2:] == 7.0).all()
+    g = np64(x) @ O.dequant_f64(O.pack_codes(codes, 4), "fp4_e2m1", (n, k), O.e8m0_decode(e), 32).T
     err = O.max_rel_err(np64(fused[:, :n // 2]), D.silu(g[:, 0::2]) * g[:, 1::2])
     assert err <= 1e-2, err
 

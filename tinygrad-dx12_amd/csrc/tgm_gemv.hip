@@ -84,17 +84,34 @@ static bool mfma_gemv_ok(const void* w, int fmt, int64_t n, int64_t k, const voi
 }
 
 extern "C" int tgm_gemv_swiglu(const void* w, int fmt, int64_t n, int64_t k, const void* scales, int scale_dtype,
-                               int64_t block_size, const void* x, int x_dtype, void* y, int y_dtype, void* stream) {
+                               int64_t block_size, const void* x, int x_dtype, int64_t m, int64_t ldx, void* y,
+                               int y_dtype, int64_t ldy, void* stream) {
   clear_error();
   TGM_CHECK_ARG(valid_format(fmt), "unknown packed format %d", fmt);
   TGM_CHECK_ARG(n >= 0 && n % 2 == 0 && k >= 0 && block_size >= 1, "n must be even (gate and up rows interleaved)");
+  TGM_CHECK_ARG(m >= 0 && m <= 16, "M must be <= 16");
+  TGM_CHECK_ARG(m <= 1 || ldx >= k, "ldx smaller than K");
+  TGM_CHECK_ARG(m <= 1 || ldy >= n / 2, "ldy smaller than N / 2");
   TGM_CHECK_ARG(y_dtype == TGM_BF16 || y_dtype == TGM_F16 || y_dtype == TGM_F32, "output must be bf16, f16 or f32");
-  if (n == 0) return TGM_OK;
+  if (n == 0 || m == 0) return TGM_OK;
   if (k == 0 || n * (k / 2) >= (1ll << 40)) TGM_UNSUPPORTED("tgm_gemv_swiglu: no kernel for this size");
-  const int st = launch_gemv_rows((hipStream_t)stream, w, fmt, n, k, scales, scale_dtype, block_size, x, x_dtype, 1, y,
-                                  y_dtype, true);
-  if (st == TGM_E_UNSUPPORTED)
-    TGM_UNSUPPORTED("tgm_gemv_swiglu: needs FP4 weights with E8M0/32 scales, bf16 x, K a multiple of 2048 up to 16384");
+  const hipStream_t s = (hipStream_t)stream;
+  if (m == 1) {
+    const int st = launch_gemv_rows(s, w, fmt, n, k, scales, scale_dtype, block_size, x, x_dtype, 1, y, y_dtype, true);
+    if (st == TGM_E_UNSUPPORTED)
+      TGM_UNSUPPORTED("tgm_gemv_swiglu: one row needs FP4 weights with E8M0/32 scales, bf16 x, K a multiple of 2048 "
+                      "up to 16384");
+    return st == TGM_OK ? launch_status("tgm_gemv_swiglu") : st;
+  }
+  if (!mfma_gemv_ok(w, fmt, n, k, scales, scale_dtype, block_size, x, x_dtype, m, ldx, y_dtype))
+    TGM_UNSUPPORTED("tgm_gemv_swiglu: 2-16 rows need FP4/FP6 weights with E8M0/32 (or no) scales, bf16 x, K % 128 == 0");
+  int st;
+  switch (fmt) {
+    case TGM_FMT_FP4_E2M1: st = launch_gemv_stream_fp4(s, w, n, k, scales, x, m, ldx, y, y_dtype, ldy, 1); break;
+    case TGM_FMT_FP6_E2M3: st = launch_gemv_stream_fp6(s, w, n, k, scales, x, m, ldx, y, y_dtype, ldy, 1); break;
+    default: st = launch_gemv_stream_bf6(s, w, n, k, scales, x, m, ldx, y, y_dtype, ldy, 1); break;
+  }
+  if (st == TGM_E_UNSUPPORTED) TGM_UNSUPPORTED("tgm_gemv_swiglu: no streaming shape for K = %lld", (long long)k);
   return st == TGM_OK ? launch_status("tgm_gemv_swiglu") : st;
 }
 

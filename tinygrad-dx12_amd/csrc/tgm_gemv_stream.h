@@ -104,7 +104,7 @@ template <int FMT, int NT, int NK, int RING, int SMAX, bool EXACT, int XV, int S
 __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __restrict__ w, int64_t N, int64_t K,
                                                           const uint8_t* __restrict__ scales, int64_t nblk,
                                                           const __bf16* __restrict__ x, int M, int64_t ldx,
-                                                          void* __restrict__ y, int ydt, int64_t ldy) {
+                                                          void* __restrict__ y, int ydt, int64_t ldy, int swiglu) {
   static_assert(SMAX % 4 == 0, "scale groups");
   constexpr int D = RING < SMAX ? RING : SMAX;  // ring depth
   constexpr bool SCALED = SC != kScaleNone, SG4 = SC == kScaleGroup4, XLDS = XV > 0;
@@ -250,6 +250,20 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __res
       for (int i = 0; i < 4; ++i) sum[i] += partial[((kk * NT + ti) * 64 + lane) * 4 + i];
   }
   // Lane (c, q) holds Y[c][n0 + 4q .. n0 + 4q + 3]: one 8- or 16-byte store when whole.
+  // swiglu: rows 2 i and 2 i + 1 are the gate and up rows of output column i, so the lane
+  // holds two whole pairs and writes silu(gate) * up to columns (n0 + 4q) / 2 + {0, 1}.
+  if (swiglu) {
+    if (c < M) {
+      const int64_t nb = n0 + 4 * q;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        if (nb + 2 * i + 1 < N) {
+          const float g = sum[2 * i], u = sum[2 * i + 1];
+          store_out(y, ydt, (int64_t)c * ldy + nb / 2 + i, g / (1.0f + expf(-g)) * u);
+        }
+    }
+    return;
+  }
   if (c < M) {
     const int64_t nb = n0 + 4 * q;
     const int64_t o = (int64_t)c * ldy + nb;
@@ -308,7 +322,7 @@ inline GemvShape gemv_shape(int64_t tiles, int64_t S, bool sg4) {
 
 template <int FMT, int NT, int NK, int SMAX, bool EXACT, int XV, int SC>
 int launch_stream(unsigned grid, size_t lds, hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales,
-                  int64_t nblk, const void* x, int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy) {
+                  int64_t nblk, const void* x, int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu) {
   auto kernel = gemv_stream<FMT, NT, NK, kGemvRing, SMAX, EXACT, XV, SC>;
   if (lds > 64 * 1024) {
     static bool raised = false;  // per instantiation
@@ -322,7 +336,7 @@ int launch_stream(unsigned grid, size_t lds, hipStream_t s, const void* w, int64
     }
   }
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(NT * NK * 64), lds, s, (const uint8_t*)w, n, k, (const uint8_t*)scales,
-                     nblk, (const __bf16*)x, (int)m, ldx, y, ydt, ldy);
+                     nblk, (const __bf16*)x, (int)m, ldx, y, ydt, ldy, swiglu);
   return TGM_OK;
 }
 
@@ -330,31 +344,32 @@ int launch_stream(unsigned grid, size_t lds, hipStream_t s, const void* w, int64
 template <int FMT, int NT, int NK, int SMAX, bool EXACT, int SC>
 int launch_stream_xv(int xv, unsigned grid, size_t lds, hipStream_t s, const void* w, int64_t n, int64_t k,
                      const void* scales, int64_t nblk, const void* x, int64_t m, int64_t ldx, void* y, int ydt,
-                     int64_t ldy) {
-  if (xv == 2) return launch_stream<FMT, NT, NK, SMAX, EXACT, 2, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy);
-  if (xv == 8) return launch_stream<FMT, NT, NK, SMAX, EXACT, 8, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy);
-  return launch_stream<FMT, NT, NK, SMAX, EXACT, 0, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy);
+                     int64_t ldy, int swiglu) {
+  if (xv == 2) return launch_stream<FMT, NT, NK, SMAX, EXACT, 2, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
+  if (xv == 8) return launch_stream<FMT, NT, NK, SMAX, EXACT, 8, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
+  return launch_stream<FMT, NT, NK, SMAX, EXACT, 0, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
 }
 
 template <int FMT, int NT, int NK>
 int launch_stream_shape(const GemvShape& g, int sc, int xv, unsigned grid, size_t lds, hipStream_t s, const void* w,
                         int64_t n, int64_t k, const void* scales, int64_t nblk, const void* x, int64_t m, int64_t ldx,
-                        void* y, int ydt, int64_t ldy) {
+                        void* y, int ydt, int64_t ldy, int swiglu) {
   if (g.exact) {  // block-32 E8M0 scales in groups of four, slices of exactly SMAX super-steps
 #define TGM_EXACT(SMAX) \
-    if (g.smax == SMAX) return launch_stream_xv<FMT, NT, NK, SMAX, true, kScaleGroup4>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy);
+    if (g.smax == SMAX) return launch_stream_xv<FMT, NT, NK, SMAX, true, kScaleGroup4>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
     TGM_EXACT(4) TGM_EXACT(8) TGM_EXACT(16) TGM_EXACT(28) TGM_EXACT(32)
 #undef TGM_EXACT
     return TGM_E_UNSUPPORTED;
   }
-  if (sc == kScaleGroup4) return launch_stream_xv<FMT, NT, NK, 32, false, kScaleGroup4>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy);
-  if (sc == kScaleDword) return launch_stream_xv<FMT, NT, NK, 32, false, kScaleDword>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy);
-  return launch_stream_xv<FMT, NT, NK, 32, false, kScaleNone>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy);
+  if (sc == kScaleGroup4) return launch_stream_xv<FMT, NT, NK, 32, false, kScaleGroup4>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
+  if (sc == kScaleDword) return launch_stream_xv<FMT, NT, NK, 32, false, kScaleDword>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
+  return launch_stream_xv<FMT, NT, NK, 32, false, kScaleNone>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
 }
 
+// swiglu: the weight rows interleave gate and up rows; y gets silu(gate) * up (N / 2 columns).
 template <int FMT>
 int launch_gemv_stream(hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales, const void* x,
-                       int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy) {
+                       int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu = 0) {
   const int64_t tiles = (n + 15) / 16;
   const int sc = scales == nullptr ? kScaleNone : (k % 512 == 0 ? kScaleGroup4 : kScaleDword);
   const GemvShape g = gemv_shape(tiles, k / 128, sc == kScaleGroup4);
@@ -367,17 +382,17 @@ int launch_gemv_stream(hipStream_t s, const void* w, int64_t n, int64_t k, const
   const int xv = !xlds ? 0 : passes <= 2 ? 2 : 8;
   const size_t lds = part + (xlds ? xbytes : 0);
   const int64_t nblk = k / 32;
-  if (g.nt == 4) return launch_stream_shape<FMT, 4, 2>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy);
-  if (g.nt == 2) return launch_stream_shape<FMT, 2, 4>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy);
-  return launch_stream_shape<FMT, 1, 8>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy);
+  if (g.nt == 4) return launch_stream_shape<FMT, 4, 2>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
+  if (g.nt == 2) return launch_stream_shape<FMT, 2, 4>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
+  return launch_stream_shape<FMT, 1, 8>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
 }
 
 // Instantiated once per format in its own translation unit.
 int launch_gemv_stream_fp4(hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales, const void* x,
-                           int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy);
+                           int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu = 0);
 int launch_gemv_stream_fp6(hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales, const void* x,
-                           int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy);
+                           int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu = 0);
 int launch_gemv_stream_bf6(hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales, const void* x,
-                           int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy);
+                           int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu = 0);
 
 }  // namespace tgm

@@ -205,6 +205,8 @@ class Decoder:
             self.probs = torch.empty((batch * cfg.heads * max_prompt * n * tp,), **b16)
         # one token: the gate|up GEMV applies SwiGLU itself when its row-streaming kernel covers the shape
         self.fuse_swiglu = (cfg.hidden % 2048 == 0 and cfg.hidden <= 16384)
+        # 2 to 16 tokens: the streaming MFMA GEMV applies it (K a multiple of 128)
+        self.fuse_swiglu_rows = cfg.hidden % 128 == 0
         ws = K.load_library().tgm_dec_attention_workspace(batch, cfg.heads, cfg.head_dim, self.splits)
         self.workspace = torch.empty(max(ws // 4, 1), **f32)
         self.workspace_bytes = ws
@@ -239,11 +241,11 @@ class Decoder:
             _packed_product(self.attn, rows, cfg.heads * cfg.head_dim, L.wo, self.delta, d, stream)
             K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr(), rows, d, L.ffn_norm.data_ptr(),
                    cfg.eps, self.xnb.data_ptr(), BF16, stream)
-            if rows == 1 and self.fuse_swiglu:  # gate|up GEMV with the SwiGLU epilogue
-                w = L.w_gate_up
+            if (rows == 1 and self.fuse_swiglu) or (1 < rows <= GEMV_MAX_ROWS and self.fuse_swiglu_rows):
+                w = L.w_gate_up  # gate|up GEMV with the SwiGLU epilogue
                 K.call("tgm_gemv_swiglu", w.data.data_ptr(), K.FORMAT_IDS[w.format], 2 * cfg.ffn, d, K.ptr(w.scales),
-                       K.dtype_id(w.scales.dtype), w.block_size, self.xnb.data_ptr(), BF16, self.act.data_ptr(), BF16,
-                       stream)
+                       K.dtype_id(w.scales.dtype), w.block_size, self.xnb.data_ptr(), BF16, rows, d,
+                       self.act.data_ptr(), BF16, cfg.ffn, stream)
             elif rows > GEMV_MAX_ROWS and L.w_gate_up.format == "fp4_e2m1":  # GEMM with the SwiGLU epilogue
                 w = L.w_gate_up
                 K.call("tgm_gemm_w_swiglu", self.xnb.data_ptr(), BF16, rows, d, w.data.data_ptr(),

@@ -50,7 +50,7 @@ _SIGNATURES = {
     "tgm_gemm_dense": (_P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _I64, _P, _INT, _I64, _P),
     "tgm_gemm_dense_batched": (_P, _INT, _I64, _I64, _I64, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P, _INT, _I64, _I64,
                                _I64, _I64, _I64, _P),
-    "tgm_gemv_swiglu": (_P, _INT, _I64, _I64, _P, _INT, _I64, _P, _INT, _P, _INT, _P),
+    "tgm_gemv_swiglu": (_P, _INT, _I64, _I64, _P, _INT, _I64, _P, _INT, _I64, _I64, _P, _INT, _I64, _P),
     "tgm_transpose16": (_P, _I64, _I64, _I64, _P, _I64, _P),
     # decoder-step kernels (include/tgm_decoder.h)
     "tgm_dec_embed": (_P, _I64, _I64, _P, _I64, _P, _P),
