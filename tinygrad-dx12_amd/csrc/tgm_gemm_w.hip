@@ -365,24 +365,25 @@ __global__ void __launch_bounds__(512) gemm_w_i4(const uint8_t* __restrict__ a, 
       }
     };
     read_a(0, af[0]);
+    f16x8 bf[2][FB];
+#pragma unroll
+    for (int t = 0; t < FB; ++t) bf[0][t] = decode_i4x8<SIGNED>(cw[t][0]);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      // one MFMA group at a time: A of MFMA j + 1 is read while MFMA j runs
+      // one MFMA group at a time: A of group j + 1 is read, and its codes decoded, while the
+      // MFMAs of group j run
       __builtin_amdgcn_sched_barrier(0);
       if (j < 7) read_a(j + 1, af[(j + 1) & 1]);
-      f16x8 bf[FB];
-#pragma unroll
-      for (int t = 0; t < FB; ++t) bf[t] = decode_i4x8<SIGNED>(cw[t][j]);
       constexpr int JPG = G ? G / 16 : 8;  // MFMAs per scale group
 #pragma unroll
       for (int ta = 0; ta < FA; ++ta)
 #pragma unroll
         for (int tb = 0; tb < FB; ++tb) {
           if constexpr (G == 0) {
-            acc[ta][tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j & 1][ta], bf[tb], acc[ta][tb], 0, 0, 0);
+            acc[ta][tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j & 1][ta], bf[j & 1][tb], acc[ta][tb], 0, 0, 0);
           } else {
-            part[ta][tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j & 1][ta], bf[tb], j % JPG ? part[ta][tb] : f32x16{},
-                                                                   0, 0, 0);
+            part[ta][tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j & 1][ta], bf[j & 1][tb],
+                                                                   j % JPG ? part[ta][tb] : f32x16{}, 0, 0, 0);
             if (j % JPG == JPG - 1) {
               const float sv = sc[tb][j / JPG];
 #pragma unroll
@@ -390,6 +391,9 @@ __global__ void __launch_bounds__(512) gemm_w_i4(const uint8_t* __restrict__ a, 
             }
           }
         }
+      if (j < 7)
+#pragma unroll
+        for (int t = 0; t < FB; ++t) bf[(j + 1) & 1][t] = decode_i4x8<SIGNED>(cw[t][j + 1]);
     }
     wait_lds_dma();  // this wave's loads of step s + 1 (and its scale loads)
     if constexpr (G != 0) {
