@@ -62,6 +62,19 @@ int tgm_dec_rope_kv(float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, i
                     const int32_t* pos, double rope_base, void* k_cache, void* v_cache, int64_t max_seq, void* q_out,
                     void* k_out, void* vt_out, int64_t ld_vt, int64_t parts, void* stream);
 
+/* Causal attention of prompt tokens in one kernel: for every sequence b, q head h and token
+ * t (rows b * seq_rows + t of qkv, whose q heads tgm_dec_rope_kv has rotated, at position
+ * p = pos[b] + t), out[row, h] = softmax over cache positions k <= p of
+ * q . K[k] / sqrt(head_dim), applied to V, with K and V the bf16 caches (kv head
+ * h / (heads / kv_heads)), which must already hold positions 0 .. p.  Scores and
+ * probabilities stay on chip (flash-attention form on bf16 MFMA); q and the probabilities are
+ * split into three bf16 terms each, so the result has the accuracy of fp32 arithmetic.
+ * head_dim 64 or 128; qkv and caches 16-byte aligned (else TGM_E_UNSUPPORTED); out f16,
+ * bf16 or f32 [rows, heads * head_dim].  The reference has no model code (decoder harness). */
+int tgm_dec_prefill_attention(const float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, int64_t kv_heads,
+                              int64_t head_dim, const int32_t* pos, const void* k_cache, const void* v_cache,
+                              int64_t max_seq, void* out, int out_dtype, void* stream);
+
 /* Causal softmax of prefill scores: for row = z * seq_rows + t (float32, row stride ld_scores),
  * p[j] = softmax over j <= t of scale * scores[row, j] is split into `parts` (1 to 3) bf16 terms
  * as in tgm_dec_rope_kv, term s at probs[row, s * ld_probs / parts + j], all 0 for

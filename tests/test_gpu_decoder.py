@@ -128,6 +128,37 @@ def test_rope_kv_prefill_outputs(dev, parts):
             assert torch.equal(vt[b, ..., s * w:s * w + T], vtt) and (vt[b, ..., s * w + T:(s + 1) * w] == 7.0).all()
 
 
+@pytest.mark.parametrize("hd,H,HK", [(128, 32, 8), (64, 4, 2), (128, 8, 8)])
+@pytest.mark.parametrize("T,starts", [(150, (0, 0)), (37, (0, 9)), (1, (3, 0)), (256, (0, 0))])
+def test_prefill_attention_kernel(dev, hd, H, HK, T, starts):
+    """The fused prompt attention against the float64 oracle fed the device's rotated q (fp32) and
+    bf16 caches (f32 output; fp32 summation noise only: the bound is half the per-token kernel's
+    1e-3), and against the
+    per-token kernel on the same inputs; earlier cache positions (a prompt after cached tokens)
+    are attended to, later ones are not."""
+    rng = np.random.default_rng(T + hd + H)
+    B, max_seq = 2, 320
+    qkv = torch.from_numpy(rng.standard_normal((B * T, (H + 2 * HK) * hd)).astype(np.float32)).to(dev)
+    kc = torch.from_numpy(rng.standard_normal((B, HK, max_seq, hd)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    vc = torch.from_numpy(rng.standard_normal((B, HK, max_seq, hd)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    pos = torch.tensor(starts, dtype=torch.int32, device=dev)
+    K.call("tgm_dec_rope_kv", qkv.data_ptr(), B * T, T, H, HK, hd, pos.data_ptr(), 10000.0, kc.data_ptr(),
+           vc.data_ptr(), max_seq, None, None, None, 0, 1, stream())
+    out = torch.full((B * T, H * hd), float("nan"), device=dev)
+    K.call("tgm_dec_prefill_attention", qkv.data_ptr(), B * T, T, H, HK, hd, pos.data_ptr(), kc.data_ptr(),
+           vc.data_ptr(), max_seq, out.data_ptr(), F32, stream())
+    split = torch.empty_like(out)
+    K.call("tgm_dec_attention", qkv.data_ptr(), B * T, T, H, HK, hd, pos.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+           max_seq, 0.0, 1, None, 0, split.data_ptr(), F32, stream())
+    q = np64(qkv).reshape(B, T, H + 2 * HK, hd)[:, :, :H].transpose(0, 2, 1, 3)
+    kn, vn = np64(kc), np64(vc)
+    for b, p0 in enumerate(starts):
+        ref = D.attention(q[b], kn[b, :, :p0 + T], vn[b, :, :p0 + T], p0 + np.arange(T))
+        got = np64(out).reshape(B, T, H, hd)[b].transpose(1, 0, 2)
+        assert O.max_rel_err(got, ref) <= 5e-4, (b, O.max_rel_err(got, ref))
+    assert O.max_rel_err(np64(out), np64(split)) <= 5e-4
+
+
 @pytest.mark.parametrize("parts", [1, 2, 3])
 @pytest.mark.parametrize("t", [1, 5, 64, 100])
 def test_causal_softmax(dev, t, parts):
@@ -283,11 +314,11 @@ def _compare_logits(dec: Decoder, ref_logits: np.ndarray, tol: float = 1e-2, whe
     assert err <= tol, (where, err)
 
 
-@pytest.mark.parametrize("gemm_prefill", [True, False])
+@pytest.mark.parametrize("attention", ["fused", "gemm", "split"])
 @pytest.mark.parametrize("batch,prompt,floor,tol", [(2, 12, 1e-3, 1e-2), (1, 8, 1e-3, 1e-2), (3, 70, 1.0, 1e-3)])
-def test_decoder_matches_oracle(dev, batch, prompt, floor, tol, gemm_prefill):
-    """Reduced config: prefill (GEMM path for 24 rows, GEMV path for 8; prompt attention as
-    batched GEMMs or with the per-token kernel) and six cached decode steps; logits within
+def test_decoder_matches_oracle(dev, batch, prompt, floor, tol, attention):
+    """Reduced config: prefill (GEMM path for 24 rows, GEMV path for 8; prompt attention fused,
+    as batched GEMMs or with the per-token kernel) and six cached decode steps; logits within
     ``tol`` of the oracle fed the same tokens, and the device's greedy token is the oracle's
     wherever the oracle's top-2 margin exceeds 2e-2 of the largest logit.
 
@@ -302,7 +333,7 @@ def test_decoder_matches_oracle(dev, batch, prompt, floor, tol, gemm_prefill):
     rng = np.random.default_rng(prompt)
     prompts = rng.integers(0, cfg.vocab, (batch, prompt))
     dec = Decoder(w, cfg, batch, max_seq, prompt)
-    dec.mfma_prefill = gemm_prefill
+    dec.prompt_attention = attention
     oracle = oracle_for(w, cfg, batch, max_seq)
     dec.history = None
     first = dec.prefill(torch.from_numpy(prompts).to(dev))
@@ -334,7 +365,7 @@ def test_mfma_prefill_attention_term_counts(dev, parts, tol):
     out = []
     for mfma in (True, False):
         dec = Decoder(w, cfg, batch, 96, prompt)
-        dec.mfma_prefill, dec.prefill_parts = mfma, parts
+        dec.prompt_attention, dec.prefill_parts = ("gemm" if mfma else "split"), parts
         dec.prefill(prompts)
         out.append((dec.logits.clone(), dec.k_cache.clone(), dec.v_cache.clone()))
     assert torch.equal(out[0][1][0], out[1][1][0]) and torch.equal(out[0][2][0], out[1][2][0])

@@ -190,19 +190,14 @@ class Decoder:
         self.v_cache = torch.zeros(cache, dtype=torch.bfloat16, device=dev)
         self.splits = min(max(1, math.ceil(max_seq / 64)), 32)
         self.fuse_rope = True
-        # prompts of several tokens: attention as two batched MFMA GEMMs around a causal softmax
-        # (scores for every (sequence, head) pair at once) instead of the per-token split kernel
-        # (3 bf16 terms per operand value: the accuracy of fp32; 1 or 2 trade it for GEMM work)
-        self.mfma_prefill = max_prompt > 1
+        # attention of prompts of several tokens:
+        #   "fused": one flash-attention kernel on MFMA (scores stay on chip);
+        #   "gemm":  two batched MFMA GEMMs around a causal softmax (scores through memory), with
+        #            ``prefill_parts`` bf16 terms per operand value (3: the accuracy of fp32);
+        #   "split": the per-token decode attention kernel.
+        self.prompt_attention = "fused"
         self.prefill_parts = 3
-        if self.mfma_prefill:
-            hd, tp, n = cfg.head_dim, -(-max_prompt // 64) * 64, 3
-            b16 = dict(dtype=torch.bfloat16, device=dev)
-            self.q_terms = torch.empty((batch * cfg.heads * max_prompt * n * hd,), **b16)
-            self.k_terms = torch.empty((batch * cfg.kv_heads * max_prompt * n * hd,), **b16)
-            self.vt = torch.zeros((batch * cfg.kv_heads * hd * n * tp,), **b16)
-            self.scores = torch.empty((batch * cfg.heads * max_prompt * tp,), **f32)
-            self.probs = torch.empty((batch * cfg.heads * max_prompt * n * tp,), **b16)
+        self._gemm_buffers: dict[str, torch.Tensor] | None = None
         # one token: the gate|up GEMV applies SwiGLU itself when its row-streaming kernel covers the shape
         self.fuse_swiglu = (cfg.hidden % 2048 == 0 and cfg.hidden <= 16384)
         # 2 to 16 tokens: the streaming MFMA GEMV applies it (K a multiple of 128)
@@ -227,7 +222,14 @@ class Decoder:
             _packed_product(self.xn16, rows, d, L.wqkv, self.qkv, cfg.qkv_rows, stream)
             kc, vc = self.k_cache[li], self.v_cache[li]
             fused = seq_rows == 1 and self.fuse_rope  # one new token per sequence: RoPE + cache store in attention
-            if seq_rows > 1 and self.mfma_prefill:
+            if seq_rows > 1 and self.prompt_attention == "fused":
+                K.call("tgm_dec_rope_kv", self.qkv.data_ptr(), rows, seq_rows, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                       self.pos.data_ptr(), cfg.rope_base, kc.data_ptr(), vc.data_ptr(), self.max_seq, None, None,
+                       None, 0, 1, stream)
+                K.call("tgm_dec_prefill_attention", self.qkv.data_ptr(), rows, seq_rows, cfg.heads, cfg.kv_heads,
+                       cfg.head_dim, self.pos.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.max_seq,
+                       self.attn.data_ptr(), F16, stream)
+            elif seq_rows > 1 and self.prompt_attention == "gemm":
                 self._prefill_attention(rows, seq_rows, kc, vc, stream)
             else:
                 if not fused:
@@ -281,14 +283,24 @@ class Decoder:
             raise ValueError("prefill_parts must be 1, 2 or 3")
         tp = -(-t // 64) * 64
         z, g = self.batch * H, H // HK
+        if self._gemm_buffers is None:  # sized for 3 terms and the longest prompt, allocated once
+            tmax = -(-self.max_prompt // 64) * 64
+            b16 = dict(dtype=torch.bfloat16, device=self.device)
+            self._gemm_buffers = {
+                "q": torch.empty((self.batch * H * self.max_prompt * 3 * hd,), **b16),
+                "k": torch.empty((self.batch * HK * self.max_prompt * 3 * hd,), **b16),
+                "vt": torch.zeros((self.batch * HK * hd * 3 * tmax,), **b16),
+                "s": torch.empty((self.batch * H * self.max_prompt * tmax,), dtype=torch.float32, device=self.device),
+                "p": torch.empty((self.batch * H * self.max_prompt * 3 * tmax,), **b16)}
+        buf = self._gemm_buffers
         K.call("tgm_dec_rope_kv", self.qkv.data_ptr(), rows, t, H, HK, hd, self.pos.data_ptr(), cfg.rope_base,
-               kc.data_ptr(), vc.data_ptr(), self.max_seq, self.q_terms.data_ptr(), self.k_terms.data_ptr(),
-               self.vt.data_ptr(), n * tp, n, stream)
-        K.call("tgm_gemm_dense_batched", self.q_terms.data_ptr(), BF16, t, n * hd, t * n * hd, self.k_terms.data_ptr(),
-               BF16, t, n * hd, t * n * hd, g, n * hd, self.scores.data_ptr(), F32, tp, t * tp, z, 0, z, stream)
-        K.call("tgm_dec_causal_softmax", self.scores.data_ptr(), z * t, t, tp, 1.0 / math.sqrt(hd),
-               self.probs.data_ptr(), n * tp, n, stream)
-        K.call("tgm_gemm_dense_batched", self.probs.data_ptr(), BF16, t, n * tp, t * n * tp, self.vt.data_ptr(), BF16,
+               kc.data_ptr(), vc.data_ptr(), self.max_seq, buf["q"].data_ptr(), buf["k"].data_ptr(),
+               buf["vt"].data_ptr(), n * tp, n, stream)
+        K.call("tgm_gemm_dense_batched", buf["q"].data_ptr(), BF16, t, n * hd, t * n * hd, buf["k"].data_ptr(),
+               BF16, t, n * hd, t * n * hd, g, n * hd, buf["s"].data_ptr(), F32, tp, t * tp, z, 0, z, stream)
+        K.call("tgm_dec_causal_softmax", buf["s"].data_ptr(), z * t, t, tp, 1.0 / math.sqrt(hd),
+               buf["p"].data_ptr(), n * tp, n, stream)
+        K.call("tgm_gemm_dense_batched", buf["p"].data_ptr(), BF16, t, n * tp, t * n * tp, buf["vt"].data_ptr(), BF16,
                hd, n * tp, hd * n * tp, g, n * tp, self.attn.data_ptr(), F16, H * hd, hd, H, t * H * hd, z, stream)
 
     def _head(self, first_row: int, row_stride: int, stream: int, advance: bool) -> None:
@@ -310,6 +322,8 @@ class Decoder:
             raise ValueError(f"prompts must be [{self.batch}, 1..{self.max_prompt}]")
         if int(prompts.min()) < 0 or int(prompts.max()) >= self.cfg.vocab:
             raise ValueError("prompt tokens out of range")
+        if self.prompt_attention not in ("fused", "gemm", "split"):
+            raise ValueError(f"prompt_attention must be 'fused', 'gemm' or 'split', not {self.prompt_attention!r}")
         t = prompts.shape[1]
         rows = self.batch * t
         stream = K.stream_of(self.h)

@@ -58,6 +58,7 @@ _SIGNATURES = {
     "tgm_dec_rope_kv": (_P, _I64, _I64, _I64, _I64, _I64, _P, ctypes.c_double, _P, _P, _I64, _P, _P, _P, _I64, _I64,
                         _P),
     "tgm_dec_causal_softmax": (_P, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _I64, _P),
+    "tgm_dec_prefill_attention": (_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _INT, _P),
     "tgm_dec_attention": (_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, ctypes.c_double, _I64, _P, _I64, _P, _INT,
                           _P),
     "tgm_dec_silu_mul": (_P, _I64, _I64, _P, _INT, _P),
