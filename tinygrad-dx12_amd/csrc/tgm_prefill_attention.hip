@@ -13,7 +13,8 @@
 //   S^T[key, query]  = K . Q^T       A = the K block (LDS),     B = q (registers)
 //   O^T[dim, query] += V^T . P^T     A = the V^T block (LDS),   B = p (registers)
 //
-// Accuracy: q (scaled by 1/sqrt(hd)) and each probability are split into three bf16 terms
+// Accuracy: q (scaled by log2(e) / sqrt(hd), so that the softmax runs on exp2) and each
+// probability are split into three bf16 terms
 // x = t0 + t1 + t2 (t0 = bf16(x), each later term the bf16 of what the earlier ones leave;
 // three terms hold the 24 bits of an fp32 value) and every term meets the bf16 K or V
 // operand in its own MFMA.  Products of bf16 values are exact in fp32, so S and O carry only
@@ -76,15 +77,18 @@ __global__ void __launch_bounds__(256) dec_prefill_attention(const float* __rest
   const int h = blockIdx.y, b = blockIdx.z, j = h / (H / HK);
   const int p0 = pos[b];
   const int64_t ld = (int64_t)(H + 2 * HK) * HD;
-  const int tq = blockIdx.x * kPaQueries + wave * 32 + l32;  // this lane's prompt token
+  // the longest query blocks (the last tokens, which see the most keys) are launched first
+  const int qblk = (int)(gridDim.x - 1 - blockIdx.x);
+  const int tq = qblk * kPaQueries + wave * 32 + l32;  // this lane's prompt token
   const bool qvalid = tq < T;
   const int tqc = qvalid ? tq : T - 1;
   const int qpos = p0 + tqc;
-  const int t_end = min((int)blockIdx.x * kPaQueries + kPaQueries, T);
+  const int t_end = min(qblk * kPaQueries + kPaQueries, T);
   const int nkeys = min(p0 + t_end, max_seq);                 // keys 0 .. nkeys - 1 serve the workgroup
   const int nblocks = nkeys > 0 ? (nkeys + kPaKeys - 1) / kPaKeys : 0;
-  const int wave_end = min((int)blockIdx.x * kPaQueries + wave * 32 + 32, T);
+  const int wave_end = min(qblk * kPaQueries + wave * 32 + 32, T);
   const int wave_maxpos = p0 + wave_end - 1;                  // blocks past it are masked for every lane
+  const int wave_minpos = p0 + min(qblk * kPaQueries + wave * 32, T - 1);  // blocks up to it need no mask
   const uint16_t* kbase = kc + ((int64_t)b * HK + j) * max_seq * HD;
   const uint16_t* vbase = vc + ((int64_t)b * HK + j) * max_seq * HD;
 
@@ -96,8 +100,8 @@ __global__ void __launch_bounds__(256) dec_prefill_attention(const float* __rest
     for (int s = 0; s < NJ; ++s) {
       const f32x4 x0 = *(const f32x4*)(qrow + 16 * s + 8 * half);
       const f32x4 x1 = *(const f32x4*)(qrow + 16 * s + 8 * half + 4);
-      float r[8] = {x0[0] * scale, x0[1] * scale, x0[2] * scale, x0[3] * scale,
-                    x1[0] * scale, x1[1] * scale, x1[2] * scale, x1[3] * scale};
+      const float sl = scale * 1.4426950408889634f;  // log2(e): the softmax runs on exp2
+      float r[8] = {x0[0] * sl, x0[1] * sl, x0[2] * sl, x0[3] * sl, x1[0] * sl, x1[1] * sl, x1[2] * sl, x1[3] * sl};
       pa_split(r, qt[s]);
     }
   }
@@ -153,33 +157,42 @@ __global__ void __launch_bounds__(256) dec_prefill_attention(const float* __rest
           for (int t = 0; t < kPaTerms; ++t) S[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qt[s][t], S[kt], 0, 0, 0);
         }
       // online softmax of this lane's query over the block (the lane pair l, l ^ 32 holds it)
+      // (scores are in log2 units: q carries scale * log2(e))
+      if (kb * kPaKeys + kPaKeys - 1 > wave_minpos) {  // the block reaches past some query: mask (uniform)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int key = kb * kPaKeys + kt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+            if (key > qpos) S[kt][v] = -INFINITY;
+          }
+      }
       float bm = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int key = kb * kPaKeys + kt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-          if (key > qpos) S[kt][v] = -INFINITY;
-          bm = fmaxf(bm, S[kt][v]);
-        }
+        for (int v = 0; v < 16; ++v) bm = fmaxf(bm, S[kt][v]);
       bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
       const float mn = fmaxf(m, bm);  // finite: block 0 holds key 0 <= qpos
-      const float alpha = m == -INFINITY ? 0.f : expf(m - mn);
       float ls = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const float p = S[kt][v] == -INFINITY ? 0.f : expf(S[kt][v] - mn);
+          const float p = exp2f(S[kt][v] - mn);  // 0 for masked keys
           S[kt][v] = p;
           ls += p;
         }
-      l = l * alpha + ls;
+      if (__any(mn != m)) {  // some lane's maximum moved: rescale (a wave-uniform branch)
+        const float alpha = m == -INFINITY ? 0.f : exp2f(m - mn);
+        l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) O[dt][v] *= alpha;
+      }
+      l += ls;
       m = mn;
-#pragma unroll
-      for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) O[dt][v] *= alpha;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
