@@ -306,7 +306,7 @@ def copy_calibration(torch, mib: int, steps: int) -> None:
 def main() -> int:
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is design-only)"}))
+        print(json.dumps({"error": "this benchmark runs on one GPU; --gpus must be 1 (multi-GPU sharding is design-only)"}))
         return 2
     import torch
 

@@ -1,7 +1,7 @@
 """CPU restatement of the Llama-style decoder around the packed path (test infrastructure only).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
-import this module; it is the checker, never the thing measured or shipped.
+import this module; it checks the device path and is never the thing measured or shipped.
 
 The reference has no model code (a decoder on it would be tinygrad ops around
 ``PackedTensor.matmul``, src/tinygrad_dx12/codegen/decomp/dx12.py:108-112), so nothing here

@@ -1,7 +1,7 @@
 """CPU oracle for the packed low-bit matmul path (test infrastructure only).
 
 This module restates, in NumPy, the reference's packed-format semantics so that
-the HIP kernels can be checked against it.  It is the checker, never the thing
+the HIP kernels can be checked against it.  It only checks; it is never the thing
 measured or shipped: only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import it.
 

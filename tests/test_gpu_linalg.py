@@ -268,7 +268,7 @@ def test_gemv_int4_one_hot_is_exact(dev, fmt):
     assert np.array_equal(y, deq[:, cols].T.astype(np.float32))
 
 
-def test_gemv_int4_north_star_shape(dev):
+def test_gemv_int4_14336x4096_shape(dev):
     """INT4 g32 fp16-scale GEMV at 14336 x 4096, fp16 x [1, 4096] -> fp16."""
     n, k = 14336, 4096
     rng = np.random.default_rng(6)

@@ -3,7 +3,7 @@
 The reference recognises scheduled rank-two matrix reductions in tinygrad's kernel graph and
 lowers them to its native LinAlg GEMM before scalar expansion, keeping autograd and JIT replay
 working (alexandreteles/tinygrad-dx12 src/tinygrad_dx12/codegen/matmul.py:13-246).  tinygrad is
-not part of this build; the graph a caller hands over here is a ``torch.fx`` GraphModule, and
+not installed here; the graph a caller hands over here is a ``torch.fx`` GraphModule, and
 the rewrite works on its nodes with the same conservative rules:
 
 * only a product of two rank-two operands with static shapes is a candidate (``match_matmul``);
