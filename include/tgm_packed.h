@@ -142,6 +142,21 @@ int tgm_gemm_w(const void* a, int a_dtype, int64_t m, int64_t lda,
                void* c, int c_dtype, int64_t ldc, void* stream);
 
 /*
+ * tgm_gemm_w with K split over up to `splits` groups of workgroups, for products with too few
+ * output tiles to fill the chip (few rows, or N of a few thousand): each group writes fp32
+ * partial products to `workspace` ([splits][M][N]), and a reduction sums them in group
+ * order (deterministic) and rounds once to c_dtype.  The effective split count makes every
+ * group hold at least one 128-wide K step; with one group, or N % 4 != 0, this is exactly
+ * tgm_gemm_w and needs no workspace.  Otherwise workspace (16-byte aligned) must hold
+ * tgm_gemm_w_split_workspace(m, n, splits) bytes.  The reference has no split-K (its GEMM is a
+ * single D3D12 dispatch, renderer/linalg.py:38-124).
+ */
+int64_t tgm_gemm_w_split_workspace(int64_t m, int64_t n, int64_t splits);
+int tgm_gemm_w_split(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n, int64_t k,
+                     const void* scales, int scale_dtype, int64_t block_size, void* c, int c_dtype, int64_t ldc,
+                     int64_t splits, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * tgm_gemm_w for FP4 weights whose rows interleave the gate (row 2 i) and up (row 2 i + 1)
  * projections of a SwiGLU block, with the activation in the epilogue:
  *

@@ -447,6 +447,59 @@ def test_gemm_w_int4_prefill_shape(dev):
     assert O.max_rel_err(c.float().cpu().numpy()[np.ix_(rows, cols)], ref) <= TOL
 
 
+def _gemm_w_call(name, a, w, c, *extra):
+    from tinygrad_mi355x.runtime import kernels as K
+    sdt = K.dtype_id(w.scales.dtype) if w.scales is not None else -1
+    K.call(name, a.data_ptr(), K.dtype_id(a.dtype), a.shape[0], a.stride(0), w.data.data_ptr(), K.FORMAT_IDS[w.format],
+           w.shape[0], w.shape[1], K.ptr(w.scales), sdt, w.block_size, c.data_ptr(), K.dtype_id(c.dtype), c.stride(0),
+           *extra, torch.cuda.current_stream().cuda_stream)
+
+
+@pytest.mark.parametrize("fmt,mnk,splits", [("fp4_e2m1", (512, 4096, 14336), 4), ("fp4_e2m1", (200, 1000, 1024), 3),
+                                            ("fp6_e3m2", (300, 512, 640), 8), ("int4", (512, 6144, 4096), 2),
+                                            ("int4", (129, 256, 1152), 5), ("fp4_e2m1", (64, 1002, 512), 4)])
+def test_gemm_w_split_k(dev, fmt, mnk, splits):
+    """Split-K (fp32 partials per K range, summed in a fixed order) against the single-pass
+    GEMM and the fp64 oracle; two runs are bit-identical; a split count beyond the K steps, or
+    N % 4 != 0 (the last case), falls back to the single pass exactly."""
+    from tinygrad_mi355x.runtime import kernels as K
+    m, n, k = mnk
+    rng = np.random.default_rng(m + n + k)
+    if fmt == "int4":
+        w, deq = int4_weight(dev, fmt, n, k, torch.float16, 128, rng)
+        a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float16)).to(dev)
+    else:
+        w, deq = make_weight(dev, fmt, n, k, "e8m0", rng)
+        a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    ws_bytes = K.load_library().tgm_gemm_w_split_workspace(m, n, splits)
+    ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=dev)
+    one = torch.empty((m, n), dtype=torch.float32, device=dev)
+    _gemm_w_call("tgm_gemm_w", a, w, one)
+    runs = []
+    for _ in range(2):
+        c = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+        _gemm_w_call("tgm_gemm_w_split", a, w, c, splits, ws.data_ptr(), ws_bytes)
+        runs.append(c)
+    assert torch.equal(runs[0], runs[1])
+    if n % 4:
+        assert torch.equal(runs[0], one)
+    ref = a.float().cpu().numpy().astype(np.float64) @ deq.T
+    # fp32 outputs: only summation order differs (K up to 14336 terms)
+    assert O.max_rel_err(runs[0].cpu().numpy(), ref) <= 1e-3
+    assert O.max_rel_err(runs[0].cpu().numpy(), one.cpu().numpy().astype(np.float64)) <= 1e-3
+
+
+def test_gemm_w_split_k_rejects_a_small_workspace(dev):
+    from tinygrad_mi355x.runtime import kernels as K
+    rng = np.random.default_rng(2)
+    w, _ = make_weight(dev, "fp4_e2m1", 256, 1024, "e8m0", rng)
+    a = torch.zeros((128, 1024), dtype=torch.bfloat16, device=dev)
+    c = torch.empty((128, 256), dtype=torch.float32, device=dev)
+    ws = torch.empty(16, dtype=torch.float32, device=dev)
+    with pytest.raises(ValueError, match="workspace"):
+        _gemm_w_call("tgm_gemm_w_split", a, w, c, 4, ws.data_ptr(), 64)
+
+
 @pytest.mark.parametrize("fa,fb", [("fp4_e2m1", "fp4_e2m1"), ("fp6_e2m3", "fp4_e2m1"), ("fp6_e3m2", "fp6_e2m3")])
 def test_gemm_mx_parity(dev, fa, fb):
     m, n, k = 64, 96, 256

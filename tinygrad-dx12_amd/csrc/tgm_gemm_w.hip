@@ -86,7 +86,8 @@ __device__ __forceinline__ void decode64(const u32x4* raw, unsigned sbits, bf16x
 template <int FMT, bool SCALED, bool SWIGLU = false>
 __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, unsigned lda_bytes,
                                                  const uint8_t* __restrict__ w, const uint8_t* __restrict__ sw,
-                                                 int M, int N, int K, void* __restrict__ c, int cdt, int64_t ldc) {
+                                                 int M, int N, int K, void* __restrict__ c, int cdt, int64_t ldc,
+                                                 int kps, float* __restrict__ part) {
   using T = GemmWTraits<FMT>;
   constexpr int FA = 2, FB = 2;
   __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kWStage];
@@ -97,7 +98,9 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
   int tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, kWGroupM, tm, tn);
   const int m0 = tm * kWM, n0 = tn * kWN;
-  const int nsteps = K / kWK;
+  // split K: blockIdx.y takes steps [s_begin, s_begin + kps) and then writes an fp32 partial tile
+  const int s_begin = (int)blockIdx.y * kps;
+  const int nsteps = min(kps, K / kWK - s_begin);
   const unsigned kbw = (unsigned)K / 8u * (FMT == TGM_FMT_FP4_E2M1 ? 4u : 6u);  // packed bytes per W row
   const unsigned kblk = (unsigned)K / 32u;
   const i32x4v ra = buffer_rsrc(a, (unsigned)(M - 1) * lda_bytes + (unsigned)K * 2u);
@@ -135,13 +138,14 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
 
   auto dma_step = [&](int s, int buf) __attribute__((always_inline)) {
     const unsigned st = lds_base + (unsigned)(buf * kWStage);
+    const unsigned sk = (unsigned)(s_begin + s);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) lds_dma16(ra, st + (unsigned)(4 * wave + q) * 1024u, voa[q] + (unsigned)s * 256u);
+    for (int q = 0; q < 4; ++q) lds_dma16(ra, st + (unsigned)(4 * wave + q) * 1024u, voa[q] + sk * 256u);
 #pragma unroll
     for (int q = 0; q < NWL; ++q)
       if (NWL * wave + q < T::kPanelLoads)
-        lds_dma16(rw, st + kAPanel + (unsigned)(NWL * wave + q) * 1024u, vow[q] + (unsigned)s * (unsigned)T::kRow);
-    if (SCALED && wave < 4) lds_dma4(rs, st + kAPanel + kWPanelMax + (unsigned)wave * 256u, vos + (unsigned)s * 4u);
+        lds_dma16(rw, st + kAPanel + (unsigned)(NWL * wave + q) * 1024u, vow[q] + sk * (unsigned)T::kRow);
+    if (SCALED && wave < 4) lds_dma4(rs, st + kAPanel + kWPanelMax + (unsigned)wave * 256u, vos + sk * 4u);
   };
 
   // ---- fragment reads
@@ -219,10 +223,33 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
   for (int i = 0; i < FA; ++i)
 #pragma unroll
     for (int j = 0; j < FB; ++j)
-      if constexpr (SWIGLU)
+      if (part)
+        store_tile32(acc[i][j], ep, lane, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, M, N,
+                     part + (int64_t)blockIdx.y * M * N, TGM_F32, N);
+      else if constexpr (SWIGLU)
         store_tile32_swiglu(acc[i][j], ep, lane, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, M, N, c, cdt, ldc);
       else
         store_tile32(acc[i][j], ep, lane, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, M, N, c, cdt, ldc);
+}
+
+// Sum of the split-K partial products [splits][M][N] (fp32) in split order, rounded once to
+// C; 4 consecutive elements of a row per thread and pass (N % 4 == 0).
+__global__ void __launch_bounds__(256) gemm_split_reduce(const float* __restrict__ part, int splits, int64_t M,
+                                                         int64_t N, void* __restrict__ c, int cdt, int64_t ldc) {
+  const int64_t total = M * N;
+  for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < total; i += (int64_t)gridDim.x * 256 * 4) {
+    f32x4 acc = *(const f32x4*)(part + i);
+    for (int z = 1; z < splits; ++z) {
+      const f32x4 v = *(const f32x4*)(part + (int64_t)z * total + i);
+      acc[0] += v[0];
+      acc[1] += v[1];
+      acc[2] += v[2];
+      acc[3] += v[3];
+    }
+    const int64_t r = i / N, col = i - r * N;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) store_c(c, cdt, r * ldc + col + e, acc[e]);
+  }
 }
 
 // ---- INT4 / UINT4 weights x f16 activations, per-group scales (f16, bf16 or f32).
@@ -266,7 +293,8 @@ __device__ __forceinline__ float scale_value(const void* p, int64_t i) {
 template <int G, int SDT, bool SIGNED>
 __global__ void __launch_bounds__(512) gemm_w_i4(const uint8_t* __restrict__ a, unsigned lda_bytes,
                                                  const uint8_t* __restrict__ w, const void* __restrict__ sw,
-                                                 int M, int N, int K, void* __restrict__ c, int cdt, int64_t ldc) {
+                                                 int M, int N, int K, void* __restrict__ c, int cdt, int64_t ldc,
+                                                 int kps, float* __restrict__ part) {
   constexpr int FA = 2, FB = 2, kRow = 64, kPanelLoads = kWN * kRow / 1024, NWL = kPanelLoads / 8;
   constexpr int GS = G ? kWK / G : 1;  // scale groups per step
   __shared__ __attribute__((aligned(16))) unsigned char lds[2 * (kAPanel + kWN * kRow)];
@@ -278,7 +306,8 @@ __global__ void __launch_bounds__(512) gemm_w_i4(const uint8_t* __restrict__ a, 
   int tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, kWGroupM, tm, tn);
   const int m0 = tm * kWM, n0 = tn * kWN;
-  const int nsteps = K / kWK;
+  const int s_begin = (int)blockIdx.y * kps;  // split K, as in gemm_w_mx
+  const int nsteps = min(kps, K / kWK - s_begin);
   const unsigned kbw = (unsigned)K / 2u;
   const i32x4v ra = buffer_rsrc(a, (unsigned)(M - 1) * lda_bytes + (unsigned)K * 2u);
   const i32x4v rw = buffer_rsrc(w, (unsigned)N * kbw);
@@ -299,11 +328,12 @@ __global__ void __launch_bounds__(512) gemm_w_i4(const uint8_t* __restrict__ a, 
   }
   auto dma_step = [&](int s, int buf) __attribute__((always_inline)) {
     const unsigned st = lds_base + (unsigned)(buf * kStage);
+    const unsigned sk = (unsigned)(s_begin + s);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) lds_dma16(ra, st + (unsigned)(4 * wave + q) * 1024u, voa[q] + (unsigned)s * 256u);
+    for (int q = 0; q < 4; ++q) lds_dma16(ra, st + (unsigned)(4 * wave + q) * 1024u, voa[q] + sk * 256u);
 #pragma unroll
     for (int q = 0; q < NWL; ++q)
-      lds_dma16(rw, st + kAPanel + (unsigned)(NWL * wave + q) * 1024u, vow[q] + (unsigned)s * (unsigned)kRow);
+      lds_dma16(rw, st + kAPanel + (unsigned)(NWL * wave + q) * 1024u, vow[q] + sk * (unsigned)kRow);
   };
   const int half = lane >> 5;
   const int a_row = wm * 64 + (lane & 31);
@@ -322,7 +352,7 @@ __global__ void __launch_bounds__(512) gemm_w_i4(const uint8_t* __restrict__ a, 
 #pragma unroll
       for (int t = 0; t < FB; ++t)
 #pragma unroll
-        for (int g = 0; g < GS; ++g) dst[t][g] = scale_value<SDT>(sw, srow[t] + (int64_t)s * GS + g);
+        for (int g = 0; g < GS; ++g) dst[t][g] = scale_value<SDT>(sw, srow[t] + (int64_t)(s_begin + s) * GS + g);
     }
   };
   f32x16 acc[FA][FB];
@@ -418,24 +448,31 @@ __global__ void __launch_bounds__(512) gemm_w_i4(const uint8_t* __restrict__ a, 
   for (int i = 0; i < FA; ++i)
 #pragma unroll
     for (int j = 0; j < FB; ++j)
-      store_tile32(acc[i][j], ep, lane, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, M, N, c, cdt, ldc);
+      if (part)
+        store_tile32(acc[i][j], ep, lane, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, M, N,
+                     part + (int64_t)blockIdx.y * M * N, TGM_F32, N);
+      else
+        store_tile32(acc[i][j], ep, lane, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, M, N, c, cdt, ldc);
 }
 
 template <int G, int SDT, bool SIGNED>
 int launch_gemm_w_i4(const void* a, int64_t lda, const void* w, const void* scales, int64_t m, int64_t n, int64_t k,
-                     void* c, int cdt, int64_t ldc, hipStream_t stream) {
+                     void* c, int cdt, int64_t ldc, hipStream_t stream, int splits = 1, float* part = nullptr) {
   const int64_t tiles = ((m + kWM - 1) / kWM) * ((n + kWN - 1) / kWN);
-  hipLaunchKernelGGL((gemm_w_i4<G, SDT, SIGNED>), dim3((unsigned)tiles), dim3(512), 0, stream, (const uint8_t*)a,
-                     (unsigned)(lda * 2), (const uint8_t*)w, scales, (int)m, (int)n, (int)k, c, cdt, ldc);
+  const int kps = (int)((k / kWK + splits - 1) / splits);
+  hipLaunchKernelGGL((gemm_w_i4<G, SDT, SIGNED>), dim3((unsigned)tiles, (unsigned)splits), dim3(512), 0, stream,
+                     (const uint8_t*)a, (unsigned)(lda * 2), (const uint8_t*)w, scales, (int)m, (int)n, (int)k, c, cdt,
+                     ldc, kps, part);
   return launch_status("tgm_gemm_w");
 }
 
 template <bool SIGNED>
 int dispatch_gemm_w_i4(const void* a, int64_t lda, const void* w, const void* scales, int sdt, int64_t bs, int64_t m,
-                       int64_t n, int64_t k, void* c, int cdt, int64_t ldc, hipStream_t st) {
-  if (!scales) return launch_gemm_w_i4<0, TGM_F32, SIGNED>(a, lda, w, scales, m, n, k, c, cdt, ldc, st);
+                       int64_t n, int64_t k, void* c, int cdt, int64_t ldc, hipStream_t st, int splits, float* part) {
+  if (!scales) return launch_gemm_w_i4<0, TGM_F32, SIGNED>(a, lda, w, scales, m, n, k, c, cdt, ldc, st, splits, part);
 #define TGM_I4_CASE(G, SDT) \
-  if (bs == G && sdt == SDT) return launch_gemm_w_i4<G, SDT, SIGNED>(a, lda, w, scales, m, n, k, c, cdt, ldc, st);
+  if (bs == G && sdt == SDT)  \
+    return launch_gemm_w_i4<G, SDT, SIGNED>(a, lda, w, scales, m, n, k, c, cdt, ldc, st, splits, part);
   TGM_I4_CASE(32, TGM_F16) TGM_I4_CASE(64, TGM_F16) TGM_I4_CASE(128, TGM_F16)
   TGM_I4_CASE(32, TGM_BF16) TGM_I4_CASE(64, TGM_BF16) TGM_I4_CASE(128, TGM_BF16)
   TGM_I4_CASE(32, TGM_F32) TGM_I4_CASE(64, TGM_F32) TGM_I4_CASE(128, TGM_F32)
@@ -445,11 +482,12 @@ int dispatch_gemm_w_i4(const void* a, int64_t lda, const void* w, const void* sc
 
 template <int FMT, bool SCALED, bool SWIGLU = false>
 int launch_gemm_w(const void* a, int64_t lda, const void* w, const void* scales, int64_t m, int64_t n, int64_t k,
-                  void* c, int cdt, int64_t ldc, hipStream_t stream) {
+                  void* c, int cdt, int64_t ldc, hipStream_t stream, int splits = 1, float* part = nullptr) {
   const int64_t tiles = ((m + kWM - 1) / kWM) * ((n + kWN - 1) / kWN);
-  hipLaunchKernelGGL((gemm_w_mx<FMT, SCALED, SWIGLU>), dim3((unsigned)tiles), dim3(512), 0, stream,
+  const int kps = (int)((k / kWK + splits - 1) / splits);
+  hipLaunchKernelGGL((gemm_w_mx<FMT, SCALED, SWIGLU>), dim3((unsigned)tiles, (unsigned)splits), dim3(512), 0, stream,
                      (const uint8_t*)a, (unsigned)(lda * 2), (const uint8_t*)w, (const uint8_t*)scales, (int)m, (int)n,
-                     (int)k, c, cdt, ldc);
+                     (int)k, c, cdt, ldc, kps, part);
   return launch_status(SWIGLU ? "tgm_gemm_w_swiglu" : "tgm_gemm_w");
 }
 
@@ -457,10 +495,11 @@ int launch_gemm_w(const void* a, int64_t lda, const void* w, const void* scales,
 
 using namespace tgm;
 
-extern "C" int tgm_gemm_w(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n,
-                          int64_t k, const void* scales, int scale_dtype, int64_t block_size, void* c, int c_dtype,
-                          int64_t ldc, void* stream) {
-  clear_error();
+// tgm_gemm_w with K split over `splits` rows of workgroups (fp32 partials in `part`, summed by
+// gemm_split_reduce); splits == 1 with part == nullptr is the plain product.
+static int gemm_w_impl(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n, int64_t k,
+                       const void* scales, int scale_dtype, int64_t block_size, void* c, int c_dtype, int64_t ldc,
+                       int splits, float* part, void* stream) {
   TGM_CHECK_ARG(a && w && c, "null operand");
   TGM_CHECK_ARG(valid_format(fmt), "unknown packed format %d", fmt);
   TGM_CHECK_ARG(m >= 0 && n >= 0 && k >= 0, "invalid gemm sizes");
@@ -485,16 +524,55 @@ extern "C" int tgm_gemm_w(const void* a, int a_dtype, int64_t m, int64_t lda, co
   const int64_t lda_eff = m > 1 ? lda : k;
   if (int4)
     return fmt == TGM_FMT_INT4
-               ? dispatch_gemm_w_i4<true>(a, lda_eff, w, scales, scale_dtype, block_size, m, n, k, c, c_dtype, ldc, st)
-               : dispatch_gemm_w_i4<false>(a, lda_eff, w, scales, scale_dtype, block_size, m, n, k, c, c_dtype, ldc, st);
+               ? dispatch_gemm_w_i4<true>(a, lda_eff, w, scales, scale_dtype, block_size, m, n, k, c, c_dtype, ldc, st,
+                                          splits, part)
+               : dispatch_gemm_w_i4<false>(a, lda_eff, w, scales, scale_dtype, block_size, m, n, k, c, c_dtype, ldc, st,
+                                           splits, part);
   switch (fmt * 2 + (scaled ? 1 : 0)) {
-    case TGM_FMT_FP4_E2M1 * 2 + 1: return launch_gemm_w<TGM_FMT_FP4_E2M1, true>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st);
-    case TGM_FMT_FP4_E2M1 * 2: return launch_gemm_w<TGM_FMT_FP4_E2M1, false>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st);
-    case TGM_FMT_FP6_E2M3 * 2 + 1: return launch_gemm_w<TGM_FMT_FP6_E2M3, true>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st);
-    case TGM_FMT_FP6_E2M3 * 2: return launch_gemm_w<TGM_FMT_FP6_E2M3, false>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st);
-    case TGM_FMT_FP6_E3M2 * 2 + 1: return launch_gemm_w<TGM_FMT_FP6_E3M2, true>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st);
-    default: return launch_gemm_w<TGM_FMT_FP6_E3M2, false>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st);
+    case TGM_FMT_FP4_E2M1 * 2 + 1: return launch_gemm_w<TGM_FMT_FP4_E2M1, true>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st, splits, part);
+    case TGM_FMT_FP4_E2M1 * 2: return launch_gemm_w<TGM_FMT_FP4_E2M1, false>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st, splits, part);
+    case TGM_FMT_FP6_E2M3 * 2 + 1: return launch_gemm_w<TGM_FMT_FP6_E2M3, true>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st, splits, part);
+    case TGM_FMT_FP6_E2M3 * 2: return launch_gemm_w<TGM_FMT_FP6_E2M3, false>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st, splits, part);
+    case TGM_FMT_FP6_E3M2 * 2 + 1: return launch_gemm_w<TGM_FMT_FP6_E3M2, true>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st, splits, part);
+    default: return launch_gemm_w<TGM_FMT_FP6_E3M2, false>(a, lda_eff, w, scales, m, n, k, c, c_dtype, ldc, st, splits, part);
   }
+}
+
+extern "C" int tgm_gemm_w(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n,
+                          int64_t k, const void* scales, int scale_dtype, int64_t block_size, void* c, int c_dtype,
+                          int64_t ldc, void* stream) {
+  clear_error();
+  return gemm_w_impl(a, a_dtype, m, lda, w, fmt, n, k, scales, scale_dtype, block_size, c, c_dtype, ldc, 1, nullptr,
+                     stream);
+}
+
+extern "C" int64_t tgm_gemm_w_split_workspace(int64_t m, int64_t n, int64_t splits) {
+  return splits > 1 && m > 0 && n > 0 ? splits * m * n * (int64_t)sizeof(float) : 0;
+}
+
+extern "C" int tgm_gemm_w_split(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n,
+                                int64_t k, const void* scales, int scale_dtype, int64_t block_size, void* c,
+                                int c_dtype, int64_t ldc, int64_t splits, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(splits >= 1 && splits <= 64, "splits must be in [1, 64]");
+  const int64_t steps = k > 0 && k % kWK == 0 ? k / kWK : 1;
+  const int64_t kps = (steps + splits - 1) / (splits < steps ? splits : steps);
+  const int64_t eff = (steps + kps - 1) / kps;  // every split gets at least one K step
+  if (eff <= 1 || n % 4 != 0 || m == 0 || n == 0)  // one split, or rows the reduction does not take
+    return gemm_w_impl(a, a_dtype, m, lda, w, fmt, n, k, scales, scale_dtype, block_size, c, c_dtype, ldc, 1, nullptr,
+                       stream);
+  TGM_CHECK_ARG(workspace && workspace_bytes >= tgm_gemm_w_split_workspace(m, n, eff) &&
+                    (uintptr_t)workspace % 16 == 0,
+                "split-K needs a 16-byte aligned workspace of tgm_gemm_w_split_workspace() bytes");
+  const int st = gemm_w_impl(a, a_dtype, m, lda, w, fmt, n, k, scales, scale_dtype, block_size, c, c_dtype, ldc,
+                             (int)eff, (float*)workspace, stream);
+  if (st != TGM_OK) return st;
+  const int64_t quads = m * n / 4;
+  const unsigned grid = (unsigned)((quads + 255) / 256 < 8192 ? (quads + 255) / 256 : 8192);
+  hipLaunchKernelGGL(gemm_split_reduce, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const float*)workspace, (int)eff,
+                     m, n, c, c_dtype, ldc);
+  return launch_status("tgm_gemm_w_split");
 }
 
 extern "C" int tgm_gemm_w_swiglu(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n,

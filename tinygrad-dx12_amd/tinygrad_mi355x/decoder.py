@@ -144,16 +144,47 @@ def load_weights(path, device: str | torch.device = "cuda") -> tuple[DecoderWeig
     return weights, cfg
 
 
-def _packed_product(x: torch.Tensor, m: int, ldx: int, w: PackedTensor, y: torch.Tensor, ldy: int, stream: int) -> None:
-    """y[:m] = x[:m] @ deq(w)^T: packed GEMV for m <= 16 rows, packed GEMM above."""
+GEMM_TILE_M, GEMM_TILE_N, GEMM_FILL = 128, 256, 192  # packed GEMM output tile; tiles that fill the chip
+
+
+def gemm_splits(m: int, n: int) -> int:
+    """K splits for a packed GEMM whose output tiles alone would leave CUs idle (at most 8)."""
+    tiles = -(-m // GEMM_TILE_M) * -(-n // GEMM_TILE_N)
+    return 1 if tiles >= GEMM_FILL else max(1, min(8, 256 // tiles))
+
+
+def _packed_product(x: torch.Tensor, m: int, ldx: int, w: PackedTensor, y: torch.Tensor, ldy: int, stream: int,
+                    workspace: "_Workspace | None" = None) -> None:
+    """y[:m] = x[:m] @ deq(w)^T: packed GEMV for m <= 16 rows, packed GEMM above (with K split
+    over ``workspace`` when the output has too few tiles)."""
     n, k = w.shape
     sdt = K.dtype_id(w.scales.dtype) if w.scales is not None else -1
     if m <= GEMV_MAX_ROWS:
         K.call("tgm_gemv", w.data.data_ptr(), K.FORMAT_IDS[w.format], n, k, K.ptr(w.scales), sdt, w.block_size,
                x.data_ptr(), K.dtype_id(x.dtype), m, ldx, y.data_ptr(), K.dtype_id(y.dtype), ldy, stream)
+        return
+    splits = gemm_splits(m, n) if workspace is not None else 1
+    if splits > 1:
+        ws = workspace.get(K.load_library().tgm_gemm_w_split_workspace(m, n, splits))
+        K.call("tgm_gemm_w_split", x.data_ptr(), K.dtype_id(x.dtype), m, ldx, w.data.data_ptr(),
+               K.FORMAT_IDS[w.format], n, k, K.ptr(w.scales), sdt, w.block_size, y.data_ptr(), K.dtype_id(y.dtype),
+               ldy, splits, ws.data_ptr(), ws.numel() * 4, stream)
     else:
         K.call("tgm_gemm_w", x.data_ptr(), K.dtype_id(x.dtype), m, ldx, w.data.data_ptr(), K.FORMAT_IDS[w.format], n,
                k, K.ptr(w.scales), sdt, w.block_size, y.data_ptr(), K.dtype_id(y.dtype), ldy, stream)
+
+
+class _Workspace:
+    """A device buffer that grows to the largest request (allocated outside graph capture: only
+    the prefill, which is never captured, asks for one)."""
+
+    def __init__(self, device: torch.device) -> None:
+        self.device, self.buf = device, None
+
+    def get(self, nbytes: int) -> torch.Tensor:
+        if self.buf is None or self.buf.numel() * 4 < nbytes:
+            self.buf = torch.empty((max(nbytes, 16) + 3) // 4, dtype=torch.float32, device=self.device)
+        return self.buf
 
 
 class Decoder:
@@ -198,6 +229,7 @@ class Decoder:
         self.prompt_attention = "fused"
         self.prefill_parts = 3
         self._gemm_buffers: dict[str, torch.Tensor] | None = None
+        self._split_ws = _Workspace(dev)  # split-K partial products of the prefill GEMMs
         # one token: the gate|up GEMV applies SwiGLU itself when its row-streaming kernel covers the shape
         self.fuse_swiglu = (cfg.hidden % 2048 == 0 and cfg.hidden <= 16384)
         # 2 to 16 tokens: the streaming MFMA GEMV applies it (K a multiple of 128)
@@ -219,7 +251,7 @@ class Decoder:
         for li, L in enumerate(self.w.layers):
             K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr() if li else None, rows, d,
                    L.attn_norm.data_ptr(), cfg.eps, self.xn16.data_ptr(), F16, stream)
-            _packed_product(self.xn16, rows, d, L.wqkv, self.qkv, cfg.qkv_rows, stream)
+            _packed_product(self.xn16, rows, d, L.wqkv, self.qkv, cfg.qkv_rows, stream, self._split_ws)
             kc, vc = self.k_cache[li], self.v_cache[li]
             fused = seq_rows == 1 and self.fuse_rope  # one new token per sequence: RoPE + cache store in attention
             if seq_rows > 1 and self.prompt_attention == "fused":
@@ -240,7 +272,7 @@ class Decoder:
                        cfg.head_dim, self.pos.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.max_seq,
                        cfg.rope_base if fused else 0.0, splits, self.workspace.data_ptr() if splits > 1 else None,
                        self.workspace_bytes if splits > 1 else 0, self.attn.data_ptr(), F16, stream)
-            _packed_product(self.attn, rows, cfg.heads * cfg.head_dim, L.wo, self.delta, d, stream)
+            _packed_product(self.attn, rows, cfg.heads * cfg.head_dim, L.wo, self.delta, d, stream, self._split_ws)
             K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr(), rows, d, L.ffn_norm.data_ptr(),
                    cfg.eps, self.xnb.data_ptr(), BF16, stream)
             if (rows == 1 and self.fuse_swiglu) or (1 < rows <= GEMV_MAX_ROWS and self.fuse_swiglu_rows):
@@ -255,9 +287,9 @@ class Decoder:
                        K.dtype_id(w.scales.dtype) if w.scales is not None else -1, w.block_size,
                        self.act.data_ptr(), BF16, cfg.ffn, stream)
             else:
-                _packed_product(self.xnb, rows, d, L.w_gate_up, self.gu, 2 * cfg.ffn, stream)
+                _packed_product(self.xnb, rows, d, L.w_gate_up, self.gu, 2 * cfg.ffn, stream, self._split_ws)
                 K.call("tgm_dec_silu_mul", self.gu.data_ptr(), rows, cfg.ffn, self.act.data_ptr(), BF16, stream)
-            _packed_product(self.act, rows, cfg.ffn, L.w_down, self.delta, d, stream)
+            _packed_product(self.act, rows, cfg.ffn, L.w_down, self.delta, d, stream, self._split_ws)
         K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr(), rows, d, self.w.final_norm.data_ptr(),
                cfg.eps, self.xnb.data_ptr(), BF16, stream)
 

@@ -43,6 +43,8 @@ _SIGNATURES = {
     "tgm_gemv": (_P, _INT, _I64, _I64, _P, _INT, _I64, _P, _INT, _I64, _I64, _P, _INT, _I64, _P),
     "tgm_gemm_w": (_P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _P, _INT, _I64, _P, _INT, _I64, _P),
     "tgm_gemm_w_swiglu": (_P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _P, _INT, _I64, _P, _INT, _I64, _P),
+    "tgm_gemm_w_split": (_P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _P, _INT, _I64, _P, _INT, _I64, _I64, _P, _I64,
+                         _P),
     "tgm_gemm_mx": (_P, _INT, _P, _I64, _P, _INT, _P, _I64, _I64, _P, _INT, _I64, _P),
     "tgm_gemm_plain": (_P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _I64, _I64, _I64, _INT, _P),
     "tgm_quantize_mx": (_P, _INT, _I64, _I64, _INT, _I64, _P, _P, _P),
@@ -65,7 +67,8 @@ _SIGNATURES = {
     "tgm_dec_gemv_bf16": (_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P),
     "tgm_dec_argmax": (_P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _P),
 }
-EXPORTS = ("tgm_abi_version", "tgm_last_error", "tgm_dec_attention_workspace", *_SIGNATURES)
+EXPORTS = ("tgm_abi_version", "tgm_last_error", "tgm_dec_attention_workspace", "tgm_gemm_w_split_workspace",
+           *_SIGNATURES)
 
 
 def library_path() -> Path:
@@ -98,6 +101,8 @@ def load_library() -> ctypes.CDLL:
             fn.restype = ctypes.c_int
         lib.tgm_dec_attention_workspace.argtypes = (_I64, _I64, _I64, _I64)
         lib.tgm_dec_attention_workspace.restype = _I64
+        lib.tgm_gemm_w_split_workspace.argtypes = (_I64, _I64, _I64)
+        lib.tgm_gemm_w_split_workspace.restype = _I64
         _lib = lib
         return lib
 
