@@ -563,3 +563,34 @@ def test_failures_are_cached_per_candidate(dev):
     x = torch.ones((2, 64), dtype=torch.float64, device=dev)
     out = matmul_nt(x, w)
     assert out.dtype is torch.float64
+
+
+def test_concurrent_callers_get_their_sequential_results(dev):
+    """Packed products issued from 6 threads at once (GEMV and GEMM families, several formats)
+    equal the same products issued one after another, bit for bit."""
+    from concurrent.futures import ThreadPoolExecutor
+    from threading import Barrier
+
+    rng = np.random.default_rng(44)
+    cases = []
+    for i, (fmt, m, n, k) in enumerate([("fp4_e2m1", 1, 512, 2048), ("fp6_e2m3", 40, 256, 256),
+                                        ("fp4_e2m1", 4, 1024, 512), ("fp6_e3m2", 1, 300, 256),
+                                        ("fp4_e2m1", 200, 512, 512), ("fp6_e2m3", 8, 128, 384)]):
+        w, _ = make_weight(dev, fmt, n, k, "e8m0", rng)
+        a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
+        cases.append((a, w))
+    expected = [matmul_nt(a, w, dtype=torch.float32) for a, w in cases]
+    torch.cuda.synchronize()
+    barrier = Barrier(len(cases))
+
+    def run(i: int) -> torch.Tensor:
+        barrier.wait()
+        out = [matmul_nt(cases[i][0], cases[i][1], dtype=torch.float32) for _ in range(5)]
+        torch.cuda.synchronize()
+        return out
+
+    with ThreadPoolExecutor(max_workers=len(cases)) as workers:
+        results = list(workers.map(run, range(len(cases))))
+    for got, want in zip(results, expected):
+        assert all(torch.equal(g, want) for g in got)
+

@@ -154,3 +154,33 @@ def test_graph_validation_without_a_gpu():
         MI355XGraph([(a, (), (1, 1, 1), (1, 1, 1), ()), (b, (), (1, 1, 1), (1, 1, 1), ())])
     with pytest.raises(ValueError, match="non-null"):
         StreamGraph(lambda: None, 0)
+
+
+def test_shared_renderer_concurrent_sources():
+    """Concurrent callers of one renderer receive exactly their sequential source (the reference's
+    test_renderer_concurrency.py:11-36 idea): 8 kernels of 4 dtypes with long bodies, rendered
+    from 8 threads released together."""
+    from concurrent.futures import ThreadPoolExecutor
+    from threading import Barrier
+
+    r = MI355XRenderer()
+    cases = []
+    for slot in range(8):
+        dt = (torch.float32, torch.float64, torch.int32, torch.float16)[slot % 4]
+        body = ["auto v = src[0];"] + ["v = v * v + src[0];"] * 2048 + ["out[0] = v;"]
+        cases.append(KernelSpec(f"thread_{slot}", (BufferParam("out", dt, True), BufferParam("src", dt)), (),
+                                tuple(body)))
+    expected = [r.render(c) for c in cases]
+    barrier = Barrier(len(cases))
+
+    def render(slot: int) -> str:
+        barrier.wait()
+        try:
+            return r.render(cases[slot])
+        except Exception as error:  # noqa: BLE001 - a failure must show up as a mismatch
+            return type(error).__name__
+
+    with ThreadPoolExecutor(max_workers=len(cases)) as workers:
+        actual = list(workers.map(render, range(len(cases))))
+    assert actual == expected
+
