@@ -62,6 +62,22 @@ int tgm_dec_rope_kv(float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, i
                     const int32_t* pos, double rope_base, void* k_cache, void* v_cache, int64_t max_seq, void* q_out,
                     void* k_out, void* vt_out, int64_t ld_vt, int64_t parts, void* stream);
 
+/* Residual add + RMSNorm folded into a one-row packed GEMV (a decoder layer's norm and the
+ * projection after it in one launch, for one token):
+ *
+ *   x = (h + delta) * (1 / sqrt(sum((h + delta)^2) / k + eps)) * norm_weight    (fp32)
+ *   y = x . deq(W)^T        (x rounded to f16 for INT4 / UINT4 weights, to bf16 for FP4)
+ *
+ * with h, delta [k] fp32 (delta may be NULL), norm_weight [k] bf16, and h + delta stored to
+ * h_out (may be NULL; must not alias h or delta).  swiglu != 0: W interleaves gate and up rows
+ * and y [n / 2] = silu(gate) * up, as tgm_gemv_swiglu.  k = 2048 or 4096; FP4 weights with
+ * E8M0/32 (or no) scales, or INT4 / UINT4 with f16, bf16 or f32 group scales per 32, 64 or
+ * 128; 16-byte aligned operands; otherwise TGM_E_UNSUPPORTED.  The reference has no model
+ * code (decoder harness). */
+int tgm_dec_norm_gemv(const float* h, const float* delta, float* h_out, const void* norm_weight, float eps,
+                      const void* w, int fmt, int64_t n, int64_t k, const void* scales, int scale_dtype,
+                      int64_t block_size, void* y, int y_dtype, int swiglu, void* stream);
+
 /* Causal attention of prompt tokens in one kernel: for every sequence b, q head h and token
  * t (rows b * seq_rows + t of qkv, whose q heads tgm_dec_rope_kv has rotated, at position
  * p = pos[b] + t), out[row, h] = softmax over cache positions k <= p of

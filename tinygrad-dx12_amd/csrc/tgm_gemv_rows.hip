@@ -19,6 +19,7 @@
 // separate kernel first decoded to fp32 (alexandreteles/tinygrad-dx12
 // src/tinygrad_dx12/renderer/linalg.py:127-166, codegen/linalg.py:244-245,
 // codegen/decomp/dx12.py:49-106).
+#include "../../include/tgm_decoder.h"
 #include "tgm_common.h"
 #include "tgm_lanes.h"
 
@@ -87,14 +88,99 @@ __device__ __forceinline__ int reduce_row(int lane) {
   return R == 8 ? reduce_row8(lane) : reduce_row4(lane);
 }
 
+// Residual add + RMSNorm in front of a one-row GEMV (a decoder layer's norm and projection
+// in one launch): x = (h + delta) / rms(h + delta) * w_norm, with h + delta stored to h_out by
+// workgroup 0.  Each workgroup normalises the row once: thread t holds the float4 chunks
+// [1024 j + 4 t, + 4) for j < 2 IPR (K = 2048 IPR values), the sum of squares is reduced over
+// the wave and then over the four waves through LDS, and x goes to LDS, rounded to the GEMV's
+// activation type, in its natural order, where the waves read it as they would read x from
+// memory.  The loads of h, delta and w_norm are issued before the weight stream's first loads,
+// so waiting for them does not wait for the weights (the vector memory counter retires in
+// order), and the norm is computed while the weights are in flight.  Same arithmetic as
+// dec_add_rmsnorm: x * (1 / sqrt(sum(x^2) / K + eps)) * w in fp32.
+struct RowsNorm {
+  const float* h = nullptr;
+  const float* delta = nullptr;  // may be null
+  const uint16_t* w = nullptr;   // bf16 norm weight
+  float eps = 0.f;
+  float* h_out = nullptr;        // may be null
+};
+
+typedef float f32x4n __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2n __attribute__((ext_vector_type(2)));
+
+template <int IPR>
+struct NormRegs {
+  f32x4n a[2 * IPR], b[2 * IPR];
+  u32x2n w[2 * IPR];
+};
+
+template <int IPR>
+__device__ __forceinline__ void norm_issue(const RowsNorm& nm, NormRegs<IPR>& r) {
+  const int t = threadIdx.x;
+  const float* d = nm.delta ? nm.delta : nm.h;  // unconditional loads; the sum selects
+#pragma unroll
+  for (int j = 0; j < 2 * IPR; ++j) {
+    const int o = 1024 * j + 4 * t;
+    r.a[j] = *(const f32x4n*)(nm.h + o);
+    r.b[j] = *(const f32x4n*)(d + o);
+    r.w[j] = *(const u32x2n*)(nm.w + o);
+  }
+}
+
+// LDS-only workgroup barrier: outstanding global loads (the weight stream) stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int IPR, typename T>
+__device__ __forceinline__ void norm_finish(const RowsNorm& nm, const NormRegs<IPR>& r, T* xs, float* red) {
+  constexpr int K = 2048 * IPR;
+  const int t = threadIdx.x;
+  const bool add = nm.delta != nullptr;
+  f32x4n v[2 * IPR];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 2 * IPR; ++j) {
+    v[j] = add ? f32x4n{r.a[j][0] + r.b[j][0], r.a[j][1] + r.b[j][1], r.a[j][2] + r.b[j][2], r.a[j][3] + r.b[j][3]}
+               : r.a[j];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += v[j][e] * v[j][e];
+  }
+  if (blockIdx.x == 0 && nm.h_out) {
+#pragma unroll
+    for (int j = 0; j < 2 * IPR; ++j) *(f32x4n*)(nm.h_out + 1024 * j + 4 * t) = v[j];
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  if ((t & 63) == 0) red[t >> 6] = ss;
+  lds_barrier();
+  ss = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = 1.0f / sqrtf(ss / (float)K + nm.eps);
+#pragma unroll
+  for (int j = 0; j < 2 * IPR; ++j) {
+    T o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const unsigned bits = (r.w[j][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+      o[e] = (T)(v[j][e] * inv * __builtin_bit_cast(float, bits << 16));
+    }
+    *(u32x2n*)(xs + 1024 * j + 4 * t) = __builtin_bit_cast(u32x2n, o);
+  }
+  lds_barrier();
+}
+
 // One wave per R (8 or 4) rows, four waves per workgroup; IPR instructions per row
 // (K = 2048 IPR); D loads in flight per wave.
 // SWIGLU: rows 2 i and 2 i + 1 are the gate and up rows of output i, which becomes
 // silu(gate) * up (the two rows are reduced in lanes l and l ^ 8 for R = 8, l ^ 16 for R = 4).
-template <int R, int IPR, int D, bool SCALED, bool SWIGLU = false>
+// NORM: x is RMSNorm(h + delta) * w_norm (RowsNorm), rounded to bf16 as it is staged.
+template <int R, int IPR, int D, bool SCALED, bool SWIGLU = false, bool NORM = false>
 __global__ void __launch_bounds__(256) gemv_rows_fp4(const uint8_t* __restrict__ w, int64_t N,
                                                    const uint8_t* __restrict__ scales, const __bf16* __restrict__ x,
-                                                   void* __restrict__ y, int ydt) {
+                                                   void* __restrict__ y, int ydt, RowsNorm nm) {
   constexpr int NI = R * IPR;  // load instructions per wave
   constexpr int K = 2048 * IPR, KB = K / 32;
   const int lane = threadIdx.x & 63;
@@ -104,12 +190,19 @@ __global__ void __launch_bounds__(256) gemv_rows_fp4(const uint8_t* __restrict__
   // a 4-dword vector and bit-casting each to a bf16 pair was miscompiled into one repeated
   // pair by the ROCm 7.2 compiler.)
   bf16x2r xr[IPR][16];
+  auto load_x = [&](const __bf16* src) __attribute__((always_inline)) {
 #pragma unroll
-  for (int h = 0; h < IPR; ++h) {
-    const bf16x2r* xp = (const bf16x2r*)(x + 2048 * h + 32 * lane);
+    for (int h = 0; h < IPR; ++h) {
+      const bf16x2r* xp = (const bf16x2r*)(src + 2048 * h + 32 * lane);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) xr[h][j] = xp[j];
-  }
+      for (int j = 0; j < 16; ++j) xr[h][j] = xp[j];
+    }
+  };
+  NormRegs<NORM ? IPR : 1> nr;
+  __shared__ __attribute__((aligned(16))) __bf16 xs[NORM ? K : 8];
+  __shared__ float red[4];
+  if constexpr (NORM) norm_issue<IPR>(nm, nr);
+  else load_x(x);
   auto row_of = [&](int i) __attribute__((always_inline)) {
     const int64_t r = r0 + i / IPR;
     return r < N ? r : N - 1;  // rows past N re-read the last row; they are not stored
@@ -149,6 +242,10 @@ __global__ void __launch_bounds__(256) gemv_rows_fp4(const uint8_t* __restrict__
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int i = 0; i < NI; ++i) sbyte[i] = sl[wv][(i / IPR) * KB + 64 * (i % IPR) + lane];
+  }
+  if constexpr (NORM) {
+    norm_finish<IPR>(nm, nr, xs, red);
+    load_x(xs);
   }
   float acc[R];
 #pragma unroll
@@ -203,11 +300,11 @@ __device__ __forceinline__ float int4_scale(const unsigned char* p) {
 }
 
 // R = 8 rows per wave; GS = log2(group size / 32); SDT = scale dtype (-1: unscaled).
-template <int R, int IPR, int D, int SDT>
+template <int R, int IPR, int D, int SDT, bool NORM = false>
 __global__ void __launch_bounds__(256) gemv_rows_int4(const uint8_t* __restrict__ w, int64_t N,
                                                     const uint8_t* __restrict__ scales, int GS, unsigned flip,
                                                     float bias, const _Float16* __restrict__ x, void* __restrict__ y,
-                                                    int ydt) {
+                                                    int ydt, RowsNorm nm) {
   constexpr int NI = R * IPR;
   constexpr int K = 2048 * IPR;
   constexpr bool SCALED = SDT >= 0;
@@ -217,18 +314,25 @@ __global__ void __launch_bounds__(256) gemv_rows_int4(const uint8_t* __restrict_
   // activations K [2048 h + 32 l, + 32) as the pairs the codes come out in: dword e of
   // the lane's 16 bytes holds codes 8e .. 8e+7, paired (0,2) (4,6) (1,3) (5,7)
   half2r xr[IPR][16];
+  auto load_x = [&](const _Float16* src) __attribute__((always_inline)) {
 #pragma unroll
-  for (int h = 0; h < IPR; ++h) {
-    const unsigned* xp = (const unsigned*)(x + 2048 * h + 32 * lane);
+    for (int h = 0; h < IPR; ++h) {
+      const unsigned* xp = (const unsigned*)(src + 2048 * h + 32 * lane);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const unsigned p0 = xp[4 * e], p1 = xp[4 * e + 1], p2 = xp[4 * e + 2], p3 = xp[4 * e + 3];  // (0,1) (2,3) (4,5) (6,7)
-      xr[h][4 * e + 0] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p1, p0, 0x05040100u));  // x0, x2
-      xr[h][4 * e + 1] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p3, p2, 0x05040100u));  // x4, x6
-      xr[h][4 * e + 2] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p1, p0, 0x07060302u));  // x1, x3
-      xr[h][4 * e + 3] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p3, p2, 0x07060302u));  // x5, x7
+      for (int e = 0; e < 4; ++e) {
+        const unsigned p0 = xp[4 * e], p1 = xp[4 * e + 1], p2 = xp[4 * e + 2], p3 = xp[4 * e + 3];  // (0,1) (2,3) (4,5) (6,7)
+        xr[h][4 * e + 0] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p1, p0, 0x05040100u));  // x0, x2
+        xr[h][4 * e + 1] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p3, p2, 0x05040100u));  // x4, x6
+        xr[h][4 * e + 2] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p1, p0, 0x07060302u));  // x1, x3
+        xr[h][4 * e + 3] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p3, p2, 0x07060302u));  // x5, x7
+      }
     }
-  }
+  };
+  NormRegs<NORM ? IPR : 1> nr;
+  __shared__ __attribute__((aligned(16))) _Float16 xs[NORM ? K : 8];
+  __shared__ float red[4];
+  if constexpr (NORM) norm_issue<IPR>(nm, nr);  // RMSNorm(h + delta) * w_norm, rounded to fp16
+  else load_x(x);
   auto row_of = [&](int i) __attribute__((always_inline)) {
     const int64_t r = r0 + i / IPR;
     return r < N ? r : N - 1;
@@ -268,6 +372,10 @@ __global__ void __launch_bounds__(256) gemv_rows_int4(const uint8_t* __restrict_
 #pragma unroll
     for (int i = 0; i < NI; ++i)
       sv[i] = int4_scale<SDT>(&sl[wv][((i / IPR) * ng + ((64 * (i % IPR) + lane) >> GS)) * SSIZE]);
+  }
+  if constexpr (NORM) {
+    norm_finish<IPR>(nm, nr, xs, red);
+    load_x(xs);
   }
   const half2r hb = {(_Float16)bias, (_Float16)bias};
   float acc[R];
@@ -318,13 +426,13 @@ int launch_gemv_rows(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k
     const unsigned grid = (unsigned)((n + 4 * R - 1) / (4 * R));                                                   \
     if (swiglu)                                                                                                    \
       hipLaunchKernelGGL((gemv_rows_fp4<R, IPR, D, true, true>), dim3(grid), dim3(256), 0, s, (const uint8_t*)w,   \
-                         n, (const uint8_t*)scales, (const __bf16*)x, y, ydt);                                     \
+                         n, (const uint8_t*)scales, (const __bf16*)x, y, ydt, RowsNorm{});                         \
     else if (scales)                                                                                               \
       hipLaunchKernelGGL((gemv_rows_fp4<R, IPR, D, true>), dim3(grid), dim3(256), 0, s, (const uint8_t*)w, n,      \
-                         (const uint8_t*)scales, (const __bf16*)x, y, ydt);                                        \
+                         (const uint8_t*)scales, (const __bf16*)x, y, ydt, RowsNorm{});                            \
     else                                                                                                           \
       hipLaunchKernelGGL((gemv_rows_fp4<R, IPR, D, false>), dim3(grid), dim3(256), 0, s, (const uint8_t*)w, n,     \
-                         (const uint8_t*)scales, (const __bf16*)x, y, ydt);                                        \
+                         (const uint8_t*)scales, (const __bf16*)x, y, ydt, RowsNorm{});                            \
     return TGM_OK;                                                                                                 \
   }
   TGM_ROWS(kRowsPerWave, 1, 8) TGM_ROWS(kRowsPerWave, 2, 16) TGM_ROWS(kRowsPerWave, 3, 16)
@@ -343,7 +451,7 @@ void launch_rows_int4(unsigned grid, hipStream_t s, const void* w, int64_t n, co
   constexpr int R = kRowsPerWaveInt4, D = R * IPR;  // every load in flight at once
   hipLaunchKernelGGL((gemv_rows_int4<R, IPR, D, SDT>), dim3(grid), dim3(256), 0, s, (const uint8_t*)w, n,
                      (const uint8_t*)scales, gs, sgn ? 0x88888888u : 0u, sgn ? 1032.0f : 1024.0f,
-                     (const _Float16*)x, y, ydt);
+                     (const _Float16*)x, y, ydt, RowsNorm{});
 }
 
 template <int IPR>
@@ -380,3 +488,88 @@ int launch_gemv_rows_int4(hipStream_t s, const void* w, int fmt, int64_t n, int6
 }
 
 }  // namespace tgm
+
+namespace tgm {
+
+// RMSNorm + one-row GEMV launches (K = 2048 or 4096).
+template <int IPR>
+static int launch_norm_rows(hipStream_t s, const void* w, int fmt, int64_t n, const void* scales, int sdt, int gs,
+                            const RowsNorm& nm, void* y, int ydt, bool swiglu) {
+  if (fmt == TGM_FMT_FP4_E2M1) {
+    const unsigned grid = (unsigned)((n + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave));
+    constexpr int D = 8 * IPR;
+    if (swiglu)
+      hipLaunchKernelGGL((gemv_rows_fp4<kRowsPerWave, IPR, D, true, true, true>), dim3(grid), dim3(256), 0, s,
+                         (const uint8_t*)w, n, (const uint8_t*)scales, (const __bf16*)nullptr, y, ydt, nm);
+    else if (scales)
+      hipLaunchKernelGGL((gemv_rows_fp4<kRowsPerWave, IPR, D, true, false, true>), dim3(grid), dim3(256), 0, s,
+                         (const uint8_t*)w, n, (const uint8_t*)scales, (const __bf16*)nullptr, y, ydt, nm);
+    else
+      hipLaunchKernelGGL((gemv_rows_fp4<kRowsPerWave, IPR, D, false, false, true>), dim3(grid), dim3(256), 0, s,
+                         (const uint8_t*)w, n, (const uint8_t*)scales, (const __bf16*)nullptr, y, ydt, nm);
+    return TGM_OK;
+  }
+  constexpr int R = kRowsPerWaveInt4, D = R * IPR;
+  const unsigned grid = (unsigned)((n + 4 * R - 1) / (4 * R));
+  const bool sgn = fmt == TGM_FMT_INT4;
+#define TGM_NORM_I4(SDT)                                                                                          \
+  hipLaunchKernelGGL((gemv_rows_int4<R, IPR, D, SDT, true>), dim3(grid), dim3(256), 0, s, (const uint8_t*)w, n,  \
+                     (const uint8_t*)scales, gs, sgn ? 0x88888888u : 0u, sgn ? 1032.0f : 1024.0f,              \
+                     (const _Float16*)nullptr, y, ydt, nm)
+  if (!scales) TGM_NORM_I4(-1);
+  else if (sdt == TGM_F16) TGM_NORM_I4(TGM_F16);
+  else if (sdt == TGM_BF16) TGM_NORM_I4(TGM_BF16);
+  else TGM_NORM_I4(TGM_F32);
+#undef TGM_NORM_I4
+  return TGM_OK;
+}
+
+}  // namespace tgm
+
+using namespace tgm;
+
+extern "C" int tgm_dec_norm_gemv(const float* h, const float* delta, float* h_out, const void* norm_weight, float eps,
+                                 const void* w, int fmt, int64_t n, int64_t k, const void* scales, int scale_dtype,
+                                 int64_t block_size, void* y, int y_dtype, int swiglu, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(h && norm_weight && w && y, "null operand");
+  TGM_CHECK_ARG(valid_format(fmt), "unknown packed format %d", fmt);
+  TGM_CHECK_ARG(n >= 0 && k > 0 && block_size >= 1, "invalid sizes");
+  TGM_CHECK_ARG(!h_out || (h_out != h && h_out != delta), "h_out must not alias h or delta");
+  TGM_CHECK_ARG(!swiglu || n % 2 == 0, "swiglu needs interleaved gate and up rows (n even)");
+  TGM_CHECK_ARG(y_dtype == TGM_BF16 || y_dtype == TGM_F16 || y_dtype == TGM_F32, "output must be bf16, f16 or f32");
+  if (n == 0) return TGM_OK;
+  if (k != 2048 && k != 4096) TGM_UNSUPPORTED("tgm_dec_norm_gemv: K must be 2048 or 4096");
+  if ((uintptr_t)h % 16 || (delta && (uintptr_t)delta % 16) || (h_out && (uintptr_t)h_out % 16) ||
+      (uintptr_t)norm_weight % 16 || (uintptr_t)w % 16)
+    TGM_UNSUPPORTED("tgm_dec_norm_gemv: operands must be 16-byte aligned");
+  int gs = 0;
+  if (fmt == TGM_FMT_FP4_E2M1) {
+    if (scales && (scale_dtype != TGM_E8M0 || block_size != 32))
+      TGM_UNSUPPORTED("tgm_dec_norm_gemv: FP4 scales must be E8M0 per 32");
+    if (swiglu && !scales) TGM_UNSUPPORTED("tgm_dec_norm_gemv: the SwiGLU epilogue needs scaled FP4 weights");
+  } else if (fmt == TGM_FMT_INT4 || fmt == TGM_FMT_UINT4) {
+    if (swiglu) TGM_UNSUPPORTED("tgm_dec_norm_gemv: the SwiGLU epilogue takes FP4 weights");
+    if (scales) {
+      if (scale_dtype != TGM_F16 && scale_dtype != TGM_BF16 && scale_dtype != TGM_F32)
+        TGM_UNSUPPORTED("tgm_dec_norm_gemv: int4 scales must be f16, bf16 or f32");
+      if (block_size != 32 && block_size != 64 && block_size != 128)
+        TGM_UNSUPPORTED("tgm_dec_norm_gemv: int4 groups must be 32, 64 or 128");
+      gs = block_size == 32 ? 0 : block_size == 64 ? 1 : 2;
+      if ((uintptr_t)scales % 16 || n * (k / block_size) * dtype_size(scale_dtype) < 16)
+        TGM_UNSUPPORTED("tgm_dec_norm_gemv: scales must be 16-byte aligned");
+    }
+  } else {
+    TGM_UNSUPPORTED("tgm_dec_norm_gemv: FP4, INT4 or UINT4 weights only");
+  }
+  RowsNorm nm;
+  nm.h = h;
+  nm.delta = delta;
+  nm.w = (const uint16_t*)norm_weight;
+  nm.eps = eps;
+  nm.h_out = h_out;
+  const hipStream_t s = (hipStream_t)stream;
+  const int st = k == 2048 ? launch_norm_rows<1>(s, w, fmt, n, scales, scale_dtype, gs, nm, y, y_dtype, swiglu != 0)
+                           : launch_norm_rows<2>(s, w, fmt, n, scales, scale_dtype, gs, nm, y, y_dtype, swiglu != 0);
+  return st == TGM_OK ? launch_status("tgm_dec_norm_gemv") : st;
+}

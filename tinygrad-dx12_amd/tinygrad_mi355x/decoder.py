@@ -234,6 +234,13 @@ class Decoder:
         self.fuse_swiglu = (cfg.hidden % 2048 == 0 and cfg.hidden <= 16384)
         # 2 to 16 tokens: the streaming MFMA GEMV applies it (K a multiple of 128)
         self.fuse_swiglu_rows = cfg.hidden % 128 == 0
+        # one token: each RMSNorm runs inside the projection after it (tgm_dec_norm_gemv), the
+        # residual stream alternating between h and h_alt
+        self.fuse_norm = (batch == 1 and cfg.hidden in (2048, 4096) and self.fuse_swiglu
+                          and all(L.wqkv.format in ("int4", "uint4", "fp4_e2m1") for L in weights.layers)
+                          and all(L.w_gate_up.format == "fp4_e2m1" and L.w_gate_up.scales is not None
+                                  for L in weights.layers))
+        self.h_alt = torch.empty((batch, d), **f32) if self.fuse_norm else None
         ws = K.load_library().tgm_dec_attention_workspace(batch, cfg.heads, cfg.head_dim, self.splits)
         self.workspace = torch.empty(max(ws // 4, 1), **f32)
         self.workspace_bytes = ws
@@ -248,10 +255,19 @@ class Decoder:
     def _layers(self, rows: int, seq_rows: int, splits: int, stream: int) -> None:
         cfg = self.cfg
         d = cfg.hidden
+        fuse_norm = rows == 1 and self.fuse_norm
         for li, L in enumerate(self.w.layers):
-            K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr() if li else None, rows, d,
-                   L.attn_norm.data_ptr(), cfg.eps, self.xn16.data_ptr(), F16, stream)
-            _packed_product(self.xn16, rows, d, L.wqkv, self.qkv, cfg.qkv_rows, stream, self._split_ws)
+            if fuse_norm:  # h + delta -> h_alt, RMSNorm and the QKV projection in one launch
+                w = L.wqkv
+                K.call("tgm_dec_norm_gemv", self.h.data_ptr(), self.delta.data_ptr() if li else None,
+                       self.h_alt.data_ptr(), L.attn_norm.data_ptr(), cfg.eps, w.data.data_ptr(),
+                       K.FORMAT_IDS[w.format], cfg.qkv_rows, d, K.ptr(w.scales),
+                       K.dtype_id(w.scales.dtype) if w.scales is not None else -1, w.block_size, self.qkv.data_ptr(),
+                       F32, 0, stream)
+            else:
+                K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr() if li else None, rows, d,
+                       L.attn_norm.data_ptr(), cfg.eps, self.xn16.data_ptr(), F16, stream)
+                _packed_product(self.xn16, rows, d, L.wqkv, self.qkv, cfg.qkv_rows, stream, self._split_ws)
             kc, vc = self.k_cache[li], self.v_cache[li]
             fused = seq_rows == 1 and self.fuse_rope  # one new token per sequence: RoPE + cache store in attention
             if seq_rows > 1 and self.prompt_attention == "fused":
@@ -273,6 +289,13 @@ class Decoder:
                        cfg.rope_base if fused else 0.0, splits, self.workspace.data_ptr() if splits > 1 else None,
                        self.workspace_bytes if splits > 1 else 0, self.attn.data_ptr(), F16, stream)
             _packed_product(self.attn, rows, cfg.heads * cfg.head_dim, L.wo, self.delta, d, stream, self._split_ws)
+            if fuse_norm:  # h_alt + delta -> h, RMSNorm and the gate|up projection with SwiGLU
+                w = L.w_gate_up
+                K.call("tgm_dec_norm_gemv", self.h_alt.data_ptr(), self.delta.data_ptr(), self.h.data_ptr(),
+                       L.ffn_norm.data_ptr(), cfg.eps, w.data.data_ptr(), K.FORMAT_IDS[w.format], 2 * cfg.ffn, d,
+                       K.ptr(w.scales), K.dtype_id(w.scales.dtype), w.block_size, self.act.data_ptr(), BF16, 1, stream)
+                _packed_product(self.act, rows, cfg.ffn, L.w_down, self.delta, d, stream, self._split_ws)
+                continue
             K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr(), rows, d, L.ffn_norm.data_ptr(),
                    cfg.eps, self.xnb.data_ptr(), BF16, stream)
             if (rows == 1 and self.fuse_swiglu) or (1 < rows <= GEMV_MAX_ROWS and self.fuse_swiglu_rows):

@@ -61,6 +61,7 @@ _SIGNATURES = {
                         _P),
     "tgm_dec_causal_softmax": (_P, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _I64, _P),
     "tgm_dec_prefill_attention": (_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _INT, _P),
+    "tgm_dec_norm_gemv": (_P, _P, _P, _P, ctypes.c_float, _P, _INT, _I64, _I64, _P, _INT, _I64, _P, _INT, _INT, _P),
     "tgm_dec_attention": (_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, ctypes.c_double, _I64, _P, _I64, _P, _INT,
                           _P),
     "tgm_dec_silu_mul": (_P, _I64, _I64, _P, _INT, _P),
