@@ -97,9 +97,13 @@ __device__ __forceinline__ void load_codes(const uint8_t* p, unsigned out[6]) {
 // as the f32 bit pattern e << 23: v_cvt_scalef32_* use the exponent field with E8M0
 // meaning (0 is 2^-127, 255 is NaN), so every E8M0 byte is exact.
 // Activations live in LDS for the whole kernel when M x (K + 8) bf16 fit (XV > 0: XV
-// straight-line 16-byte loads per thread, then a loop); lanes whose B column c >= M read
-// activation row 0: those D columns are never stored and MFMA columns do not mix, so
-// they need no zeroing.  The NK partial tiles of a weight tile are summed through LDS.
+// straight-line 16-byte loads per thread, then a loop).  Otherwise (XV = 0) each lane's
+// 64 activation bytes of a super-step ride in the ring beside its weights: they are loaded
+// with the super-step's codes, D steps ahead, so that waiting for them (the vector memory
+// counter retires in order) never drains the weight loads behind them.  Lanes whose B
+// column c >= M read activation row 0: those D columns are never stored and MFMA columns
+// do not mix, so they need no zeroing.  The NK partial tiles of a weight tile are summed
+// through LDS.
 template <int FMT, int NT, int NK, int RING, int SMAX, bool EXACT, int XV, int SC>
 __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __restrict__ w, int64_t N, int64_t K,
                                                           const uint8_t* __restrict__ scales, int64_t nblk,
@@ -183,11 +187,20 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __res
       }
     }
   }
+  const __bf16* xg = x + (int64_t)xr * ldx + (int64_t)t_begin * 128 + q * 32;
   unsigned buf[D][6];
+  bf16x8 xq[XLDS ? 1 : D][4];  // XV = 0: the ring's activations
+  auto load_x = [&](int t, int slot) __attribute__((always_inline)) {
+    if constexpr (!XLDS) {
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) xq[slot][s4] = *(const bf16x8*)(xg + (int64_t)(t - t_begin) * 128 + 8 * s4);
+    }
+  };
 #pragma unroll
   for (int j = 0; j < D; ++j) {
     const int t = t_begin + j < t_last ? t_begin + j : t_last;
     load_codes<FMT>(wptr(t), buf[j]);
+    load_x(t, j);
   }
   if constexpr (XLDS) {
 #pragma unroll
@@ -199,7 +212,6 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __res
     }
     __syncthreads();
   }
-  const __bf16* xg = x + (int64_t)xr * ldx + (int64_t)t_begin * 128 + q * 32;
   const __bf16* xl = xs + (int64_t)xr * xstride + (int64_t)t_begin * 128 + q * 32;
   f32x4 acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
   auto step = [&](int j) __attribute__((always_inline)) {
@@ -209,7 +221,7 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __res
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int kk = j * 128 + 8 * s;
-      const bf16x8 b = XLDS ? *(const bf16x8*)(xl + kk) : *(const bf16x8*)(xg + kk);
+      const bf16x8 b = XLDS ? *(const bf16x8*)(xl + kk) : xq[XLDS ? 0 : j % D][s];
       acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s], b, acc[s], 0, 0, 0);
     }
   };
@@ -217,6 +229,7 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __res
     if (j + D < SMAX) {  // compile-time: refill slot j % D with step j + D
       const int t = t_begin + j + D < t_last ? t_begin + j + D : t_last;
       load_codes<FMT>(wptr(t), buf[j % D]);
+      load_x(t, j % D);
     }
   };
   if constexpr (EXACT) {
@@ -292,6 +305,7 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __res
 }
 
 constexpr int kGemvRing = 8;            // super-steps of weights in flight per wave
+constexpr int kGemvRingX = 4;           // the same when the activations ride in the ring
 constexpr size_t kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 
 // Launch shape of the streaming GEMV: eight waves per workgroup, NT 16-row tiles x NK
@@ -323,7 +337,7 @@ inline GemvShape gemv_shape(int64_t tiles, int64_t S, bool sg4) {
 template <int FMT, int NT, int NK, int SMAX, bool EXACT, int XV, int SC>
 int launch_stream(unsigned grid, size_t lds, hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales,
                   int64_t nblk, const void* x, int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu) {
-  auto kernel = gemv_stream<FMT, NT, NK, kGemvRing, SMAX, EXACT, XV, SC>;
+  auto kernel = gemv_stream<FMT, NT, NK, (XV > 0 ? kGemvRing : kGemvRingX), SMAX, EXACT, XV, SC>;
   if (lds > 64 * 1024) {
     static bool raised = false;  // per instantiation
     if (!raised) {
@@ -340,13 +354,14 @@ int launch_stream(unsigned grid, size_t lds, hipStream_t s, const void* w, int64
   return TGM_OK;
 }
 
-// xv: 2 or 8 straight-line activation passes, 0 for activations read from global memory.
+// xv: 2, 8 or 16 straight-line activation passes, 0 for activations in the load ring.
 template <int FMT, int NT, int NK, int SMAX, bool EXACT, int SC>
 int launch_stream_xv(int xv, unsigned grid, size_t lds, hipStream_t s, const void* w, int64_t n, int64_t k,
                      const void* scales, int64_t nblk, const void* x, int64_t m, int64_t ldx, void* y, int ydt,
                      int64_t ldy, int swiglu) {
   if (xv == 2) return launch_stream<FMT, NT, NK, SMAX, EXACT, 2, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
   if (xv == 8) return launch_stream<FMT, NT, NK, SMAX, EXACT, 8, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
+  if (xv == 16) return launch_stream<FMT, NT, NK, SMAX, EXACT, 16, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
   return launch_stream<FMT, NT, NK, SMAX, EXACT, 0, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
 }
 
@@ -379,7 +394,9 @@ int launch_gemv_stream(hipStream_t s, const void* w, int64_t n, int64_t k, const
   const size_t xbytes = (size_t)m * (size_t)(k + 8) * 2;
   const bool xlds = part + xbytes <= kMaxLds;
   const int64_t passes = (m * k + 8 * 64 * 8 - 1) / (8 * 64 * 8);  // XSTEP of an 8-wave workgroup
-  const int xv = !xlds ? 0 : passes <= 2 ? 2 : 8;
+  // every staging load is issued before the weight ring up to 16 passes: a load in the
+  // staging loop after it waits for the whole ring (the vector memory counter retires in order)
+  const int xv = !xlds ? 0 : passes <= 2 ? 2 : passes <= 8 ? 8 : 16;
   const size_t lds = part + (xlds ? xbytes : 0);
   const int64_t nblk = k / 32;
   if (g.nt == 4) return launch_stream_shape<FMT, 4, 2>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
