@@ -338,7 +338,7 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
   const int64_t kvbase = ((int64_t)b * HK + j) * max_seq;
   // own: rotate q, k and store this token's k, v
   const bool mine = own && p >= c_begin && p < c_end;   // this split holds the token's position
-  __shared__ float kp[HD], vp[HD];
+  __shared__ __attribute__((aligned(16))) uint16_t kp[HD], vp[HD];  // bf16 bits
   const float* qrow = qkv + (int64_t)r * ld + (int64_t)hq0 * HD;
   // k (4 lanes per position, a quarter of head_dim each) and v (lane l: dims 2 l, 2 l + 1 of
   // the wave's positions w, w + 4, ...) of a chunk; the first chunk's loads are issued before
@@ -385,10 +385,10 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
         vc[o + tid] = v1;
         vc[o + tid + NP] = v2;
       }
-      kp[tid] = bf16_to_f32(k1);
-      kp[tid + NP] = bf16_to_f32(k2);
-      vp[tid] = bf16_to_f32(v1);
-      vp[tid + NP] = bf16_to_f32(v2);
+      kp[tid] = k1;
+      kp[tid + NP] = k2;
+      vp[tid] = v1;
+      vp[tid + NP] = v2;
     }
   } else {
     for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = qrow[i] * scale;
@@ -403,6 +403,16 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
   __syncthreads();
   for (int c0 = c_begin; c0 < c_end; c0 += CH) {
     if (c0 != c_begin) load_chunk(c0);
+    if (mine) {  // uniform: the loaded k, v of the token's own position predate its store
+      if (c0 + pi == p)
+#pragma unroll
+        for (int e = 0; e < QD / 8; ++e) kreg[e] = *(const dec_u32x4*)(kp + qd * QD + 8 * e);
+      if (lane < NP) {
+        const unsigned own_v = *(const unsigned*)(vp + 2 * lane);
+#pragma unroll
+        for (int i = 0; i < CH / 4; ++i) vreg[i] = c0 + wave + 4 * i == p ? own_v : vreg[i];
+      }
+    }
     {
       const int tt = c0 + pi;
       float s[G];
@@ -413,11 +423,7 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
         const dec_u32x4 kv = kreg[e / 8];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          float k0 = lo_bf16(kv[q]), k1 = hi_bf16(kv[q]);
-          if (mine && tt == p) {
-            k0 = kp[qd * QD + e + 2 * q];
-            k1 = kp[qd * QD + e + 2 * q + 1];
-          }
+          const float k0 = lo_bf16(kv[q]), k1 = hi_bf16(kv[q]);
 #pragma unroll
           for (int g = 0; g < G; ++g) s[g] += qs[g][qd * QD + e + 2 * q] * k0 + qs[g][qd * QD + e + 2 * q + 1] * k1;
         }
@@ -456,13 +462,9 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
     if (lane < NP) {
 #pragma unroll
       for (int i = 0; i < CH / 4; ++i) {
-        const int pv_i = wave + 4 * i, tt = c0 + pv_i;
+        const int pv_i = wave + 4 * i;
         const unsigned vv = vreg[i];
-        float v0 = lo_bf16(vv), v1 = hi_bf16(vv);
-        if (mine && tt == p) {
-          v0 = vp[2 * lane];
-          v1 = vp[2 * lane + 1];
-        }
+        const float v0 = lo_bf16(vv), v1 = hi_bf16(vv);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           const float pg = sc[g][pv_i];
