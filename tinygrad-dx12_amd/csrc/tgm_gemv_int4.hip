@@ -72,7 +72,7 @@ __device__ __forceinline__ void transpose4(unsigned& r0, unsigned& r1, unsigned&
 // refills past the slice re-read its last super-step, so every load is unconditional.  The
 // activations are copied to LDS once ([M][K + 8] fp16) and each step's operands are read
 // one step ahead.  G = blocks per scale group (1, 2 or 4).
-template <int NT, int NK, int SMAX, int G, int SDT>
+template <int NT, int NK, int SMAX, int G, int SDT, int XP>
 __global__ void __launch_bounds__(NT * NK * 64) gemv_int4(const uint8_t* __restrict__ w, int64_t N, int64_t K,
                                                         const uint8_t* __restrict__ scales, int64_t ngroups,
                                                         unsigned flip, float bias, const _Float16* __restrict__ x,
@@ -102,6 +102,22 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_int4(const uint8_t* __restr
   const uint8_t* srow = scales + (SCALED ? row * ngroups * SSIZE : 0);
   const half2v hbias = {(_Float16)bias, (_Float16)bias};
 
+  // Activations to LDS (16-byte chunks; K % 128 == 0 and ldx % 8 == 0 on the host).  The
+  // first XP passes (all of them when M x K fits) are loaded before the weight ring and
+  // stored after it is issued: the vector memory counter retires in order, so a staging load
+  // issued after the ring would wait for all of it.  Chunks past the end re-read the last one
+  // and store nothing.
+  const int64_t xstride = K + 8;
+  const int chunks_per_row = (int)(K / 8);
+  const int xtotal = M * chunks_per_row;
+  u32x4 xv[XP];
+#pragma unroll
+  for (int it = 0; it < XP; ++it) {
+    int i = (int)threadIdx.x + it * NW * 64;
+    i = i < xtotal ? i : xtotal - 1;
+    const int m = i / chunks_per_row, kc = i - m * chunks_per_row;
+    xv[it] = *(const u32x4*)(x + m * ldx + 8 * kc);
+  }
   u32x4 codes[D];
   unsigned sraw[D][SWORDS];
   auto load = [&](int j, int slot) __attribute__((always_inline)) {
@@ -125,10 +141,15 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_int4(const uint8_t* __restr
 #pragma unroll
   for (int j = 0; j < D; ++j) load(j, j);
 
-  // Activations to LDS (16-byte chunks; K % 128 == 0 and ldx % 8 == 0 on the host).
-  const int64_t xstride = K + 8;
-  const int chunks_per_row = (int)(K / 8);
-  for (int i = threadIdx.x; i < M * chunks_per_row; i += NW * 64) {
+#pragma unroll
+  for (int it = 0; it < XP; ++it) {
+    const int i = (int)threadIdx.x + it * NW * 64;
+    if (i < xtotal) {
+      const int m = i / chunks_per_row, kc = i - m * chunks_per_row;
+      *(u32x4*)(xs + m * xstride + 8 * kc) = xv[it];
+    }
+  }
+  for (int i = (int)threadIdx.x + XP * NW * 64; i < xtotal; i += NW * 64) {
     const int m = i / chunks_per_row, kc = i - m * chunks_per_row;
     *(u32x4*)(xs + m * xstride + 8 * kc) = *(const u32x4*)(x + m * ldx + 8 * kc);
   }
@@ -203,19 +224,22 @@ int launch_int4_shape(unsigned grid, hipStream_t s, const void* w, int64_t n, in
                       int per) {
   const size_t lds = (NK > 1 ? NT * NK * 64 * 16 : 0) + (size_t)m * (size_t)(k + 8) * 2;
   if (lds > kInt4MaxLds) return TGM_E_UNSUPPORTED;
+  const int64_t passes = (m * (k / 8) + NT * NK * 64 - 1) / (NT * NK * 64);  // staging passes
+  const int xp = passes <= 2 ? 2 : passes <= 8 ? 8 : 16;
 #define TGM_INT4(SMAX)                                                                                              \
   if (per <= SMAX) {                                                                                                \
-    auto kernel = gemv_int4<NT, NK, SMAX, G, SDT>;                                                             \
+    auto kernel = xp == 2 ? gemv_int4<NT, NK, SMAX, G, SDT, 2>                                                    \
+                          : xp == 8 ? gemv_int4<NT, NK, SMAX, G, SDT, 8> : gemv_int4<NT, NK, SMAX, G, SDT, 16>;  \
     if (lds > 64 * 1024) {                                                                                          \
-      static bool raised = false;                                                                                   \
-      if (!raised) {                                                                                                \
+      static bool raised[3] = {};                                                                                   \
+      if (!raised[xp / 8]) {                                                                                              \
         const hipError_t err = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, \
                                                    (int)kInt4MaxLds);                                               \
         if (err != hipSuccess) {                                                                                    \
           set_error("tgm_gemv: cannot raise the LDS limit: %s", hipGetErrorString(err));                           \
           return (int)err;                                                                                          \
         }                                                                                                           \
-        raised = true;                                                                                              \
+        raised[xp / 8] = true;                                                                                            \
       }                                                                                                             \
     }                                                                                                               \
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(NT * NK * 64), lds, s,                                              \
