@@ -243,6 +243,18 @@ def int4_weight(dev, fmt, n, k, sdt, bs, rng):
     return w, O.dequant_f64(data, fmt, (n, k), s_np, bs)
 
 
+@pytest.mark.parametrize("nkm", [(640, 4096, 4), (640, 4096, 8), (384, 4096, 16), (256, 6144, 12)])
+def test_gemv_int4_mfma_staging_passes(dev, nkm):
+    """The f16-MFMA INT4 GEMV stages X in LDS in 2, 8 or 16 straight-line passes and a loop
+    beyond: 4 and 8 rows (8-pass variant), 16 rows (16 passes), 12 x 6144 (16 passes + loop)."""
+    n, k, m = nkm
+    rng = np.random.default_rng(n + k + m)
+    w, deq = int4_weight(dev, "int4", n, k, torch.float16, 128, rng)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float16)).to(dev)
+    y = matmul_nt(x, w, dtype=torch.float32)
+    assert O.max_rel_err(y.cpu().numpy(), x.float().cpu().numpy().astype(np.float64) @ deq.T) <= TOL
+
+
 @pytest.mark.parametrize("fmt", ["int4", "uint4"])
 @pytest.mark.parametrize("sdt,bs", [(torch.float16, 32), (torch.bfloat16, 64), (torch.float32, 128), (None, 32)])
 @pytest.mark.parametrize("m", [1, 5, 16])
