@@ -554,10 +554,11 @@ def test_gemm_mx_fp4_one_hot_is_exact(dev):
     assert np.array_equal(c, deq_b[:, cols].T.astype(np.float32))
 
 
-def test_gemm_mx_fp4_full_size_sampled(dev):
-    """Config 4a at full size (M = N = K = 8192, operands MX-quantised from N(0,1)):
-    64 sampled rows of C against the exact-dequant fp64 oracle."""
-    m = n = k = 8192
+@pytest.mark.parametrize("mnk", [(8192, 8192, 8192), (4096, 14336, 4096)])
+def test_gemm_mx_fp4_full_size_sampled(dev, mnk):
+    """Config 4 at full size (operands MX-quantised from N(0,1)): 64 sampled rows of C
+    against the exact-dequant fp64 oracle."""
+    m, n, k = mnk
     g = torch.Generator(device=dev)
     g.manual_seed(0)
     a = quantize_mx(torch.randn((m, k), device=dev, generator=g), "fp4_e2m1")
