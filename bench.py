@@ -141,6 +141,22 @@ def measured_traffic(profile: str) -> int | None:
     return None
 
 
+def settle(torch, stream, launch, warmup: int, min_ms: float = 60.0) -> None:
+    """Untimed launches of a compute-bound kernel: at least ``warmup`` of them and at least
+    ``min_ms`` of GPU time, since the clocks keep rising over the first tens of milliseconds of
+    sustained MFMA load (a 4096 x 14336 x 4096 FP4 GEMM measured 180 us cold and 157 us after
+    about 30 ms of the same work)."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    done, spent = 0, 0.0
+    while done < warmup or spent < min_ms:
+        e0.record(stream)
+        for _ in range(5):
+            launch()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        done, spent = done + 5, spent + e0.elapsed_time(e1)
+
+
 def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup: int):
     """FP4 x FP4 + E8M0/32 GEMM C[M,N] = deq(A) deq(B)^T, bf16 out, timed with HIP events on
     the launch stream (each launch is long enough that launch overhead is negligible).  The
@@ -160,9 +176,7 @@ def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup:
         K.check("tgm_gemm_mx", lib.tgm_gemm_mx(a.data_ptr(), fp4, sa.data_ptr(), m, b.data_ptr(), fp4, sb.data_ptr(), n, k,
                                                c.data_ptr(), bf16, n, stream.cuda_stream))
 
-    for _ in range(warmup):
-        launch()
-    torch.cuda.synchronize()
+    settle(torch, stream, launch, warmup)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for _ in range(steps):
@@ -193,9 +207,7 @@ def fp6_gemm_workload(torch, K, dev, fmt: str, steps: int, warmup: int, m: int =
         K.check("tgm_gemm_w", lib.tgm_gemm_w(a.data_ptr(), bf16, m, k, w.data_ptr(), f, n, k, s.data_ptr(), e8m0, 32,
                                              c.data_ptr(), bf16, n, stream.cuda_stream))
 
-    for _ in range(warmup):
-        launch()
-    torch.cuda.synchronize()
+    settle(torch, stream, launch, warmup)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for _ in range(steps):
