@@ -235,3 +235,30 @@ def test_header_enums_match_binding():
         assert re.search(rf"TGM_FMT_{enum} = {value},", text)
     assert "TGM_E8M0 = 15" in text and K.DTYPE_IDS[torch.float8_e8m0fnu] == 15
     assert "TGM_BF16 = 12" in text and K.DTYPE_IDS[torch.bfloat16] == 12
+
+
+@pytest.mark.parametrize("fmt,sdt,bs,swiglu,fits", [
+    ("fp4_e2m1", torch.float8_e8m0fnu, 32, True, True),
+    ("fp4_e2m1", torch.float8_e8m0fnu, 32, False, True),
+    ("fp4_e2m1", None, 32, False, True),
+    ("fp4_e2m1", None, 32, True, False),
+    ("fp4_e2m1", torch.float16, 32, False, False),
+    ("int4", torch.float16, 128, False, True),
+    ("uint4", torch.bfloat16, 64, False, True),
+    ("int4", torch.float32, 32, False, True),
+    ("int4", torch.float16, 256, False, False),
+    ("int4", torch.float16, 128, True, False),
+    ("fp6_e2m3", torch.float8_e8m0fnu, 32, False, False),
+])
+def test_decoder_fuses_norms_only_into_supported_weights(fmt, sdt, bs, swiglu, fits):
+    """The one-token decoder folds RMSNorm into a projection only for weights that
+    tgm_dec_norm_gemv takes; any other weight keeps the separate norm launch."""
+    from tinygrad_mi355x.decoder import _norm_gemv_fits
+    n, k = 64, 2048
+    bits = FORMATS[fmt][0]
+    data = torch.zeros(n * k * bits // 8, dtype=torch.uint8)
+    scales = None
+    if sdt is not None:
+        scales = torch.full((n, k // bs), 127, dtype=torch.uint8).view(sdt) if sdt == torch.float8_e8m0fnu \
+            else torch.ones((n, k // bs), dtype=sdt)
+    assert _norm_gemv_fits(PackedTensor(data, fmt, (n, k), scales, bs), swiglu) is fits

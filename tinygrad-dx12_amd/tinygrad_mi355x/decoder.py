@@ -147,6 +147,20 @@ def load_weights(path, device: str | torch.device = "cuda") -> tuple[DecoderWeig
 GEMM_TILE_M, GEMM_TILE_N, GEMM_FILL = 128, 256, 192  # packed GEMM output tile; tiles that fill the chip
 
 
+def _norm_gemv_fits(w: PackedTensor, swiglu: bool) -> bool:
+    """Whether tgm_dec_norm_gemv takes this weight: FP4 with E8M0 scales per 32 (required with
+    the SwiGLU epilogue) or none, INT4 / UINT4 with f16, bf16 or f32 group scales per 32, 64 or
+    128 or none."""
+    if w.format == "fp4_e2m1":
+        if w.scales is None:
+            return not swiglu
+        return w.scales.dtype == torch.float8_e8m0fnu and w.block_size == 32
+    if w.format in ("int4", "uint4") and not swiglu:
+        return w.scales is None or (w.scales.dtype in (torch.float16, torch.bfloat16, torch.float32)
+                                    and w.block_size in (32, 64, 128))
+    return False
+
+
 def gemm_splits(m: int, n: int) -> int:
     """K splits for a packed GEMM whose output tiles alone would leave CUs idle (at most 8)."""
     tiles = -(-m // GEMM_TILE_M) * -(-n // GEMM_TILE_N)
@@ -237,8 +251,7 @@ class Decoder:
         # one token: each RMSNorm runs inside the projection after it (tgm_dec_norm_gemv), the
         # residual stream alternating between h and h_alt
         self.fuse_norm = (batch == 1 and cfg.hidden in (2048, 4096) and self.fuse_swiglu
-                          and all(L.wqkv.format in ("int4", "uint4", "fp4_e2m1") for L in weights.layers)
-                          and all(L.w_gate_up.format == "fp4_e2m1" and L.w_gate_up.scales is not None
+                          and all(_norm_gemv_fits(L.wqkv, False) and _norm_gemv_fits(L.w_gate_up, True)
                                   for L in weights.layers))
         self.h_alt = torch.empty((batch, d), **f32) if self.fuse_norm else None
         ws = K.load_library().tgm_dec_attention_workspace(batch, cfg.heads, cfg.head_dim, self.splits)
