@@ -34,8 +34,8 @@ FP4_PEAK_TFLOPS = 10100.0
 N_COPIES = 18
 
 
-EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_cfg1", "int4_gemv_n14336", "fp6_e3m2_gemm_cfg3", "fp6_e2m3_gemm_cfg3", "fp4_gemm_8192",
-          "fp4_gemm_4096x14336x4096", "decoder_cfg5_b1", "decoder_cfg5_b8")
+EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_n4096", "int4_gemv_n14336", "fp6_e3m2_gemm_m2048", "fp6_e2m3_gemm_m2048", "fp4_gemm_8192",
+          "fp4_gemm_4096x14336x4096", "decoder_b1", "decoder_b8")
 
 
 def parse() -> argparse.Namespace:
@@ -222,7 +222,7 @@ def fp6_gemm_workload(torch, K, dev, fmt: str, steps: int, warmup: int, m: int =
 
 
 def decoder_workload(torch, dev, batch: int, prompt: int = 512, new_tokens: int = 128):
-    """Config-5 decoder (8 layers, hidden 4096, 32 / 8 heads x 128, SwiGLU 14336, vocab 32000;
+    """Llama-style decoder (8 layers, hidden 4096, 32 / 8 heads x 128, SwiGLU 14336, vocab 32000;
     INT4 g128 attention, FP4 + E8M0 FFN, bf16 head): a 512-token prefill, then greedy decode of
     128 tokens, the decode steps replayed as a HIP graph and timed with HIP events on the
     graph's stream.  Random-init weights and prompts."""
@@ -262,7 +262,7 @@ def decoder_workload(torch, dev, batch: int, prompt: int = 512, new_tokens: int 
     mean_ctx = prompt + 1 + (steps + 1) / 2
     kv_bytes = int(cfg.layers * batch * cfg.kv_heads * mean_ctx * cfg.head_dim * 2 * 2)
     step_bytes = cfg.weight_bytes_per_token() + kv_bytes
-    return {"workload": f"config-5 decoder batch {batch}: {prompt}-token prefill + greedy decode of {new_tokens} tokens "
+    return {"workload": f"8-layer decoder (hidden 4096, INT4 attention, FP4 FFN) batch {batch}: {prompt}-token prefill + greedy decode of {new_tokens} tokens "
                         "(decode steps replayed as a HIP graph)",
             "decode_ms_per_step": step_ms, "tokens_per_s": batch / step_ms * 1e3,
             "bytes_per_step": step_bytes, "GB/s": step_bytes / step_ms / 1e6,
@@ -337,14 +337,14 @@ def main() -> int:
     extras = {
         "fp4_gemv_m4": lambda: fp4_gemv_workload(torch, K, dev, 4, half, args.warmup),
         "fp4_gemv_m16": lambda: fp4_gemv_workload(torch, K, dev, 16, half, args.warmup),
-        "int4_gemv_cfg1": lambda: int4_gemv_workload(torch, K, dev, half, args.warmup),
+        "int4_gemv_n4096": lambda: int4_gemv_workload(torch, K, dev, half, args.warmup),
         "int4_gemv_n14336": lambda: int4_gemv_workload(torch, K, dev, half, args.warmup, copies=12, n=14336),
-        "fp6_e3m2_gemm_cfg3": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e3m2", 20, 20),
-        "fp6_e2m3_gemm_cfg3": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e2m3", 20, 20),
+        "fp6_e3m2_gemm_m2048": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e3m2", 20, 20),
+        "fp6_e2m3_gemm_m2048": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e2m3", 20, 20),
         "fp4_gemm_8192": lambda: fp4_gemm_workload(torch, K, dev, 8192, 8192, 8192, 20, 20),
         "fp4_gemm_4096x14336x4096": lambda: fp4_gemm_workload(torch, K, dev, 4096, 14336, 4096, 20, 20),
-        "decoder_cfg5_b1": lambda: decoder_workload(torch, dev, 1),
-        "decoder_cfg5_b8": lambda: decoder_workload(torch, dev, 8),
+        "decoder_b1": lambda: decoder_workload(torch, dev, 1),
+        "decoder_b8": lambda: decoder_workload(torch, dev, 8),
     }
     if args.only:
         print(json.dumps({args.only: extras[args.only]()}))

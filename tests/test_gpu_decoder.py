@@ -389,7 +389,7 @@ def test_graph_replay_matches_eager_decode(dev):
     assert torch.equal(eager2, dec.generate(prompts.flip(1), 5, graph=True))
 
 
-def test_config5_full_size_prefill_and_graph_decode(dev):
+def test_decoder_full_size_prefill_and_graph_decode(dev):
     """8 layers, hidden 4096, 32/8 heads, SwiGLU 14336, vocab 32000: 512-token prefill at batch
     1 and graph-replayed decode agree with eager decode bit for bit; logits are finite."""
     cfg = DecoderConfig()

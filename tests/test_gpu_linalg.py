@@ -215,7 +215,7 @@ def test_gemv_general_parity(dev, fmt, scale_kind, xdt):
     assert O.max_rel_err(y.cpu().numpy(), ref) <= TOL
 
 
-def test_int4_config1_shape(dev):
+def test_int4_gemv_4096x4096_shape(dev):
     """INT4 g32 fp16-scale GEMV, N=K=4096, x fp16 [1,4096] -> fp16."""
     rng = np.random.default_rng(0)
     x_np = rng.standard_normal((1, 4096)).astype(np.float16)
@@ -401,8 +401,8 @@ def test_gemm_w_one_hot_is_exact(dev, fmt):
 
 
 @pytest.mark.parametrize("fmt", ["fp6_e3m2", "fp6_e2m3"])
-def test_gemm_w_config3_full_size_sampled(dev, fmt):
-    """Config 3 at full size: A bf16 [2048, 4096], W = MX-quantised N(0, 0.02) [11008, 4096]
+def test_gemm_w_fp6_2048x11008x4096_full_size_sampled(dev, fmt):
+    """The FP6 prefill GEMM at full size: A bf16 [2048, 4096], W = MX-quantised N(0, 0.02) [11008, 4096]
     (block-32 E8M0); 64 x 512 sampled outputs against the exact-dequant fp64 oracle."""
     m, n, k = 2048, 11008, 4096
     g = torch.Generator(device=dev)
@@ -556,7 +556,7 @@ def test_gemm_mx_fp4_one_hot_is_exact(dev):
 
 @pytest.mark.parametrize("mnk", [(8192, 8192, 8192), (4096, 14336, 4096)])
 def test_gemm_mx_fp4_full_size_sampled(dev, mnk):
-    """Config 4 at full size (operands MX-quantised from N(0,1)): 64 sampled rows of C
+    """The FP4 x FP4 GEMMs at full size (operands MX-quantised from N(0,1)): 64 sampled rows of C
     against the exact-dequant fp64 oracle."""
     m, n, k = mnk
     g = torch.Generator(device=dev)

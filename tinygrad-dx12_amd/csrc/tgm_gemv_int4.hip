@@ -1,5 +1,5 @@
 // Kernel family 1, integer path: INT4 / UINT4 weights with fp16 / bf16 / f32 group scales
-// (groups of 32, 64 or 128) x fp16 activations -- the config-1 decode GEMV (fp16 x, int4
+// (groups of 32, 64 or 128) x fp16 activations -- e.g. the 4096 x 4096 decode GEMV (fp16 x, int4
 // codes, fp16 scales per 32).
 //
 // Replaces the reference's thread-scope matvec / N=1 LinAlg matmul over weights that a
