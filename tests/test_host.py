@@ -262,3 +262,22 @@ def test_decoder_fuses_norms_only_into_supported_weights(fmt, sdt, bs, swiglu, f
         scales = torch.full((n, k // bs), 127, dtype=torch.uint8).view(sdt) if sdt == torch.float8_e8m0fnu \
             else torch.ones((n, k // bs), dtype=sdt)
     assert _norm_gemv_fits(PackedTensor(data, fmt, (n, k), scales, bs), swiglu) is fits
+
+
+def test_profile_commands_name_existing_bench_workloads():
+    """Every rocprofv3 summary under profiles/ gives the command that made it; the workloads
+    those commands select with --only must exist in bench.py."""
+    root = Path(__file__).resolve().parents[1]
+    sys.path.insert(0, str(root))
+    try:
+        import bench
+    finally:
+        sys.path.remove(str(root))
+    keys = set(bench.EXTRAS)
+    summaries = sorted((root / "profiles").glob("*.txt"))
+    assert summaries
+    for path in summaries:
+        text = path.read_text()
+        assert "rocprofv3" in text, path.name
+        for key in re.findall(r"--only (\S+)", text):
+            assert key in keys, (path.name, key)
