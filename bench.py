@@ -2,23 +2,32 @@
 
 A step is one FP4 E2M1 (+ E8M0 per 32 K-elements) decode GEMV, W [14336, 4096],
 x bf16 [1, 4096] -> y bf16 [1, 14336], fp32 accumulation -- one call of the C-ABI
-entry point ``tgm_gemv``.  Every step reads a different copy of the weights (18
-copies, 562 MB, more than twice the 256 MB Infinity Cache) so each launch streams
-its weights from HBM.  The K timed steps are captured once in a HIP graph and
-replayed, and timed with HIP events on the launch stream.
+entry point ``tgm_gemv``.  Consecutive steps read different copies of the weights (a
+copy set of at least 600 MB, over twice the 256 MB Infinity Cache, walked in order, so a
+copy is read again only after every other copy has been), so each launch streams its
+weights from HBM.  A trial is exactly K steps captured in one HIP graph, replayed and
+timed with HIP events on the launch stream; ``value`` comes from the median of several
+trials (each trial's graph continues the rotation where the previous one stopped).
 
 ``value`` is the achieved algorithmic bandwidth of the step (bytes of packed weights,
 scales, x and y per step / time per step).  Secondary workloads (skinny M=4/16, the
-INT4 g32 GEMV, the FP6-weight x bf16 GEMMs and the FP4xFP4 GEMMs) are reported under ``workloads``.
+INT4 g32 GEMVs, the FP6-weight x bf16 GEMMs, the FP4xFP4 GEMMs and the 8-layer
+decoder) are reported under ``workloads``, each with its own roofline.
 ``cpu_baseline`` times the C restatement of the reference's CPU path
-(oracle/cpu_path.c: materialise fp32 weights, fp32 GEMV, RNE to bf16) on the host.
+(oracle/cpu_path.c: materialise fp32 weights, fp32 GEMV, RNE to bf16 / fp16) on the host
+cores, for the headline GEMV and, under the INT4 4096 x 4096 workload, for that GEMV.
+
+``--summarize-profile DIR --only W`` turns the rocprofv3 runs of workload W (the commands
+it prints in its header) into the summary committed under ``profiles/``.
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
 import ctypes
 import json
+import math
 import os
 import statistics
 import sys
@@ -31,62 +40,108 @@ sys.path.insert(0, str(ROOT / "tinygrad-dx12_amd"))
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP4_PEAK_TFLOPS = 10100.0
-N_COPIES = 18
+ROTATION_BYTES = 600_000_000  # every GEMV copy set: > 2 x the 256 MB Infinity Cache
+MIN_TRIALS = 5
 
+EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_n4096", "int4_gemv_n14336", "fp6_e3m2_gemm_m2048",
+          "fp6_e2m3_gemm_m2048", "fp4_gemm_8192", "fp4_gemm_4096x14336x4096", "decoder_b1", "decoder_b8")
+PRIMARY = "fp4_gemv_m1"
 
-EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_n4096", "int4_gemv_n14336", "fp6_e3m2_gemm_m2048", "fp6_e2m3_gemm_m2048", "fp4_gemm_8192",
-          "fp4_gemm_4096x14336x4096", "decoder_b1", "decoder_b8")
+# workload -> (committed rocprof summary, substring of the dominant kernel's name)
+PROFILES = {
+    "fp4_gemv_m1": ("gemv_fp4_e2m1_n14336_k4096_m1.txt", "gemv_rows_fp4"),
+    "fp4_gemv_m4": ("gemv_fp4_e2m1_n14336_k4096_m4.txt", "gemv_stream"),
+    "fp4_gemv_m16": ("gemv_fp4_e2m1_n14336_k4096_m16.txt", "gemv_stream"),
+    "int4_gemv_n4096": ("gemv_int4_g32_n4096_k4096_m1.txt", "gemv_rows_int4"),
+    "int4_gemv_n14336": ("gemv_int4_g32_n14336_k4096_m1.txt", "gemv_rows_int4"),
+    "fp6_e3m2_gemm_m2048": ("gemm_w_fp6_e3m2_m2048_n11008_k4096.txt", "gemm_w_mx"),
+    "fp6_e2m3_gemm_m2048": ("gemm_w_fp6_e2m3_m2048_n11008_k4096.txt", "gemm_w_mx"),
+    "fp4_gemm_8192": ("gemm_mx_fp4_m8192_n8192_k8192.txt", "gemm_mx"),
+    "fp4_gemm_4096x14336x4096": ("gemm_mx_fp4_m4096_n14336_k4096.txt", "gemm_mx"),
+}
 
 
 def parse() -> argparse.Namespace:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--steps", type=int, default=200, help="steps per timed trial (K)")
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
-    p.add_argument("--only", choices=sorted(EXTRAS), default=None,
-                   help="run only this secondary workload and print its figures (for profiling)")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of each CPU baseline sample")
+    p.add_argument("--only", choices=sorted((PRIMARY,) + EXTRAS), default=None,
+                   help="run only this workload and print its figures (for profiling)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run --steps device-to-device copies of MIB MiB (reference for HBM byte counters)")
+    p.add_argument("--summarize-profile", type=Path, default=None, metavar="DIR",
+                   help="summarise the rocprofv3 output folders under DIR for the --only workload")
     return p.parse_args()
 
 
-def gemv_bytes(n: int, k: int, m: int, bits: int, scale_bytes: float, act_bytes: int, out_bytes: int) -> int:
-    return n * k * bits // 8 + int(n * (k // 32) * scale_bytes) + m * k * act_bytes + m * n * out_bytes
+def gemv_bytes(n: int, k: int, m: int, bits: int, scale_bytes: float, act_bytes: int, out_bytes: int,
+               block: int = 32) -> int:
+    return n * k * bits // 8 + int(n * (k // block) * scale_bytes) + m * k * act_bytes + m * n * out_bytes
 
 
-class Timer:
-    """Captures ``steps`` launches of ``launch(i)`` in a HIP graph; replays and times them."""
+def median_trials(torch, launch, steps: int, warmup: int, copies: int) -> tuple[float, int, int]:
+    """Median ms per step over trials of exactly ``steps`` launches.
 
-    def __init__(self, torch, launch, steps: int, warmup: int):
-        self.torch, self.launch, self.steps, self.warmup = torch, launch, steps, warmup
+    ``launch(i)`` runs step ``i`` on copy ``i % copies``.  Trial ``r`` is a HIP graph of steps
+    [r * steps, (r + 1) * steps); the trial count makes the trials cover the copy ring a whole
+    number of times (and is at least MIN_TRIALS), so every copy is reread only after all the
+    others, also across the untimed first pass over every graph (graph upload) and the timed
+    second pass.  Returns (median ms per step, trials, timed dispatches).
+    """
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    cycle = copies // math.gcd(steps, copies)
+    trials = cycle * max(1, -(-MIN_TRIALS // cycle))
+    stream = torch.cuda.Stream()
+    graphs = []
+    for r in range(trials):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream), torch.cuda.graph(g, stream=stream):
+            for i in range(steps):
+                launch(r * steps + i)
+        graphs.append(g)
+    with torch.cuda.stream(stream):
+        for g in graphs:  # untimed pass: graph upload and first touch
+            g.replay()
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in graphs]
+    with torch.cuda.stream(stream):
+        for g, (e0, e1) in zip(graphs, events):
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+    torch.cuda.synchronize()
+    ms = statistics.median(e0.elapsed_time(e1) for e0, e1 in events) / steps
+    return ms, trials, trials * steps
 
-    def run(self) -> float:
-        torch = self.torch
-        for i in range(self.warmup):
-            self.launch(i)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        stream = torch.cuda.Stream()
-        with torch.cuda.stream(stream):
-            with torch.cuda.graph(graph, stream=stream):
-                for i in range(self.steps):
-                    self.launch(i)
-        graph.replay()  # untimed replay: graph upload and first-touch
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(stream):
-            start.record(stream)
-            graph.replay()
-            end.record(stream)
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / self.steps  # ms per step
+
+def copies_for(nbytes: int) -> int:
+    return max(2, -(-ROTATION_BYTES // nbytes))
 
 
-def fp4_gemv_workload(torch, K, dev, m: int, steps: int, warmup: int, copies: int = N_COPIES):
+def hbm_roofline(nbytes: int, ms: float) -> dict:
+    achieved = nbytes / ms / 1e6
+    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4)}
+
+
+def mfma_roofline(flops: int, ms: float, peak: float, what: str) -> dict:
+    achieved = flops / ms / 1e9
+    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4), "peak_of": what}
+
+
+def fp4_gemv_workload(torch, K, dev, m: int, steps: int, warmup: int) -> dict:
+    """FP4 E2M1 + E8M0/32 GEMV W [14336, 4096], bf16 X [M, 4096] -> bf16 Y [M, 14336]: codes uniform
+    over the 16 E2M1 values, E8M0 bytes 127 + [-4, 2], X ~ N(0, 1) rounded to bf16."""
     n, k = 14336, 4096
+    nbytes = gemv_bytes(n, k, m, 4, 1, 2, 2)
+    copies = copies_for(nbytes)
     g = torch.Generator(device=dev)
     g.manual_seed(0)
     ws = [torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device=dev, generator=g) for _ in range(copies)]
@@ -101,14 +156,17 @@ def fp4_gemv_workload(torch, K, dev, m: int, steps: int, warmup: int, copies: in
         K.check("tgm_gemv", lib.tgm_gemv(ws[j].data_ptr(), fmt, n, k, ss[j].data_ptr(), e8m0, 32, x.data_ptr(), bf16,
                                          m, k, y.data_ptr(), bf16, n, K.stream_of(x)))
 
-    ms = Timer(torch, launch, steps, warmup).run()
-    nbytes = gemv_bytes(n, k, m, 4, 1, 2, 2)
+    ms, trials, timed = median_trials(torch, launch, steps, warmup, copies)
     return {"workload": f"fp4_e2m1 e8m0/32 GEMV N=14336 K=4096 M={m}", "ms": ms, "bytes": nbytes,
-            "GB/s": nbytes / ms / 1e6, "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS,
-            "TFLOPS": 2 * m * n * k / ms / 1e9}
+            "GB/s": nbytes / ms / 1e6, "TFLOPS": 2 * m * n * k / ms / 1e9, "copies": copies,
+            "copy_set_bytes": copies * nbytes, "trials": trials, "steps_per_trial": steps,
+            "timed_dispatches": timed, "roofline": hbm_roofline(nbytes, ms)}
 
 
-def int4_gemv_workload(torch, K, dev, steps: int, warmup: int, copies: int = 40, n: int = 4096, k: int = 4096):
+def int4_gemv_workload(torch, K, dev, n: int, steps: int, warmup: int, k: int = 4096) -> dict:
+    """INT4 g32 GEMV W [N, 4096] with fp16 scales ~ U(0.005, 0.02), fp16 x [1, 4096] -> fp16 y."""
+    nbytes = gemv_bytes(n, k, 1, 4, 2, 2, 2)
+    copies = copies_for(nbytes)
     g = torch.Generator(device=dev)
     g.manual_seed(1)
     ws = [torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device=dev, generator=g) for _ in range(copies)]
@@ -123,22 +181,10 @@ def int4_gemv_workload(torch, K, dev, steps: int, warmup: int, copies: int = 40,
         K.check("tgm_gemv", lib.tgm_gemv(ws[j].data_ptr(), fmt, n, k, ss[j].data_ptr(), f16, 32, x.data_ptr(), f16,
                                          1, k, y.data_ptr(), f16, n, K.stream_of(x)))
 
-    ms = Timer(torch, launch, steps, warmup).run()
-    nbytes = gemv_bytes(n, k, 1, 4, 2, 2, 2)
+    ms, trials, timed = median_trials(torch, launch, steps, warmup, copies)
     return {"workload": f"int4 g32 fp16-scale GEMV N={n} K={k} M=1 fp16", "ms": ms, "bytes": nbytes,
-            "GB/s": nbytes / ms / 1e6, "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
-
-
-def measured_traffic(profile: str) -> int | None:
-    """HBM bytes per launch of the dominant kernel from its committed rocprofv3 summary
-    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by a plain copy of known size)."""
-    path = ROOT / "profiles" / profile
-    if not path.exists():
-        return None
-    for line in path.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch="):
-            return int(line.split("=", 1)[1])
-    return None
+            "GB/s": nbytes / ms / 1e6, "copies": copies, "copy_set_bytes": copies * nbytes, "trials": trials,
+            "steps_per_trial": steps, "timed_dispatches": timed, "roofline": hbm_roofline(nbytes, ms)}
 
 
 def settle(torch, stream, launch, warmup: int, min_ms: float = 60.0) -> None:
@@ -157,75 +203,78 @@ def settle(torch, stream, launch, warmup: int, min_ms: float = 60.0) -> None:
         done, spent = done + 5, spent + e0.elapsed_time(e1)
 
 
-def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup: int):
-    """FP4 x FP4 + E8M0/32 GEMM C[M,N] = deq(A) deq(B)^T, bf16 out, timed with HIP events on
-    the launch stream (each launch is long enough that launch overhead is negligible).  The
-    warmup launches let the clocks settle under MFMA load (the first few run ~15% slower)."""
+def median_launch_ms(torch, stream, launch, steps: int) -> float:
+    """Median over ``steps`` back-to-back launches, each bracketed by HIP events on ``stream``."""
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for e0, e1 in events:
+        e0.record(stream)
+        launch()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return statistics.median(e0.elapsed_time(e1) for e0, e1 in events)
+
+
+def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup: int) -> dict:
+    """FP4 x FP4 + E8M0/32 GEMM C[M,N] = deq(A) deq(B)^T, bf16 out: A [M, K] and B [N, K] drawn
+    N(0, 1) and MX-quantised along K (round to nearest even, shared exponent per 32)."""
+    from tinygrad_mi355x.codegen.decomp.mi355x import quantize_mx
+
     g = torch.Generator(device=dev)
     g.manual_seed(2)
-    a = torch.randint(0, 256, (m * k // 2,), dtype=torch.uint8, device=dev, generator=g)
-    b = torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device=dev, generator=g)
-    sa = torch.randint(123, 130, (m, k // 32), dtype=torch.uint8, device=dev, generator=g)
-    sb = torch.randint(123, 130, (n, k // 32), dtype=torch.uint8, device=dev, generator=g)
+    a = quantize_mx(torch.randn((m, k), device=dev, generator=g), "fp4_e2m1")
+    b = quantize_mx(torch.randn((n, k), device=dev, generator=g), "fp4_e2m1")
     c = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
     fp4, bf16 = K.FORMAT_IDS["fp4_e2m1"], K.DTYPE_IDS[torch.bfloat16]
     lib = K.load_library()
     stream = torch.cuda.current_stream(dev)
 
     def launch() -> None:
-        K.check("tgm_gemm_mx", lib.tgm_gemm_mx(a.data_ptr(), fp4, sa.data_ptr(), m, b.data_ptr(), fp4, sb.data_ptr(), n, k,
-                                               c.data_ptr(), bf16, n, stream.cuda_stream))
+        K.check("tgm_gemm_mx", lib.tgm_gemm_mx(a.data.data_ptr(), fp4, a.scales.data_ptr(), m, b.data.data_ptr(), fp4,
+                                               b.scales.data_ptr(), n, k, c.data_ptr(), bf16, n, stream.cuda_stream))
 
     settle(torch, stream, launch, warmup)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        launch()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
-    tflops = 2 * m * n * k / ms / 1e9
+    ms = median_launch_ms(torch, stream, launch, steps)
+    flops = 2 * m * n * k
     nbytes = (m + n) * k // 2 + (m + n) * k // 32 + m * n * 2
-    return {"workload": f"fp4xfp4 e8m0/32 GEMM M={m} N={n} K={k} bf16 out", "ms": ms, "TFLOPS": tflops,
-            "mfma_frac": tflops / FP4_PEAK_TFLOPS, "bytes": nbytes, "GB/s": nbytes / ms / 1e6}
+    return {"workload": f"fp4xfp4 e8m0/32 GEMM M={m} N={n} K={k} bf16 out", "ms": ms, "TFLOPS": flops / ms / 1e9,
+            "flops": flops, "bytes": nbytes, "GB/s": nbytes / ms / 1e6, "timed_dispatches": steps,
+            "roofline": mfma_roofline(flops, ms, FP4_PEAK_TFLOPS, "dense MXFP4 MFMA")}
 
 
-def fp6_gemm_workload(torch, K, dev, fmt: str, steps: int, warmup: int, m: int = 2048, n: int = 11008, k: int = 4096):
-    """Packed FP6 weight x bf16 activation prefill GEMM C[M,N] = A deq(W)^T (E8M0 per 32),
-    bf16 out, on the dequant-to-bf16 MFMA kernel; timed like the FP4 GEMM."""
+def fp6_gemm_workload(torch, K, dev, fmt: str, steps: int, warmup: int, m: int = 2048, n: int = 11008,
+                      k: int = 4096) -> dict:
+    """Packed FP6 weight x bf16 activation prefill GEMM C[M,N] = A deq(W)^T, bf16 out: A ~ N(0, 1)
+    in bf16, W [N, K] drawn N(0, 0.02) and MX-quantised along K to ``fmt`` (E8M0 per 32)."""
+    from tinygrad_mi355x.codegen.decomp.mi355x import quantize_mx
+
     g = torch.Generator(device=dev)
     g.manual_seed(4)
     a = torch.randn((m, k), device=dev, generator=g).to(torch.bfloat16)
-    w = torch.randint(0, 256, (n * k * 6 // 8,), dtype=torch.uint8, device=dev, generator=g)
-    s = torch.randint(123, 130, (n, k // 32), dtype=torch.uint8, device=dev, generator=g)
+    w = quantize_mx(torch.randn((n, k), device=dev, generator=g) * 0.02, fmt)
     c = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
     f, bf16, e8m0 = K.FORMAT_IDS[fmt], K.DTYPE_IDS[torch.bfloat16], K.DTYPE_IDS[torch.float8_e8m0fnu]
     lib = K.load_library()
     stream = torch.cuda.current_stream(dev)
 
     def launch() -> None:
-        K.check("tgm_gemm_w", lib.tgm_gemm_w(a.data_ptr(), bf16, m, k, w.data_ptr(), f, n, k, s.data_ptr(), e8m0, 32,
-                                             c.data_ptr(), bf16, n, stream.cuda_stream))
+        K.check("tgm_gemm_w", lib.tgm_gemm_w(a.data_ptr(), bf16, m, k, w.data.data_ptr(), f, n, k, w.scales.data_ptr(),
+                                             e8m0, 32, c.data_ptr(), bf16, n, stream.cuda_stream))
 
     settle(torch, stream, launch, warmup)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        launch()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
-    tflops = 2 * m * n * k / ms / 1e9
+    ms = median_launch_ms(torch, stream, launch, steps)
+    flops = 2 * m * n * k
     nbytes = m * k * 2 + n * k * 6 // 8 + n * (k // 32) + m * n * 2
-    return {"workload": f"{fmt} e8m0/32 weight x bf16 GEMM M={m} N={n} K={k} bf16 out", "ms": ms, "TFLOPS": tflops,
-            "bf16_mfma_frac": tflops / BF16_PEAK_TFLOPS, "bytes": nbytes, "GB/s": nbytes / ms / 1e6}
+    return {"workload": f"{fmt} e8m0/32 weight x bf16 GEMM M={m} N={n} K={k} bf16 out", "ms": ms,
+            "TFLOPS": flops / ms / 1e9, "flops": flops, "bytes": nbytes, "GB/s": nbytes / ms / 1e6,
+            "timed_dispatches": steps,
+            "roofline": mfma_roofline(flops, ms, BF16_PEAK_TFLOPS, "dense bf16 MFMA (the activations stay bf16)")}
 
 
-def decoder_workload(torch, dev, batch: int, prompt: int = 512, new_tokens: int = 128):
+def decoder_workload(torch, dev, batch: int, prompt: int = 512, new_tokens: int = 128) -> dict:
     """Llama-style decoder (8 layers, hidden 4096, 32 / 8 heads x 128, SwiGLU 14336, vocab 32000;
     INT4 g128 attention, FP4 + E8M0 FFN, bf16 head): a 512-token prefill, then greedy decode of
-    128 tokens, the decode steps replayed as a HIP graph and timed with HIP events on the
-    graph's stream.  Random-init weights and prompts."""
+    128 tokens, the decode steps replayed as a HIP graph, each replay bracketed by HIP events on
+    the graph's stream (median step reported).  Random-init weights and prompts."""
     from tinygrad_mi355x.decoder import Decoder, DecoderConfig, random_weights
 
     cfg = DecoderConfig()
@@ -242,37 +291,61 @@ def decoder_workload(torch, dev, batch: int, prompt: int = 512, new_tokens: int 
         torch.cuda.synchronize()
         if time.perf_counter() - t_warm >= 0.06:
             break
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(cur)
-    dec.prefill(prompts)
-    e1.record(cur)
-    torch.cuda.synchronize()
-    prefill_ms = e0.elapsed_time(e1)
+    prefills = []
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
+        dec.prefill(prompts)
+        e1.record(cur)
+        torch.cuda.synchronize()
+        prefills.append(e0.elapsed_time(e1))
+    prefill_ms = statistics.median(prefills)
     dec.step()  # first decode step eagerly (kernel set-up), then the graph
     graph = dec.capture()
     s = dec.graph_stream
     s.wait_stream(cur)
     steps = new_tokens - 2
-    e0.record(s)
-    for _ in range(steps):
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for e0, e1 in events:
+        e0.record(s)
         graph.launch()
-    e1.record(s)
+        e1.record(s)
     torch.cuda.synchronize()
-    step_ms = e0.elapsed_time(e1) / steps
+    step_ms = statistics.median(e0.elapsed_time(e1) for e0, e1 in events)
     mean_ctx = prompt + 1 + (steps + 1) / 2
     kv_bytes = int(cfg.layers * batch * cfg.kv_heads * mean_ctx * cfg.head_dim * 2 * 2)
     step_bytes = cfg.weight_bytes_per_token() + kv_bytes
-    return {"workload": f"8-layer decoder (hidden 4096, INT4 attention, FP4 FFN) batch {batch}: {prompt}-token prefill + greedy decode of {new_tokens} tokens "
-                        "(decode steps replayed as a HIP graph)",
+    return {"workload": f"8-layer decoder (hidden 4096, INT4 attention, FP4 FFN) batch {batch}: {prompt}-token "
+                        f"prefill + greedy decode of {new_tokens} tokens (decode steps replayed as a HIP graph)",
             "decode_ms_per_step": step_ms, "tokens_per_s": batch / step_ms * 1e3,
             "bytes_per_step": step_bytes, "GB/s": step_bytes / step_ms / 1e6,
-            "hbm_frac": step_bytes / step_ms / 1e6 / HBM_PEAK_GBS,
             "prefill_ms": prefill_ms, "prefill_tokens_per_s": batch * prompt / prefill_ms * 1e3,
-            "final_pos": int(dec.pos[0])}
+            "final_pos": int(dec.pos[0]), "roofline": hbm_roofline(step_bytes, step_ms)}
 
 
-def cpu_baseline(budget_s: float) -> dict:
-    """The reference CPU path restated in C (oracle/cpu_path.c), timed on the host cores."""
+def _host_description() -> dict:
+    model = ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count()}
+
+
+def _time_cpu(once, budget_s: float, max_runs: int = 200) -> tuple[float, int]:
+    once()  # warm the pages
+    times, start = [], time.perf_counter()
+    while time.perf_counter() - start < budget_s and len(times) < max_runs:
+        times.append(once())
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline_fp4(budget_s: float) -> dict:
+    """The reference CPU path restated in C (oracle/cpu_path.c) on the headline GEMV: FP4 E2M1 +
+    E8M0/32 W [14336, 4096] decoded to fp32 (materialised), fp32 GEMV, RNE to bf16."""
     import numpy as np
 
     lib = ctypes.CDLL(str(ROOT / "oracle" / "liboracle_cpu.so"))
@@ -283,9 +356,7 @@ def cpu_baseline(budget_s: float) -> dict:
     scales = np.ldexp(np.float32(1.0), (e - 127)).astype(np.float32)
     x = rng.standard_normal((m, k)).astype(np.float32)
     x = ((x.view(np.uint32) + 0x8000) & 0xFFFF0000).view(np.float32)  # bf16-valued activations
-    wdeq = np.empty(n * k, np.float32)
-    yf = np.empty(m * n, np.float32)
-    y = np.empty(m * n, np.uint16)
+    wdeq, yf, y = np.empty(n * k, np.float32), np.empty(m * n, np.float32), np.empty(m * n, np.uint16)
     p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
     i64 = ctypes.c_int64
 
@@ -295,16 +366,46 @@ def cpu_baseline(budget_s: float) -> dict:
                             p(yf), p(y), 16)
         return time.perf_counter() - t
 
-    once()  # warm the pages
-    times, start = [], time.perf_counter()
-    while time.perf_counter() - start < budget_s and len(times) < 200:
-        times.append(once())
-    med = statistics.median(times)
+    med, runs = _time_cpu(once, budget_s)
     nbytes = gemv_bytes(n, k, m, 4, 1, 2, 2)
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"full fp4 e8m0/32 GEMV 14336x4096 M=1 (dequant to fp32 + fp32 GEMV + bf16), "
-                      f"median of {len(times)} runs, {med * 1e3:.1f} ms each"}
+            "sample": f"the full fp4 e8m0/32 GEMV 14336x4096 M=1 (dequant to fp32 + fp32 GEMV + bf16), "
+                      f"median of {runs} runs, {med * 1e3:.1f} ms each", "ms": round(med * 1e3, 3),
+            **_host_description()}
+
+
+def cpu_baseline_int4(budget_s: float) -> dict:
+    """The reference CPU path on the INT4 GEMV of the CPU-device configuration, exactly: seed 0,
+    x fp16 [1, 4096] ~ N(0, 1); codes uniform in [-8, 7] packed 2 per byte; fp16 group-32 scales
+    ~ U(0.005, 0.02); y = fp16(x . deq(W)^T) with fp32 accumulation."""
+    import numpy as np
+
+    lib = ctypes.CDLL(str(ROOT / "oracle" / "liboracle_cpu.so"))
+    n = k = 4096
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((1, k)).astype(np.float16).astype(np.float32)
+    codes = rng.integers(-8, 8, (n, k))
+    scales = rng.uniform(0.005, 0.02, (n, k // 32)).astype(np.float16).astype(np.float32)
+    flat = (codes & 0xF).astype(np.uint8).reshape(-1)
+    data = (flat[0::2] | (flat[1::2] << 4)).astype(np.uint8)
+    wdeq, yf, y = np.empty(n * k, np.float32), np.empty(n, np.float32), np.empty(n, np.uint16)
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    i64 = ctypes.c_int64
+
+    def once() -> float:
+        t = time.perf_counter()
+        lib.oracle_cpu_path(p(data), i64(data.size), 0, i64(n), i64(k), p(scales), i64(32), p(x), i64(1), p(wdeq),
+                            p(yf), p(y), 17)
+        return time.perf_counter() - t
+
+    med, runs = _time_cpu(once, budget_s)
+    nbytes = gemv_bytes(n, k, 1, 4, 2, 2, 2)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the whole int4 g32 GEMV 4096x4096 M=1 fp16 (dequant to fp32 + fp32 GEMV + fp16), "
+                      f"median of {runs} runs, {med * 1e3:.2f} ms each", "ms": round(med * 1e3, 4),
+            **_host_description()}
 
 
 def copy_calibration(torch, mib: int, steps: int) -> None:
@@ -319,10 +420,119 @@ def copy_calibration(torch, mib: int, steps: int) -> None:
     print(json.dumps({"copy_calibration_bytes": n, "steps": steps}))
 
 
+def measured_traffic(workload: str) -> int | None:
+    """HBM bytes per launch of a workload's dominant kernel from its committed rocprofv3 summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by a plain copy of known size)."""
+    entry = PROFILES.get(workload)
+    path = ROOT / "profiles" / entry[0] if entry else None
+    if path is None or not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch="):
+            return int(line.split("=", 1)[1])
+    return None
+
+
+# ----------------------------------------------------------------------------- profile summaries
+def profile_commands(workload: str) -> list[str]:
+    """The rocprofv3 runs a summary is made from (OUT = the folder given to --summarize-profile)."""
+    run = f"python3 bench.py --only {workload} --steps 20 --warmup 5"
+    cmds = [f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o run -- {run}",
+            f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o run -- {run}",
+            f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o run -- {run}"]
+    if "gemm" in workload:
+        cmds.append(f"rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES GRBM_GUI_ACTIVE --output-format csv "
+                    f"-d OUT/mfma -o run -- {run}")
+    cmds += ["rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/cfetch -o copy -- python3 bench.py "
+             "--copy-calibration 64 --steps 10",
+             "rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/cwrite -o copy -- python3 bench.py "
+             "--copy-calibration 64 --steps 10"]
+    return cmds
+
+
+def _csv_rows(folder: Path, suffix: str) -> list[dict]:
+    files = sorted(folder.rglob(f"*{suffix}"))
+    if not files:
+        raise FileNotFoundError(f"no *{suffix} under {folder}")
+    with open(files[0], newline="") as fh:
+        return list(csv.DictReader(fh))
+
+
+def _counter(folder: Path, counter: str, pattern: str) -> tuple[float, int]:
+    values: dict[str, float] = {}
+    for r in _csv_rows(folder, "counter_collection.csv"):
+        if pattern in r["Kernel_Name"] and r["Counter_Name"] == counter:
+            key = r.get("Dispatch_Id") or r.get("Correlation_Id") or str(len(values))
+            values[key] = values.get(key, 0.0) + float(r["Counter_Value"])
+    if not values:
+        raise ValueError(f"{counter} has no dispatch of a kernel matching {pattern!r} in {folder}")
+    return statistics.median(values.values()), len(values)
+
+
+def summarize_profile(folder: Path, workload: str) -> str:
+    """Text summary of the rocprofv3 runs of ``workload`` under ``folder`` (see profile_commands)."""
+    name, pattern = PROFILES[workload]
+    run = json.loads((folder / "kt" / "bench.json").read_text())[workload]
+    trace = [r for r in _csv_rows(folder / "kt", "kernel_trace.csv") if pattern in r["Kernel_Name"]]
+    durations = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in trace]
+    timed = durations[-run["timed_dispatches"]:]
+    fetch, nf = _counter(folder / "fetch", "FETCH_SIZE", pattern)
+    write, nw = _counter(folder / "write", "WRITE_SIZE", pattern)
+    cfetch, _ = _counter(folder / "cfetch", "FETCH_SIZE", "copyBuffer")
+    cwrite, _ = _counter(folder / "cwrite", "WRITE_SIZE", "copyBuffer")
+    kf, kw = 65536 / cfetch, 65536 / cwrite
+    traffic = int(round((fetch * kf + write * kw) * 1024))
+    mean_ns, median_ns = statistics.mean(timed), statistics.median(timed)
+    lines = [f"# {name[:-4]}", "# rocprofv3 on one MI355X (gfx950); commands run from the repository root, "
+             "OUT = any output folder:"]
+    lines += [f"#   {c}" for c in profile_commands(workload)]
+    lines += [f"#   (the kernel-trace run's stdout saved as OUT/kt/bench.json)",
+              f"#   python3 bench.py --summarize-profile OUT --only {workload}",
+              f"workload: {run['workload']}",
+              f"kernel: {trace[-1]['Kernel_Name'][:150]}",
+              f"kernel_trace: dispatches={len(durations)} timed={len(timed)} (the last {len(timed)} dispatches: "
+              f"the timed launches of the bench run)",
+              f"timed: mean_ns={mean_ns:.0f} median_ns={median_ns:.0f} min_ns={min(timed)} max_ns={max(timed)}",
+              f"bench_ms_per_step_under_trace={run.get('ms', run.get('decode_ms_per_step')):.6f}",
+              f"pmc FETCH_SIZE median per dispatch: {fetch:.1f} KiB ({nf} dispatches); WRITE_SIZE: {write:.1f} KiB "
+              f"({nw} dispatches)",
+              f"copy calibration (64 MiB device copy, copyBuffer kernel): FETCH_SIZE {cfetch:.1f} KiB -> factor "
+              f"{kf:.4f}; WRITE_SIZE {cwrite:.1f} KiB -> factor {kw:.4f}",
+              f"traffic_bytes_per_launch={traffic}"]
+    if "bytes" in run:
+        lines += [f"algorithmic_bytes_per_launch={run['bytes']}",
+                  f"traffic/algorithmic={traffic / run['bytes']:.4f}"]
+    roof = run["roofline"]
+    if roof["bound"] == "hbm":
+        lines.append(f"achieved_GBps_from_timed_median={run['bytes'] / median_ns:.1f} "
+                     f"(frac {run['bytes'] / median_ns / HBM_PEAK_GBS:.4f} of {HBM_PEAK_GBS:.0f})")
+    else:
+        flops = run["flops"]
+        lines.append(f"algorithmic_flops_per_launch={flops}")
+        lines.append(f"achieved_TFLOPS_from_timed_median={flops / median_ns / 1e3:.1f} "
+                     f"(frac {flops / median_ns / 1e3 / roof['peak']:.4f} of {roof['peak']:.0f}, {roof['peak_of']})")
+        busy, nb = _counter(folder / "mfma", "SQ_VALU_MFMA_BUSY_CYCLES", pattern)
+        active, _ = _counter(folder / "mfma", "GRBM_GUI_ACTIVE", pattern)
+        sq_busy, _ = _counter(folder / "mfma", "SQ_BUSY_CYCLES", pattern)
+        lines.append(f"pmc SQ_VALU_MFMA_BUSY_CYCLES median {busy:.0f}, GRBM_GUI_ACTIVE {active:.0f}, SQ_BUSY_CYCLES "
+                     f"{sq_busy:.0f} ({nb} dispatches)")
+        lines.append(f"mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs) = "
+                     f"{busy / (active * 1024):.4f}")
+    return "\n".join(lines) + "\n"
+
+
+# ----------------------------------------------------------------------------- main
 def main() -> int:
     args = parse()
+    if args.summarize_profile is not None:
+        if not args.only:
+            print("--summarize-profile needs --only WORKLOAD", file=sys.stderr)
+            return 2
+        print(summarize_profile(args.summarize_profile, args.only), end="")
+        return 0
     if args.gpus != 1:
-        print(json.dumps({"error": "this benchmark runs on one GPU; --gpus must be 1 (multi-GPU sharding is design-only)"}))
+        print(json.dumps({"error": "this benchmark runs on one GPU; --gpus must be 1 (multi-GPU sharding is "
+                                   "design-only)"}))
         return 2
     import torch
 
@@ -333,54 +543,61 @@ def main() -> int:
         copy_calibration(torch, args.copy_calibration, args.steps)
         return 0
     K.load_library()
-    half = max(args.steps // 2, 1)
-    extras = {
-        "fp4_gemv_m4": lambda: fp4_gemv_workload(torch, K, dev, 4, half, args.warmup),
-        "fp4_gemv_m16": lambda: fp4_gemv_workload(torch, K, dev, 16, half, args.warmup),
-        "int4_gemv_n4096": lambda: int4_gemv_workload(torch, K, dev, half, args.warmup),
-        "int4_gemv_n14336": lambda: int4_gemv_workload(torch, K, dev, half, args.warmup, copies=12, n=14336),
-        "fp6_e3m2_gemm_m2048": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e3m2", 20, 20),
-        "fp6_e2m3_gemm_m2048": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e2m3", 20, 20),
-        "fp4_gemm_8192": lambda: fp4_gemm_workload(torch, K, dev, 8192, 8192, 8192, 20, 20),
-        "fp4_gemm_4096x14336x4096": lambda: fp4_gemm_workload(torch, K, dev, 4096, 14336, 4096, 20, 20),
+    steps, warmup = args.steps, args.warmup
+    gemm_steps = max(min(steps, 50), 10)
+    workloads = {
+        "fp4_gemv_m1": lambda: fp4_gemv_workload(torch, K, dev, 1, steps, warmup),
+        "fp4_gemv_m4": lambda: fp4_gemv_workload(torch, K, dev, 4, steps, warmup),
+        "fp4_gemv_m16": lambda: fp4_gemv_workload(torch, K, dev, 16, steps, warmup),
+        "int4_gemv_n4096": lambda: int4_gemv_workload(torch, K, dev, 4096, steps, warmup),
+        "int4_gemv_n14336": lambda: int4_gemv_workload(torch, K, dev, 14336, steps, warmup),
+        "fp6_e3m2_gemm_m2048": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e3m2", gemm_steps, 20),
+        "fp6_e2m3_gemm_m2048": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e2m3", gemm_steps, 20),
+        "fp4_gemm_8192": lambda: fp4_gemm_workload(torch, K, dev, 8192, 8192, 8192, gemm_steps, 20),
+        "fp4_gemm_4096x14336x4096": lambda: fp4_gemm_workload(torch, K, dev, 4096, 14336, 4096, gemm_steps, 20),
         "decoder_b1": lambda: decoder_workload(torch, dev, 1),
         "decoder_b8": lambda: decoder_workload(torch, dev, 8),
     }
     if args.only:
-        print(json.dumps({args.only: extras[args.only]()}))
+        print(json.dumps({args.only: workloads[args.only]()}))
         return 0
     torch.cuda.synchronize()
     wall = time.perf_counter()
-    primary = fp4_gemv_workload(torch, K, dev, 1, args.steps, args.warmup)
-    workloads = {}
-    if not args.no_extras:
-        for name in EXTRAS:
-            workloads[name] = extras[name]()
+    primary = workloads[PRIMARY]()
+    extras = {} if args.no_extras else {name: workloads[name]() for name in EXTRAS}
     torch.cuda.synchronize()
     gpu_wall = time.perf_counter() - wall
-    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
-    gbs = primary["GB/s"]
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_fp4(args.cpu_seconds)
+        if "int4_gemv_n4096" in extras:
+            extras["int4_gemv_n4096"]["cpu_baseline"] = cpu_baseline_int4(args.cpu_seconds)
+    for name, w in extras.items():
+        if name in PROFILES:
+            w["roofline"]["traffic"] = measured_traffic(name)
+    roofline = dict(primary["roofline"], traffic=measured_traffic(PRIMARY))
     line = {
         "metric": "low-bit GEMV GB/s (% HBM peak) + FP4 GEMM TFLOPS (% MFMA peak), 1 GPU",
-        "value": round(gbs, 2),
+        "value": roofline["achieved"],
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(primary["ms"], 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp4_e2m1 x bf16 -> fp32 acc -> bf16",
-        "data": "synthetic (uniform E2M1 codes, E8M0 exponents 123..129, N(0,1) bf16 activations), 18 rotating weight copies",
+        "data": (f"synthetic (uniform E2M1 codes, E8M0 exponents 123..129, N(0,1) bf16 activations), "
+                 f"{primary['copies']} rotating weight copies ({primary['copy_set_bytes'] / 1e6:.0f} MB)"),
         "config": {"workload": primary["workload"], "N": 14336, "K": 4096, "M": 1, "block": 32,
-                   "launch": "hip graph of the timed steps", "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("gemv_fp4_e2m1_n14336_k4096_m1.txt")},
+                   "launch": (f"median of {primary['trials']} trials, each a HIP graph of exactly {steps} steps "
+                              f"timed with HIP events"),
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "workloads": {name: {k: (round(v, 6) if isinstance(v, float) else v) for k, v in w.items()}
-                      for name, w in workloads.items()},
+                      for name, w in extras.items()},
         "gpu_wall_s": round(gpu_wall, 2),
     }
     print(json.dumps(line))

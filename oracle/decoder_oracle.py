@@ -113,32 +113,65 @@ class OracleDecoder:
         self.k = np.zeros((L, batch, kv_heads, max_seq, head_dim))
         self.v = np.zeros((L, batch, kv_heads, max_seq, head_dim))
 
-    def forward(self, tokens: np.ndarray, start: int) -> np.ndarray:
-        """Run tokens [B, T] at positions start .. start + T - 1; returns logits [B, T, V]."""
-        B, T = tokens.shape
+    def attn_input(self, li: int, h: np.ndarray) -> np.ndarray:
+        """The f16 input of layer ``li``'s QKV projection: RMSNorm(h) * w_attn."""
+        return f16(rmsnorm(h, self.w.layers[li].attn_norm, self.eps))
+
+    def qkv(self, li: int, x: np.ndarray, start: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+        """q, k rotated to positions start .. start + T - 1 and v, from the projection input x
+        [B, T, D]: q [B, H, T, hd], k and v [B, HK, T, hd], unrounded."""
+        B, T = x.shape[:2]
         H, HK, hd = self.H, self.HK, self.hd
         pos = np.arange(start, start + T)
-        h = self.w.embed[tokens].astype(np.float64)
-        for li, L in enumerate(self.w.layers):
-            x = f16(rmsnorm(h, L.attn_norm, self.eps))
-            qkv = x @ L.wqkv.T
-            q = qkv[..., :H * hd].reshape(B, T, H, hd).transpose(0, 2, 1, 3)
-            k = qkv[..., H * hd:(H + HK) * hd].reshape(B, T, HK, hd).transpose(0, 2, 1, 3)
-            v = qkv[..., (H + HK) * hd:].reshape(B, T, HK, hd).transpose(0, 2, 1, 3)
-            q = rope(q, pos, self.base)
-            k = rope(k, pos, self.base)
-            self.k[li, :, :, start:start + T] = bf16(k)
-            self.v[li, :, :, start:start + T] = bf16(v)
-            att = np.stack([attention(q[b], self.k[li, b, :, :start + T], self.v[li, b, :, :start + T], pos)
-                            for b in range(B)])
-            att = f16(att.transpose(0, 2, 1, 3).reshape(B, T, H * hd))
-            h = h + att @ L.wo.T
-            x = bf16(rmsnorm(h, L.ffn_norm, self.eps))
-            gu = x @ L.w_gate_up.T
-            a = bf16(silu(gu[..., 0::2]) * gu[..., 1::2])  # gate and up rows interleaved
-            h = h + a @ L.w_down.T
+        qkv = x @ self.w.layers[li].wqkv.T
+        q = qkv[..., :H * hd].reshape(B, T, H, hd).transpose(0, 2, 1, 3)
+        k = qkv[..., H * hd:(H + HK) * hd].reshape(B, T, HK, hd).transpose(0, 2, 1, 3)
+        v = qkv[..., (H + HK) * hd:].reshape(B, T, HK, hd).transpose(0, 2, 1, 3)
+        return rope(q, pos, self.base), rope(k, pos, self.base), v
+
+    def attend(self, li: int, q: np.ndarray, start: int) -> np.ndarray:
+        """Causal attention of q [B, H, T, hd] at positions start .. over layer ``li``'s cache,
+        as [B, T, H * hd], unrounded."""
+        B, H, T, hd = q.shape
+        pos = np.arange(start, start + T)
+        att = np.stack([attention(q[b], self.k[li, b, :, :start + T], self.v[li, b, :, :start + T], pos)
+                        for b in range(B)])
+        return att.transpose(0, 2, 1, 3).reshape(B, T, H * hd)
+
+    def attention_delta(self, li: int, h: np.ndarray, start: int) -> np.ndarray:
+        """Layer ``li``'s attention half for residual h [B, T, D] at positions start .. start + T - 1:
+        stores the new k, v in the layer's cache and returns attn @ Wo^T (what the layer adds to h)."""
+        T = h.shape[1]
+        q, k, v = self.qkv(li, self.attn_input(li, h), start)
+        self.k[li, :, :, start:start + T] = bf16(k)
+        self.v[li, :, :, start:start + T] = bf16(v)
+        return f16(self.attend(li, q, start)) @ self.w.layers[li].wo.T
+
+    def ffn_input(self, li: int, h: np.ndarray) -> np.ndarray:
+        """The bf16 input of layer ``li``'s gate|up projection: RMSNorm(h) * w_ffn."""
+        return bf16(rmsnorm(h, self.w.layers[li].ffn_norm, self.eps))
+
+    def swiglu(self, li: int, x: np.ndarray) -> np.ndarray:
+        """silu(gate) * up of the gate|up projection of x (gate and up rows interleaved), unrounded."""
+        gu = x @ self.w.layers[li].w_gate_up.T
+        return silu(gu[..., 0::2]) * gu[..., 1::2]
+
+    def ffn_delta(self, li: int, h: np.ndarray) -> np.ndarray:
+        """Layer ``li``'s feed-forward half for residual h: what it adds to h."""
+        return bf16(self.swiglu(li, self.ffn_input(li, h))) @ self.w.layers[li].w_down.T
+
+    def head(self, h: np.ndarray) -> np.ndarray:
+        """Logits of residual rows h [..., D]."""
         x = bf16(rmsnorm(h, self.w.final_norm, self.eps))
         return x @ self.w.lm_head.T
+
+    def forward(self, tokens: np.ndarray, start: int) -> np.ndarray:
+        """Run tokens [B, T] at positions start .. start + T - 1; returns logits [B, T, V]."""
+        h = self.w.embed[tokens].astype(np.float64)
+        for li in range(len(self.w.layers)):
+            h = h + self.attention_delta(li, h, start)
+            h = h + self.ffn_delta(li, h)
+        return self.head(h)
 
     def generate(self, prompts: np.ndarray, new_tokens: int) -> tuple[np.ndarray, np.ndarray]:
         """Greedy decode: ([B, new_tokens] token ids, [B, new_tokens, V] logits that chose them)."""

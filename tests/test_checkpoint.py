@@ -83,6 +83,18 @@ def test_malformed_files_raise_value_error(tmp_path):
          "smaller than the declared shape"),
         ({"tgm.packed": json.dumps({"w": {"format": "fp4_e2m1", "shape": [7, 96], "block_size": 16, "scales": True}})},
          "incompatible shape"),
+        ({"tgm.packed": json.dumps({"w": {"format": "fp4_e2m1", "block_size": 32, "scales": True}})}, "shape must be"),
+        ({"tgm.packed": json.dumps({"w": {"format": "fp4_e2m1", "shape": [7, 96.0], "block_size": 32,
+                                          "scales": True}})}, "shape must be"),
+        ({"tgm.packed": json.dumps({"w": {"format": "fp4_e2m1", "shape": [7, 96], "scales": True}})},
+         "block_size must be"),
+        ({"tgm.packed": json.dumps({"w": {"format": "fp4_e2m1", "shape": [7, 96], "block_size": "32",
+                                          "scales": True}})}, "block_size must be"),
+        ({"tgm.packed": json.dumps({"w": {"format": "fp4_e2m1", "shape": [7, 96], "block_size": 32}})},
+         "scales must be"),
+        ({"tgm.packed": json.dumps({"w": {"format": "fp4_e2m1", "shape": [7, 96], "block_size": 32,
+                                          "scales": False}})}, "declared unscaled"),
+        ({"tgm.packed": json.dumps({})}, "no declared packed tensor"),
     ]
     for metadata, message in cases:
         save_file(arrays, str(path), metadata=metadata)

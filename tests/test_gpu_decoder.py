@@ -315,10 +315,13 @@ def _compare_logits(dec: Decoder, ref_logits: np.ndarray, tol: float = 1e-2, whe
 
 
 @pytest.mark.parametrize("attention", ["fused", "gemm", "split"])
-@pytest.mark.parametrize("batch,prompt,floor,tol", [(2, 12, 1e-3, 1e-2), (1, 8, 1e-3, 1e-2), (3, 70, 1.0, 1e-3)])
+@pytest.mark.parametrize("batch,prompt,floor,tol", [(2, 12, 1e-3, 1e-2), (1, 8, 1e-3, 1e-2), (8, 6, 1.0, 1e-3),
+                                                    (3, 70, 1.0, 1e-3)])
 def test_decoder_matches_oracle(dev, batch, prompt, floor, tol, attention):
-    """Reduced config: prefill (GEMM path for 24 rows, GEMV path for 8; prompt attention fused,
-    as batched GEMMs or with the per-token kernel) and six cached decode steps; logits within
+    """Reduced config: prefill (GEMM path for 24 and 48 rows, GEMV path for 8; prompt attention
+    fused, as batched GEMMs or with the per-token kernel) and six cached decode steps (batch 8:
+    eight sequences share every multi-row GEMV, the SwiGLU GEMV, decode attention and the batched
+    head GEMV); logits within
     ``tol`` of the oracle fed the same tokens, and the device's greedy token is the oracle's
     wherever the oracle's top-2 margin exceeds 2e-2 of the largest logit.
 
@@ -326,8 +329,9 @@ def test_decoder_matches_oracle(dev, batch, prompt, floor, tol, attention):
     device and the oracle round activations at the same points, but fp32 against float64 can
     still put a value on the other side of a bf16 / f16 rounding boundary; one such flip moves
     the logits by up to about 5e-4 of the largest one (with either attention path).  The short
-    prompts meet the elementwise bound (floor 1e-3); the 210-row prompt, where flips occur, is
-    held to 1e-3 of the largest logit."""
+    prompts of one and two sequences meet the elementwise bound (floor 1e-3); the 48-row and
+    210-row prompts, where flips occur, are held to 1e-3 of the largest logit here and
+    elementwise, layer by layer, in test_decoder_layers_match_oracle_elementwise."""
     cfg, max_seq, steps = SMALL, 160, 6
     w = random_weights(cfg, dev, seed=batch)
     rng = np.random.default_rng(prompt)
@@ -352,6 +356,83 @@ def test_decoder_matches_oracle(dev, batch, prompt, floor, tol, attention):
         toks = dec.tokens[:batch].cpu().numpy()
     assert dec.pos.tolist() == [prompt + steps] * batch
     assert checked >= steps * batch // 2
+
+
+# rounding points: a value rounded on both sides may land one unit apart when the device's fp32
+# and the oracle's float64 put it on either side of a rounding boundary
+F16_ROUNDING, BF16_ROUNDING = 2.0 ** -10, 2.0 ** -7
+
+
+@pytest.mark.parametrize("attention", ["fused", "gemm", "split"])
+@pytest.mark.parametrize("batch,prompt", [(8, 6), (1, 9), (3, 40)])
+def test_decoder_layers_match_oracle_elementwise(dev, batch, prompt, attention):
+    """Teacher-forced parity of every operation of every layer, elementwise.  Each operation is
+    recomputed by the oracle from the device's own input to it (the device's residual, normed
+    activations, KV cache, attention output and SwiGLU output of that layer), so an activation
+    rounding flip in one operation cannot compound into the next:
+
+    * matrix products (attention output x Wo, SwiGLU output x Wdown) and the attention and SwiGLU
+      results: max relative error 1e-2, floor 1e-3 of the largest element;
+    * values the device rounds (the f16 / bf16 normed activations, the bf16 k and v it stores):
+      within one unit of the rounding (relative 2^-10 for f16, 2^-7 for bf16, same floor);
+    * the logits of the device's last residual: 1e-2.
+
+    Prefill (GEMM path at 48 and 120 rows, GEMV path at 9), then three cached decode steps
+    (batch 8: eight sequences per multi-row GEMV, SwiGLU GEMV and decode attention launch)."""
+    cfg, max_seq = SMALL, 64
+    w = random_weights(cfg, dev, seed=batch + 20)
+    prompts = np.random.default_rng(prompt).integers(0, cfg.vocab, (batch, prompt))
+    dec = Decoder(w, cfg, batch, max_seq, prompt)
+    dec.prompt_attention = attention
+    oracle = oracle_for(w, cfg, batch, max_seq)
+    embed = np64(w.embed)
+
+    def close(got, want, tol, what):
+        err = O.max_rel_err(got, want)
+        assert err <= tol, (what, err)
+
+    def check(tokens: np.ndarray, start: int, where: str) -> None:
+        T = tokens.shape[1]
+        shape = (batch, T, -1)
+        h = embed[tokens]  # [B, T, D], the layer-0 input
+        assert len(dec.layer_trace) == cfg.layers
+        for li, tr in enumerate(dec.layer_trace):
+            at = f"{where} layer {li}"
+            mid, delta = np64(tr["h"]).reshape(shape), np64(tr["delta"]).reshape(shape)
+            attn, act = np64(tr["attn"]).reshape(shape), np64(tr["act"]).reshape(shape)
+            x = oracle.attn_input(li, h)
+            if tr["x16"] is not None:
+                x16 = np64(tr["x16"]).reshape(shape)
+                close(x16, x, F16_ROUNDING, f"{at}: attention RMSNorm")
+                x = x16
+            q, k, v = oracle.qkv(li, x, start)
+            kc, vc = np64(dec.k_cache[li]), np64(dec.v_cache[li])
+            close(kc[:, :, start:start + T], D.bf16(k), BF16_ROUNDING, f"{at}: k cache")
+            close(vc[:, :, start:start + T], D.bf16(v), BF16_ROUNDING, f"{at}: v cache")
+            oracle.k[li, :, :, :start + T] = kc[:, :, :start + T]
+            oracle.v[li, :, :, :start + T] = vc[:, :, :start + T]
+            close(attn, oracle.attend(li, q, start), 1e-2, f"{at}: attention")
+            close(mid - h, attn @ oracle.w.layers[li].wo.T, 1e-2, f"{at}: output projection")
+            xb = oracle.ffn_input(li, mid)
+            if tr["xb"] is not None:
+                xb_dev = np64(tr["xb"]).reshape(shape)
+                close(xb_dev, xb, BF16_ROUNDING, f"{at}: feed-forward RMSNorm")
+                xb = xb_dev
+            close(act, oracle.swiglu(li, xb), 1e-2, f"{at}: gate|up + SwiGLU")
+            close(delta, act @ oracle.w.layers[li].w_down.T, 1e-2, f"{at}: down projection")
+            h = mid + delta
+        close(np64(dec.logits), oracle.head(h[:, -1]), 1e-2, f"{where}: logits")
+
+    dec.layer_trace = []
+    first = dec.prefill(torch.from_numpy(prompts).to(dev))
+    check(prompts, 0, "prefill")
+    toks = first.cpu().numpy()
+    for i in range(3):
+        dec.layer_trace = []
+        dec.step()
+        check(toks[:, None], prompt + i, f"step {i}")
+        toks = dec.tokens[:batch].cpu().numpy()
+    dec.layer_trace = None
 
 
 @pytest.mark.parametrize("parts,tol", [(3, 1e-3), (2, 5e-2), (1, 1.0)])
@@ -389,19 +470,34 @@ def test_graph_replay_matches_eager_decode(dev):
     assert torch.equal(eager2, dec.generate(prompts.flip(1), 5, graph=True))
 
 
-def test_decoder_full_size_prefill_and_graph_decode(dev):
+@pytest.mark.parametrize("batch", [1, 8])
+def test_decoder_full_size_prefill_and_graph_decode(dev, batch):
     """8 layers, hidden 4096, 32/8 heads, SwiGLU 14336, vocab 32000: 512-token prefill at batch
-    1 and graph-replayed decode agree with eager decode bit for bit; logits are finite."""
+    1 and 8, then graph-replayed decode agrees with eager decode bit for bit and logits are
+    finite.  At batch 8 the prefill logits of one sequence also match those of the same prompt
+    run alone at batch 1 (other GEMM launch shapes: split K at 512 rows, none at 4096) to 1e-2
+    of the largest logit."""
     cfg = DecoderConfig()
     w = random_weights(cfg, dev, seed=0)
-    prompts = torch.randint(0, cfg.vocab, (1, 512), device=dev)
-    dec = Decoder(w, cfg, 1, 640, 512)
+    g = torch.Generator(device=dev)
+    g.manual_seed(batch)
+    prompts = torch.randint(0, cfg.vocab, (batch, 512), device=dev, generator=g)
+    dec = Decoder(w, cfg, batch, 640, 512)
     eager = dec.generate(prompts, 4, graph=False)
     graphed = dec.generate(prompts, 4, graph=True)
     torch.cuda.synchronize()
     assert torch.equal(eager, graphed)
     assert torch.isfinite(dec.logits).all()
-    assert dec.pos.tolist() == [512 + 3]
+    assert dec.pos.tolist() == [512 + 3] * batch
+    if batch > 1:
+        # the batched launches do per-sequence arithmetic: sequence 5 alone gives the same logits
+        # to within the bf16 / f16 activation roundings the two launch shapes may order differently
+        solo = Decoder(w, cfg, 1, 640, 512)
+        solo.prefill(prompts[5:6])
+        batched = Decoder(w, cfg, batch, 640, 512)
+        batched.prefill(prompts)
+        err = O.max_rel_err(np64(batched.logits[5:6]), np64(solo.logits), 1.0)
+        assert err <= 1e-2, err
 
 
 def test_decoder_weights_file_round_trip(dev, tmp_path):

@@ -144,6 +144,42 @@ def test_gemv_mx_parity(dev, fmt, m, nk):
     assert O.max_rel_err(y2.cpu().numpy(), ref.T) <= TOL
 
 
+@pytest.fixture(scope="module")
+def fp4_decode_weight_14336x4096(dev):
+    """The FP4 decode weight at its full size, drawn in the documented order with seed 0:
+    codes = integers(0, 16, (14336, 4096)) (all 16 E2M1 codes, -0 included), E8M0 bytes
+    127 + integers(-4, 3, (14336, 128)).  Returns the device PackedTensor, the fp64 values
+    dequantised on the host from the host's own codes, and the generator, positioned where the
+    activation draw follows."""
+    n, k = 14336, 4096
+    rng = np.random.default_rng(0)
+    codes = rng.integers(0, 16, (n, k)).astype(np.uint8)
+    e = (127 + rng.integers(-4, 3, (n, k // 32))).astype(np.uint8)
+    data = O.pack_codes(codes, 4)
+    w = PackedTensor(torch.from_numpy(data).to(dev), "fp4_e2m1", (n, k),
+                     torch.from_numpy(e).to(dev).view(torch.float8_e8m0fnu), 32)
+    return w, O.dequant_f64(data, "fp4_e2m1", (n, k), O.e8m0_decode(e), 32), rng.bit_generator.state
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_gemv_fp4_decode_full_shape_against_oracle(dev, fp4_decode_weight_14336x4096, m):
+    """The benchmarked decode GEMV at its own shape: W FP4 E2M1 + E8M0/32 [14336, 4096], X bf16
+    [M, 4096] ~ N(0, 1) (drawn after W), bf16 out.  Every one of the M x 14336 outputs is held to
+    max relative error 1e-2 against the fp64 product of the host-dequantised weight (M = 1 runs
+    the row-streaming kernel with its full 1792-wave grid, M = 4 and 16 the streaming MFMA GEMV)."""
+    w, deq, state = fp4_decode_weight_14336x4096
+    rng = np.random.default_rng(0)
+    rng.bit_generator.state = state
+    x_np = rng.standard_normal((m, 4096)).astype(np.float32)
+    x = torch.from_numpy(x_np).to(dev).to(torch.bfloat16)
+    y = matmul_nt(x, w, dtype=torch.bfloat16)
+    assert y.shape == (m, 14336) and y.dtype is torch.bfloat16
+    ref = bf16_np(x).astype(np.float64) @ deq.T
+    assert O.max_rel_err(bf16_np(y), ref) <= TOL
+    # the same launch again on the same inputs is bit-identical (no run-to-run order change)
+    assert torch.equal(matmul_nt(x, w, dtype=torch.bfloat16), y)
+
+
 @pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e3m2"])
 @pytest.mark.parametrize("nkm", [(12288, 2048, 1), (6144, 4096, 4), (4096, 14336, 1), (2048, 3584, 2),
                                  (256, 14336, 16), (1000, 4096, 16), (64, 1536, 7), (4096, 14336, 8),
@@ -571,13 +607,61 @@ def test_gemm_mx_fp4_full_size_sampled(dev, mnk):
     assert O.max_rel_err(bf16_np(c)[rows], ref) <= TOL
 
 
-def test_failures_are_cached_per_candidate(dev):
+def test_failures_are_cached_per_candidate(dev, monkeypatch):
+    """A native rejection (an MX pair whose K is not a whole number of 32-element blocks: the
+    block-scaled MFMA GEMM has no kernel for it) is cached under its exact candidate key: the
+    first auto call tries the native kernel once and falls back, a repeat skips the native
+    attempt, and an explicit scope re-raises the cached reason (linalg.py:188-198, :216-223)."""
     linalg.matrix_failures.clear()
     rng = np.random.default_rng(2)
-    w, _ = make_weight(dev, "int4", 32, 64, "none", rng)
+    m, n, k = 64, 96, 48
+    a, deq_a = make_weight(dev, "fp4_e2m1", m, k, "e8m0", rng)
+    b, deq_b = make_weight(dev, "fp4_e2m1", n, k, "e8m0", rng)
+    attempts = []
+    native = linalg._mx_nt
+
+    def counting(*args):
+        attempts.append(args)
+        return native(*args)
+
+    monkeypatch.setattr(linalg, "_mx_nt", counting)
+    ref = deq_a @ deq_b.T
+    first = matmul_nt(a, b, dtype=torch.float32)
+    assert len(attempts) == 1 and len(linalg.matrix_failures) == 1
+    (key, reason), = linalg.matrix_failures.items()
+    assert key[0] == "tgm_gemm_mx" and "tgm_gemm_mx" in reason
+    second = matmul_nt(a, b, dtype=torch.float32)
+    assert len(attempts) == 1  # the cached rejection skips the native kernel
+    # the fallback decodes both operands and runs the exact-width GEMM: exact here
+    assert np.array_equal(first.cpu().numpy(), ref.astype(np.float32))
+    assert torch.equal(first, second)
+    with pytest.raises(RuntimeError, match="candidate rejected"):
+        matmul_nt(a, b, scope="Wave", dtype=torch.float32)
+    assert len(attempts) == 1
+    linalg.matrix_failures.clear()
+
+
+def test_fp64_operands_choose_no_native_kernel(dev):
+    """fp64 activations have no native family: auto computes exactly at fp64, nothing is cached."""
+    linalg.matrix_failures.clear()
+    rng = np.random.default_rng(2)
+    w, deq = make_weight(dev, "int4", 32, 64, "none", rng)
     x = torch.ones((2, 64), dtype=torch.float64, device=dev)
     out = matmul_nt(x, w)
-    assert out.dtype is torch.float64
+    assert out.dtype is torch.float64 and not linalg.matrix_failures
+    assert np.array_equal(out.cpu().numpy(), np.ones((2, 64)) @ deq.T)
+
+
+def test_transpose16_honours_the_column_stride_of_a_single_row(dev):
+    """A single-row view read at every other column (base[0:1, ::2], the right operand of a
+    K = 1 product) is staged with its column stride; so are multi-row strided views."""
+    base = torch.arange(64, dtype=torch.float32, device=dev).reshape(2, 32).to(torch.bfloat16)
+    for view in (base[0:1, ::2], base[:, ::2], base[:, 1::4], base[0:1, :]):
+        assert torch.equal(linalg.transpose16(view), view.t().contiguous()), view.stride()
+    b = base[0:1, ::2]
+    a = torch.arange(1, 33, dtype=torch.float32, device=dev).reshape(32, 1).to(torch.bfloat16)
+    c = matmul(a, b, dtype=torch.float32)
+    assert torch.equal(c.cpu(), a.float().cpu() @ b.float().cpu())
 
 
 def test_concurrent_callers_get_their_sequential_results(dev):

@@ -2,6 +2,7 @@
 the no-CPU-fallback rule and the C-ABI library's exports."""
 
 import ctypes
+import json
 import re
 import subprocess
 import sys
@@ -273,7 +274,7 @@ def test_profile_commands_name_existing_bench_workloads():
         import bench
     finally:
         sys.path.remove(str(root))
-    keys = set(bench.EXTRAS)
+    keys = set(bench.EXTRAS) | {bench.PRIMARY}
     summaries = sorted((root / "profiles").glob("*.txt"))
     assert summaries
     for path in summaries:
@@ -281,3 +282,59 @@ def test_profile_commands_name_existing_bench_workloads():
         assert "rocprofv3" in text, path.name
         for key in re.findall(r"--only (\S+)", text):
             assert key in keys, (path.name, key)
+
+
+def _write_csv(path: Path, rows: list[dict]) -> None:
+    import csv
+
+    path.parent.mkdir(parents=True, exist_ok=True)
+    with open(path, "w", newline="") as fh:
+        writer = csv.DictWriter(fh, fieldnames=list(rows[0]))
+        writer.writeheader()
+        writer.writerows(rows)
+
+
+def test_profile_summary_from_rocprof_csvs(tmp_path):
+    """bench.py --summarize-profile on synthetic rocprofv3 CSVs: the timed dispatches are the last
+    ones of the matching kernel, counters are medians per dispatch scaled by the copy calibration,
+    and the MFMA busy fraction is SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024)."""
+    root = Path(__file__).resolve().parents[1]
+    sys.path.insert(0, str(root))
+    try:
+        import bench
+    finally:
+        sys.path.remove(str(root))
+    kernel = "void tgm::gemm_mx_fp4<4, 2>(unsigned char const*)"
+    durations = [400_000] * 5 + [300_000, 290_000, 310_000]  # 5 warm-up dispatches, then 3 timed
+    trace = [{"Kernel_Name": kernel, "Start_Timestamp": 1000 * i, "End_Timestamp": 1000 * i + d}
+             for i, d in enumerate(durations)]
+    trace.insert(2, {"Kernel_Name": "other_kernel", "Start_Timestamp": 0, "End_Timestamp": 5})
+    _write_csv(tmp_path / "kt" / "run_kernel_trace.csv", trace)
+    flops, nbytes = 2 * 8192 ** 3, 205_520_896
+    run = {"workload": "fp4xfp4", "ms": 0.3, "flops": flops, "bytes": nbytes, "timed_dispatches": 3,
+           "roofline": bench.mfma_roofline(flops, 0.3, bench.FP4_PEAK_TFLOPS, "dense MXFP4 MFMA")}
+    (tmp_path / "kt" / "bench.json").write_text(json.dumps({"fp4_gemm_8192": run}))
+
+    def counters(folder, name, values, kname=kernel):
+        _write_csv(tmp_path / folder / "run_counter_collection.csv",
+                   [{"Dispatch_Id": i, "Kernel_Name": kname, "Counter_Name": name, "Counter_Value": v}
+                    for i, v in enumerate(values)])
+
+    counters("fetch", "FETCH_SIZE", [100_000.0, 200_000.0, 150_000.0])
+    counters("write", "WRITE_SIZE", [131_072.0] * 3)
+    counters("cfetch", "FETCH_SIZE", [32_768.0], "__amd_rocclr_copyBuffer")
+    counters("cwrite", "WRITE_SIZE", [65_536.0], "__amd_rocclr_copyBuffer")
+    rows = []
+    for i in range(2):
+        rows += [{"Dispatch_Id": i, "Kernel_Name": kernel, "Counter_Name": "SQ_VALU_MFMA_BUSY_CYCLES",
+                  "Counter_Value": 512_000.0},
+                 {"Dispatch_Id": i, "Kernel_Name": kernel, "Counter_Name": "GRBM_GUI_ACTIVE", "Counter_Value": 1000.0},
+                 {"Dispatch_Id": i, "Kernel_Name": kernel, "Counter_Name": "SQ_BUSY_CYCLES", "Counter_Value": 900.0}]
+    _write_csv(tmp_path / "mfma" / "run_counter_collection.csv", rows)
+    text = bench.summarize_profile(tmp_path, "fp4_gemm_8192")
+    assert "timed: mean_ns=300000 median_ns=300000" in text
+    # FETCH median 150000 KiB x 2 (copy: 32768 KiB read for 64 MiB) + WRITE 131072 KiB x 1
+    assert f"traffic_bytes_per_launch={(150_000 * 2 + 131_072) * 1024}" in text
+    assert "mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs) = 0.5000" in text
+    assert f"algorithmic_flops_per_launch={flops}" in text
+    assert "--only fp4_gemm_8192" in text and "--pmc SQ_VALU_MFMA_BUSY_CYCLES" in text

@@ -156,31 +156,168 @@ def test_graph_validation_without_a_gpu():
         StreamGraph(lambda: None, 0)
 
 
-def test_shared_renderer_concurrent_sources():
-    """Concurrent callers of one renderer receive exactly their sequential source (the reference's
-    test_renderer_concurrency.py:11-36 idea): 8 kernels of 4 dtypes with long bodies, rendered
-    from 8 threads released together."""
-    from concurrent.futures import ThreadPoolExecutor
-    from threading import Barrier
+def test_one_renderer_serves_many_threads():
+    """Threads that share one renderer each get the source they would get alone.  Twelve kernel
+    specifications differ in name, parameter count, dtypes and body length (up to a few thousand
+    statements, so renders overlap in time); each thread renders its own spec three times after
+    a common start signal, and every result must equal the single-threaded render."""
+    import threading
 
     r = MI355XRenderer()
-    cases = []
-    for slot in range(8):
-        dt = (torch.float32, torch.float64, torch.int32, torch.float16)[slot % 4]
-        body = ["auto v = src[0];"] + ["v = v * v + src[0];"] * 2048 + ["out[0] = v;"]
-        cases.append(KernelSpec(f"thread_{slot}", (BufferParam("out", dt, True), BufferParam("src", dt)), (),
-                                tuple(body)))
-    expected = [r.render(c) for c in cases]
-    barrier = Barrier(len(cases))
+    kinds = (torch.float16, torch.int64, torch.bfloat16, torch.float32, torch.uint8, torch.float64)
+    specs = []
+    for i in range(12):
+        dt = kinds[i % len(kinds)]
+        params = (BufferParam("dst", dt, True),) + tuple(BufferParam(f"in{j}", dt) for j in range(1 + i % 3))
+        body = ("auto acc = in0[gidx0];",) + ("acc = acc + in0[gidx0];",) * (300 * (i + 1)) + ("dst[gidx0] = acc;",)
+        specs.append(KernelSpec(f"accumulate_{i}", params, (("n", "i64"),) if i % 2 else (), body))
+    alone = [r.render(spec) for spec in specs]
+    start = threading.Event()
+    results: dict[int, list] = {}
 
-    def render(slot: int) -> str:
-        barrier.wait()
-        try:
-            return r.render(cases[slot])
-        except Exception as error:  # noqa: BLE001 - a failure must show up as a mismatch
-            return type(error).__name__
+    def worker(i: int) -> None:
+        start.wait()
+        out = []
+        for _ in range(3):
+            try:
+                out.append(r.render(specs[i]))
+            except Exception as error:  # noqa: BLE001 -- recorded so that a failure reads as a mismatch
+                out.append(repr(error))
+        results[i] = out
 
-    with ThreadPoolExecutor(max_workers=len(cases)) as workers:
-        actual = list(workers.map(render, range(len(cases))))
-    assert actual == expected
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(specs))]
+    for t in threads:
+        t.start()
+    start.set()
+    for t in threads:
+        t.join(60)
+    assert sorted(results) == list(range(len(specs)))
+    for i, got in results.items():
+        assert got == [alone[i]] * 3, specs[i].name
 
+
+class _StubHip:
+    """A HIP binding with no GPU behind it: every call succeeds, except the names the test
+    arms to fail once; host allocations are real host memory so staging copies can run."""
+
+    H2D, D2H, D2D = 1, 2, 3
+
+    def __init__(self) -> None:
+        self.calls: list[str] = []
+        self.armed: set[str] = set()
+        self._events = 0
+        self._host: dict[int, object] = {}
+
+    def call(self, name: str, *args) -> None:
+        self.calls.append(name)
+        if name in self.armed:
+            self.armed.discard(name)
+            raise RuntimeError(f"{name} failed: 1 (injected)")
+        if name == "hipHostFree":
+            self._host.pop(args[0], None)
+
+    def launch(self, function, grid, block, kernargs, stream, shared=0) -> None:
+        self.call("hipModuleLaunchKernel", function, *grid, *block, shared, stream)
+
+    def event_create(self) -> int:
+        self._events += 1
+        return self._events
+
+    def host_malloc(self, size: int) -> int:
+        import ctypes
+
+        buf = ctypes.create_string_buffer(max(size, 1))
+        self._host[ctypes.addressof(buf)] = buf
+        return ctypes.addressof(buf)
+
+    def query(self, name: str, handle: int) -> bool:
+        return True
+
+    def set_device(self, ordinal: int) -> None:
+        pass
+
+    def elapsed_ms(self, start: int, stop: int) -> float:
+        return 0.0
+
+
+def _stub_device(name: str = "MI355X", ordinal: int = 0) -> R.MI355XDevice:
+    import threading
+
+    dev = object.__new__(R.MI355XDevice)
+    dev.device, dev.ordinal, dev.lock, dev.failure = name, ordinal, threading.RLock(), None
+    dev.stream, dev.inflight = 0x51, []
+    dev.allocator = R.MI355XAllocator(dev)
+    return dev
+
+
+def _stub_program(dev: R.MI355XDevice) -> R.MI355XProgram:
+    prog = object.__new__(R.MI355XProgram)
+    prog.dev, prog.name, prog.function, prog.module = dev, "k", 0x99, 0
+    prog.signature = KernelSignature("k", ("ptr", "i32"))
+    return prog
+
+
+def _buffer_on(dev, size=64):
+    return R.MI355XBuffer(dev, R._Allocation(0x1000, size), size)
+
+
+def test_a_failed_launch_is_sticky(monkeypatch):
+    """A launch whose hipModuleLaunchKernel fails raises that error and is kept as the device's
+    failure; every later launch, copy, transfer and synchronize raises from it, without reaching
+    HIP (ops_dx12.py:196-198, :275-295; test_execution.py:128-165)."""
+    stub = _StubHip()
+    monkeypatch.setattr(R, "hip", stub)
+    dev = _stub_device()
+    prog, buf = _stub_program(dev), _buffer_on(dev)
+    prog(buf, vals=(3,))  # a good launch first
+    assert dev.failure is None and stub.calls.count("hipModuleLaunchKernel") == 1
+    stub.armed.add("hipModuleLaunchKernel")
+    with pytest.raises(RuntimeError, match="injected"):
+        prog(buf, vals=(3,))
+    assert isinstance(dev.failure, RuntimeError) and "injected" in str(dev.failure)
+    before = len(stub.calls)
+    later = [lambda: prog(buf, vals=(3,)), lambda: prog(buf, vals=(3,), wait=True),
+             lambda: dev.allocator._copyin(buf, memoryview(bytes(8))),
+             lambda: dev.allocator._copyout(memoryview(bytearray(8)), buf),
+             lambda: dev.allocator._transfer(_buffer_on(dev), buf, 8, dev, dev),
+             lambda: dev.synchronize()]
+    for action in later:
+        with pytest.raises(RuntimeError, match="submission/transfer failed") as info:
+            action()
+        assert info.value.__cause__ is dev.failure
+    assert len(stub.calls) == before  # nothing after the failure reached HIP
+
+
+@pytest.mark.parametrize("which", ["copyin", "copyout", "transfer"])
+def test_a_failed_copy_is_sticky(monkeypatch, which):
+    """A copy whose hipMemcpyAsync fails sets the failure too; later launches raise."""
+    stub = _StubHip()
+    monkeypatch.setattr(R, "hip", stub)
+    dev = _stub_device()
+    prog, buf = _stub_program(dev), _buffer_on(dev)
+    stub.armed.add("hipMemcpyAsync")
+    action = {"copyin": lambda: dev.allocator._copyin(buf, memoryview(bytes(8))),
+              "copyout": lambda: dev.allocator._copyout(memoryview(bytearray(8)), buf),
+              "transfer": lambda: dev.allocator._transfer(_buffer_on(dev), buf, 8, dev, dev)}[which]
+    with pytest.raises(RuntimeError, match="injected"):
+        action()
+    assert dev.failure is not None
+    assert all(name != "hipHostMalloc" for name in stub.calls)
+    assert not stub._host  # staging memory of the failed copy was released
+    with pytest.raises(RuntimeError, match="submission/transfer failed"):
+        prog(buf, vals=(1,))
+    with pytest.raises(RuntimeError, match="submission/transfer failed"):
+        dev.synchronize()
+
+
+def test_a_failed_cross_device_transfer_marks_both_devices(monkeypatch):
+    stub = _StubHip()
+    monkeypatch.setattr(R, "hip", stub)
+    src, dst = _stub_device("MI355X", 0), _stub_device("MI355X:1", 1)
+    stub.armed.add("hipMemcpyPeerAsync")
+    with pytest.raises(RuntimeError, match="injected"):
+        dst.allocator._transfer(_buffer_on(dst), _buffer_on(src), 16, src, dst)
+    assert src.failure is dst.failure is not None
+    for dev in (src, dst):
+        with pytest.raises(RuntimeError, match="submission/transfer failed"):
+            dev.synchronize()

@@ -550,29 +550,44 @@ extern "C" int64_t tgm_gemm_w_split_workspace(int64_t m, int64_t n, int64_t spli
   return splits > 1 && m > 0 && n > 0 ? splits * m * n * (int64_t)sizeof(float) : 0;
 }
 
+// Number of K groups a split-K call runs: every group holds at least one kWK step; 1 means
+// the single-pass product (also when N % 4 != 0, which the reduction does not take).
+static int64_t effective_splits(int64_t m, int64_t n, int64_t k, int64_t splits) {
+  const int64_t steps = k > 0 && k % kWK == 0 ? k / kWK : 1;
+  const int64_t kps = (steps + splits - 1) / (splits < steps ? splits : steps);
+  const int64_t eff = (steps + kps - 1) / kps;
+  return eff <= 1 || n % 4 != 0 || m == 0 || n == 0 ? 1 : eff;
+}
+
+// Split-K product into the fp32 partial buffer `part` ([eff][M][N]), then the ordered reduction.
+static int gemm_w_split_run(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n,
+                            int64_t k, const void* scales, int scale_dtype, int64_t block_size, void* c, int c_dtype,
+                            int64_t ldc, int64_t eff, float* part, void* stream, const char* what) {
+  const int st = gemm_w_impl(a, a_dtype, m, lda, w, fmt, n, k, scales, scale_dtype, block_size, c, c_dtype, ldc,
+                             (int)eff, part, stream);
+  if (st != TGM_OK) return st;
+  const int64_t quads = m * n / 4;
+  const unsigned grid = (unsigned)((quads + 255) / 256 < 8192 ? (quads + 255) / 256 : 8192);
+  hipLaunchKernelGGL(gemm_split_reduce, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const float*)part, (int)eff, m,
+                     n, c, c_dtype, ldc);
+  return launch_status(what);
+}
+
 extern "C" int tgm_gemm_w_split(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n,
                                 int64_t k, const void* scales, int scale_dtype, int64_t block_size, void* c,
                                 int c_dtype, int64_t ldc, int64_t splits, void* workspace, int64_t workspace_bytes,
                                 void* stream) {
   clear_error();
   TGM_CHECK_ARG(splits >= 1 && splits <= 64, "splits must be in [1, 64]");
-  const int64_t steps = k > 0 && k % kWK == 0 ? k / kWK : 1;
-  const int64_t kps = (steps + splits - 1) / (splits < steps ? splits : steps);
-  const int64_t eff = (steps + kps - 1) / kps;  // every split gets at least one K step
-  if (eff <= 1 || n % 4 != 0 || m == 0 || n == 0)  // one split, or rows the reduction does not take
+  const int64_t eff = effective_splits(m, n, k, splits);
+  if (eff == 1)
     return gemm_w_impl(a, a_dtype, m, lda, w, fmt, n, k, scales, scale_dtype, block_size, c, c_dtype, ldc, 1, nullptr,
                        stream);
   TGM_CHECK_ARG(workspace && workspace_bytes >= tgm_gemm_w_split_workspace(m, n, eff) &&
                     (uintptr_t)workspace % 16 == 0,
                 "split-K needs a 16-byte aligned workspace of tgm_gemm_w_split_workspace() bytes");
-  const int st = gemm_w_impl(a, a_dtype, m, lda, w, fmt, n, k, scales, scale_dtype, block_size, c, c_dtype, ldc,
-                             (int)eff, (float*)workspace, stream);
-  if (st != TGM_OK) return st;
-  const int64_t quads = m * n / 4;
-  const unsigned grid = (unsigned)((quads + 255) / 256 < 8192 ? (quads + 255) / 256 : 8192);
-  hipLaunchKernelGGL(gemm_split_reduce, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const float*)workspace, (int)eff,
-                     m, n, c, c_dtype, ldc);
-  return launch_status("tgm_gemm_w_split");
+  return gemm_w_split_run(a, a_dtype, m, lda, w, fmt, n, k, scales, scale_dtype, block_size, c, c_dtype, ldc, eff,
+                          (float*)workspace, stream, "tgm_gemm_w_split");
 }
 
 extern "C" int tgm_gemm_w_swiglu(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n,

@@ -172,6 +172,22 @@ __device__ __forceinline__ void norm_finish(const RowsNorm& nm, const NormRegs<I
   lds_barrier();
 }
 
+// Activations for the one-row kernels, staged once per 256-thread workgroup: K = 2048 IPR
+// 16-bit values = IPR 16-byte chunks per thread, issued before the weight stream (so that
+// waiting for them does not wait for the weights: the vector memory counter retires in order)
+// and written to LDS once they land, where every wave reads the values its lanes need.
+template <int IPR>
+__device__ __forceinline__ void stage_issue(const unsigned char* x, u32x4r (&xg)[IPR]) {
+#pragma unroll
+  for (int j = 0; j < IPR; ++j) xg[j] = *(const u32x4r*)(x + 4096 * j + 16 * threadIdx.x);
+}
+template <int IPR>
+__device__ __forceinline__ void stage_finish(const u32x4r (&xg)[IPR], unsigned char* xs) {
+#pragma unroll
+  for (int j = 0; j < IPR; ++j) *(u32x4r*)(xs + 4096 * j + 16 * threadIdx.x) = xg[j];
+  lds_barrier();
+}
+
 // One wave per R (8 or 4) rows, four waves per workgroup; IPR instructions per row
 // (K = 2048 IPR); D loads in flight per wave.
 // SWIGLU: rows 2 i and 2 i + 1 are the gate and up rows of output i, which becomes
@@ -198,11 +214,14 @@ __global__ void __launch_bounds__(256) gemv_rows_fp4(const uint8_t* __restrict__
       for (int j = 0; j < 16; ++j) xr[h][j] = xp[j];
     }
   };
+  // x reaches the waves through LDS: the workgroup reads it from memory once (IPR 16-byte
+  // chunks per thread) instead of every wave reading all of it
   NormRegs<NORM ? IPR : 1> nr;
-  __shared__ __attribute__((aligned(16))) __bf16 xs[NORM ? K : 8];
+  __shared__ __attribute__((aligned(16))) __bf16 xs[K];
   __shared__ float red[4];
+  u32x4r xg[NORM ? 1 : IPR];
   if constexpr (NORM) norm_issue<IPR>(nm, nr);
-  else load_x(x);
+  else stage_issue<IPR>((const unsigned char*)x, xg);
   auto row_of = [&](int i) __attribute__((always_inline)) {
     const int64_t r = r0 + i / IPR;
     return r < N ? r : N - 1;  // rows past N re-read the last row; they are not stored
@@ -221,14 +240,14 @@ __global__ void __launch_bounds__(256) gemv_rows_fp4(const uint8_t* __restrict__
     for (int j = 0; j < SL; ++j) {
       int64_t off = r0 * KB + 1024 * j + 16 * lane;
       off = off < limit ? off : limit;
-      sraw[j] = *(const u32x4r*)(scales + off);
+      sraw[j] = __builtin_nontemporal_load((const u32x4r*)(scales + off));
     }
   }
   u32x4r codes[D];
   auto load = [&](int i, int slot) __attribute__((always_inline)) {
     const int64_t r = row_of(i);
     const int h = i % IPR;
-    codes[slot] = *(const u32x4r*)(w + r * (K / 2) + 1024 * h + 16 * lane);
+    codes[slot] = __builtin_nontemporal_load((const u32x4r*)(w + r * (K / 2) + 1024 * h + 16 * lane));
   };
 #pragma unroll
   for (int i = 0; i < D; ++i) load(i, i);
@@ -243,10 +262,9 @@ __global__ void __launch_bounds__(256) gemv_rows_fp4(const uint8_t* __restrict__
 #pragma unroll
     for (int i = 0; i < NI; ++i) sbyte[i] = sl[wv][(i / IPR) * KB + 64 * (i % IPR) + lane];
   }
-  if constexpr (NORM) {
-    norm_finish<IPR>(nm, nr, xs, red);
-    load_x(xs);
-  }
+  if constexpr (NORM) norm_finish<IPR>(nm, nr, xs, red);
+  else stage_finish<IPR>(xg, (unsigned char*)xs);
+  load_x(xs);
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
@@ -329,10 +347,11 @@ __global__ void __launch_bounds__(256) gemv_rows_int4(const uint8_t* __restrict_
     }
   };
   NormRegs<NORM ? IPR : 1> nr;
-  __shared__ __attribute__((aligned(16))) _Float16 xs[NORM ? K : 8];
+  __shared__ __attribute__((aligned(16))) _Float16 xs[K];
   __shared__ float red[4];
+  u32x4r xg[NORM ? 1 : IPR];
   if constexpr (NORM) norm_issue<IPR>(nm, nr);  // RMSNorm(h + delta) * w_norm, rounded to fp16
-  else load_x(x);
+  else stage_issue<IPR>((const unsigned char*)x, xg);
   auto row_of = [&](int i) __attribute__((always_inline)) {
     const int64_t r = r0 + i / IPR;
     return r < N ? r : N - 1;
@@ -351,13 +370,13 @@ __global__ void __launch_bounds__(256) gemv_rows_int4(const uint8_t* __restrict_
     for (int j = 0; j < SL; ++j) {
       int64_t off = r0 * ng * SSIZE + 1024 * j + 16 * lane;
       off = off < limit ? off : limit;
-      sraw[j] = *(const u32x4r*)(scales + off);
+      sraw[j] = __builtin_nontemporal_load((const u32x4r*)(scales + off));
     }
   }
   u32x4r codes[D];
   auto load = [&](int i, int slot) __attribute__((always_inline)) {
     const int64_t r = row_of(i);
-    codes[slot] = *(const u32x4r*)(w + r * (K / 2) + 1024 * (i % IPR) + 16 * lane);
+    codes[slot] = __builtin_nontemporal_load((const u32x4r*)(w + r * (K / 2) + 1024 * (i % IPR) + 16 * lane));
   };
 #pragma unroll
   for (int i = 0; i < D; ++i) load(i, i);
@@ -373,10 +392,9 @@ __global__ void __launch_bounds__(256) gemv_rows_int4(const uint8_t* __restrict_
     for (int i = 0; i < NI; ++i)
       sv[i] = int4_scale<SDT>(&sl[wv][((i / IPR) * ng + ((64 * (i % IPR) + lane) >> GS)) * SSIZE]);
   }
-  if constexpr (NORM) {
-    norm_finish<IPR>(nm, nr, xs, red);
-    load_x(xs);
-  }
+  if constexpr (NORM) norm_finish<IPR>(nm, nr, xs, red);
+  else stage_finish<IPR>(xg, (unsigned char*)xs);
+  load_x(xs);
   const half2r hb = {(_Float16)bias, (_Float16)bias};
   float acc[R];
 #pragma unroll

@@ -55,6 +55,20 @@ def save(path: str | Path, tensors: dict[str, PackedTensor | torch.Tensor], meta
     save_file(arrays, str(path), metadata=metadata)
 
 
+def _check_spec(name: str, spec) -> tuple[tuple[int, ...], int, bool]:
+    """Validate one ``tgm.packed`` entry's field types; returns (shape, block_size, scaled)."""
+    if not isinstance(spec, dict) or spec.get("format") not in FORMATS:
+        raise ValueError(f"packed tensor {name!r}: unknown or missing format")
+    shape, block, scaled = spec.get("shape"), spec.get("block_size"), spec.get("scales")
+    if not isinstance(shape, list) or not all(isinstance(x, int) and not isinstance(x, bool) for x in shape):
+        raise ValueError(f"packed tensor {name!r}: shape must be a list of integers, got {shape!r}")
+    if not isinstance(block, int) or isinstance(block, bool):
+        raise ValueError(f"packed tensor {name!r}: block_size must be an integer, got {block!r}")
+    if not isinstance(scaled, bool):
+        raise ValueError(f"packed tensor {name!r}: scales must be true or false, got {scaled!r}")
+    return tuple(shape), block, scaled
+
+
 def load(path: str | Path, device: str | torch.device = "cpu") -> tuple[dict[str, PackedTensor | torch.Tensor], dict]:
     """Read a file written by ``save``; returns (tensors, meta) with tensors on ``device``."""
     from safetensors import safe_open
@@ -71,15 +85,18 @@ def load(path: str | Path, device: str | torch.device = "cpu") -> tuple[dict[str
             raise ValueError(f"corrupt packed-tensor metadata in {path}")
         names = set(f.keys())
         for name, spec in packed.items():
-            if not isinstance(spec, dict) or spec.get("format") not in FORMATS:
-                raise ValueError(f"packed tensor {name!r}: unknown or missing format")
-            if name not in names or (spec.get("scales") and name + SCALE_SUFFIX not in names):
+            shape, block, scaled = _check_spec(name, spec)
+            if name not in names or (scaled and name + SCALE_SUFFIX not in names):
                 raise ValueError(f"packed tensor {name!r}: missing data or scales array")
+            if not scaled and name + SCALE_SUFFIX in names:
+                raise ValueError(f"packed tensor {name!r}: declared unscaled but the file holds {name + SCALE_SUFFIX!r}")
             data = f.get_tensor(name)
-            scales = f.get_tensor(name + SCALE_SUFFIX) if spec.get("scales") else None
-            tensors[name] = PackedTensor(data, spec["format"], tuple(spec["shape"]), scales, int(spec["block_size"]))
+            scales = f.get_tensor(name + SCALE_SUFFIX) if scaled else None
+            tensors[name] = PackedTensor(data, spec["format"], shape, scales, block)
         for name in names:
             if name in tensors or (name.endswith(SCALE_SUFFIX) and name[: -len(SCALE_SUFFIX)] in packed):
                 continue
+            if name.endswith(SCALE_SUFFIX):
+                raise ValueError(f"{name!r} holds block scales of no declared packed tensor")
             tensors[name] = f.get_tensor(name)
     return tensors, meta

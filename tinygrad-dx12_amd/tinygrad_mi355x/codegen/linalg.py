@@ -80,7 +80,9 @@ def transpose16(x: torch.Tensor) -> torch.Tensor:
     K.require_device(x)
     rows, cols = x.shape
     out = torch.empty((cols, rows), dtype=x.dtype, device=x.device)
-    if x.stride(1) != 1 and rows > 1 and cols > 1:
+    # the kernel reads row i at x + i * ld_in with unit column stride: any other column
+    # stride (a single-row view included) is staged first
+    if x.stride(1) != 1 and cols > 1:
         x = x.contiguous()
     K.call("tgm_transpose16", x.data_ptr(), rows, cols, x.stride(0) if rows > 1 else cols, out.data_ptr(), rows,
            K.stream_of(x))

@@ -263,6 +263,12 @@ class Decoder:
         self.prompt_len = 0
         self._graph: StreamGraph | None = None
         self.graph_stream: torch.cuda.Stream | None = None
+        # when a list (eager runs only): per layer, a dict of copies of the layer's activations --
+        # "h" the residual after attention and "delta" the feed-forward output (fp32, the layer's
+        # output is their sum), "x16" the normed f16 input of the QKV projection, "attn" the f16
+        # attention output, "xb" the normed bf16 input of gate|up and "act" the bf16 SwiGLU
+        # output; "x16" and "xb" are None when the norm runs inside the projection
+        self.layer_trace: list[dict[str, torch.Tensor | None]] | None = None
 
     # ---------------------------------------------------------------- building blocks
     def _layers(self, rows: int, seq_rows: int, splits: int, stream: int) -> None:
@@ -308,6 +314,7 @@ class Decoder:
                        L.ffn_norm.data_ptr(), cfg.eps, w.data.data_ptr(), K.FORMAT_IDS[w.format], 2 * cfg.ffn, d,
                        K.ptr(w.scales), K.dtype_id(w.scales.dtype), w.block_size, self.act.data_ptr(), BF16, 1, stream)
                 _packed_product(self.act, rows, cfg.ffn, L.w_down, self.delta, d, stream, self._split_ws)
+                self._trace(rows, fused_norm=True)
                 continue
             K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr(), rows, d, L.ffn_norm.data_ptr(),
                    cfg.eps, self.xnb.data_ptr(), BF16, stream)
@@ -326,8 +333,16 @@ class Decoder:
                 _packed_product(self.xnb, rows, d, L.w_gate_up, self.gu, 2 * cfg.ffn, stream, self._split_ws)
                 K.call("tgm_dec_silu_mul", self.gu.data_ptr(), rows, cfg.ffn, self.act.data_ptr(), BF16, stream)
             _packed_product(self.act, rows, cfg.ffn, L.w_down, self.delta, d, stream, self._split_ws)
+            self._trace(rows)
         K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr(), rows, d, self.w.final_norm.data_ptr(),
                cfg.eps, self.xnb.data_ptr(), BF16, stream)
+
+    def _trace(self, rows: int, fused_norm: bool = False) -> None:
+        if self.layer_trace is not None:
+            self.layer_trace.append({
+                "h": self.h[:rows].clone(), "delta": self.delta[:rows].clone(), "attn": self.attn[:rows].clone(),
+                "act": self.act[:rows].clone(), "x16": None if fused_norm else self.xn16[:rows].clone(),
+                "xb": None if fused_norm else self.xnb[:rows].clone()})
 
     def _prefill_attention(self, rows: int, t: int, kc: torch.Tensor, vc: torch.Tensor, stream: int) -> None:
         """Causal attention of a whole prompt (positions 0 .. t - 1 of every sequence) as two

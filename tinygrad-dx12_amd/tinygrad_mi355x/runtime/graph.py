@@ -139,8 +139,7 @@ class MI355XGraph:
             if self._graph is None or self._key(calls) != self._recorded:
                 self._record(calls)
                 self.calls = calls
-            with self.dev.lock:
-                self.dev.check_failure()
+            with self.dev.lock, self.dev.submitting():
                 owners = tuple(b.owner for _, bufs, *_ in calls for b in bufs)
                 if not wait:
                     self._graph.launch()

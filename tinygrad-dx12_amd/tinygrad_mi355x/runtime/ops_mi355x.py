@@ -5,7 +5,10 @@ src/tinygrad_dx12/runtime/ops_dx12.py:150-744), with the same surface and contra
 
 * ``MI355XDevice(device)`` -- ``.renderer``, ``.runtime(name, lib)``, ``.synchronize(timeout)``,
   ``.count()``; a per-device ``RLock`` around submission (ops_dx12.py:155) and a sticky
-  failure re-raised on later calls (:197-198, :294-295).
+  failure: a HIP call that fails while enqueueing a launch, copy or transfer is kept as
+  ``dev.failure``, and every later launch, copy, transfer and synchronize raises
+  ``RuntimeError("MI355X submission/transfer failed")`` from it (:197-198, :275-295); a
+  failed cross-device transfer marks both devices.
 * ``MI355XAllocator(dev)`` -- ``_alloc`` rejects ``external_ptr`` and zero-fills on
   ``zero`` (:440-447); ``_copyin`` owns the caller's bytes before returning and is
   asynchronous (:455-461); ``_copyout`` blocks (:463-470); ``_offset`` is bounds checked
@@ -25,6 +28,7 @@ descriptor tables.  No stream is created at a non-default priority.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import struct
 import threading
@@ -161,11 +165,15 @@ class MI355XAllocator:
             raise ValueError("MI355X upload exceeds view size")
         if nbytes == 0:
             return
-        with self.dev.lock:
+        with self.dev.lock, self.dev.submitting():
             self.dev.select()
             staging = hip.host_malloc(nbytes)
             ctypes.memmove(staging, (ctypes.c_char * nbytes).from_buffer_copy(src.cast("B")), nbytes)
-            hip.call("hipMemcpyAsync", dest.address, staging, nbytes, hip.H2D, self.dev.stream)
+            try:
+                hip.call("hipMemcpyAsync", dest.address, staging, nbytes, hip.H2D, self.dev.stream)
+            except RuntimeError:
+                hip.call("hipHostFree", staging)
+                raise
             self.dev.submitted((dest.owner,), lambda: hip.call("hipHostFree", staging))
 
     def _copyout(self, dest: memoryview, src: MI355XBuffer) -> None:
@@ -176,11 +184,13 @@ class MI355XAllocator:
         if nbytes == 0:
             return
         with self.dev.lock:
-            self.dev.select()
-            staging = hip.host_malloc(nbytes)
+            with self.dev.submitting():
+                self.dev.select()
+                staging = hip.host_malloc(nbytes)
             try:
-                hip.call("hipMemcpyAsync", staging, src.address, nbytes, hip.D2H, self.dev.stream)
-                event = self.dev.submitted((src.owner,))
+                with self.dev.submitting():
+                    hip.call("hipMemcpyAsync", staging, src.address, nbytes, hip.D2H, self.dev.stream)
+                    event = self.dev.submitted((src.owner,))
                 self.dev.wait_event(event)
                 ctypes.memmove((ctypes.c_char * nbytes).from_buffer(dest.cast("B")), staging, nbytes)
             finally:
@@ -196,7 +206,7 @@ class MI355XAllocator:
         if src_dev is dest_dev:
             if src.owner is dest.owner and src.offset == dest.offset:
                 return
-            with self.dev.lock:
+            with self.dev.lock, self.dev.submitting():
                 self.dev.select()
                 overlap = (src.owner is dest.owner and src.offset < dest.offset + sz and dest.offset < src.offset + sz)
                 if overlap:
@@ -211,7 +221,7 @@ class MI355XAllocator:
             return
         # Cross-device: order after the source device's work, copy on the destination's stream.
         src_dev.synchronize()
-        with dest_dev.lock:
+        with dest_dev.lock, dest_dev.submitting(src_dev):
             dest_dev.select()
             hip.call("hipMemcpyPeerAsync", dest.address, dest_dev.ordinal, src.address, src_dev.ordinal, sz,
                      dest_dev.stream)
@@ -274,21 +284,16 @@ class MI355XProgram:
         global_size, local_size = self.validate(bufs, global_size, local_size, vals)
         if 0 in global_size:
             return 0.0 if wait else None
-        with self.dev.lock:
-            self.dev.check_failure()
+        with self.dev.lock, self.dev.submitting():
             self.dev.select()
             # timing events belong to this call only (the device retires and destroys its own)
             start, stop = (hip.event_create(), hip.event_create()) if wait else (0, 0)
-            try:
-                if wait:
-                    hip.call("hipEventRecord", start, self.dev.stream)
-                self.enqueue(bufs, global_size, local_size, vals)
-                if wait:
-                    hip.call("hipEventRecord", stop, self.dev.stream)
-                self.dev.submitted(tuple(b.owner for b in bufs))
-            except RuntimeError as exc:
-                self.dev.failure = exc
-                raise
+            if wait:
+                hip.call("hipEventRecord", start, self.dev.stream)
+            self.enqueue(bufs, global_size, local_size, vals)
+            if wait:
+                hip.call("hipEventRecord", stop, self.dev.stream)
+            self.dev.submitted(tuple(b.owner for b in bufs))
         if not wait:
             return None
         try:
@@ -346,11 +351,28 @@ class MI355XDevice:
         hip.set_device(self.ordinal)
 
     def check_failure(self) -> None:
+        """Re-raise a failed submission: the stream's contents are unknown after it."""
         if self.failure is not None:
-            raise RuntimeError(f"{self.device} submission failed") from self.failure
+            raise RuntimeError(f"{self.device} submission/transfer failed") from self.failure
+
+    @contextlib.contextmanager
+    def submitting(self, *others: "MI355XDevice"):
+        """Guard one enqueue: refuse it after an earlier failure, and keep a HIP failure raised
+        inside it as this device's (and ``others``') sticky failure."""
+        self.check_failure()
+        for dev in others:
+            dev.check_failure()
+        try:
+            yield
+        except RuntimeError as exc:
+            for dev in (self, *others):
+                if dev.failure is None:
+                    dev.failure = exc
+            raise
 
     def submitted(self, owners: tuple[_Allocation, ...], callback: Callable[[], None] | None = None) -> int:
         """Record a completion event after the work just enqueued; owners stay busy until it fires."""
+        self.check_failure()
         event = hip.event_create()
         hip.call("hipEventRecord", event, self.stream)
         for owner in owners:
