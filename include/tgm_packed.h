@@ -157,6 +157,24 @@ int tgm_gemm_w_split(const void* a, int a_dtype, int64_t m, int64_t lda, const v
                      int64_t splits, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * tgm_gemm_w_split without a workspace argument: the same kernels, the same split choice and
+ * bit-identical results, with the fp32 partials in a static array of device memory that the
+ * library holds on each GPU it runs on (tgm_gemm_w_split_noalloc_capacity() bytes, 32 MiB) from
+ * the code object's load until the process ends.  No counterpart in the reference.  It is for
+ * callers that cannot allocate device memory: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  It calls no hipMalloc, hipFree or allocating library
+ * routine.  A product whose partials exceed the capacity (splits x M x N x 4 bytes) is rejected
+ * with TGM_E_INVALID.  All calls on one GPU share its array and each call overwrites it, so
+ * calls that overlap in time on one GPU (other streams, other threads) race: the caller orders
+ * them.  The first call on each device looks up that device's address of the array
+ * (hipGetSymbolAddress); make that first call outside graph capture.
+ */
+int64_t tgm_gemm_w_split_noalloc_capacity(void);
+int tgm_gemm_w_split_noalloc(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n,
+                             int64_t k, const void* scales, int scale_dtype, int64_t block_size, void* c, int c_dtype,
+                             int64_t ldc, int64_t splits, void* stream);
+
+/*
  * tgm_gemm_w for FP4 weights whose rows interleave the gate (row 2 i) and up (row 2 i + 1)
  * projections of a SwiGLU block, with the activation in the epilogue:
  *

@@ -229,6 +229,16 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     assert K.load_library().tgm_last_error().decode().startswith("pack width")
 
 
+def test_noalloc_split_k_rejects_oversized_partials_before_any_gpu_call():
+    """The allocation-free split-K GEMM checks its partials against the static scratch size on the
+    host: 4 splits of 4096 x 4096 fp32 partials (256 MiB) exceed the 32 MiB array."""
+    lib = K.load_library()
+    assert lib.tgm_gemm_w_split_noalloc_capacity() == 32 << 20
+    with pytest.raises(ValueError, match="static scratch"):
+        K.call("tgm_gemm_w_split_noalloc", None, 12, 4096, 4096, None, 2, 4096, 4096, None, 15, 32, None, 13, 4096, 4,
+               None)
+
+
 def test_header_enums_match_binding():
     text = HEADER.read_text()
     for name, value in K.FORMAT_IDS.items():

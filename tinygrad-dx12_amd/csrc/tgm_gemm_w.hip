@@ -24,6 +24,8 @@
 // packed W panel (256 rows x 96 B for FP6, 64 B for FP4) and the step's scale dwords are
 // loaded straight into a double-buffered LDS stage (buffer_load ... lds, zero-filled past
 // M and N); the loads of step s + 2 run while step s + 1 computes.
+#include <mutex>
+
 #include "tgm_mfma_common.h"
 
 namespace tgm {
@@ -588,6 +590,66 @@ extern "C" int tgm_gemm_w_split(const void* a, int a_dtype, int64_t m, int64_t l
                 "split-K needs a 16-byte aligned workspace of tgm_gemm_w_split_workspace() bytes");
   return gemm_w_split_run(a, a_dtype, m, lda, w, fmt, n, k, scales, scale_dtype, block_size, c, c_dtype, ldc, eff,
                           (float*)workspace, stream, "tgm_gemm_w_split");
+}
+
+// ---- tgm_gemm_w_split without a caller workspace (for callers that cannot allocate).
+//
+// The fp32 partials go to `scratch`, a fixed array in device memory that every GPU the library
+// runs on holds once, from the code object's load until the process ends.  Its device address
+// differs per GPU and is only known to the runtime: host code never passes `scratch` itself (in
+// host code that name is a stand-in, not a device address) but the address hipGetSymbolAddress
+// returns for the current device, looked up on the first call on each device and kept.  Each
+// call overwrites every partial it later reads (every split writes its whole [M][N] slab), so
+// nothing is cleared between calls.  All calls on one GPU share its array: calls that overlap in
+// time on one GPU (two streams, two threads) race on it and must be ordered by the caller.
+static constexpr int64_t kScratchBytes = int64_t(32) << 20;  // 32 MiB
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+static constexpr int kMaxDevices = 64;
+static std::mutex scratch_lock;
+static float* scratch_ptr[kMaxDevices];
+
+// The current device's address of `scratch` (nullptr with the error text set on failure).
+static float* scratch_address() {
+  int device = -1;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
+    set_error("tgm_gemm_w_split_noalloc: no usable current HIP device (%d)", device);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> guard(scratch_lock);
+  if (!scratch_ptr[device]) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr) {
+      set_error("tgm_gemm_w_split_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s (%d)", device,
+                hipGetErrorString(err), (int)err);
+      return nullptr;
+    }
+    scratch_ptr[device] = (float*)ptr;
+  }
+  return scratch_ptr[device];
+}
+
+extern "C" int64_t tgm_gemm_w_split_noalloc_capacity(void) { return kScratchBytes; }
+
+extern "C" int tgm_gemm_w_split_noalloc(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt,
+                                        int64_t n, int64_t k, const void* scales, int scale_dtype, int64_t block_size,
+                                        void* c, int c_dtype, int64_t ldc, int64_t splits, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(splits >= 1 && splits <= 64, "splits must be in [1, 64]");
+  const int64_t eff = effective_splits(m, n, k, splits);
+  if (eff == 1)
+    return gemm_w_impl(a, a_dtype, m, lda, w, fmt, n, k, scales, scale_dtype, block_size, c, c_dtype, ldc, 1, nullptr,
+                       stream);
+  const int64_t need = tgm_gemm_w_split_workspace(m, n, eff);
+  TGM_CHECK_ARG(need <= kScratchBytes,
+                "tgm_gemm_w_split_noalloc: %lld split(s) of %lld x %lld fp32 partials need %lld bytes, more than the "
+                "%lld-byte static scratch; use fewer splits or tgm_gemm_w_split with a workspace",
+                (long long)eff, (long long)m, (long long)n, (long long)need, (long long)kScratchBytes);
+  float* part = scratch_address();
+  if (!part) return (int)hipErrorInvalidSymbol;
+  return gemm_w_split_run(a, a_dtype, m, lda, w, fmt, n, k, scales, scale_dtype, block_size, c, c_dtype, ldc, eff,
+                          part, stream, "tgm_gemm_w_split_noalloc");
 }
 
 extern "C" int tgm_gemm_w_swiglu(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n,

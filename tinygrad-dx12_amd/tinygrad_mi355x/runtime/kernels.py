@@ -45,6 +45,8 @@ _SIGNATURES = {
     "tgm_gemm_w_swiglu": (_P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _P, _INT, _I64, _P, _INT, _I64, _P),
     "tgm_gemm_w_split": (_P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _P, _INT, _I64, _P, _INT, _I64, _I64, _P, _I64,
                          _P),
+    "tgm_gemm_w_split_noalloc": (_P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _P, _INT, _I64, _P, _INT, _I64, _I64,
+                                 _P),
     "tgm_gemm_mx": (_P, _INT, _P, _I64, _P, _INT, _P, _I64, _I64, _P, _INT, _I64, _P),
     "tgm_gemm_plain": (_P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _I64, _I64, _I64, _INT, _P),
     "tgm_quantize_mx": (_P, _INT, _I64, _I64, _INT, _I64, _P, _P, _P),
@@ -69,7 +71,7 @@ _SIGNATURES = {
     "tgm_dec_argmax": (_P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _P),
 }
 EXPORTS = ("tgm_abi_version", "tgm_last_error", "tgm_dec_attention_workspace", "tgm_gemm_w_split_workspace",
-           *_SIGNATURES)
+           "tgm_gemm_w_split_noalloc_capacity", *_SIGNATURES)
 
 
 def library_path() -> Path:
@@ -104,6 +106,8 @@ def load_library() -> ctypes.CDLL:
         lib.tgm_dec_attention_workspace.restype = _I64
         lib.tgm_gemm_w_split_workspace.argtypes = (_I64, _I64, _I64)
         lib.tgm_gemm_w_split_workspace.restype = _I64
+        lib.tgm_gemm_w_split_noalloc_capacity.argtypes = ()
+        lib.tgm_gemm_w_split_noalloc_capacity.restype = _I64
         _lib = lib
         return lib
 
