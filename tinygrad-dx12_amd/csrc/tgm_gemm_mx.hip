@@ -19,11 +19,12 @@
 //
 // Workgroup: 256 x 256 output tile, eight waves in 4 x 2, each wave 64 x 128 = 2 x 4 MFMA
 // tiles (128 fp32 accumulators per lane, two waves per SIMD).  K advances in steps of 256
-// elements (128 bytes per row and operand): each step's A and B panels (32 KB each) and
-// E8M0 scales are loaded straight from global memory into a double-buffered LDS tile
-// (buffer_load ... lds), XOR-swizzled so the 32 rows one ds_read_b128 touches fall in
-// distinct banks.  The loads of step s + 2 run while step s + 1's MFMAs do.  Tiles are
-// mapped XCD-aware (tile_of).
+// elements (128 bytes per row and operand): each step's A and B panels (32 KB each) are
+// loaded straight from global memory into a double-buffered LDS tile (buffer_load ... lds),
+// XOR-swizzled so the 32 rows one ds_read_b128 touches fall in distinct banks; the E8M0
+// scales take the same route four steps at a time into their own double buffer (160 KB of
+// LDS in all).  The loads of step s + 2 run while step s + 1's MFMAs do.  Tiles are mapped
+// XCD-aware (tile_of).
 #include "tgm_mfma_common.h"
 
 namespace tgm {
@@ -32,8 +33,11 @@ constexpr int kBM = 256, kBN = 256;  // output tile
 constexpr int kBK = 256;             // K elements per step
 constexpr int kRowBytes = kBK / 2;   // FP4 bytes per row and step
 constexpr int kPanel = kBM * kRowBytes;          // one operand, one buffer (32 KB)
-constexpr int kScalePanel = kBM * (kBK / 32);    // E8M0 bytes of one operand per step (2 KB)
-constexpr int kBuffer = 2 * kPanel + 2 * kScalePanel;  // A, B, A scales, B scales (68 KB)
+constexpr int kBuffer = 2 * kPanel;              // A and B panels of one step (64 KB)
+constexpr int kBatchSteps = 4;                   // steps per batch of E8M0 scales
+constexpr int kBatchRow = kBatchSteps * (kBK / 32);  // scale bytes of one row per batch (32)
+constexpr int kBatch = 2 * kBM * kBatchRow;      // A and B scales of one batch (16 KB)
+constexpr int kLds = 2 * kBuffer + 2 * kBatch;   // two step buffers, two scale batches: 160 KB
 constexpr int kGroupM = 8;
 constexpr int kWavesM = 4, kWavesN = 2;  // wave grid of the launched kernel
 
@@ -42,12 +46,12 @@ template <int WM, int WN>
 __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __restrict__ a, const uint8_t* __restrict__ sa,
                                                    const uint8_t* __restrict__ b, const uint8_t* __restrict__ sb,
                                                    int M, int N, int K, void* __restrict__ c, int cdt, int64_t ldc) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kBuffer];  // two buffers
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   constexpr int NW = WM * WN, FA = 8 / WM, FB = 8 / WN;  // 32-row fragments per wave
-  constexpr int SW = NW < 8 ? NW : 8;                     // waves that load scales
-  constexpr int NI = 32 / NW, NJ = 8 / SW;                // panel / scale loads per wave and operand
+  constexpr int NI = 32 / NW;                             // panel loads per wave, operand and step
+  static_assert(NW == 4 || NW == 8, "scale batches are loaded by 4 or 8 waves");
   const int wm = wave / WN, wn = wave % WN;
   const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
   int tm, tn;
@@ -76,31 +80,32 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __res
   const int lrow = wave * (256 / NW) + (lane >> 3);  // + 8 i
   const unsigned lcol = (unsigned)(((lane & 7) ^ (lane >> 4)) * 16);
   const unsigned voa = (unsigned)(m0 + lrow) * kb, vob = (unsigned)(n0 + lrow) * kb;
-  // Scales take the same route: step s's 8 E8M0 bytes of row r land at byte r * 8 of the
-  // buffer's scale panel, 4 bytes per lane (two lanes per row, 32 rows per instruction;
-  // with SW = min(NW, 8) loading waves, wave w < SW loads rows [256 w / SW, 256 (w + 1) / SW)
-  // of both operands).
-  const int srow_l = (wave % SW) * (256 / SW) + (lane >> 1);  // + 32 j
-  const unsigned vsa = (unsigned)(m0 + srow_l) * kblk + (unsigned)((lane & 1) * 4);
-  const unsigned vsb = (unsigned)(n0 + srow_l) * kblk + (unsigned)((lane & 1) * 4);
   const unsigned lds_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds;
-  // One load instruction of step s into buffer buf: piece 2i / 2i + 1 is A / B load i,
-  // piece 2 NI + 2j / + 1 is A / B scale load j.
-  constexpr int NP = 2 * NI + 2 * NJ;
+  // One panel load instruction of step s into buffer buf: piece 2i / 2i + 1 is A / B load i.
+  constexpr int NP = 2 * NI;
   auto dma_piece = [&](int s, int buf, int p) __attribute__((always_inline)) {
-    if (p < 2 * NI) {
-      const int i = p >> 1;
-      const unsigned step_off = (unsigned)(8 * i) * kb + (unsigned)(s * kRowBytes);  // uniform
-      const unsigned col = lcol ^ (unsigned)((i & 1) * 64);
-      const unsigned la = lds_base + (unsigned)(buf * kBuffer + (p & 1) * kPanel + wave * (2048 / NW) * 16 + i * 1024);
-      lds_dma16((p & 1) ? rb : ra, la, ((p & 1) ? vob : voa) + col + step_off);
-    } else {
-      if (NW > SW && wave >= SW) return;
-      const int q = p - 2 * NI, j = q >> 1;
-      const unsigned step_off = (unsigned)(32 * j) * kblk + (unsigned)(s * 8);  // uniform
-      const unsigned ls = lds_base + (unsigned)(buf * kBuffer + 2 * kPanel + (q & 1) * kScalePanel +
-                                                (wave % SW) * (256 / SW) * 8 + j * 256);
-      lds_dma4((q & 1) ? rsb : rsa, ls, ((q & 1) ? vsb : vsa) + step_off);
+    const int i = p >> 1;
+    const unsigned step_off = (unsigned)(8 * i) * kb + (unsigned)(s * kRowBytes);  // uniform
+    const unsigned col = lcol ^ (unsigned)((i & 1) * 64);
+    const unsigned la = lds_base + (unsigned)(buf * kBuffer + (p & 1) * kPanel + wave * (2048 / NW) * 16 + i * 1024);
+    lds_dma16((p & 1) ? rb : ra, la, ((p & 1) ? vob : voa) + col + step_off);
+  };
+  // Scales arrive in batches of kBatchSteps steps: batch b's 32 E8M0 bytes of row r (steps
+  // 4b .. 4b + 3) land at byte r * 32 of scale buffer b & 1 (A rows, then B rows), two 16-byte
+  // lanes per row, 32 rows per instruction.  Fetching a row's 8 bytes of one step at a time
+  // costs a cache-line access per row and step -- as many as the operand panels themselves --
+  // and measured half again the panels' load time; batches of four cut that to a quarter.
+  // Bytes past the end of a row (K not a multiple of 1024) belong to steps that do not exist.
+  const unsigned vbat = (unsigned)((lane & 1) * 16);
+  auto issue_batch = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 8 / NW; ++i) {
+      const int g = wave * (8 / NW) + i;  // rows [32 g, 32 g + 32)
+      const int r = 32 * g + (lane >> 1);
+      const unsigned boff = (unsigned)(b * kBatchRow) + vbat;
+      const unsigned la = lds_base + (unsigned)(2 * kBuffer + (b & 1) * kBatch + g * 1024);
+      lds_dma16(rsa, la, (unsigned)(m0 + r) * kblk + boff);
+      lds_dma16(rsb, la + kBM * kBatchRow, (unsigned)(n0 + r) * kblk + boff);
     }
   };
   auto dma_pieces = [&](int s, int buf, int p0, int p1) __attribute__((always_inline)) {
@@ -134,10 +139,11 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __res
     if (t < FA) f.a[t < FA ? t : 0] = *(const u32x4*)(la + fa_row + col + t * 32 * kRowBytes);
     else f.b[t < FA ? 0 : t - FA] = *(const u32x4*)(la + kPanel + fb_row + col + (t - FA) * 32 * kRowBytes);
   };
-  auto scale_item = [&](int buf, int t) __attribute__((always_inline)) {
-    const unsigned char* ls = lds + buf * kBuffer + 2 * kPanel;
-    if (t < FA) scl_a[t < FA ? t : 0] = *(const u32x2*)(ls + (wm * FA * 32 + t * 32 + (lane & 31)) * 8);
-    else scl_b[t < FA ? 0 : t - FA] = *(const u32x2*)(ls + kScalePanel + (wn * FB * 32 + (t - FA) * 32 + (lane & 31)) * 8);
+  auto scale_item = [&](int sn, int t) __attribute__((always_inline)) {  // scales of step sn
+    const unsigned char* ls = lds + 2 * kBuffer + ((sn / kBatchSteps) & 1) * kBatch + (sn % kBatchSteps) * 8;
+    if (t < FA) scl_a[t < FA ? t : 0] = *(const u32x2*)(ls + (wm * FA * 32 + t * 32 + (lane & 31)) * kBatchRow);
+    else scl_b[t < FA ? 0 : t - FA] =
+        *(const u32x2*)(ls + kBM * kBatchRow + (wn * FB * 32 + (t - FA) * 32 + (lane & 31)) * kBatchRow);
   };
   auto mfmas = [&](const Frags& f, int u, auto&& hook) __attribute__((always_inline)) {
     // scale of block 2u + half of this step: byte (2u + half) % 4 of word (2u + half) / 4
@@ -166,13 +172,13 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __res
   //   wait for this wave's loads of step s + 1, barrier: step s + 1 is complete in the other
   //       buffer and every read of this buffer has been issued and completed
   //   u3 (f1): read the scale words and f0 <- u0 of step s + 1; first half of step s + 2's
-  //       loads (into this buffer)
+  //       loads (into this buffer); on steps s = 4b, scale batch b + 1
   // Each piece of memory work sits between scheduling barriers so that the order holds.  Past
   // the last step the loads re-read step nsteps - 1 into a buffer nobody reads again; the body
   // has no branches.
   constexpr int kMaxItems = 2 * (FA + FB) + NP;
-  auto substep = [&](const Frags& fc, int u, Frags& fn, int rbuf, int ru, bool scales, int ds, int dbuf, int p0,
-                     int p1) __attribute__((always_inline)) {
+  auto substep = [&](const Frags& fc, int u, Frags& fn, int rbuf, int ru, bool scales, int sn, int ds, int dbuf,
+                     int p0, int p1) __attribute__((always_inline)) {
     const int nr = (FA + FB) * (scales ? 2 : 1);
     const int ni = nr + (p1 - p0);
     mfmas(fc, u, [&](int idx) __attribute__((always_inline)) {
@@ -182,7 +188,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __res
           __builtin_amdgcn_sched_barrier(0);
           if (it >= nr) dma_piece(ds, dbuf, p0 + it - nr);
           else if (!scales) read_item(fn, rbuf, ru, it);
-          else if (it < FA + FB) scale_item(rbuf, it);  // scales first: the next substep starts with them
+          else if (it < FA + FB) scale_item(sn, it);  // scales first: the next substep starts with them
           else read_item(fn, rbuf, ru, it - (FA + FB));
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -190,6 +196,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __res
     });
   };
   const int s1 = nsteps > 1 ? 1 : 0;
+  issue_batch(0);
   dma_pieces(0, 0, 0, NP);
   dma_pieces(s1, 1, 0, NP / 2);
   wait_lds_dma();
@@ -207,19 +214,34 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __res
     read_item(f0, 0, 0, t);
   }
   __builtin_amdgcn_sched_barrier(0);
-  for (int s = 0; s < nsteps; ++s) {
-    const int cur = s & 1;
+  // One step; ``batch`` (a literal at every call) adds the scale batch load.  The loop is
+  // unrolled by the batch length so that the batch load needs no branch: a branch in the
+  // body splits the schedule and spilled half the accumulators.
+  auto step = [&](int s, int cur, bool batch) __attribute__((always_inline)) {
     const int s1n = s + 1 < nsteps ? s + 1 : nsteps - 1;
     const int s2 = s + 2 < nsteps ? s + 2 : nsteps - 1;
-    substep(f0, 0, f1, cur, 1, false, s1n, cur ^ 1, NP / 2, NP);
-    substep(f1, 1, f0, cur, 2, false, 0, 0, 0, 0);
-    substep(f0, 2, f1, cur, 3, false, 0, 0, 0, 0);
+    substep(f0, 0, f1, cur, 1, false, 0, s1n, cur ^ 1, NP / 2, NP);
+    substep(f1, 1, f0, cur, 2, false, 0, 0, 0, 0, 0);
+    substep(f0, 2, f1, cur, 3, false, 0, 0, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    wait_lds_dma();  // this wave's loads of step s + 1
+    wait_lds_dma();  // this wave's loads of step s + 1 (and of a scale batch issued at step s - 1)
     __syncthreads();
-    substep(f1, 3, f0, cur ^ 1, 0, true, s2, cur, 0, NP / 2);
+    substep(f1, 3, f0, cur ^ 1, 0, true, s + 1, s2, cur, 0, NP / 2);
     __builtin_amdgcn_sched_barrier(0);
+    // Batch b + 1 goes to the buffer batch b - 1 used; its last scale reads (step 4b - 1's, in
+    // step 4b - 2) are behind this step's barrier.  It is complete after the next step's wait.
+    if (batch) issue_batch(s / kBatchSteps + 1);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  static_assert(kBatchSteps == 4, "the step loop is unrolled by four");
+  int s = 0;
+  for (; s + kBatchSteps <= nsteps; s += kBatchSteps) {
+    step(s, 0, true);
+    step(s + 1, 1, false);
+    step(s + 2, 0, false);
+    step(s + 3, 1, false);
   }
+  for (; s < nsteps; ++s) step(s, s & 1, false);  // the last batch was issued by the loop above
   wait_lds_dma();
   __syncthreads();  // the epilogue reuses the operand LDS
 
