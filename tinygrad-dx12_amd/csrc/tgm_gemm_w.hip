@@ -40,8 +40,9 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 constexpr int kWM = 128, kWN = 256, kWK = 128;  // output tile and K step
 constexpr int kAPanel = kWM * kWK * 2;           // 32 KB of bf16 A per stage
 constexpr int kWPanelMax = kWN * 96;             // 24 KB of packed W (FP6) per stage
-constexpr int kWScales = kWN * 4;                // one E8M0 dword (4 blocks) per W row per stage
-constexpr int kWStage = kAPanel + kWPanelMax + kWScales;
+constexpr int kWStage = kAPanel + kWPanelMax;
+constexpr int kWBatchSteps = 4;                  // steps per batch of E8M0 scales
+constexpr int kWBatch = kWN * 4 * kWBatchSteps;  // one E8M0 dword per W row and step (4 KB)
 constexpr int kWGroupM = 8;
 
 template <int FMT>
@@ -92,7 +93,7 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
                                                  int kps, float* __restrict__ part) {
   using T = GemmWTraits<FMT>;
   constexpr int FA = 2, FB = 2;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kWStage];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kWStage + 2 * kWBatch];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;
@@ -136,7 +137,16 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
       vow[q] = (unsigned)(n0 + f / 96) * kbw + (unsigned)(f % 96);
     }
   }
-  const unsigned vos = (unsigned)(n0 + 64 * (wave & 3) + lane) * kblk;  // scale dword of row, waves 0..3
+  // E8M0 scales arrive four steps at a time: batch b (local steps 4b .. 4b + 3) puts the 16 scale
+  // bytes of W row r at byte 16 r of scale buffer b & 1, one 16-byte lane per row, waves 0..3
+  // loading 64 rows each.  A row's scale bytes of one step are one dword: fetching them step by
+  // step costs a cache-line access per row and step, as many as the A panel's.  Bytes past a
+  // row's end (the last batch of a K range) belong to steps that do not exist.
+  const unsigned vos = (unsigned)(n0 + 64 * (wave & 3) + lane) * kblk + (unsigned)s_begin * 4u;
+  auto issue_batch = [&](int b) __attribute__((always_inline)) {
+    if (SCALED && wave < 4)
+      lds_dma16(rs, lds_base + (unsigned)(2 * kWStage + (b & 1) * kWBatch + wave * 1024), vos + (unsigned)b * 16u);
+  };
 
   auto dma_step = [&](int s, int buf) __attribute__((always_inline)) {
     const unsigned st = lds_base + (unsigned)(buf * kWStage);
@@ -147,7 +157,6 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
     for (int q = 0; q < NWL; ++q)
       if (NWL * wave + q < T::kPanelLoads)
         lds_dma16(rw, st + kAPanel + (unsigned)(NWL * wave + q) * 1024u, vow[q] + sk * (unsigned)T::kRow);
-    if (SCALED && wave < 4) lds_dma4(rs, st + kAPanel + kWPanelMax + (unsigned)wave * 256u, vos + sk * 4u);
   };
 
   // ---- fragment reads
@@ -164,9 +173,9 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
     }
   };
   bf16x8 bfr[FB][8];
-  auto read_decode_b = [&](int buf) __attribute__((always_inline)) {
+  auto read_decode_b = [&](int buf, int s) __attribute__((always_inline)) {
     const unsigned char* pw = lds + buf * kWStage + kAPanel;
-    const unsigned* ps = (const unsigned*)(lds + buf * kWStage + kAPanel + kWPanelMax);
+    const unsigned* ps = (const unsigned*)(lds + 2 * kWStage + ((s / kWBatchSteps) & 1) * kWBatch) + (s % kWBatchSteps);
 #pragma unroll
     for (int t = 0; t < FB; ++t) {
       const int row = b_row + 32 * t;
@@ -181,7 +190,7 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
 #pragma unroll
         for (int q = 0; q < 3; ++q) raw[q] = *(const u32x4*)(pw + row * 96 + 48 * half + 16 * q);
       }
-      const unsigned sbits = SCALED ? ps[row] >> (16 * half) : 0x7F7Fu;  // blocks 2 h, 2 h + 1
+      const unsigned sbits = SCALED ? ps[4 * row] >> (16 * half) : 0x7F7Fu;  // blocks 2 h, 2 h + 1
       decode64<FMT>(raw, sbits, bfr[t]);
     }
   };
@@ -193,6 +202,7 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
     for (int j = 0; j < FB; ++j) acc[i][j] = f32x16{};
 
   const int s1 = nsteps > 1 ? 1 : 0;
+  issue_batch(0);
   dma_step(0, 0);
   dma_step(s1, 1);
   wait_lds_dma();
@@ -200,7 +210,7 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
   for (int s = 0; s < nsteps; ++s) {
     const int cur = s & 1;
     const int s2 = s + 2 < nsteps ? s + 2 : nsteps - 1;
-    read_decode_b(cur);
+    read_decode_b(cur, s);
     bf16x8 af[2][FA];
     read_a(cur, 0, af[0]);
 #pragma unroll
@@ -212,9 +222,11 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
         for (int tb = 0; tb < FB; ++tb)
           acc[ta][tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[j & 1][ta], bfr[tb][j], acc[ta][tb], 0, 0, 0);
     }
-    wait_lds_dma();  // this wave's loads of step s + 1
+    wait_lds_dma();  // this wave's loads of step s + 1 (and a scale batch issued at step s - 1)
     __syncthreads();  // every wave is done with this buffer; step s + 1 is complete in the other
     dma_step(s2, cur);
+    // batch b + 1 replaces batch b - 1, last read at step 4b - 1; complete after the next wait
+    if (s % kWBatchSteps == 0) issue_batch(s / kWBatchSteps + 1);
   }
   wait_lds_dma();
   __syncthreads();  // the epilogue reuses the LDS
