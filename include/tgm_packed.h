@@ -189,18 +189,42 @@ int tgm_gemm_w_swiglu(const void* a, int a_dtype, int64_t m, int64_t lda, const 
                       void* stream);
 
 /*
- * Kernel family 2 -- block-scaled FP4/FP6 x FP4/FP6 GEMM on gfx950 scaled MFMA
- * (replaces linalg_source for two packed operands, renderer/linalg.py:38-124;
- * the reference decodes both to fp32 first, dx12.py:115-138).
+ * Kernel family 2 -- FP4/FP6 x FP4/FP6 GEMM on gfx950 scaled MFMA
+ * (replaces linalg_source for two packed operands, renderer/linalg.py:38-124; the
+ * reference decodes both to their common intermediate first -- FP8 when both are
+ * unscaled, fp32 when either is scaled -- dx12.py:115-138).
  *
  *   C[m, n] = sum_k deq(A)[m, k] * deq(B)[n, k]
  *
- * A packed [M, K], B packed [N, K], both K contiguous with E8M0 scales per 32
- * K-elements ([M, K/32] and [N, K/32]).  C (BF16, F16 or F32) row stride ldc.
+ * A packed [M, K], B packed [N, K] (FP4 E2M1, FP6 E2M3 or FP6 E3M2), both K contiguous,
+ * each with E8M0 scales per 32 K-elements ([M, K/32] / [N, K/32]) or NULL (unscaled:
+ * every scale 1).  C (BF16, F16 or F32) row stride ldc; fp32 accumulation.  FP4 x FP4
+ * with both scales and K a multiple of 256 runs the 256 x 256-tile FP4 kernel; every
+ * other pair needs K a multiple of 128.  INT4 / UINT4 and FP6 E3M2 x E3M2 (whose MFMA
+ * sums are not exact on gfx950) give TGM_E_UNSUPPORTED.
  */
 int tgm_gemm_mx(const void* a, int a_fmt, const void* a_scales, int64_t m,
                 const void* b, int b_fmt, const void* b_scales, int64_t n, int64_t k,
                 void* c, int c_dtype, int64_t ldc, void* stream);
+
+/*
+ * Kernel family 2 -- ordinary FP8 x FP8 GEMM: both operands decoded to bf16 in registers (every
+ * FP8 value is exact in bf16) on the bf16 MFMA of tgm_gemm_dense (the reference's LinAlg
+ * lowering takes FP8 operands as they are, renderer/linalg.py:12-13, through the
+ * scheduled-matmul rewrite, codegen/matmul.py:51-128).
+ *
+ *   C[m, n] = (sum_k A[m, k] * B[n, k]) * scale_a * scale_b
+ *
+ * A [M, K] and B [N, K] of dtype FP8E4M3 or FP8E5M2 (the two may differ), K contiguous, row
+ * strides lda / ldb in elements (multiples of 16, rows 16-byte aligned); scale_a / scale_b are
+ * optional fp32 device scalars (NULL = 1; torch._scaled_mm's per-tensor scales) applied to the
+ * fp32 sum before it is rounded to C (BF16, F16 or F32, row stride ldc).  Products are exact in
+ * fp32, accumulation fp32.  K must be a multiple of 128; otherwise TGM_E_UNSUPPORTED.  (The
+ * gfx950 FP8 MFMA is not used: it sums at ~2e-4 of sum |products|, measured.)
+ */
+int tgm_gemm_fp8(const void* a, int a_dtype, int64_t lda, int64_t m, const void* b, int b_dtype, int64_t ldb,
+                 int64_t n, int64_t k, const float* scale_a, const float* scale_b, void* c, int c_dtype,
+                 int64_t ldc, void* stream);
 
 /*
  * Kernel family 2 -- ordinary bf16 x bf16 or f16 x f16 GEMM on MFMA (the reference's LinAlg
@@ -237,6 +261,10 @@ int tgm_gemm_dense_batched(const void* a, int a_dtype, int64_t m, int64_t lda, i
  */
 int tgm_transpose16(const void* in, int64_t rows, int64_t cols, int64_t ld_in, void* out, int64_t ld_out,
                     void* stream);
+
+/* The same for 8-bit elements: stages a row-major FP8 [K, N] operand as [N, K] for tgm_gemm_fp8. */
+int tgm_transpose8(const void* in, int64_t rows, int64_t cols, int64_t ld_in, void* out, int64_t ld_out,
+                   void* stream);
 
 /*
  * Exact-width GEMM for operands the families above do not cover (the reference's

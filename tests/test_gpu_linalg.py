@@ -607,6 +607,86 @@ def test_gemm_mx_fp4_full_size_sampled(dev, mnk):
     assert O.max_rel_err(bf16_np(c)[rows], ref) <= TOL
 
 
+MX_PAIRS = [(fa, fb) for fa in ("fp4_e2m1", "fp6_e2m3", "fp6_e3m2") for fb in ("fp4_e2m1", "fp6_e2m3", "fp6_e3m2")]
+
+
+@pytest.mark.parametrize("fa,fb", MX_PAIRS)
+@pytest.mark.parametrize("scaled", [(True, True), (True, False), (False, True), (False, False)])
+def test_gemm_mx_every_fp4_fp6_pair(dev, fa, fb, scaled):
+    """Every FP4 / FP6 pair, each side E8M0 block-32 scaled or unscaled, on the native scaled MFMA
+    (scope="Wave" raises instead of falling back): ragged 256 x 128 tiles, K = 640 (five steps,
+    two scale batches)."""
+    m, n, k = 300, 200, 640
+    rng = np.random.default_rng(MX_PAIRS.index((fa, fb)) * 4 + 2 * scaled[0] + scaled[1])
+    a, deq_a = make_weight(dev, fa, m, k, "e8m0" if scaled[0] else None, rng)
+    b, deq_b = make_weight(dev, fb, n, k, "e8m0" if scaled[1] else None, rng)
+    c = matmul_nt(a, b, scope="Wave", dtype=torch.float32)
+    assert c.shape == (m, n)
+    assert O.max_rel_err(c.cpu().numpy(), deq_a @ deq_b.T) <= TOL
+
+
+@pytest.mark.parametrize("fa,fb", [("fp6_e2m3", "fp6_e3m2"), ("fp4_e2m1", "fp6_e3m2"), ("fp6_e3m2", "fp4_e2m1")])
+def test_gemm_mx_unscaled_pair_is_exact(dev, fa, fb):
+    """Two unscaled packed operands (the reference's FP8 intermediate, dx12.py:115-138) with one
+    nonzero code per row of A: every output is one exact product, so the result is bit-exact."""
+    m, n, k = 256, 128, 256
+    rng = np.random.default_rng(5)
+    b, deq_b = make_weight(dev, fb, n, k, None, rng)
+    cols = rng.choice(k, m)
+    bits = FORMATS[fa][0]
+    codes = np.zeros((m, k), np.uint8)
+    codes[np.arange(m), cols] = rng.integers(1, 1 << bits, m)
+    a = PackedTensor(torch.from_numpy(O.pack_codes(codes, bits)).to(dev), fa, (m, k))
+    deq_a = O.dequant_f64(O.pack_codes(codes, bits), fa, (m, k), None, 32)
+    c = matmul_nt(a, b, scope="Wave")
+    assert c.dtype is torch.float32
+    assert np.array_equal(c.cpu().numpy(), (deq_a @ deq_b.T).astype(np.float32))
+
+
+@pytest.mark.parametrize("mnk", [(128, 128, 128), (257, 130, 384), (1024, 1024, 1024)])
+def test_gemm_mx_fp4_pairs_with_k_a_multiple_of_128(dev, mnk):
+    """FP4 x FP4 with both scales and K not a multiple of 256 takes the general kernel."""
+    m, n, k = mnk
+    rng = np.random.default_rng(k)
+    a, deq_a = make_weight(dev, "fp4_e2m1", m, k, "e8m0", rng)
+    b, deq_b = make_weight(dev, "fp4_e2m1", n, k, "e8m0", rng)
+    c = matmul_nt(a, b, scope="Wave", dtype=torch.bfloat16)
+    assert O.max_rel_err(bf16_np(c), deq_a @ deq_b.T) <= TOL
+
+
+def _fp8(dev, shape, dt, rng):
+    x = torch.from_numpy(rng.standard_normal(shape).astype(np.float32) * 4).to(dev)
+    return x.to(dt)
+
+
+@pytest.mark.parametrize("da,db", [(torch.float8_e4m3fn, torch.float8_e4m3fn), (torch.float8_e5m2, torch.float8_e5m2),
+                                   (torch.float8_e4m3fn, torch.float8_e5m2)])
+@pytest.mark.parametrize("mnk", [(300, 200, 640), (64, 1100, 128)])
+def test_gemm_fp8_parity(dev, da, db, mnk):
+    """Ordinary FP8 operands on the scaled MFMA with unit scales: matmul_nt binds both K-last;
+    matmul stages a row-major right operand with tgm_transpose8."""
+    m, n, k = mnk
+    rng = np.random.default_rng(m + n + k)
+    a, b = _fp8(dev, (m, k), da, rng), _fp8(dev, (n, k), db, rng)
+    ref = a.float().cpu().numpy().astype(np.float64) @ b.float().cpu().numpy().astype(np.float64).T
+    c = matmul_nt(a, b, scope="Wave")
+    assert c.dtype is torch.float32 and O.max_rel_err(c.cpu().numpy(), ref) <= TOL
+    rowmajor = torch.empty((k, n), dtype=db, device=dev)
+    rowmajor.view(torch.uint8).copy_(b.view(torch.uint8).t())
+    c2 = matmul(a, rowmajor, scope="Wave", dtype=torch.bfloat16)
+    assert O.max_rel_err(bf16_np(c2), ref) <= TOL
+
+
+def test_gemm_fp8_per_tensor_scales(dev):
+    """Per-tensor fp32 factors (torch._scaled_mm's) multiply the fp32 sums before rounding."""
+    rng = np.random.default_rng(3)
+    a, b = _fp8(dev, (256, 256), torch.float8_e4m3fn, rng), _fp8(dev, (128, 256), torch.float8_e4m3fn, rng)
+    sa, sb = torch.tensor(0.125, device=dev), torch.tensor(3.0, device=dev)
+    c = linalg.dense_matmul_nt(a, b, torch.float32, sa, sb)
+    ref = a.float().cpu().numpy().astype(np.float64) @ b.float().cpu().numpy().astype(np.float64).T * 0.375
+    assert O.max_rel_err(c.cpu().numpy(), ref) <= TOL
+
+
 def test_failures_are_cached_per_candidate(dev, monkeypatch):
     """A native rejection (an MX pair whose K is not a whole number of 32-element blocks: the
     block-scaled MFMA GEMM has no kernel for it) is cached under its exact candidate key: the

@@ -229,6 +229,54 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     assert K.load_library().tgm_last_error().decode().startswith("pack width")
 
 
+def test_scaled_mfma_routes_reject_unsupported_pairs_without_a_gpu():
+    """tgm_gemm_mx rejects integer codes and E3M2 x E3M2 (whose gfx950 MFMA sums are not exact);
+    tgm_gemm_fp8 takes only FP8 dtypes.  All before any launch."""
+    fmt = K.FORMAT_IDS
+    with pytest.raises(K.UnsupportedKernel, match="not integers"):
+        K.call("tgm_gemm_mx", 16, fmt["int4"], None, 64, 16, fmt["fp4_e2m1"], None, 64, 128, 16, 13, 64, None)
+    with pytest.raises(K.UnsupportedKernel, match="E3M2 x E3M2"):
+        K.call("tgm_gemm_mx", 16, fmt["fp6_e3m2"], None, 64, 16, fmt["fp6_e3m2"], None, 64, 128, 16, 13, 64, None)
+    with pytest.raises(K.UnsupportedKernel, match="multiple of 128"):
+        K.call("tgm_gemm_mx", 16, fmt["fp6_e2m3"], None, 64, 16, fmt["fp4_e2m1"], None, 64, 96, 16, 13, 64, None)
+    with pytest.raises(ValueError, match="FP8 E4M3 / E5M2"):
+        K.call("tgm_gemm_fp8", 16, 12, 128, 64, 16, 12, 128, 64, 128, None, None, 16, 13, 64, None)
+    with pytest.raises(K.UnsupportedKernel, match="multiple of 128"):
+        K.call("tgm_gemm_fp8", 16, 9, 96, 64, 16, 10, 96, 64, 96, None, None, 16, 13, 64, None)
+
+
+def test_matrix_routing_table():
+    """Static kernel choice (the analogue of the reference's LinAlg capability query,
+    linalg.py:90-133): every FP4 / FP6 pair, scaled (E8M0 / 32) or not, takes the scaled MFMA;
+    integer codes and non-E8M0 scales do not; FP8 tensors take the FP8 GEMM."""
+    from tinygrad_mi355x.codegen.linalg import _dense_kernel, choose_matrix
+    from tinygrad_mi355x.renderer.linalg import GEMM_DENSE, GEMM_FP8, GEMM_MX
+
+    def packed(fmt, scales):
+        n, k = 4, 64
+        data = u8([0] * (n * k * FORMATS[fmt][0] // 8))
+        sc = None if scales is None else torch.ones(n, k // 32, dtype=scales)
+        return PackedTensor(data, fmt, (n, k), sc, 32)
+
+    f32 = torch.float32
+    for fa in ("fp4_e2m1", "fp6_e2m3", "fp6_e3m2"):
+        for fb in ("fp4_e2m1", "fp6_e2m3", "fp6_e3m2"):
+            for sa in (None, torch.float8_e8m0fnu):
+                for sb in (None, torch.float8_e8m0fnu):
+                    a, b = packed(fa, sa), packed(fb, sb)
+                    assert choose_matrix(b, a, matrix_intermediate(a, b), f32, 4) is GEMM_MX
+    ints = packed("int4", None)
+    assert choose_matrix(packed("fp4_e2m1", None), ints, matrix_intermediate(ints, ints), f32, 4) is None
+    f16s = packed("fp4_e2m1", torch.float16)
+    assert choose_matrix(f16s, packed("fp4_e2m1", None), f32, f32, 4) is None
+    x8, y8 = torch.zeros(2, 128, dtype=torch.float8_e4m3fn), torch.zeros(2, 128, dtype=torch.float8_e5m2)
+    assert _dense_kernel(x8, y8, f32, None, "auto") is GEMM_FP8
+    assert _dense_kernel(x8, y8, f32, None, "tiled") is None
+    assert _dense_kernel(torch.zeros(2, 2, dtype=torch.bfloat16), torch.zeros(2, 2, dtype=torch.bfloat16), f32, None,
+                         "auto") is GEMM_DENSE
+    assert _dense_kernel(x8, torch.zeros(2, 128, dtype=torch.bfloat16), f32, None, "auto") is None
+
+
 def test_noalloc_split_k_rejects_oversized_partials_before_any_gpu_call():
     """The allocation-free split-K GEMM checks its partials against the static scratch size on the
     host: 4 splits of 4096 x 4096 fp32 partials (256 MiB) exceed the 32 MiB array."""

@@ -266,14 +266,20 @@ extern "C" int tgm_gemm_mx(const void* a, int a_fmt, const void* a_scales, int64
                            void* stream) {
   clear_error();
   TGM_CHECK_ARG(valid_format(a_fmt) && valid_format(b_fmt), "unknown packed format");
+  TGM_CHECK_ARG(a && b && c, "null operand");
   TGM_CHECK_ARG(m >= 0 && n >= 0 && k >= 0, "invalid gemm sizes");
-  TGM_CHECK_ARG(a_scales && b_scales, "block-scaled GEMM needs E8M0 scales for both operands");
   TGM_CHECK_ARG(c_dtype == TGM_BF16 || c_dtype == TGM_F16 || c_dtype == TGM_F32, "output must be bf16, f16 or f32");
   TGM_CHECK_ARG(m <= 1 || ldc >= n, "ldc smaller than N");
   if (m == 0 || n == 0) return TGM_OK;
-  if (a_fmt != TGM_FMT_FP4_E2M1 || b_fmt != TGM_FMT_FP4_E2M1)
-    TGM_UNSUPPORTED("tgm_gemm_mx: only FP4 x FP4 has a scaled-MFMA kernel");
-  if (k == 0 || k % kBK != 0) TGM_UNSUPPORTED("tgm_gemm_mx: K must be a positive multiple of %d", kBK);
+  const int ta = f8f6f4_code_of_format(a_fmt), tb = f8f6f4_code_of_format(b_fmt);
+  if (ta < 0 || tb < 0) TGM_UNSUPPORTED("tgm_gemm_mx: the scaled MFMA takes FP4 and FP6 codes, not integers");
+  const bool fp4_pair = a_fmt == TGM_FMT_FP4_E2M1 && b_fmt == TGM_FMT_FP4_E2M1 && a_scales && b_scales;
+  if (!fp4_pair || k == 0 || k % kBK != 0) {
+    // every other FP4 / FP6 pair (or K a multiple of 128 only): the general scaled-MFMA kernel
+    const int64_t rba = k / 8 * (a_fmt == TGM_FMT_FP4_E2M1 ? 4 : 6), rbb = k / 8 * (b_fmt == TGM_FMT_FP4_E2M1 ? 4 : 6);
+    return launch_f8f6f4((hipStream_t)stream, ta, a, rba, a_scales, m, tb, b, rbb, b_scales, n, k, c, c_dtype, ldc,
+                         "tgm_gemm_mx");
+  }
   if (m >= (1ll << 31) || n >= (1ll << 31) || m * (k / 2) >= (1ll << 32) || n * (k / 2) >= (1ll << 32))
     TGM_UNSUPPORTED("tgm_gemm_mx: operands must be under 4 GiB (32-bit offsets)");
   if ((uintptr_t)a % 16 || (uintptr_t)b % 16 || (uintptr_t)a_scales % 8 || (uintptr_t)b_scales % 8)

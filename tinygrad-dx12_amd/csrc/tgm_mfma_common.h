@@ -148,4 +148,12 @@ __device__ __forceinline__ void store_tile32_swiglu(const f32x16& t, float* ep, 
   }
 }
 
+// Scaled-MFMA GEMM over an FP6 / FP4 operand pair (tgm_gemm_f8f6f4.hip): operand type codes
+// ta / tb (f8f6f4_code_of_format), row strides in bytes, scales E8M0 per 32 K-elements or null.
+// Returns a TGM_* status (TGM_E_UNSUPPORTED with the reason set, E3M2 x E3M2 included).
+int f8f6f4_code_of_format(int fmt);
+int launch_f8f6f4(hipStream_t s, int ta, const void* a, int64_t lda, const void* sa, int64_t m, int tb,
+                  const void* b, int64_t ldb, const void* sb, int64_t n, int64_t k, void* c, int cdt, int64_t ldc,
+                  const char* who);
+
 }  // namespace tgm

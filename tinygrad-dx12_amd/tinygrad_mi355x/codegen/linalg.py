@@ -7,8 +7,11 @@ scopes raise" behaviour.  What changes is what runs:
 
 * a packed K-blocked weight times activations goes to kernel family 1 (fused
   dequant GEMV, M <= 16) or family 2 (dequant-to-bf16 MFMA GEMM);
-* two packed MX operands (``matmul_nt``) go to the block-scaled FP4/FP6 MFMA GEMM;
-* two ordinary bf16 or f16 operands go to the ordinary MFMA GEMM (``tgm_gemm_dense``);
+* two packed FP4 / FP6 operands (``matmul_nt``), each E8M0 block-32 scaled or unscaled, go to
+  the scaled-MFMA GEMM (E3M2 x E3M2, which that MFMA does not sum exactly, decodes A to bf16
+  for the weight GEMM);
+* two ordinary bf16 or f16 operands go to the ordinary MFMA GEMM (``tgm_gemm_dense``), two
+  FP8 operands to the same GEMM with the FP8 values decoded to bf16 (``tgm_gemm_fp8``);
 * everything else runs the exact-width device GEMM ``tgm_gemm_plain`` -- the
   analogue of the reference's ordinary-matmul fallback.
 
@@ -27,9 +30,9 @@ import torch
 
 from tinygrad_mi355x import dtype as D
 from tinygrad_mi355x.codegen.decomp.mi355x import MX_FORMATS, PackedTensor, matrix_intermediate
-from tinygrad_mi355x.renderer.linalg import (ACTIVATION_DTYPES, DENSE_DTYPES, GEMM_DENSE, GEMM_MX, GEMM_W, GEMV,
-                                             GEMV_MAX_ROWS, OUTPUT_DTYPES, WEIGHT_SCALE_DTYPES, MatrixKernel,
-                                             _accumulator)
+from tinygrad_mi355x.renderer.linalg import (ACTIVATION_DTYPES, DENSE_DTYPES, FP8_DTYPES, GEMM_DENSE, GEMM_FP8,
+                                             GEMM_MX, GEMM_W, GEMV, GEMV_MAX_ROWS, OUTPUT_DTYPES,
+                                             WEIGHT_SCALE_DTYPES, MatrixKernel, _accumulator)
 from tinygrad_mi355x.runtime import kernels as K
 
 SCOPES = ("auto", "Wave", "ThreadGroup", "tiled")
@@ -75,8 +78,8 @@ def plain_matmul(lhs: torch.Tensor, rhs: torch.Tensor, out_dtype: torch.dtype, a
 
 
 def transpose16(x: torch.Tensor) -> torch.Tensor:
-    """Contiguous transpose of a 2-D 16-bit tensor on the device (the staging copy of a
-    row-major right operand for the NT GEMM)."""
+    """Contiguous transpose of a 2-D 16-bit (or, for FP8, 8-bit) tensor on the device (the
+    staging copy of a row-major right operand for the NT GEMM)."""
     K.require_device(x)
     rows, cols = x.shape
     out = torch.empty((cols, rows), dtype=x.dtype, device=x.device)
@@ -84,8 +87,8 @@ def transpose16(x: torch.Tensor) -> torch.Tensor:
     # stride (a single-row view included) is staged first
     if x.stride(1) != 1 and cols > 1:
         x = x.contiguous()
-    K.call("tgm_transpose16", x.data_ptr(), rows, cols, x.stride(0) if rows > 1 else cols, out.data_ptr(), rows,
-           K.stream_of(x))
+    name = "tgm_transpose8" if x.element_size() == 1 else "tgm_transpose16"
+    K.call(name, x.data_ptr(), rows, cols, x.stride(0) if rows > 1 else cols, out.data_ptr(), rows, K.stream_of(x))
     return out
 
 
@@ -94,24 +97,35 @@ def _k_rows(x: torch.Tensor) -> torch.Tensor:
     return x if x.stride(1) == 1 or x.shape[1] == 1 else x.contiguous()
 
 
-def dense_matmul_nt(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
-    """C[M, N] = a[M, K] @ b[N, K]^T on the ordinary MFMA GEMM (bf16 or f16 operands)."""
+def dense_matmul_nt(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype, scale_a: torch.Tensor | None = None,
+                    scale_b: torch.Tensor | None = None) -> torch.Tensor:
+    """C[M, N] = a[M, K] @ b[N, K]^T on the ordinary MFMA GEMM (bf16 or f16 operands) or, for
+    FP8 operands, on the scaled MFMA with unit block scales; ``scale_a`` / ``scale_b`` are
+    optional fp32 device scalars (FP8 only) that multiply the fp32 sums before rounding."""
     a, b = _k_rows(a), _k_rows(b)
     m, k = a.shape
     n = b.shape[0]
     c = torch.empty((m, n), dtype=out_dtype, device=a.device)
-    K.call("tgm_gemm_dense", a.data_ptr(), K.dtype_id(a.dtype), m, a.stride(0) if m > 1 else k, b.data_ptr(),
-           K.dtype_id(b.dtype), n, b.stride(0) if n > 1 else k, k, c.data_ptr(), K.dtype_id(out_dtype), n,
-           K.stream_of(a))
+    lda, ldb = a.stride(0) if m > 1 else k, b.stride(0) if n > 1 else k
+    if a.dtype in FP8_DTYPES:
+        K.call("tgm_gemm_fp8", a.data_ptr(), K.dtype_id(a.dtype), lda, m, b.data_ptr(), K.dtype_id(b.dtype), ldb, n,
+               k, K.ptr(scale_a), K.ptr(scale_b), c.data_ptr(), K.dtype_id(out_dtype), n, K.stream_of(a))
+        return c
+    K.call("tgm_gemm_dense", a.data_ptr(), K.dtype_id(a.dtype), m, lda, b.data_ptr(), K.dtype_id(b.dtype), n, ldb, k,
+           c.data_ptr(), K.dtype_id(out_dtype), n, K.stream_of(a))
     return c
 
 
 def _dense_kernel(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype, tile, scope: str) -> MatrixKernel | None:
-    if scope == "tiled" or not MI355X_LINALG or a.dtype not in DENSE_DTYPES or b.dtype is not a.dtype:
+    if scope == "tiled" or not MI355X_LINALG or out_dtype not in OUTPUT_DTYPES:
         return None
-    if out_dtype not in OUTPUT_DTYPES or (tile is not None and tuple(tile) != GEMM_DENSE.tile):
+    if a.dtype in FP8_DTYPES and b.dtype in FP8_DTYPES:
+        kernel = GEMM_FP8
+    elif a.dtype in DENSE_DTYPES and b.dtype is a.dtype:
+        kernel = GEMM_DENSE
+    else:
         return None
-    return GEMM_DENSE
+    return kernel if tile is None or tuple(tile) == kernel.tile else None
 
 
 def _decoded(x: torch.Tensor | PackedTensor, intermediate: torch.dtype) -> torch.Tensor:
@@ -128,13 +142,19 @@ def choose_matrix(weight: PackedTensor | None, activation: torch.Tensor | Packed
     """
     if scope == "tiled" or not MI355X_LINALG or weight is None or len(weight.shape) != 2:
         return None
-    if intermediate not in (torch.float16, torch.bfloat16, torch.float32) or out_dtype not in OUTPUT_DTYPES:
+    if out_dtype not in OUTPUT_DTYPES:
         return None
     if isinstance(activation, PackedTensor):
-        ok = (weight.format in MX_FORMATS and activation.format in MX_FORMATS and weight.block_size == 32
-              and activation.block_size == 32 and weight.scales is not None and activation.scales is not None
-              and weight.scales.dtype is torch.float8_e8m0fnu and activation.scales.dtype is torch.float8_e8m0fnu)
-        kernel = GEMM_MX if ok else None
+        # two FP4 / FP6 operands, each E8M0 block-32 scaled or unscaled (the FP8 intermediate of
+        # two unscaled codes, or fp32 when either is scaled): the scaled MFMA multiplies exactly
+        # the decoded values
+        def mx_operand(t: PackedTensor) -> bool:
+            return t.format in MX_FORMATS and (t.scales is None or (
+                t.block_size == 32 and t.scales.dtype is torch.float8_e8m0fnu))
+
+        kernel = GEMM_MX if mx_operand(weight) and mx_operand(activation) else None
+    elif intermediate not in (torch.float16, torch.bfloat16, torch.float32):
+        return None
     else:
         if activation is None or activation.dtype not in ACTIVATION_DTYPES:
             return None
@@ -174,9 +194,9 @@ def _mx_nt(a: PackedTensor, b: PackedTensor, out_dtype: torch.dtype) -> torch.Te
     n = b.shape[0]
     c = torch.empty((m, n), dtype=out_dtype, device=a.device)
     ad, bd = (t.data if t.data.is_contiguous() else t.data.contiguous() for t in (a, b))
-    sa, sb = (t.scales.contiguous() for t in (a, b))
-    K.call("tgm_gemm_mx", ad.data_ptr(), K.FORMAT_IDS[a.format], sa.data_ptr(), m, bd.data_ptr(),
-           K.FORMAT_IDS[b.format], sb.data_ptr(), n, k, c.data_ptr(), K.dtype_id(out_dtype), n, K.stream_of(ad))
+    sa, sb = (None if t.scales is None else t.scales.contiguous() for t in (a, b))
+    K.call("tgm_gemm_mx", ad.data_ptr(), K.FORMAT_IDS[a.format], K.ptr(sa), m, bd.data_ptr(),
+           K.FORMAT_IDS[b.format], K.ptr(sb), n, k, c.data_ptr(), K.dtype_id(out_dtype), n, K.stream_of(ad))
     return c
 
 
@@ -276,9 +296,10 @@ def matmul_nt(a: torch.Tensor | PackedTensor, b: torch.Tensor | PackedTensor, sc
               tile: tuple[int, int, int] | None = None, dtype: torch.dtype | None = None) -> torch.Tensor:
     """``a @ b.T`` with both operands stored K-last: a [M, K], b [N, K] -> [M, N].
 
-    Dtype rules are those of ``matmul(a, b.T)``.  Two packed MX operands with E8M0
-    block-32 scales run the block-scaled FP4/FP6 MFMA GEMM; one packed operand runs the
-    fused-dequant families; anything else runs ordinary exact compute.
+    Dtype rules are those of ``matmul(a, b.T)``.  Two packed FP4 / FP6 operands (E8M0
+    block-32 scales or none) run the scaled-MFMA GEMM; one packed operand runs the
+    fused-dequant families; bf16 / f16 / FP8 pairs run the ordinary MFMA GEMM; anything else
+    runs ordinary exact compute.
     """
     device = _validate(a, b, scope, tile)
     if len(a.shape) != 2 or len(b.shape) != 2 or a.shape[1] != b.shape[1]:
@@ -300,7 +321,14 @@ def matmul_nt(a: torch.Tensor | PackedTensor, b: torch.Tensor | PackedTensor, sc
     if isinstance(a, PackedTensor) and isinstance(b, PackedTensor):
         kernel = choose_matrix(b, a, intermediate, out_dtype, m, tile, scope)
         key = _key(kernel, a, b, out_dtype=out_dtype, m=m)
-        return _dispatch(lambda: _mx_nt(a, b, out_dtype), generic, kernel, scope, key)
+        if kernel is GEMM_MX and a.format == b.format == "fp6_e3m2":
+            # gfx950's scaled MFMA does not sum E3M2 x E3M2 products exactly; A decodes exactly to
+            # bf16 and B stays packed in the weight GEMM (or GEMV for a few rows of A)
+            family = GEMV if m <= GEMV_MAX_ROWS else GEMM_W
+            native = lambda: _weight_left(family, b, a.unpack(torch.bfloat16), out_dtype)  # noqa: E731
+        else:
+            native = lambda: _mx_nt(a, b, out_dtype)  # noqa: E731
+        return _dispatch(native, generic, kernel, scope, key)
     if isinstance(b, PackedTensor):
         kernel = choose_matrix(b, a, intermediate, out_dtype, m, tile, scope)
         key = _key(kernel, b, a, out_dtype=out_dtype, m=m)

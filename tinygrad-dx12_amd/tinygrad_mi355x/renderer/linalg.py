@@ -36,12 +36,18 @@ class MatrixKernel:
 GEMV = MatrixKernel("tgm_gemv", "Wave", (16, 16, 128), 256)
 # Family 2: dequant-to-bf16 MFMA GEMM (replaces linalg_source for one packed operand).
 GEMM_W = MatrixKernel("tgm_gemm_w", "ThreadGroup", (256, 128, 128), 512)
-# Family 2: block-scaled FP4/FP6 MFMA GEMM (two packed MX operands).
+# Family 2: scaled-MFMA GEMM of two packed FP4 / FP6 operands, each with E8M0 block-32 scales or
+# unscaled (FP4 x FP4 with both scales: 256 x 256 tiles, K steps of 256; every other pair
+# 256 x 128 tiles, K steps of 128).
 GEMM_MX = MatrixKernel("tgm_gemm_mx", "ThreadGroup", (256, 256, 256), 512)
 # Family 2: ordinary bf16 x bf16 / f16 x f16 MFMA GEMM (the reference's LinAlg lowering of an
 # ordinary matrix product, codegen/matmul.py:156-246).
 GEMM_DENSE = MatrixKernel("tgm_gemm_dense", "ThreadGroup", (256, 128, 64), 512)
 DENSE_DTYPES = (torch.bfloat16, torch.float16)
+# Family 2: ordinary FP8 x FP8 GEMM on the scaled MFMA with unit scales (the reference's LinAlg
+# takes FP8 operands as they are, renderer/linalg.py:12-13).
+GEMM_FP8 = MatrixKernel("tgm_gemm_fp8", "ThreadGroup", (256, 128, 128), 512)
+FP8_DTYPES = (torch.float8_e4m3fn, torch.float8_e5m2)
 # Exact-width fallback (the reference's ordinary matmul); never a "native" candidate.
 PLAIN = MatrixKernel("tgm_gemm_plain", "tiled", (16, 16, 1), 256)
 

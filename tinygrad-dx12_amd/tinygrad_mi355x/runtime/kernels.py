@@ -48,6 +48,7 @@ _SIGNATURES = {
     "tgm_gemm_w_split_noalloc": (_P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _P, _INT, _I64, _P, _INT, _I64, _I64,
                                  _P),
     "tgm_gemm_mx": (_P, _INT, _P, _I64, _P, _INT, _P, _I64, _I64, _P, _INT, _I64, _P),
+    "tgm_gemm_fp8": (_P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _I64, _P, _P, _P, _INT, _I64, _P),
     "tgm_gemm_plain": (_P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _P, _INT, _I64, _I64, _I64, _I64, _I64, _INT, _P),
     "tgm_quantize_mx": (_P, _INT, _I64, _I64, _INT, _I64, _P, _P, _P),
     "tgm_pack_codes": (_P, _I64, _INT, _P, _P),
@@ -56,6 +57,7 @@ _SIGNATURES = {
                                _I64, _I64, _I64, _P),
     "tgm_gemv_swiglu": (_P, _INT, _I64, _I64, _P, _INT, _I64, _P, _INT, _I64, _I64, _P, _INT, _I64, _P),
     "tgm_transpose16": (_P, _I64, _I64, _I64, _P, _I64, _P),
+    "tgm_transpose8": (_P, _I64, _I64, _I64, _P, _I64, _P),
     # decoder-step kernels (include/tgm_decoder.h)
     "tgm_dec_embed": (_P, _I64, _I64, _P, _I64, _P, _P),
     "tgm_dec_add_rmsnorm": (_P, _P, _I64, _I64, _P, ctypes.c_float, _P, _INT, _P),
