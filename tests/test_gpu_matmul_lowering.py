@@ -122,3 +122,26 @@ def test_packed_weight_product_is_not_materialised(dev):
     assert O.max_rel_err(f64(y), f64(x) @ deq.T) <= 1e-2
     y.float().sum().backward()
     assert O.max_rel_err(f64(xg.grad), np.ones((40, n)) @ deq) <= 1e-2
+
+
+@pytest.mark.parametrize("k", [256, 96])
+def test_scaled_fp8_product_is_lowered(dev, k):
+    """A traced torch._scaled_mm runs the FP8 GEMM (K = 96 has no 128-element tiling: the
+    exact-width device GEMM, then the scales); both match the exact fp64 product times the
+    per-tensor scales."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(k)
+    a = (torch.randn((130, k), device=dev, generator=g) * 3).to(torch.float8_e4m3fn)
+    w = (torch.randn((200, k), device=dev, generator=g) * 3).to(torch.float8_e5m2)
+    sa, sb = torch.tensor(0.25, device=dev), torch.tensor(1.5, device=dev)
+
+    def f(a, w, sa, sb):
+        return torch._scaled_mm(a, w.t(), sa, sb, out_dtype=torch.float32)
+
+    # shapes are propagated on CPU copies (torch runs _scaled_mm there), the product runs on the GPU
+    gm = MM.lower_matmul(MM.trace(f), *(t.cpu() for t in (a, w, sa, sb)))
+    assert gm.lowered_matmuls == [(130, 200, k)]
+    out = gm(a, w, sa, sb)
+    ref = a.float().cpu().numpy().astype(np.float64) @ w.float().cpu().numpy().astype(np.float64).T * 0.375
+    assert out.dtype is torch.float32
+    assert O.max_rel_err(out.cpu().numpy(), ref) <= 1e-2

@@ -87,3 +87,29 @@ def test_lowering_replaces_products_and_keeps_the_rest():
     assert targets.count(MM.native_matmul) == 2
     assert torch.bmm in targets  # batched product untouched
     assert sorted(gm.lowered_matmuls) == [(16, 48, 32), (24, 24, 64)]
+
+
+def test_recognizes_fp8_scaled_products():
+    """torch._scaled_mm with per-tensor fp32 scales and a bf16 / f16 / f32 output is an FP8
+    product on the FP8 GEMM; an fp8 output or a bias keeps torch's lowering (CPU tensors: torch
+    runs _scaled_mm here for shape propagation)."""
+    a = torch.randn(16, 128).to(torch.float8_e4m3fn)
+    w = torch.randn(48, 128).to(torch.float8_e5m2)
+    sa, sb = torch.tensor(0.5), torch.tensor(2.0)
+
+    def f(a, w, sa, sb):
+        return torch._scaled_mm(a, w.t(), sa, sb, out_dtype=torch.bfloat16)
+
+    gm, (spec,) = specs(f, a, w, sa, sb)
+    assert (spec.m, spec.n, spec.k) == (16, 48, 128)
+    assert spec.right.name == "w" and spec.transposed == (False, True)
+    assert spec.scaled[2] is torch.bfloat16 and spec.scaled[0].name == "sa"
+    lowered = MM.lower_matmul(MM.trace(f), a, w, sa, sb)
+    assert lowered.lowered_matmuls == [(16, 48, 128)]
+    assert any(n.target is MM.scaled_fp8_matmul for n in lowered.graph.nodes)
+    _, found = specs(lambda a, w, sa, sb: torch._scaled_mm(a, w.t(), sa, sb), a, w.to(torch.float8_e4m3fn), sa, sb)
+    assert found == [None]  # FP8 output
+    bias = torch.zeros(48, dtype=torch.bfloat16)
+    _, found = specs(lambda a, w, sa, sb: torch._scaled_mm(a, w.t(), sa, sb, bias=bias, out_dtype=torch.bfloat16),
+                     a, w.to(torch.float8_e4m3fn), sa, sb)
+    assert found == [None]

@@ -16,6 +16,11 @@ the rewrite works on its nodes with the same conservative rules:
 * a right operand that is ``unpack(packed)`` -- the decode of a PackedTensor -- feeds the
   packed-weight kernels directly (family 1 GEMV / family 2 GEMM), so the decoded weight is never
   materialised;
+* an FP8 product -- torch's ``torch._scaled_mm(a, b, scale_a, scale_b, out_dtype=...)`` with
+  per-tensor fp32 scales, a [M, K] row-major and b [K, N] column-major (the layout it requires)
+  -- runs the FP8 GEMM (``tgm_gemm_fp8``: FP8 values decoded exactly to bf16, fp32 sums times
+  scale_a * scale_b, rounded once to out_dtype), as the reference's rewrite hands FP8 operands
+  to its LinAlg GEMM (matmul.py:51-128 with renderer/linalg.py:12-13);
 * operands whose rows are not 16-byte aligned are staged by a copy at run time (the
   reference's ``dx12_matrix_input`` staging, matmul.py:218-226).
 
@@ -36,10 +41,12 @@ from torch.fx.passes.shape_prop import ShapeProp
 
 from tinygrad_mi355x.codegen import linalg
 from tinygrad_mi355x.codegen.decomp.mi355x import PackedTensor, unpack
-from tinygrad_mi355x.renderer.linalg import DENSE_DTYPES
+from tinygrad_mi355x.renderer.linalg import DENSE_DTYPES, FP8_DTYPES, OUTPUT_DTYPES
+from tinygrad_mi355x.runtime import kernels as K
 
 MATMUL_FUNCTIONS = (torch.matmul, torch.mm, operator.matmul)
 MATMUL_METHODS = ("matmul", "mm", "__matmul__")
+SCALED_MM = getattr(torch, "_scaled_mm", None)  # torch's FP8 matrix product
 KEEP = "tgm_keep"
 ELEMENTWISE = (torch.relu, F.relu, F.gelu, F.silu, torch.sigmoid, torch.tanh, operator.add, operator.mul, torch.add,
                torch.mul)
@@ -59,6 +66,7 @@ class MatmulSpec:
     epilogue: bool
     transposed: tuple[bool, bool]    # (left is stored [K, M], right is stored [N, K])
     packed: bool = False             # right is a packed weight [N, K] used as deq(W)^T
+    scaled: tuple | None = None      # FP8 product: (scale_a node, scale_b node, out_dtype)
 
 
 def _meta(node) -> object | None:
@@ -130,15 +138,48 @@ class PackedTracer(torch.fx.Tracer):
 
 
 def _is_matmul(node: torch.fx.Node) -> bool:
-    return ((node.op == "call_function" and node.target in MATMUL_FUNCTIONS)
+    return ((node.op == "call_function" and (node.target in MATMUL_FUNCTIONS or
+                                             (SCALED_MM is not None and node.target is SCALED_MM)))
             or (node.op == "call_method" and node.target in MATMUL_METHODS))
+
+
+def _scalar_f32(node) -> bool:
+    m = _meta(node)
+    return m is not None and m.dtype is torch.float32 and int(torch.Size(m.shape).numel()) == 1
+
+
+def _match_scaled_mm(node: torch.fx.Node) -> MatmulSpec | None:
+    """``torch._scaled_mm(a, b, scale_a, scale_b[, out_dtype=...])`` with FP8 a [M, K] (row-major),
+    b [K, N] (column-major, i.e. the transpose of an [N, K] row-major tensor), per-tensor fp32
+    scales and a bf16 / f16 / f32 output; no bias or result scale."""
+    if len(node.args) != 4 or set(node.kwargs) - {"out_dtype", "bias", "scale_result", "use_fast_accum"}:
+        return None
+    if node.kwargs.get("bias") is not None or node.kwargs.get("scale_result") is not None:
+        return None
+    left, right, sa, sb = node.args
+    out, lm, rm = _meta(node), _meta(left), _meta(right)
+    if out is None or lm is None or rm is None or len(lm.shape) != 2 or len(rm.shape) != 2:
+        return None
+    if lm.dtype not in FP8_DTYPES or rm.dtype not in FP8_DTYPES or out.dtype not in OUTPUT_DTYPES:
+        return None
+    if not (_scalar_f32(sa) and _scalar_f32(sb)) or lm.stride[1] != 1 or rm.stride[0] != 1:
+        return None
+    m, k = lm.shape
+    n = rm.shape[1]
+    right_src = _transpose_source(right)
+    return MatmulSpec(m, n, k, node, left, right_src if right_src is not None else right, torch.float32,
+                      _has_epilogue(node), (False, right_src is not None), scaled=(sa, sb, out.dtype))
 
 
 def match_matmul(node: torch.fx.Node, root: torch.nn.Module | None = None) -> MatmulSpec | None:
     """Match a rank-two matrix product of a shape-propagated graph, or return None.
 
     ``root`` resolves the packed weights a traced graph refers to by attribute."""
-    if not _is_matmul(node) or node.meta.get(KEEP) or len(node.args) != 2 or node.kwargs:
+    if not _is_matmul(node) or node.meta.get(KEEP):
+        return None
+    if SCALED_MM is not None and node.target is SCALED_MM:
+        return _match_scaled_mm(node)
+    if len(node.args) != 2 or node.kwargs:
         return None
     out = _meta(node)
     left, right = node.args
@@ -217,6 +258,18 @@ def native_matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return _NativeMatmul.apply(a, b)
 
 
+def scaled_fp8_matmul(a: torch.Tensor, b_nk: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
+                      out_dtype: torch.dtype) -> torch.Tensor:
+    """``(a @ b_nk^T) * scale_a * scale_b`` rounded once to ``out_dtype``: FP8 a [M, K] and b_nk
+    [N, K] on the FP8 GEMM.  Shapes it cannot tile (K not a multiple of 128) run the exact-width
+    device GEMM, then the scale and the rounding."""
+    try:
+        return linalg.dense_matmul_nt(a, b_nk, out_dtype, scale_a, scale_b)
+    except K.UnsupportedKernel:
+        acc = linalg.matmul_nt(a, b_nk, dtype=torch.float32)
+        return (acc * (scale_a * scale_b)).to(out_dtype)
+
+
 def packed_matmul(x: torch.Tensor, w: PackedTensor) -> torch.Tensor:
     return _PackedMatmul.apply(x, w)
 
@@ -226,6 +279,10 @@ def _lower(graph: torch.fx.Graph, spec: MatmulSpec) -> None:
     with graph.inserting_before(node):
         if spec.packed:
             new = graph.call_function(packed_matmul, (node.args[0], spec.right))
+        elif spec.scaled is not None:
+            sa, sb, out_dtype = spec.scaled
+            right = spec.right if spec.transposed[1] else graph.call_method("t", (spec.right,))
+            new = graph.call_function(scaled_fp8_matmul, (spec.left, right, sa, sb, out_dtype))
         else:
             left = graph.call_method("t", (spec.left,)) if spec.transposed[0] else spec.left
             right = graph.call_method("t", (spec.right,)) if spec.transposed[1] else spec.right
