@@ -74,6 +74,14 @@ int tgm_abi_version(void);
 const char* tgm_last_error(void);
 
 /*
+ * The gcnArchName of HIP device ``ordinal`` (e.g. "gfx950:sramecc+:xnack-"), written to out
+ * (at most len bytes, NUL-terminated).  Replaces the reference's adapter description query
+ * (runtime/support/dx12.py:298-336) for the plugin's renderer target, so the runtime needs no
+ * other library to learn the architecture.  Returns a hipError_t on failure.
+ */
+int tgm_device_arch(int ordinal, char* out, int64_t len);
+
+/*
  * Decode ``count`` packed elements to ``out_dtype`` (replaces PackedTensor.unpack,
  * dx12.py:49-106).  ``k`` is the logical last dimension (scales index
  * [i / k, (i % k) / block]).  ``scales`` may be NULL (scale_dtype ignored).

@@ -92,6 +92,19 @@ extern "C" int tgm_abi_version(void) { return TGM_ABI_VERSION; }
 
 extern "C" const char* tgm_last_error(void) { return g_last_error; }
 
+extern "C" int tgm_device_arch(int ordinal, char* out, int64_t len) {
+  clear_error();
+  TGM_CHECK_ARG(out && len > 0, "null output");
+  hipDeviceProp_t prop;
+  const hipError_t e = hipGetDeviceProperties(&prop, ordinal);
+  if (e != hipSuccess) {
+    set_error("hipGetDeviceProperties(%d) failed: %s", ordinal, hipGetErrorString(e));
+    return (int)e;
+  }
+  snprintf(out, (size_t)len, "%s", prop.gcnArchName);
+  return TGM_OK;
+}
+
 extern "C" int tgm_unpack(const void* data, int64_t nbytes, int fmt, int64_t count, int64_t k, const void* scales,
                           int scale_dtype, int64_t block_size, void* out, int out_dtype, void* stream) {
   clear_error();

@@ -21,17 +21,16 @@ from dataclasses import dataclass
 import torch
 
 from tinygrad_mi355x import dtype as D
+from tinygrad_mi355x.codegen.decomp.formats import FORMATS, MX_FORMATS  # noqa: F401  (dx12.py:10)
+from tinygrad_mi355x.codegen.program import unpack_program
 from tinygrad_mi355x.runtime import kernels as K
 
-# (total bits, exponent bits, mantissa bits, exponent bias); integers have no exponent.  (dx12.py:10)
-FORMATS = {"int4": (4, 0, 0, 0), "uint4": (4, 0, 0, 0), "fp4_e2m1": (4, 2, 1, 1), "fp6_e2m3": (6, 2, 3, 1), "fp6_e3m2": (6, 3, 2, 3)}
 # Exact unscaled FP8 destinations (dx12.py:11).
 FP8_CANDIDATES = {
     "fp4_e2m1": (torch.float8_e4m3fn, torch.float8_e5m2),
     "fp6_e2m3": (torch.float8_e4m3fn,),
     "fp6_e3m2": (torch.float8_e4m3fn, torch.float8_e5m2),
 }
-MX_FORMATS = ("fp4_e2m1", "fp6_e2m3", "fp6_e3m2")
 
 
 @dataclass(frozen=True)
@@ -73,6 +72,16 @@ class PackedTensor:
     def device(self) -> torch.device:
         return self.data.device
 
+    def desc(self, data: torch.Tensor | None = None, scales: torch.Tensor | None = None):
+        """The kernel programs' view of this operand (``codegen/program.PackedDesc``), for the
+        given contiguous storage (default: this record's)."""
+        from tinygrad_mi355x.codegen.program import PackedDesc
+
+        data = self.data if data is None else data
+        scales = self.scales if scales is None else scales
+        return PackedDesc(self.format, self.shape, data.numel(), None if scales is None else scales.data_ptr(),
+                          None if scales is None else str(scales.dtype).rsplit(".", 1)[-1], self.block_size)
+
     @property
     def bits(self) -> int:
         return FORMATS[self.format][0]
@@ -102,9 +111,9 @@ class PackedTensor:
         if self.scales is not None:
             scales = self.scales if self.scales.is_contiguous() else self.scales.contiguous()
         out = torch.empty(self.shape, dtype=dtype, device=self.data.device)
-        K.call("tgm_unpack", data.data_ptr(), data.numel(), K.FORMAT_IDS[self.format], count, self.shape[-1],
-               K.ptr(scales), K.dtype_id(scales.dtype) if scales is not None else -1, self.block_size,
-               out.data_ptr(), K.dtype_id(dtype), K.stream_of(self.data))
+        K.dtype_id(dtype)  # ValueError for dtypes the kernels do not write
+        program = unpack_program(self.desc(data, scales), str(dtype).rsplit(".", 1)[-1])
+        program.launch(out.data_ptr(), data.data_ptr(), 0, K.stream_of(self.data))
         return out
 
     def matmul(self, other: torch.Tensor | "PackedTensor") -> torch.Tensor:

@@ -29,6 +29,7 @@ import os
 import torch
 
 from tinygrad_mi355x import dtype as D
+from tinygrad_mi355x.codegen import program as P
 from tinygrad_mi355x.codegen.decomp.mi355x import MX_FORMATS, PackedTensor, matrix_intermediate
 from tinygrad_mi355x.renderer.linalg import (ACTIVATION_DTYPES, DENSE_DTYPES, FP8_DTYPES, GEMM_DENSE, GEMM_FP8,
                                              GEMM_MX, GEMM_W, GEMV, GEMV_MAX_ROWS, OUTPUT_DTYPES,
@@ -42,6 +43,12 @@ MI355X_LINALG = int(os.environ.get("MI355X_LINALG", "1"))
 matrix_failures: dict[tuple, str] = {}
 
 _ACC_IDS = {torch.float32: 13, torch.float64: 14, torch.int32: 5, torch.uint32: 6, torch.int64: 7, torch.uint64: 8}
+
+
+def _name(dt: torch.dtype) -> str:
+    """A torch dtype's name in the kernel programs (ValueError for dtypes the kernels lack)."""
+    K.dtype_id(dt)
+    return str(dt).rsplit(".", 1)[-1]
 
 
 def _device(x: torch.Tensor | PackedTensor) -> torch.device:
@@ -99,20 +106,17 @@ def _k_rows(x: torch.Tensor) -> torch.Tensor:
 
 def dense_matmul_nt(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype, scale_a: torch.Tensor | None = None,
                     scale_b: torch.Tensor | None = None) -> torch.Tensor:
-    """C[M, N] = a[M, K] @ b[N, K]^T on the ordinary MFMA GEMM (bf16 or f16 operands) or, for
-    FP8 operands, on the scaled MFMA with unit block scales; ``scale_a`` / ``scale_b`` are
-    optional fp32 device scalars (FP8 only) that multiply the fp32 sums before rounding."""
+    """C[M, N] = a[M, K] @ b[N, K]^T on the ordinary MFMA GEMM (bf16 or f16 operands; FP8
+    operands decoded exactly to bf16 in registers); ``scale_a`` / ``scale_b`` are optional fp32
+    device scalars (FP8 only) that multiply the fp32 sums before rounding."""
     a, b = _k_rows(a), _k_rows(b)
     m, k = a.shape
     n = b.shape[0]
     c = torch.empty((m, n), dtype=out_dtype, device=a.device)
     lda, ldb = a.stride(0) if m > 1 else k, b.stride(0) if n > 1 else k
-    if a.dtype in FP8_DTYPES:
-        K.call("tgm_gemm_fp8", a.data_ptr(), K.dtype_id(a.dtype), lda, m, b.data_ptr(), K.dtype_id(b.dtype), ldb, n,
-               k, K.ptr(scale_a), K.ptr(scale_b), c.data_ptr(), K.dtype_id(out_dtype), n, K.stream_of(a))
-        return c
-    K.call("tgm_gemm_dense", a.data_ptr(), K.dtype_id(a.dtype), m, lda, b.data_ptr(), K.dtype_id(b.dtype), n, ldb, k,
-           c.data_ptr(), K.dtype_id(out_dtype), n, K.stream_of(a))
+    program = P.dense_program(_name(a.dtype), m, lda, _name(b.dtype), n, ldb, k, _name(out_dtype), n,
+                              K.ptr(scale_a) or 0, K.ptr(scale_b) or 0)
+    program.launch(c.data_ptr(), a.data_ptr(), b.data_ptr(), K.stream_of(a))
     return c
 
 
@@ -178,13 +182,10 @@ def _weight_left(kernel: MatrixKernel, w: PackedTensor, x: torch.Tensor, out_dty
         scales = scales.contiguous()
     y = torch.empty((m, n), dtype=out_dtype, device=x.device)
     ldx = x.stride(0) if m > 1 else k
-    sdt = K.dtype_id(scales.dtype) if scales is not None else -1
-    if kernel is GEMV:
-        K.call("tgm_gemv", data.data_ptr(), K.FORMAT_IDS[w.format], n, k, K.ptr(scales), sdt, w.block_size,
-               x.data_ptr(), K.dtype_id(x.dtype), m, ldx, y.data_ptr(), K.dtype_id(out_dtype), n, K.stream_of(x))
-    else:
-        K.call("tgm_gemm_w", x.data_ptr(), K.dtype_id(x.dtype), m, ldx, data.data_ptr(), K.FORMAT_IDS[w.format], n, k,
-               K.ptr(scales), sdt, w.block_size, y.data_ptr(), K.dtype_id(out_dtype), n, K.stream_of(x))
+    program = P.weight_program(w.desc(data, scales), m, _name(x.dtype), ldx, _name(out_dtype), n)
+    if program.kernel is not kernel:
+        raise K.UnsupportedKernel(f"{kernel.name}: {m} activation rows belong to {program.kernel.name}")
+    program.launch(y.data_ptr(), data.data_ptr(), x.data_ptr(), K.stream_of(x))
     return y
 
 
@@ -195,8 +196,8 @@ def _mx_nt(a: PackedTensor, b: PackedTensor, out_dtype: torch.dtype) -> torch.Te
     c = torch.empty((m, n), dtype=out_dtype, device=a.device)
     ad, bd = (t.data if t.data.is_contiguous() else t.data.contiguous() for t in (a, b))
     sa, sb = (None if t.scales is None else t.scales.contiguous() for t in (a, b))
-    K.call("tgm_gemm_mx", ad.data_ptr(), K.FORMAT_IDS[a.format], K.ptr(sa), m, bd.data_ptr(),
-           K.FORMAT_IDS[b.format], K.ptr(sb), n, k, c.data_ptr(), K.dtype_id(out_dtype), n, K.stream_of(ad))
+    program = P.mx_program(a.desc(ad, sa), b.desc(bd, sb), _name(out_dtype), n)
+    program.launch(c.data_ptr(), ad.data_ptr(), bd.data_ptr(), K.stream_of(ad))
     return c
 
 

@@ -18,17 +18,19 @@ from __future__ import annotations
 import threading
 from dataclasses import dataclass, field
 
-import torch
-
 from tinygrad_mi355x.runtime.support.compiler_hip import MI355XCompiler
 
-# torch dtype -> HIP C++ element type
+# dtype name -> HIP C++ element type
 TYPE_MAP = {
-    torch.bool: "bool", torch.int8: "signed char", torch.uint8: "unsigned char", torch.int16: "short",
-    torch.uint16: "unsigned short", torch.int32: "int", torch.uint32: "unsigned int", torch.int64: "long long",
-    torch.uint64: "unsigned long long", torch.float16: "_Float16", torch.bfloat16: "__hip_bfloat16",
-    torch.float32: "float", torch.float64: "double",
+    "bool": "bool", "int8": "signed char", "uint8": "unsigned char", "int16": "short", "uint16": "unsigned short",
+    "int32": "int", "uint32": "unsigned int", "int64": "long long", "uint64": "unsigned long long",
+    "float16": "_Float16", "bfloat16": "__hip_bfloat16", "float32": "float", "float64": "double",
 }
+
+
+def dtype_name(dt) -> str:
+    """The name of a dtype given by name or as a torch / tinygrad dtype object (no import of either)."""
+    return dt if isinstance(dt, str) else str(dt).rsplit(".", 1)[-1]
 SCALAR_TYPES = {"i32": "int", "u32": "unsigned int", "i64": "long long", "u64": "unsigned long long", "f32": "float",
                 "f64": "double"}
 
@@ -36,7 +38,7 @@ SCALAR_TYPES = {"i32": "int", "u32": "unsigned int", "i64": "long long", "u64": 
 @dataclass(frozen=True)
 class BufferParam:
     name: str
-    dtype: torch.dtype
+    dtype: object  # a dtype name ("float32") or a dtype object whose str() ends in one
     mutable: bool = False
 
 
@@ -68,13 +70,14 @@ class MI355XRenderer:
         self.matrix_failures: dict[str, str] = {}
         self.compiler = MI355XCompiler(arch)
 
-    def supported_dtypes(self) -> set[torch.dtype]:
-        """Arithmetic dtypes rendered kernels may use (packed formats are storage, not arithmetic)."""
+    def supported_dtypes(self) -> set[str]:
+        """Names of the arithmetic dtypes rendered kernels may use (packed formats are storage, not
+        arithmetic)."""
         return set(TYPE_MAP)
 
     def render(self, spec: KernelSpec) -> str:
         """Complete ``extern "C" __global__`` source for ``spec``."""
-        if any(b.dtype not in TYPE_MAP for b in spec.buffers):
+        if any(dtype_name(b.dtype) not in TYPE_MAP for b in spec.buffers):
             raise ValueError(f"kernel {spec.name}: unsupported buffer dtype")
         if any(kind not in SCALAR_TYPES for _, kind in spec.scalars):
             raise ValueError(f"kernel {spec.name}: unsupported scalar kind")
@@ -82,7 +85,8 @@ class MI355XRenderer:
         if min(spec.local_size) < 1 or lx * ly * lz > self.local_total_max:
             raise ValueError(f"kernel {spec.name}: invalid local size {spec.local_size}")
         with self._render_lock:
-            params = [f"{'' if b.mutable else 'const '}{TYPE_MAP[b.dtype]}* __restrict__ {b.name}" for b in spec.buffers]
+            params = [f"{'' if b.mutable else 'const '}{TYPE_MAP[dtype_name(b.dtype)]}* __restrict__ {b.name}"
+                      for b in spec.buffers]
             params += [f"{SCALAR_TYPES[kind]} {name}" for name, kind in spec.scalars]
             lines = ["#include <hip/hip_runtime.h>", "#include <hip/hip_bf16.h>", *spec.includes,
                      f'extern "C" __global__ void __launch_bounds__({lx * ly * lz}) {spec.name}({", ".join(params)}) {{',

@@ -10,11 +10,11 @@ compiled into libtgm_mi355x.so.
 
 from __future__ import annotations
 
-from dataclasses import dataclass
-
 import torch
 
 from tinygrad_mi355x import dtype as D
+from tinygrad_mi355x.renderer.matrix import (GEMM_DENSE, GEMM_FP8, GEMM_MX, GEMM_W, GEMV, GEMV_MAX_ROWS,  # noqa: F401
+                                             PLAIN, MatrixKernel)
 
 
 def _accumulator(a: torch.dtype, b: torch.dtype) -> torch.dtype:
@@ -22,36 +22,8 @@ def _accumulator(a: torch.dtype, b: torch.dtype) -> torch.dtype:
     return D.strong_dtype(D.sum_acc_dtype(D.strong_dtype(D.least_upper_dtype(a, b))))
 
 
-@dataclass(frozen=True)
-class MatrixKernel:
-    """One native kernel family: the scope name it answers to, its tile and workgroup size."""
-
-    name: str  # C-ABI entry point
-    scope: str  # reference scope it replaces
-    tile: tuple[int, int, int]  # (rows of W / C per workgroup, activation rows, K per step)
-    threads: int
-
-
-# Family 1: fused dequant GEMV / skinny GEMM (replaces thread_source and the N=1 linalg_source).
-GEMV = MatrixKernel("tgm_gemv", "Wave", (16, 16, 128), 256)
-# Family 2: dequant-to-bf16 MFMA GEMM (replaces linalg_source for one packed operand).
-GEMM_W = MatrixKernel("tgm_gemm_w", "ThreadGroup", (256, 128, 128), 512)
-# Family 2: scaled-MFMA GEMM of two packed FP4 / FP6 operands, each with E8M0 block-32 scales or
-# unscaled (FP4 x FP4 with both scales: 256 x 256 tiles, K steps of 256; every other pair
-# 256 x 128 tiles, K steps of 128).
-GEMM_MX = MatrixKernel("tgm_gemm_mx", "ThreadGroup", (256, 256, 256), 512)
-# Family 2: ordinary bf16 x bf16 / f16 x f16 MFMA GEMM (the reference's LinAlg lowering of an
-# ordinary matrix product, codegen/matmul.py:156-246).
-GEMM_DENSE = MatrixKernel("tgm_gemm_dense", "ThreadGroup", (256, 128, 64), 512)
 DENSE_DTYPES = (torch.bfloat16, torch.float16)
-# Family 2: ordinary FP8 x FP8 GEMM on the scaled MFMA with unit scales (the reference's LinAlg
-# takes FP8 operands as they are, renderer/linalg.py:12-13).
-GEMM_FP8 = MatrixKernel("tgm_gemm_fp8", "ThreadGroup", (256, 128, 128), 512)
 FP8_DTYPES = (torch.float8_e4m3fn, torch.float8_e5m2)
-# Exact-width fallback (the reference's ordinary matmul); never a "native" candidate.
-PLAIN = MatrixKernel("tgm_gemm_plain", "tiled", (16, 16, 1), 256)
-
-GEMV_MAX_ROWS = 16
 ACTIVATION_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 OUTPUT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 WEIGHT_SCALE_DTYPES = (torch.float8_e8m0fnu, torch.float16, torch.bfloat16, torch.float32)

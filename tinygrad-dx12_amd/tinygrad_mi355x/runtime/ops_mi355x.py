@@ -435,12 +435,16 @@ class MI355XDevice:
 
 
 def _arch_of(ordinal: int) -> str:
-    try:
-        import torch
+    """The device's architecture from the kernel library (hipGetDeviceProperties' gcnArchName);
+    gfx950, the only target the library is built for, when the library is not built."""
+    from tinygrad_mi355x.runtime import library
 
-        return torch.cuda.get_device_properties(ordinal).gcnArchName.split(":")[0]
-    except Exception:  # noqa: BLE001 -- torch without HIP: the build targets gfx950 only
-        return "gfx950"
+    try:
+        return library.device_arch(ordinal)
+    except (OSError, RuntimeError) as error:
+        if "not built" in str(error):
+            return "gfx950"
+        raise
 
 
 _devices: dict[str, MI355XDevice] = {}

@@ -6,9 +6,10 @@ plain ``hipError_t`` functions.  Every failure becomes ``RuntimeError("<op> fail
 <code> (<hipGetErrorString>)")``, the shape of the reference's ``check``
 (runtime/support/dx12.py:11-15).
 
-The library is the HIP runtime already loaded by torch when torch is imported first
-(its soname is libamdhip64.so.7), so device memory, streams and modules are shared with
-torch and with libtgm_mi355x.so.  Nothing here touches the GPU at import time.
+The runtime is opened by its soname (libamdhip64.so.7): a process that already loaded one
+(torch does, and so does libtgm_mi355x.so, which links it) shares that instance, so device
+memory, streams and modules are shared with the kernel library.  Nothing here imports torch
+or touches the GPU at import time.
 """
 
 from __future__ import annotations
@@ -74,14 +75,10 @@ _initialised = False
 
 
 def library() -> ctypes.CDLL:
-    """Load and type the HIP runtime once (after torch, so both use the same runtime)."""
+    """Load and type the HIP runtime once (the instance already in the process, if any)."""
     global _lib
     with _lock:
         if _lib is None:
-            try:
-                import torch  # noqa: F401  -- binds the runtime torch ships first
-            except ImportError:
-                pass
             name = os.environ.get("MI355X_HIP_RUNTIME", "libamdhip64.so.7")
             try:
                 lib = ctypes.CDLL(name)
