@@ -10,7 +10,8 @@ timed with HIP events on the launch stream; ``value`` comes from the median of s
 trials (each trial's graph continues the rotation where the previous one stopped).
 
 ``value`` is the achieved algorithmic bandwidth of the step (bytes of packed weights,
-scales, x and y per step / time per step).  Secondary workloads (skinny M=4/16, the
+scales, x and y per step / time per step); every workload's algorithmic bytes and flops are
+the Estimates of the kernel program it launches (tinygrad_mi355x/codegen/program.py).  Secondary workloads (skinny M=4/16, the
 INT4 g32 GEMVs, the FP6-weight x bf16 GEMMs, the FP4xFP4 GEMMs and the 8-layer
 decoder) are reported under ``workloads``, each with its own roofline.
 ``cpu_baseline`` times the C restatement of the reference's CPU path
@@ -36,6 +37,8 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "tinygrad-dx12_amd"))
+
+from tinygrad_mi355x.codegen import program as P  # noqa: E402  (torch-free: kernel programs and their estimates)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
@@ -76,11 +79,6 @@ def parse() -> argparse.Namespace:
     p.add_argument("--summarize-profile", type=Path, default=None, metavar="DIR",
                    help="summarise the rocprofv3 output folders under DIR for the --only workload")
     return p.parse_args()
-
-
-def gemv_bytes(n: int, k: int, m: int, bits: int, scale_bytes: float, act_bytes: int, out_bytes: int,
-               block: int = 32) -> int:
-    return n * k * bits // 8 + int(n * (k // block) * scale_bytes) + m * k * act_bytes + m * n * out_bytes
 
 
 def median_trials(torch, launch, steps: int, warmup: int, copies: int) -> tuple[float, int, int]:
@@ -140,7 +138,8 @@ def fp4_gemv_workload(torch, K, dev, m: int, steps: int, warmup: int) -> dict:
     """FP4 E2M1 + E8M0/32 GEMV W [14336, 4096], bf16 X [M, 4096] -> bf16 Y [M, 14336]: codes uniform
     over the 16 E2M1 values, E8M0 bytes 127 + [-4, 2], X ~ N(0, 1) rounded to bf16."""
     n, k = 14336, 4096
-    nbytes = gemv_bytes(n, k, m, 4, 1, 2, 2)
+    nbytes = P.weight_program(P.PackedDesc("fp4_e2m1", (n, k), n * k // 2, 1, "float8_e8m0fnu"), m, "bfloat16", k,
+                              "bfloat16", n).estimates.mem
     copies = copies_for(nbytes)
     g = torch.Generator(device=dev)
     g.manual_seed(0)
@@ -148,13 +147,13 @@ def fp4_gemv_workload(torch, K, dev, m: int, steps: int, warmup: int) -> dict:
     ss = [torch.randint(123, 130, (n, k // 32), dtype=torch.uint8, device=dev, generator=g) for _ in range(copies)]
     x = torch.randn((m, k), device=dev, generator=g).to(torch.bfloat16)
     y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-    fmt, bf16, e8m0 = K.FORMAT_IDS["fp4_e2m1"], K.DTYPE_IDS[torch.bfloat16], K.DTYPE_IDS[torch.float8_e8m0fnu]
-    lib = K.load_library()
+    # one program per weight copy (each binds its copy's scales); slots (out, a, b) = (Y, W, X)
+    progs = [P.weight_program(P.PackedDesc("fp4_e2m1", (n, k), n * k // 2, s.data_ptr(), "float8_e8m0fnu"), m,
+                              "bfloat16", k, "bfloat16", n) for s in ss]
 
     def launch(i: int) -> None:
         j = i % copies
-        K.check("tgm_gemv", lib.tgm_gemv(ws[j].data_ptr(), fmt, n, k, ss[j].data_ptr(), e8m0, 32, x.data_ptr(), bf16,
-                                         m, k, y.data_ptr(), bf16, n, K.stream_of(x)))
+        progs[j].launch(y.data_ptr(), ws[j].data_ptr(), x.data_ptr(), K.stream_of(x))
 
     ms, trials, timed = median_trials(torch, launch, steps, warmup, copies)
     return {"workload": f"fp4_e2m1 e8m0/32 GEMV N=14336 K=4096 M={m}", "ms": ms, "bytes": nbytes,
@@ -165,7 +164,8 @@ def fp4_gemv_workload(torch, K, dev, m: int, steps: int, warmup: int) -> dict:
 
 def int4_gemv_workload(torch, K, dev, n: int, steps: int, warmup: int, k: int = 4096) -> dict:
     """INT4 g32 GEMV W [N, 4096] with fp16 scales ~ U(0.005, 0.02), fp16 x [1, 4096] -> fp16 y."""
-    nbytes = gemv_bytes(n, k, 1, 4, 2, 2, 2)
+    nbytes = P.weight_program(P.PackedDesc("int4", (n, k), n * k // 2, 1, "float16"), 1, "float16", k, "float16",
+                              n).estimates.mem
     copies = copies_for(nbytes)
     g = torch.Generator(device=dev)
     g.manual_seed(1)
@@ -173,13 +173,12 @@ def int4_gemv_workload(torch, K, dev, n: int, steps: int, warmup: int, k: int = 
     ss = [(torch.rand((n, k // 32), device=dev, generator=g) * 0.015 + 0.005).half() for _ in range(copies)]
     x = torch.randn((1, k), device=dev, generator=g).half()
     y = torch.empty((1, n), dtype=torch.float16, device=dev)
-    fmt, f16 = K.FORMAT_IDS["int4"], K.DTYPE_IDS[torch.float16]
-    lib = K.load_library()
+    progs = [P.weight_program(P.PackedDesc("int4", (n, k), n * k // 2, s.data_ptr(), "float16"), 1, "float16", k,
+                              "float16", n) for s in ss]
 
     def launch(i: int) -> None:
         j = i % copies
-        K.check("tgm_gemv", lib.tgm_gemv(ws[j].data_ptr(), fmt, n, k, ss[j].data_ptr(), f16, 32, x.data_ptr(), f16,
-                                         1, k, y.data_ptr(), f16, n, K.stream_of(x)))
+        progs[j].launch(y.data_ptr(), ws[j].data_ptr(), x.data_ptr(), K.stream_of(x))
 
     ms, trials, timed = median_trials(torch, launch, steps, warmup, copies)
     return {"workload": f"int4 g32 fp16-scale GEMV N={n} K={k} M=1 fp16", "ms": ms, "bytes": nbytes,
@@ -224,18 +223,15 @@ def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup:
     a = quantize_mx(torch.randn((m, k), device=dev, generator=g), "fp4_e2m1")
     b = quantize_mx(torch.randn((n, k), device=dev, generator=g), "fp4_e2m1")
     c = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-    fp4, bf16 = K.FORMAT_IDS["fp4_e2m1"], K.DTYPE_IDS[torch.bfloat16]
-    lib = K.load_library()
     stream = torch.cuda.current_stream(dev)
+    prog = P.mx_program(a.desc(), b.desc(), "bfloat16", n)
 
     def launch() -> None:
-        K.check("tgm_gemm_mx", lib.tgm_gemm_mx(a.data.data_ptr(), fp4, a.scales.data_ptr(), m, b.data.data_ptr(), fp4,
-                                               b.scales.data_ptr(), n, k, c.data_ptr(), bf16, n, stream.cuda_stream))
+        prog.launch(c.data_ptr(), a.data.data_ptr(), b.data.data_ptr(), stream.cuda_stream)
 
     settle(torch, stream, launch, warmup)
     ms = median_launch_ms(torch, stream, launch, steps)
-    flops = 2 * m * n * k
-    nbytes = (m + n) * k // 2 + (m + n) * k // 32 + m * n * 2
+    flops, nbytes = prog.estimates.ops, prog.estimates.mem
     return {"workload": f"fp4xfp4 e8m0/32 GEMM M={m} N={n} K={k} bf16 out", "ms": ms, "TFLOPS": flops / ms / 1e9,
             "flops": flops, "bytes": nbytes, "GB/s": nbytes / ms / 1e6, "timed_dispatches": steps,
             "roofline": mfma_roofline(flops, ms, FP4_PEAK_TFLOPS, "dense MXFP4 MFMA")}
@@ -252,18 +248,15 @@ def fp6_gemm_workload(torch, K, dev, fmt: str, steps: int, warmup: int, m: int =
     a = torch.randn((m, k), device=dev, generator=g).to(torch.bfloat16)
     w = quantize_mx(torch.randn((n, k), device=dev, generator=g) * 0.02, fmt)
     c = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-    f, bf16, e8m0 = K.FORMAT_IDS[fmt], K.DTYPE_IDS[torch.bfloat16], K.DTYPE_IDS[torch.float8_e8m0fnu]
-    lib = K.load_library()
     stream = torch.cuda.current_stream(dev)
+    prog = P.weight_program(w.desc(), m, "bfloat16", k, "bfloat16", n)  # slots (out, a, b) = (C, W, A)
 
     def launch() -> None:
-        K.check("tgm_gemm_w", lib.tgm_gemm_w(a.data_ptr(), bf16, m, k, w.data.data_ptr(), f, n, k, w.scales.data_ptr(),
-                                             e8m0, 32, c.data_ptr(), bf16, n, stream.cuda_stream))
+        prog.launch(c.data_ptr(), w.data.data_ptr(), a.data_ptr(), stream.cuda_stream)
 
     settle(torch, stream, launch, warmup)
     ms = median_launch_ms(torch, stream, launch, steps)
-    flops = 2 * m * n * k
-    nbytes = m * k * 2 + n * k * 6 // 8 + n * (k // 32) + m * n * 2
+    flops, nbytes = prog.estimates.ops, prog.estimates.mem
     return {"workload": f"{fmt} e8m0/32 weight x bf16 GEMM M={m} N={n} K={k} bf16 out", "ms": ms,
             "TFLOPS": flops / ms / 1e9, "flops": flops, "bytes": nbytes, "GB/s": nbytes / ms / 1e6,
             "timed_dispatches": steps,
@@ -367,7 +360,8 @@ def cpu_baseline_fp4(budget_s: float) -> dict:
         return time.perf_counter() - t
 
     med, runs = _time_cpu(once, budget_s)
-    nbytes = gemv_bytes(n, k, m, 4, 1, 2, 2)
+    nbytes = P.weight_program(P.PackedDesc("fp4_e2m1", (n, k), n * k // 2, 1, "float8_e8m0fnu"), m, "bfloat16", k,
+                              "bfloat16", n).estimates.mem
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"the full fp4 e8m0/32 GEMV 14336x4096 M=1 (dequant to fp32 + fp32 GEMV + bf16), "
@@ -400,7 +394,8 @@ def cpu_baseline_int4(budget_s: float) -> dict:
         return time.perf_counter() - t
 
     med, runs = _time_cpu(once, budget_s)
-    nbytes = gemv_bytes(n, k, 1, 4, 2, 2, 2)
+    nbytes = P.weight_program(P.PackedDesc("int4", (n, k), n * k // 2, 1, "float16"), 1, "float16", k, "float16",
+                              n).estimates.mem
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"the whole int4 g32 GEMV 4096x4096 M=1 fp16 (dequant to fp32 + fp32 GEMV + fp16), "
