@@ -436,7 +436,7 @@ def profile_commands(workload: str) -> list[str]:
             f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o run -- {run}",
             f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o run -- {run}"]
     if "gemm" in workload:
-        cmds.append(f"rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES GRBM_GUI_ACTIVE --output-format csv "
+        cmds.append(f"rocprofv3 --pmc MfmaUtil SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE --output-format csv "
                     f"-d OUT/mfma -o run -- {run}")
     cmds += ["rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/cfetch -o copy -- python3 bench.py "
              "--copy-calibration 64 --steps 10",
@@ -506,13 +506,16 @@ def summarize_profile(folder: Path, workload: str) -> str:
         lines.append(f"algorithmic_flops_per_launch={flops}")
         lines.append(f"achieved_TFLOPS_from_timed_median={flops / median_ns / 1e3:.1f} "
                      f"(frac {flops / median_ns / 1e3 / roof['peak']:.4f} of {roof['peak']:.0f}, {roof['peak_of']})")
-        busy, nb = _counter(folder / "mfma", "SQ_VALU_MFMA_BUSY_CYCLES", pattern)
+        util, nb = _counter(folder / "mfma", "MfmaUtil", pattern)
+        busy, _ = _counter(folder / "mfma", "SQ_VALU_MFMA_BUSY_CYCLES", pattern)
         active, _ = _counter(folder / "mfma", "GRBM_GUI_ACTIVE", pattern)
-        sq_busy, _ = _counter(folder / "mfma", "SQ_BUSY_CYCLES", pattern)
-        lines.append(f"pmc SQ_VALU_MFMA_BUSY_CYCLES median {busy:.0f}, GRBM_GUI_ACTIVE {active:.0f}, SQ_BUSY_CYCLES "
-                     f"{sq_busy:.0f} ({nb} dispatches)")
-        lines.append(f"mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs) = "
-                     f"{busy / (active * 1024):.4f}")
+        lines.append(f"pmc MfmaUtil median {util:.2f} % ({nb} dispatches): rocprofv3's derived metric, "
+                     f"sum(SQ_VALU_MFMA_BUSY_CYCLES) / (max over XCCs of GRBM_GUI_ACTIVE x SIMD count)")
+        lines.append(f"pmc SQ_VALU_MFMA_BUSY_CYCLES median {busy:.0f} (summed over SIMDs), GRBM_GUI_ACTIVE {active:.0f} "
+                     f"(summed over the 8 XCCs)")
+        lines.append(f"shader clock during the kernel = GRBM_GUI_ACTIVE / 8 / timed median = "
+                     f"{active / 8 / median_ns:.3f} GHz; peak at that clock = {roof['peak'] * active / 8 / median_ns / 2.4:.0f} "
+                     f"TFLOP/s (the nominal peak is quoted at 2.4 GHz)")
     return "\n".join(lines) + "\n"
 
 

@@ -355,7 +355,8 @@ def _write_csv(path: Path, rows: list[dict]) -> None:
 def test_profile_summary_from_rocprof_csvs(tmp_path):
     """bench.py --summarize-profile on synthetic rocprofv3 CSVs: the timed dispatches are the last
     ones of the matching kernel, counters are medians per dispatch scaled by the copy calibration,
-    and the MFMA busy fraction is SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024)."""
+    MfmaUtil is reported as rocprofv3 derives it, and the shader clock is GRBM_GUI_ACTIVE (summed
+    over 8 XCCs) / 8 / the kernel's duration."""
     root = Path(__file__).resolve().parents[1]
     sys.path.insert(0, str(root))
     try:
@@ -386,13 +387,14 @@ def test_profile_summary_from_rocprof_csvs(tmp_path):
     for i in range(2):
         rows += [{"Dispatch_Id": i, "Kernel_Name": kernel, "Counter_Name": "SQ_VALU_MFMA_BUSY_CYCLES",
                   "Counter_Value": 512_000.0},
-                 {"Dispatch_Id": i, "Kernel_Name": kernel, "Counter_Name": "GRBM_GUI_ACTIVE", "Counter_Value": 1000.0},
-                 {"Dispatch_Id": i, "Kernel_Name": kernel, "Counter_Name": "SQ_BUSY_CYCLES", "Counter_Value": 900.0}]
+                 {"Dispatch_Id": i, "Kernel_Name": kernel, "Counter_Name": "GRBM_GUI_ACTIVE", "Counter_Value": 4_800_000.0},
+                 {"Dispatch_Id": i, "Kernel_Name": kernel, "Counter_Name": "MfmaUtil", "Counter_Value": 54.5}]
     _write_csv(tmp_path / "mfma" / "run_counter_collection.csv", rows)
     text = bench.summarize_profile(tmp_path, "fp4_gemm_8192")
     assert "timed: mean_ns=300000 median_ns=300000" in text
     # FETCH median 150000 KiB x 2 (copy: 32768 KiB read for 64 MiB) + WRITE 131072 KiB x 1
     assert f"traffic_bytes_per_launch={(150_000 * 2 + 131_072) * 1024}" in text
-    assert "mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs) = 0.5000" in text
+    assert "pmc MfmaUtil median 54.50 %" in text
+    assert "GRBM_GUI_ACTIVE / 8 / timed median = 2.000 GHz" in text  # 4.8e6 / 8 cycles in 300 us
     assert f"algorithmic_flops_per_launch={flops}" in text
-    assert "--only fp4_gemm_8192" in text and "--pmc SQ_VALU_MFMA_BUSY_CYCLES" in text
+    assert "--only fp4_gemm_8192" in text and "--pmc MfmaUtil SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE" in text
