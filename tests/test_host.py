@@ -245,6 +245,39 @@ def test_scaled_mfma_routes_reject_unsupported_pairs_without_a_gpu():
         K.call("tgm_gemm_fp8", 16, 9, 96, 64, 16, 10, 96, 64, 96, None, None, 16, 13, 64, None)
 
 
+def test_automatic_fallbacks_are_recorded_and_warned_once():
+    """auto falls back to the exact-width GEMM (linalg.py:219-223) but does not hide it: every
+    fallback is recorded with its reason, and one that drops a packed product or follows a
+    native rejection warns once per operand key; explicit scopes still raise."""
+    from tinygrad_mi355x.codegen import linalg
+    from tinygrad_mi355x.renderer.linalg import GEMV
+
+    linalg.fallbacks.clear()
+    linalg.matrix_failures.clear()
+
+    def rejected():
+        raise K.UnsupportedKernel("tgm_gemv: no kernel for this shape")
+
+    key = ("tgm_gemv", 1, "k1")
+    with pytest.warns(linalg.MatrixFallbackWarning, match="no kernel for this shape"):
+        assert linalg._dispatch(rejected, lambda: "plain", GEMV, "auto", key) == "plain"
+    assert linalg.fallbacks[key] == "tgm_gemv: no kernel for this shape" and key in linalg.matrix_failures
+    import warnings
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        assert linalg._dispatch(rejected, lambda: "plain", GEMV, "auto", key) == "plain"  # cached: no second warning
+        # an ordinary product with no native kernel is recorded without a warning
+        assert linalg._dispatch(None, lambda: "plain", None, "auto", (None, 2, "f32")) == "plain"
+    assert (None, 2, "f32") in linalg.fallbacks
+    with pytest.warns(linalg.MatrixFallbackWarning, match="no native kernel"):
+        linalg._dispatch(None, lambda: "plain", None, "auto", (None, 3, "packed"), True)
+    with pytest.raises(RuntimeError, match="candidate rejected"):
+        linalg._dispatch(rejected, lambda: "plain", GEMV, "Wave", key)
+    assert linalg._dispatch(None, lambda: "plain", None, "tiled", ("t",)) == "plain" and ("t",) not in linalg.fallbacks
+    linalg.fallbacks.clear()
+    linalg.matrix_failures.clear()
+
+
 def test_matrix_routing_table():
     """Static kernel choice (the analogue of the reference's LinAlg capability query,
     linalg.py:90-133): every FP4 / FP6 pair, scaled (E8M0 / 32) or not, takes the scaled MFMA;

@@ -25,6 +25,7 @@ express ``A @ W.T`` there (its ``b.shape[0] == K`` check, linalg.py:166).
 from __future__ import annotations
 
 import os
+import warnings
 
 import torch
 
@@ -201,23 +202,46 @@ def _mx_nt(a: PackedTensor, b: PackedTensor, out_dtype: torch.dtype) -> torch.Te
     return c
 
 
-def _dispatch(native, generic, kernel: MatrixKernel | None, scope: str, key: tuple):
-    """Run ``native`` when a kernel was chosen; auto falls back, explicit scopes raise (linalg.py:193-223)."""
+class MatrixFallbackWarning(UserWarning):
+    """A product of packed operands, or one a native kernel rejected, ran on the exact-width
+    device GEMM ``tgm_gemm_plain`` (decoded operands, scalar products) instead of a native
+    MFMA / GEMV kernel: correct, and much slower."""
+
+
+# Automatic fallbacks to the exact-width GEMM: operand key -> reason (each warned once).
+fallbacks: dict[tuple, str] = {}
+
+
+def _fall_back(generic, key: tuple, reason: str, warn: bool):
+    if key not in fallbacks:
+        fallbacks[key] = reason
+        if warn:
+            warnings.warn(f"MI355X matrix product on tgm_gemm_plain ({reason}); operands {key[1:]}",
+                          MatrixFallbackWarning, stacklevel=4)
+    return generic()
+
+
+def _dispatch(native, generic, kernel: MatrixKernel | None, scope: str, key: tuple, packed: bool = False):
+    """Run ``native`` when a kernel was chosen; auto falls back, explicit scopes raise
+    (linalg.py:193-223).  An automatic fallback is recorded in ``fallbacks`` and, for packed
+    operands or a native rejection, warned once per operand key (``MatrixFallbackWarning``)."""
     automatic = scope == "auto"
     if kernel is None:
-        if automatic or scope == "tiled":
+        if scope == "tiled":
             return generic()
+        if automatic:
+            return _fall_back(generic, key, "no native kernel for this operand combination", packed)
         raise RuntimeError(f"MI355X {scope} candidate rejected: no native kernel for this operand combination")
     if key in matrix_failures:
         if automatic:
-            return generic()
+            return _fall_back(generic, key, matrix_failures[key], True)
         raise RuntimeError(f"MI355X {scope} candidate rejected: {matrix_failures[key]}")
     try:
         return native()
     except (K.UnsupportedKernel, ValueError) as error:
         matrix_failures[key] = str(error)
         if automatic:
-            return generic()
+            return _fall_back(generic, key, str(error), True)
         raise RuntimeError(f"MI355X {scope} candidate rejected: {error}") from error
 
 
@@ -283,14 +307,14 @@ def matmul(a: torch.Tensor | PackedTensor, b: torch.Tensor | PackedTensor, scope
     if isinstance(a, PackedTensor) and isinstance(b, torch.Tensor):
         kernel = choose_matrix(a, b, intermediate, out_dtype, n, tile, scope)
         key = _key(kernel, a, b, out_dtype=out_dtype, m=n)
-        return _dispatch(lambda: _weight_left(kernel, a, b.t(), out_dtype).t(), generic, kernel, scope, key)
+        return _dispatch(lambda: _weight_left(kernel, a, b.t(), out_dtype).t(), generic, kernel, scope, key, True)
     if not packed:
         kernel = _dense_kernel(a, b, out_dtype, tile, scope)
         key = _key(kernel, a, b, out_dtype=out_dtype, m=m)
         # b [K, N]: a transposed view of a K-last tensor binds directly, a row-major one is staged
         native = lambda: dense_matmul_nt(a, b.t() if b.stride(0) == 1 else transpose16(b), out_dtype)  # noqa: E731
         return _dispatch(native, generic, kernel, scope, key)
-    return _dispatch(None, generic, None, scope, ())
+    return _dispatch(None, generic, None, scope, _key(None, a, b, out_dtype=out_dtype, m=m), True)
 
 
 def matmul_nt(a: torch.Tensor | PackedTensor, b: torch.Tensor | PackedTensor, scope: str = "auto",
@@ -329,15 +353,15 @@ def matmul_nt(a: torch.Tensor | PackedTensor, b: torch.Tensor | PackedTensor, sc
             native = lambda: _weight_left(family, b, a.unpack(torch.bfloat16), out_dtype)  # noqa: E731
         else:
             native = lambda: _mx_nt(a, b, out_dtype)  # noqa: E731
-        return _dispatch(native, generic, kernel, scope, key)
+        return _dispatch(native, generic, kernel, scope, key, True)
     if isinstance(b, PackedTensor):
         kernel = choose_matrix(b, a, intermediate, out_dtype, m, tile, scope)
         key = _key(kernel, b, a, out_dtype=out_dtype, m=m)
-        return _dispatch(lambda: _weight_left(kernel, b, a, out_dtype), generic, kernel, scope, key)
+        return _dispatch(lambda: _weight_left(kernel, b, a, out_dtype), generic, kernel, scope, key, True)
     if isinstance(a, PackedTensor):
         kernel = choose_matrix(a, b, intermediate, out_dtype, n, tile, scope)
         key = _key(kernel, a, b, out_dtype=out_dtype, m=n)
-        return _dispatch(lambda: _weight_left(kernel, a, b, out_dtype).t(), generic, kernel, scope, key)
+        return _dispatch(lambda: _weight_left(kernel, a, b, out_dtype).t(), generic, kernel, scope, key, True)
     kernel = _dense_kernel(a, b, out_dtype, tile, scope)
     key = _key(kernel, a, b, out_dtype=out_dtype, m=m)
     return _dispatch(lambda: dense_matmul_nt(a, b, out_dtype), generic, kernel, scope, key)
