@@ -47,7 +47,8 @@ ROTATION_BYTES = 600_000_000  # every GEMV copy set: > 2 x the 256 MB Infinity C
 MIN_TRIALS = 5
 
 EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_n4096", "int4_gemv_n14336", "fp6_e3m2_gemm_m2048",
-          "fp6_e2m3_gemm_m2048", "fp4_gemm_8192", "fp4_gemm_4096x14336x4096", "decoder_b1", "decoder_b8")
+          "fp6_e2m3_gemm_m2048", "fp4_gemm_8192", "fp4_gemm_4096x14336x4096", "decoder_b1", "decoder_b8",
+          "read_ceiling_31232000", "read_ceiling_470000000", "mfma_fp4_ceiling_8192")
 PRIMARY = "fp4_gemv_m1"
 
 # workload -> (committed rocprof summary, substring of the dominant kernel's name)
@@ -261,6 +262,46 @@ def fp6_gemm_workload(torch, K, dev, fmt: str, steps: int, warmup: int, m: int =
             "TFLOPS": flops / ms / 1e9, "flops": flops, "bytes": nbytes, "GB/s": nbytes / ms / 1e6,
             "timed_dispatches": steps,
             "roofline": mfma_roofline(flops, ms, BF16_PEAK_TFLOPS, "dense bf16 MFMA (the activations stay bf16)")}
+
+
+def read_ceiling_workload(torch, K, dev, nbytes: int, steps: int, warmup: int) -> dict:
+    """tgm_probe_read: ``nbytes`` read with the decode GEMV's access shape and discarded, over a
+    rotating copy set timed like the GEMV -- the single-launch read ceiling for that many bytes
+    (31,232,000 B: the FP4 decode GEMV's algorithmic bytes)."""
+    copies = copies_for(nbytes)
+    pool = torch.empty((copies, nbytes), dtype=torch.uint8, device=dev)
+    pool.fill_(1)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    lib = K.load_library()
+
+    def launch(i: int) -> None:
+        K.check("tgm_probe_read", lib.tgm_probe_read(pool[i % copies].data_ptr(), nbytes, sink.data_ptr(),
+                                                     K.stream_of(sink)))
+
+    ms, trials, timed = median_trials(torch, launch, steps, warmup, copies)
+    return {"workload": f"streaming read of {nbytes} B (the decode GEMV's access shape)", "ms": ms, "bytes": nbytes,
+            "GB/s": nbytes / ms / 1e6, "copies": copies, "trials": trials, "steps_per_trial": steps,
+            "timed_dispatches": timed, "roofline": hbm_roofline(nbytes, ms)}
+
+
+def mfma_ceiling_workload(torch, K, dev, steps: int, warmup: int) -> dict:
+    """tgm_probe_mfma_fp4 on the 8192^3 FP4 GEMM's grid (1024 workgroups of 8 waves, 2^23 FP4
+    MFMAs = the GEMM's 1.0995e12 flops), operands from registers changing every round: the FP4
+    MFMA ceiling with no data movement, timed like the GEMM."""
+    blocks, iters = 1024, 128
+    flops = blocks * 8 * iters * (1 << 20)
+    sink = torch.zeros(4, dtype=torch.float32, device=dev)
+    lib = K.load_library()
+    stream = torch.cuda.current_stream(dev)
+
+    def launch() -> None:
+        K.check("tgm_probe_mfma_fp4", lib.tgm_probe_mfma_fp4(blocks, iters, sink.data_ptr(), stream.cuda_stream))
+
+    settle(torch, stream, launch, warmup)
+    ms = median_launch_ms(torch, stream, launch, steps)
+    return {"workload": "FP4 scaled MFMA from registers, operands changing every round, on the 8192^3 GEMM's grid",
+            "ms": ms, "TFLOPS": flops / ms / 1e9, "flops": flops, "timed_dispatches": steps,
+            "roofline": mfma_roofline(flops, ms, FP4_PEAK_TFLOPS, "dense MXFP4 MFMA")}
 
 
 def decoder_workload(torch, dev, batch: int, prompt: int = 512, new_tokens: int = 128) -> dict:
@@ -555,6 +596,9 @@ def main() -> int:
         "fp4_gemm_4096x14336x4096": lambda: fp4_gemm_workload(torch, K, dev, 4096, 14336, 4096, gemm_steps, 20),
         "decoder_b1": lambda: decoder_workload(torch, dev, 1),
         "decoder_b8": lambda: decoder_workload(torch, dev, 8),
+        "read_ceiling_31232000": lambda: read_ceiling_workload(torch, K, dev, 31_232_000, steps, warmup),
+        "read_ceiling_470000000": lambda: read_ceiling_workload(torch, K, dev, 470_000_000, steps, warmup),
+        "mfma_fp4_ceiling_8192": lambda: mfma_ceiling_workload(torch, K, dev, gemm_steps, 20),
     }
     if args.only:
         print(json.dumps({args.only: workloads[args.only]()}))

@@ -307,6 +307,18 @@ int tgm_quantize_mx(const void* x, int x_dtype, int64_t rows, int64_t k, int fmt
  */
 int tgm_pack_codes(const void* codes, int64_t count, int bits, void* out, void* stream);
 
+/*
+ * Measurement probes (no reference counterpart; bench.py reports them beside the kernels they
+ * bound).  tgm_probe_read reads ``nbytes`` (a multiple of 16) with the decode GEMV's access
+ * shape -- contiguous 8 KB per wave, 16-byte non-temporal loads, all in flight -- and discards
+ * them: the single-launch read ceiling for that many bytes.  tgm_probe_mfma_fp4 runs ``blocks``
+ * workgroups of 8 waves, each wave ``iters`` rounds of 8 FP4 v_mfma_scale_f32_32x32x64_f8f6f4
+ * from registers with operand bits changing every round: the FP4 MFMA ceiling with no data
+ * movement (2^20 flops per wave and round).  ``sink`` is a 4-byte device scratch word.
+ */
+int tgm_probe_read(const void* p, int64_t nbytes, void* sink, void* stream);
+int tgm_probe_mfma_fp4(int64_t blocks, int64_t iters, void* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

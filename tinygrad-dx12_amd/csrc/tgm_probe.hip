@@ -1,0 +1,98 @@
+// Measurement probes: the ceilings the packed kernels are judged against on this machine.
+//
+// No reference counterpart (the reference has no kernels of its own to measure).  bench.py
+// times them like the kernels they bound:
+//
+//  * tgm_probe_read streams ``nbytes`` from device memory with the decode GEMV's access shape
+//    (each wave reads a contiguous run, 16 bytes per lane per instruction, all of a wave's loads
+//    in flight, non-temporal) and discards the data: the fastest a single launch can read the
+//    bytes a GEMV of that size must read.
+//  * tgm_probe_mfma_fp4 issues v_mfma_scale_f32_32x32x64_f8f6f4 on FP4 operands from registers
+//    only, with operand bits changing every instruction as a GEMM's do (the chip's power draw,
+//    and with it the clock it sustains, depends on operand toggling): the FP4 MFMA throughput
+//    the FP4 GEMM could reach with no data movement at all, on the GEMM's grid (1024
+//    workgroups of 8 waves at 8192^3).
+#include "tgm_mfma_common.h"
+
+namespace tgm {
+
+typedef unsigned u32x4p __attribute__((ext_vector_type(4)));
+
+constexpr int kProbeRun = 8;  // 1 KB loads per wave: 8 KB contiguous per wave
+
+__global__ void __launch_bounds__(256) probe_read(const unsigned char* __restrict__ p, int64_t nbytes,
+                                                  unsigned* __restrict__ sink) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t base = wave * kProbeRun * 1024;
+  u32x4p v[kProbeRun];
+#pragma unroll
+  for (int i = 0; i < kProbeRun; ++i) {
+    int64_t off = base + (int64_t)i * 1024 + 16 * lane;
+    off = off + 16 <= nbytes ? off : nbytes - 16;  // clamped inside the buffer
+    v[i] = __builtin_nontemporal_load((const u32x4p*)(p + off));
+  }
+  unsigned x = 0;
+#pragma unroll
+  for (int i = 0; i < kProbeRun; ++i) x ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3];
+  if (x == 0x9E3779B9u) sink[0] = x;  // keeps the loads; practically never stores
+}
+
+__global__ void __launch_bounds__(512) probe_mfma_fp4(int iters, unsigned seed, float* __restrict__ sink) {
+  const int lane = threadIdx.x & 63;
+  unsigned h = (blockIdx.x * 512u + threadIdx.x) * 2654435761u ^ seed;
+  int a[8], b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    h = h * 1664525u + 1013904223u;
+    a[i] = (int)h;
+    h = h * 1664525u + 1013904223u;
+    b[i] = (int)h;
+  }
+  const int sa = 124 + lane % 6, sb = 125 + lane % 5;  // E8M0 scales 2^-3 .. 2^2
+  f32x16 acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = f32x16{};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const i32x8 fa = {a[j & 3], a[(j + 1) & 3], a[(j + 2) & 3], a[(j + 3) & 3], 0, 0, 0, 0};
+      const i32x8 fb = {b[j & 7], b[(j + 1) & 7], b[(j + 2) & 7], b[(j + 3) & 7], 0, 0, 0, 0};
+      acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa, fb, acc[j], 4, 4, 0, sa, 0, sb);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // new operand bits for the next round
+      a[i] ^= it * 0x9E3779B9;
+      b[i] += it * 0x85EBCA6B;
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s += acc[j][0] + acc[j][15];
+  if (s == 1234.5f) sink[0] = s;  // keeps the MFMAs; practically never stores
+}
+
+}  // namespace tgm
+
+using namespace tgm;
+
+extern "C" int tgm_probe_read(const void* p, int64_t nbytes, void* sink, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(p && sink, "null operand");
+  TGM_CHECK_ARG(nbytes >= 16 && nbytes % 16 == 0, "nbytes must be a positive multiple of 16");
+  const int64_t per_block = 4 * kProbeRun * 1024;
+  const int64_t grid = (nbytes + per_block - 1) / per_block;
+  TGM_CHECK_ARG(grid < (1ll << 31), "too many bytes");
+  hipLaunchKernelGGL(probe_read, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, (const unsigned char*)p,
+                     nbytes, (unsigned*)sink);
+  return launch_status("tgm_probe_read");
+}
+
+extern "C" int tgm_probe_mfma_fp4(int64_t blocks, int64_t iters, void* sink, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(sink, "null operand");
+  TGM_CHECK_ARG(blocks > 0 && blocks < (1ll << 31) && iters > 0 && iters < (1ll << 31), "invalid sizes");
+  hipLaunchKernelGGL(probe_mfma_fp4, dim3((unsigned)blocks), dim3(512), 0, (hipStream_t)stream, (int)iters, 0x5EEDu,
+                     (float*)sink);
+  return launch_status("tgm_probe_mfma_fp4");
+}
