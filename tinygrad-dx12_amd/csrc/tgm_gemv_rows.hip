@@ -301,12 +301,18 @@ __global__ void __launch_bounds__(256) gemv_rows_fp4(const uint8_t* __restrict__
 
 // ------------------------------------------------------------------ INT4 / UINT4
 // Same row-streaming structure for 4-bit integer codes with fp16 activations and fp16 / bf16
-// / f32 group scales (groups of 32, 64 or 128 along K).  Codes become fp16 exactly: each
-// nibble n (n ^ 8 for int4) goes under the fp16 byte 0x64 (1024 + n) and a packed f16 add
-// removes 1024 (+ 8).  One v_perm builds a pair from two nibbles of the same byte lane,
-// so a dword's codes come out as pairs (0,2) (4,6) (1,3) (5,7); the activation pairs are
-// reordered the same way once, at load time.  v_dot2_f32_f16 products (fp16 x integer) are
-// exact in fp32; each lane's 32-code partial is then scaled by its group's scale in fp32.
+// / f32 group scales (groups of 32, 64 or 128 along K).  Each code becomes an fp16 subnormal
+// with one bitwise op: masking a dword with 0x000F000F leaves codes 0 and 4 at bits [3:0] of
+// each half, i.e. the fp16 values u * 2^-24; masking with 0x00F000F0 leaves codes 1 and 5 as
+// 16 u * 2^-24; the dword shifted right by 8 gives codes 2, 6 and 3, 7 the same way.  For
+// int4 the mask is followed by an xor of bit 3 of each nibble (v_bitop3 does both), which
+// stores u = code + 8, and the 8 * sum(x) this adds is taken off once per lane.  The
+// activations are paired (x0, x4) (x1, x5) (x2, x6) (x3, x7) to match, once per wave.
+// v_dot2_f32_f16 products of an fp16 subnormal (at most 4 significant bits) and an fp16
+// activation are exact in fp32, so codes 0/2/4/6 and 1/3/5/7 accumulate in two fp32 chains
+// scaled by 2^-24 and 2^-20, combined as chain0 + chain1 / 16 (exact scaling), multiplied by
+// the group's scale in fp32, and the row sum is scaled back by 2^24 (exact) before storing.
+// Nine VALU instructions per 8 codes: 1 shift, 4 bitop3 and 4 dot2.
 typedef _Float16 half2r __attribute__((ext_vector_type(2)));
 
 template <int SDT>
@@ -321,7 +327,7 @@ __device__ __forceinline__ float int4_scale(const unsigned char* p) {
 template <int R, int IPR, int D, int SDT, bool NORM = false>
 __global__ void __launch_bounds__(256) gemv_rows_int4(const uint8_t* __restrict__ w, int64_t N,
                                                     const uint8_t* __restrict__ scales, int GS, unsigned flip,
-                                                    float bias, const _Float16* __restrict__ x, void* __restrict__ y,
+                                                    const _Float16* __restrict__ x, void* __restrict__ y,
                                                     int ydt, RowsNorm nm) {
   constexpr int NI = R * IPR;
   constexpr int K = 2048 * IPR;
@@ -330,20 +336,29 @@ __global__ void __launch_bounds__(256) gemv_rows_int4(const uint8_t* __restrict_
   const int lane = threadIdx.x & 63;
   const int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
   // activations K [2048 h + 32 l, + 32) as the pairs the codes come out in: dword e of
-  // the lane's 16 bytes holds codes 8e .. 8e+7, paired (0,2) (4,6) (1,3) (5,7)
+  // the lane's 16 bytes holds codes 8e .. 8e+7, paired (0,4) (1,5) (2,6) (3,7); bias[h]
+  // = -8 sum(x) * 2^-24 over the lane's 32 activations of half-row h (int4; 0 for uint4)
   half2r xr[IPR][16];
+  float bias[IPR];
   auto load_x = [&](const _Float16* src) __attribute__((always_inline)) {
+    const half2r one = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
     for (int h = 0; h < IPR; ++h) {
       const unsigned* xp = (const unsigned*)(src + 2048 * h + 32 * lane);
+      float s0 = 0.f, s1 = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const unsigned p0 = xp[4 * e], p1 = xp[4 * e + 1], p2 = xp[4 * e + 2], p3 = xp[4 * e + 3];  // (0,1) (2,3) (4,5) (6,7)
-        xr[h][4 * e + 0] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p1, p0, 0x05040100u));  // x0, x2
-        xr[h][4 * e + 1] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p3, p2, 0x05040100u));  // x4, x6
-        xr[h][4 * e + 2] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p1, p0, 0x07060302u));  // x1, x3
-        xr[h][4 * e + 3] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p3, p2, 0x07060302u));  // x5, x7
+        xr[h][4 * e + 0] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p2, p0, 0x05040100u));  // x0, x4
+        xr[h][4 * e + 1] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p2, p0, 0x07060302u));  // x1, x5
+        xr[h][4 * e + 2] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p3, p1, 0x05040100u));  // x2, x6
+        xr[h][4 * e + 3] = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(p3, p1, 0x07060302u));  // x3, x7
+        s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2r, p0), one, s0, false);
+        s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2r, p1), one, s1, false);
+        s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2r, p2), one, s0, false);
+        s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2r, p3), one, s1, false);
       }
+      bias[h] = flip ? -0x1p-21f * (s0 + s1) : 0.f;
     }
   };
   NormRegs<NORM ? IPR : 1> nr;
@@ -395,33 +410,32 @@ __global__ void __launch_bounds__(256) gemv_rows_int4(const uint8_t* __restrict_
   if constexpr (NORM) norm_finish<IPR>(nm, nr, xs, red);
   else stage_finish<IPR>(xg, (unsigned char*)xs);
   load_x(xs);
-  const half2r hb = {(_Float16)bias, (_Float16)bias};
+  const unsigned xlo = flip & 0x00080008u, xhi = flip & 0x00800080u;  // bit 3 of the nibbles kept
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int slot = i % D, h = i % IPR;
-    float a[2] = {0.f, 0.f};
+    float a0 = bias[h], a1 = 0.f;  // codes 0,2,4,6 (units 2^-24) / 1,3,5,7 (units 2^-20)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const unsigned d = codes[slot][e] ^ flip;
-      const unsigned lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;  // codes 0,2,4,6 / 1,3,5,7
-      const half2r c0 = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(0x64646464u, lo, 0x05010400u)) - hb;  // 0, 2
-      const half2r c1 = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(0x64646464u, lo, 0x07030602u)) - hb;  // 4, 6
-      const half2r c2 = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(0x64646464u, hi, 0x05010400u)) - hb;  // 1, 3
-      const half2r c3 = __builtin_bit_cast(half2r, __builtin_amdgcn_perm(0x64646464u, hi, 0x07030602u)) - hb;  // 5, 7
-      a[e >> 1] = __builtin_amdgcn_fdot2(c0, xr[h][4 * e + 0], a[e >> 1], false);
-      a[e >> 1] = __builtin_amdgcn_fdot2(c1, xr[h][4 * e + 1], a[e >> 1], false);
-      a[e >> 1] = __builtin_amdgcn_fdot2(c2, xr[h][4 * e + 2], a[e >> 1], false);
-      a[e >> 1] = __builtin_amdgcn_fdot2(c3, xr[h][4 * e + 3], a[e >> 1], false);
+      const unsigned d = codes[slot][e], d8 = d >> 8;
+      const half2r c0 = __builtin_bit_cast(half2r, __builtin_amdgcn_bitop3_b32(d, 0x000F000Fu, xlo, 0x6A));   // (d & m) ^ x: 0, 4
+      const half2r c1 = __builtin_bit_cast(half2r, __builtin_amdgcn_bitop3_b32(d, 0x00F000F0u, xhi, 0x6A));   // 1, 5
+      const half2r c2 = __builtin_bit_cast(half2r, __builtin_amdgcn_bitop3_b32(d8, 0x000F000Fu, xlo, 0x6A));  // 2, 6
+      const half2r c3 = __builtin_bit_cast(half2r, __builtin_amdgcn_bitop3_b32(d8, 0x00F000F0u, xhi, 0x6A));  // 3, 7
+      a0 = __builtin_amdgcn_fdot2(c0, xr[h][4 * e + 0], a0, false);
+      a1 = __builtin_amdgcn_fdot2(c1, xr[h][4 * e + 1], a1, false);
+      a0 = __builtin_amdgcn_fdot2(c2, xr[h][4 * e + 2], a0, false);
+      a1 = __builtin_amdgcn_fdot2(c3, xr[h][4 * e + 3], a1, false);
     }
-    const float part = a[0] + a[1];
+    const float part = __builtin_fmaf(a1, 0.0625f, a0);
     acc[i / IPR] = SCALED ? __builtin_fmaf(sv[i], part, acc[i / IPR]) : acc[i / IPR] + part;
     if (i + D < NI) load(i + D, slot);
     __builtin_amdgcn_sched_barrier(0);
   }
-  const float v = reduce_rows<R>(acc, lane);
+  const float v = reduce_rows<R>(acc, lane) * 0x1p24f;
   const int64_t row = r0 + reduce_row<R>(lane);
   if ((lane & (64 / R - 1)) == 0 && row < N) store_from_f32(y, ydt, row, v);
 }
@@ -468,8 +482,7 @@ void launch_rows_int4(unsigned grid, hipStream_t s, const void* w, int64_t n, co
                       const void* x, void* y, int ydt) {
   constexpr int R = kRowsPerWaveInt4, D = R * IPR;  // every load in flight at once
   hipLaunchKernelGGL((gemv_rows_int4<R, IPR, D, SDT>), dim3(grid), dim3(256), 0, s, (const uint8_t*)w, n,
-                     (const uint8_t*)scales, gs, sgn ? 0x88888888u : 0u, sgn ? 1032.0f : 1024.0f,
-                     (const _Float16*)x, y, ydt, RowsNorm{});
+                     (const uint8_t*)scales, gs, sgn ? 0x88888888u : 0u, (const _Float16*)x, y, ydt, RowsNorm{});
 }
 
 template <int IPR>
@@ -532,7 +545,7 @@ static int launch_norm_rows(hipStream_t s, const void* w, int fmt, int64_t n, co
   const bool sgn = fmt == TGM_FMT_INT4;
 #define TGM_NORM_I4(SDT)                                                                                          \
   hipLaunchKernelGGL((gemv_rows_int4<R, IPR, D, SDT, true>), dim3(grid), dim3(256), 0, s, (const uint8_t*)w, n,  \
-                     (const uint8_t*)scales, gs, sgn ? 0x88888888u : 0u, sgn ? 1032.0f : 1024.0f,              \
+                     (const uint8_t*)scales, gs, sgn ? 0x88888888u : 0u,                                     \
                      (const _Float16*)nullptr, y, ydt, nm)
   if (!scales) TGM_NORM_I4(-1);
   else if (sdt == TGM_F16) TGM_NORM_I4(TGM_F16);
