@@ -69,22 +69,28 @@ constexpr int kScaleNone = 0, kScaleDword = 1, kScaleGroup4 = 2;
 // 4-byte aligned 16-byte vector: global_load_dwordx4 needs only dword alignment on gfx950.
 typedef unsigned u32x4a __attribute__((ext_vector_type(4), aligned(4)));
 
+// Weight codes are read once per launch: non-temporal loads keep them from evicting the
+// activations and scales that every workgroup reads from L2.
 template <int FMT>
 __device__ __forceinline__ void load_codes(const uint8_t* p, unsigned out[6]) {
   if constexpr (FMT == TGM_FMT_FP4_E2M1) {
-    const u32x4 v = *(const u32x4*)p;
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
     out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3]; out[4] = 0; out[5] = 0;
   } else {
-    const u32x2 a = *(const u32x2*)p;
-    const u32x2 b = *(const u32x2*)(p + 8);
-    const u32x2 c = *(const u32x2*)(p + 16);
+    const u32x2 a = __builtin_nontemporal_load((const u32x2*)p);
+    const u32x2 b = __builtin_nontemporal_load((const u32x2*)(p + 8));
+    const u32x2 c = __builtin_nontemporal_load((const u32x2*)(p + 16));
     out[0] = a[0]; out[1] = a[1]; out[2] = b[0]; out[3] = b[1]; out[4] = c[0]; out[5] = c[1];
   }
 }
 
-// Streaming MX GEMV.  A workgroup holds NT x NK waves: wave (ti, ki) owns weight tile
-// blockIdx.x * NT + ti (16 rows) and the ki-th of NK contiguous slices of its K
-// super-steps, at most SMAX of them.  The slice is walked by a fully unrolled loop (all
+// Streaming MX GEMV.  A workgroup owns RPW consecutive weight rows (RPW <= 16 NT, a
+// multiple of 4) and holds NT x NK waves: wave (ti, ki) owns the 16-row tile starting at
+// row blockIdx.x * RPW + 16 ti (rows past the workgroup's range are clamped to its last
+// row and not stored) and the ki-th of NK contiguous slices of its K super-steps, at most
+// SMAX of them.  RPW below 16 NT spreads a matrix whose tile count is not a multiple of NT
+// times the CU count evenly over the CUs (14336 rows: 256 workgroups of 56 rows instead of
+// 224 of 64).  The slice is walked by a fully unrolled loop (all
 // register indices are compile-time constants) with a ring of D super-steps of weights
 // in flight: the load refilling a ring slot is issued right after the slot's MFMAs, so
 // every wave keeps D x 1 KB (FP4) outstanding and consumes data in arrival order.
@@ -108,7 +114,8 @@ template <int FMT, int NT, int NK, int RING, int SMAX, bool EXACT, int XV, int S
 __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __restrict__ w, int64_t N, int64_t K,
                                                           const uint8_t* __restrict__ scales, int64_t nblk,
                                                           const __bf16* __restrict__ x, int M, int64_t ldx,
-                                                          void* __restrict__ y, int ydt, int64_t ldy, int swiglu) {
+                                                          void* __restrict__ y, int ydt, int64_t ldy, int swiglu,
+                                                          int rpw) {
   static_assert(SMAX % 4 == 0, "scale groups");
   constexpr int D = RING < SMAX ? RING : SMAX;  // ring depth
   constexpr bool SCALED = SC != kScaleNone, SG4 = SC == kScaleGroup4, XLDS = XV > 0;
@@ -121,8 +128,10 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __res
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps K control flow scalar
   const int ti = wave % NT, ki = wave / NT;
   const int r = lane & 15, q = lane >> 4;
-  const int64_t n0 = ((int64_t)blockIdx.x * NT + ti) * 16;
-  const int64_t row = n0 + r < N ? n0 + r : N - 1;  // clamped: rows >= N are computed but not stored
+  const int64_t wg0 = (int64_t)blockIdx.x * rpw;
+  const int64_t wg_end = wg0 + rpw < N ? wg0 + rpw : N;  // rows of this workgroup: [wg0, wg_end)
+  const int64_t n0 = wg0 + 16 * ti;
+  const int64_t row = n0 + r < wg_end ? n0 + r : wg_end - 1;  // clamped rows are computed but not stored
   const int64_t row_bytes = K * format_info(FMT).bits / 8;
   const unsigned* srow = (const unsigned*)(scales + row * nblk);  // dereferenced only when SCALED
   const int S = (int)(K / 128);
@@ -270,7 +279,7 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __res
       const int64_t nb = n0 + 4 * q;
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        if (nb + 2 * i + 1 < N) {
+        if (nb + 2 * i + 1 < wg_end) {
           const float g = sum[2 * i], u = sum[2 * i + 1];
           store_out(y, ydt, (int64_t)c * ldy + nb / 2 + i, g / (1.0f + expf(-g)) * u);
         }
@@ -280,7 +289,7 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __res
   if (c < M) {
     const int64_t nb = n0 + 4 * q;
     const int64_t o = (int64_t)c * ldy + nb;
-    if (nb + 3 < N && (o & 3) == 0) {
+    if (nb + 3 < wg_end && (o & 3) == 0) {
       if (ydt == TGM_F32) {
         *(f32x4*)((float*)y + o) = sum;
       } else {
@@ -299,7 +308,7 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __res
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (nb + i < N) store_out(y, ydt, o + i, sum[i]);
+        if (nb + i < wg_end) store_out(y, ydt, o + i, sum[i]);
     }
   }
 }
@@ -307,6 +316,19 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __res
 constexpr int kGemvRing = 8;            // super-steps of weights in flight per wave
 constexpr int kGemvRingX = 4;           // the same when the activations ride in the ring
 constexpr size_t kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
+
+// Compute units of the current device (cached per device; 0 if the query fails).
+inline int device_cus() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = v;
+  }
+  return cached[dev];
+}
 
 // Launch shape of the streaming GEMV: eight waves per workgroup, NT 16-row tiles x NK
 // slices of K, at most 32 super-steps per wave.  Shapes are tried in an order that
@@ -336,7 +358,7 @@ inline GemvShape gemv_shape(int64_t tiles, int64_t S, bool sg4) {
 
 template <int FMT, int NT, int NK, int SMAX, bool EXACT, int XV, int SC>
 int launch_stream(unsigned grid, size_t lds, hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales,
-                  int64_t nblk, const void* x, int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu) {
+                  int64_t nblk, const void* x, int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu, int rpw) {
   auto kernel = gemv_stream<FMT, NT, NK, (XV > 0 ? kGemvRing : kGemvRingX), SMAX, EXACT, XV, SC>;
   if (lds > 64 * 1024) {
     static bool raised = false;  // per instantiation
@@ -350,7 +372,7 @@ int launch_stream(unsigned grid, size_t lds, hipStream_t s, const void* w, int64
     }
   }
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(NT * NK * 64), lds, s, (const uint8_t*)w, n, k, (const uint8_t*)scales,
-                     nblk, (const __bf16*)x, (int)m, ldx, y, ydt, ldy, swiglu);
+                     nblk, (const __bf16*)x, (int)m, ldx, y, ydt, ldy, swiglu, rpw);
   return TGM_OK;
 }
 
@@ -358,27 +380,27 @@ int launch_stream(unsigned grid, size_t lds, hipStream_t s, const void* w, int64
 template <int FMT, int NT, int NK, int SMAX, bool EXACT, int SC>
 int launch_stream_xv(int xv, unsigned grid, size_t lds, hipStream_t s, const void* w, int64_t n, int64_t k,
                      const void* scales, int64_t nblk, const void* x, int64_t m, int64_t ldx, void* y, int ydt,
-                     int64_t ldy, int swiglu) {
-  if (xv == 2) return launch_stream<FMT, NT, NK, SMAX, EXACT, 2, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
-  if (xv == 8) return launch_stream<FMT, NT, NK, SMAX, EXACT, 8, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
-  if (xv == 16) return launch_stream<FMT, NT, NK, SMAX, EXACT, 16, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
-  return launch_stream<FMT, NT, NK, SMAX, EXACT, 0, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
+                     int64_t ldy, int swiglu, int rpw) {
+  if (xv == 2) return launch_stream<FMT, NT, NK, SMAX, EXACT, 2, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  if (xv == 8) return launch_stream<FMT, NT, NK, SMAX, EXACT, 8, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  if (xv == 16) return launch_stream<FMT, NT, NK, SMAX, EXACT, 16, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  return launch_stream<FMT, NT, NK, SMAX, EXACT, 0, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
 }
 
 template <int FMT, int NT, int NK>
 int launch_stream_shape(const GemvShape& g, int sc, int xv, unsigned grid, size_t lds, hipStream_t s, const void* w,
                         int64_t n, int64_t k, const void* scales, int64_t nblk, const void* x, int64_t m, int64_t ldx,
-                        void* y, int ydt, int64_t ldy, int swiglu) {
+                        void* y, int ydt, int64_t ldy, int swiglu, int rpw) {
   if (g.exact) {  // block-32 E8M0 scales in groups of four, slices of exactly SMAX super-steps
 #define TGM_EXACT(SMAX) \
-    if (g.smax == SMAX) return launch_stream_xv<FMT, NT, NK, SMAX, true, kScaleGroup4>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
+    if (g.smax == SMAX) return launch_stream_xv<FMT, NT, NK, SMAX, true, kScaleGroup4>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
     TGM_EXACT(4) TGM_EXACT(8) TGM_EXACT(16) TGM_EXACT(28) TGM_EXACT(32)
 #undef TGM_EXACT
     return TGM_E_UNSUPPORTED;
   }
-  if (sc == kScaleGroup4) return launch_stream_xv<FMT, NT, NK, 32, false, kScaleGroup4>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
-  if (sc == kScaleDword) return launch_stream_xv<FMT, NT, NK, 32, false, kScaleDword>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
-  return launch_stream_xv<FMT, NT, NK, 32, false, kScaleNone>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
+  if (sc == kScaleGroup4) return launch_stream_xv<FMT, NT, NK, 32, false, kScaleGroup4>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  if (sc == kScaleDword) return launch_stream_xv<FMT, NT, NK, 32, false, kScaleDword>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  return launch_stream_xv<FMT, NT, NK, 32, false, kScaleNone>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
 }
 
 // swiglu: the weight rows interleave gate and up rows; y gets silu(gate) * up (N / 2 columns).
@@ -389,7 +411,6 @@ int launch_gemv_stream(hipStream_t s, const void* w, int64_t n, int64_t k, const
   const int sc = scales == nullptr ? kScaleNone : (k % 512 == 0 ? kScaleGroup4 : kScaleDword);
   const GemvShape g = gemv_shape(tiles, k / 128, sc == kScaleGroup4);
   if (g.nt == 0) return TGM_E_UNSUPPORTED;
-  const unsigned grid = (unsigned)((tiles + g.nt - 1) / g.nt);
   const size_t part = (size_t)g.nt * g.nk * 64 * 16;
   const size_t xbytes = (size_t)m * (size_t)(k + 8) * 2;
   const bool xlds = part + xbytes <= kMaxLds;
@@ -399,9 +420,23 @@ int launch_gemv_stream(hipStream_t s, const void* w, int64_t n, int64_t k, const
   const int xv = !xlds ? 0 : passes <= 2 ? 2 : passes <= 8 ? 8 : 16;
   const size_t lds = part + (xlds ? xbytes : 0);
   const int64_t nblk = k / 32;
-  if (g.nt == 4) return launch_stream_shape<FMT, 4, 2>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
-  if (g.nt == 2) return launch_stream_shape<FMT, 2, 4>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
-  return launch_stream_shape<FMT, 1, 8>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu);
+  // Rows per workgroup: 16 NT, unless the workgroups would leave part of the last round of
+  // CUs idle; then the rows are spread evenly over whole rounds (a multiple of 4 rows each).
+  int rpw = 16 * g.nt;
+  int64_t wgs = (n + rpw - 1) / rpw;
+  const int cus = device_cus();
+  if (cus > 0 && wgs % cus != 0) {
+    const int64_t rounds = (wgs + cus - 1) / cus;
+    const int64_t even = ((n + rounds * cus - 1) / (rounds * cus) + 3) / 4 * 4;
+    if (even > 16 * (g.nt - 1) && even < rpw) {  // every tile of the shape keeps rows
+      rpw = (int)even;
+      wgs = (n + rpw - 1) / rpw;
+    }
+  }
+  const unsigned grid = (unsigned)wgs;
+  if (g.nt == 4) return launch_stream_shape<FMT, 4, 2>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  if (g.nt == 2) return launch_stream_shape<FMT, 2, 4>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  return launch_stream_shape<FMT, 1, 8>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
 }
 
 // Instantiated once per format in its own translation unit.
