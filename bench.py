@@ -48,7 +48,8 @@ MIN_TRIALS = 5
 
 EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_n4096", "int4_gemv_n14336", "fp6_e3m2_gemm_m2048",
           "fp6_e2m3_gemm_m2048", "fp4_gemm_8192", "fp4_gemm_4096x14336x4096", "decoder_b1", "decoder_b8",
-          "read_ceiling_31232000", "read_ceiling_470000000", "mfma_fp4_ceiling_8192")
+          "read_ceiling_31232000", "read_ceiling_470000000", "mfma_fp4_ceiling_8192", "bf16_gemm_8192",
+          "fp8_gemm_8192")
 PRIMARY = "fp4_gemv_m1"
 
 # workload -> (committed rocprof summary, substring of the dominant kernel's name)
@@ -262,6 +263,47 @@ def fp6_gemm_workload(torch, K, dev, fmt: str, steps: int, warmup: int, m: int =
             "TFLOPS": flops / ms / 1e9, "flops": flops, "bytes": nbytes, "GB/s": nbytes / ms / 1e6,
             "timed_dispatches": steps,
             "roofline": mfma_roofline(flops, ms, BF16_PEAK_TFLOPS, "dense bf16 MFMA (the activations stay bf16)")}
+
+
+def dense_gemm_workload(torch, K, dev, dtype: str, n: int, steps: int, warmup: int) -> dict:
+    """Ordinary product C[N,N] = A B^T (A, B [N, N], K-contiguous) on this library's kernel
+    (tgm_gemm_dense for bf16, tgm_gemm_fp8 for float8_e4m3fn with per-tensor scales 1), bf16 out,
+    with hipBLASLt timed on the same operands in the same run for comparison (torch.matmul for
+    bf16, torch._scaled_mm for fp8)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    tdt = getattr(torch, dtype)
+    a = torch.randn((n, n), device=dev, generator=g).to(tdt)
+    b = torch.randn((n, n), device=dev, generator=g).to(tdt)
+    c = torch.empty((n, n), dtype=torch.bfloat16, device=dev)
+    one = torch.ones((), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    fp8 = dtype.startswith("float8")
+    prog = (P.dense_program(dtype, n, n, dtype, n, n, n, "bfloat16", n, one.data_ptr(), one.data_ptr()) if fp8
+            else P.dense_program(dtype, n, n, dtype, n, n, n, "bfloat16", n))
+
+    def launch() -> None:
+        prog.launch(c.data_ptr(), a.data_ptr(), b.data_ptr(), stream.cuda_stream)
+
+    settle(torch, stream, launch, warmup)
+    ms = median_launch_ms(torch, stream, launch, steps)
+    bt = b.t()  # column-major [K, N] view: hipBLASLt's natural B layout for C = A B^T
+    if fp8:
+        def library() -> None:
+            torch._scaled_mm(a, bt, scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+    else:
+        bt_c = bt.contiguous()
+
+        def library() -> None:
+            torch.matmul(a, bt_c)
+    settle(torch, stream, library, warmup)
+    lib_ms = median_launch_ms(torch, stream, library, steps)
+    flops, nbytes = prog.estimates.ops, prog.estimates.mem
+    peak = 5000.0 if fp8 else BF16_PEAK_TFLOPS
+    return {"workload": f"{dtype} x {dtype} GEMM M=N=K={n} bf16 out ({prog.name})", "ms": ms,
+            "TFLOPS": flops / ms / 1e9, "flops": flops, "bytes": nbytes, "timed_dispatches": steps,
+            "hipblaslt_ms": lib_ms, "hipblaslt_TFLOPS": flops / lib_ms / 1e9,
+            "roofline": mfma_roofline(flops, ms, peak, "dense fp8 MFMA" if fp8 else "dense bf16 MFMA")}
 
 
 def read_ceiling_workload(torch, K, dev, nbytes: int, steps: int, warmup: int) -> dict:
@@ -599,6 +641,8 @@ def main() -> int:
         "read_ceiling_31232000": lambda: read_ceiling_workload(torch, K, dev, 31_232_000, steps, warmup),
         "read_ceiling_470000000": lambda: read_ceiling_workload(torch, K, dev, 470_000_000, steps, warmup),
         "mfma_fp4_ceiling_8192": lambda: mfma_ceiling_workload(torch, K, dev, gemm_steps, 20),
+        "bf16_gemm_8192": lambda: dense_gemm_workload(torch, K, dev, "bfloat16", 8192, gemm_steps, 20),
+        "fp8_gemm_8192": lambda: dense_gemm_workload(torch, K, dev, "float8_e4m3fn", 8192, gemm_steps, 20),
     }
     if args.only:
         print(json.dumps({args.only: workloads[args.only]()}))
