@@ -41,29 +41,35 @@ __global__ void __launch_bounds__(256) probe_read(const unsigned char* __restric
 __global__ void __launch_bounds__(512) probe_mfma_fp4(int iters, unsigned seed, float* __restrict__ sink) {
   const int lane = threadIdx.x & 63;
   unsigned h = (blockIdx.x * 512u + threadIdx.x) * 2654435761u ^ seed;
-  int a[8], b[8];
+  // four operand tuples held in place (no per-instruction register copies); consecutive MFMAs
+  // alternate between them and one dword of each changes every round
+  i32x8 ta[2], tb[2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    h = h * 1664525u + 1013904223u;
-    a[i] = (int)h;
-    h = h * 1664525u + 1013904223u;
-    b[i] = (int)h;
-  }
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h = h * 1664525u + 1013904223u;
+      ta[t][i] = (int)h;
+      h = h * 1664525u + 1013904223u;
+      tb[t][i] = (int)h;
+      ta[t][4 + i] = 0;
+      tb[t][4 + i] = 0;
+    }
   const int sa = 124 + lane % 6, sb = 125 + lane % 5;  // E8M0 scales 2^-3 .. 2^2
   f32x16 acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = f32x16{};
-  for (int it = 0; it < iters; ++it) {
+  for (int it = 0; it < iters; it += 4) {  // iters is a multiple of 4 (host)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const i32x8 fa = {a[j & 3], a[(j + 1) & 3], a[(j + 2) & 3], a[(j + 3) & 3], 0, 0, 0, 0};
-      const i32x8 fb = {b[j & 7], b[(j + 1) & 7], b[(j + 2) & 7], b[(j + 3) & 7], 0, 0, 0, 0};
-      acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa, fb, acc[j], 4, 4, 0, sa, 0, sb);
-    }
+    for (int r = 0; r < 4; ++r) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {  // new operand bits for the next round
-      a[i] ^= it * 0x9E3779B9;
-      b[i] += it * 0x85EBCA6B;
+      for (int j = 0; j < 8; ++j)
+        acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ta[j & 1], tb[(j >> 1) & 1], acc[j], 4, 4, 0, sa, 0, sb);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {  // new operand bits for the next round
+        ta[t][r] ^= (int)(0x9E3779B9u * (unsigned)(it + r + 1));
+        tb[t][(r + 1) & 3] += (int)(0x85EBCA6Bu * (unsigned)(it + r + 2));
+      }
     }
   }
   float s = 0.f;
@@ -91,7 +97,8 @@ extern "C" int tgm_probe_read(const void* p, int64_t nbytes, void* sink, void* s
 extern "C" int tgm_probe_mfma_fp4(int64_t blocks, int64_t iters, void* sink, void* stream) {
   clear_error();
   TGM_CHECK_ARG(sink, "null operand");
-  TGM_CHECK_ARG(blocks > 0 && blocks < (1ll << 31) && iters > 0 && iters < (1ll << 31), "invalid sizes");
+  TGM_CHECK_ARG(blocks > 0 && blocks < (1ll << 31) && iters > 0 && iters < (1ll << 31) && iters % 4 == 0,
+                "invalid sizes (iters a positive multiple of 4)");
   hipLaunchKernelGGL(probe_mfma_fp4, dim3((unsigned)blocks), dim3(512), 0, (hipStream_t)stream, (int)iters, 0x5EEDu,
                      (float*)sink);
   return launch_status("tgm_probe_mfma_fp4");
