@@ -63,6 +63,11 @@ PROFILES = {
     "fp6_e2m3_gemm_m2048": ("gemm_w_fp6_e2m3_m2048_n11008_k4096.txt", "gemm_w_mx"),
     "fp4_gemm_8192": ("gemm_mx_fp4_m8192_n8192_k8192.txt", "gemm_mx"),
     "fp4_gemm_4096x14336x4096": ("gemm_mx_fp4_m4096_n14336_k4096.txt", "gemm_mx"),
+    "bf16_gemm_8192": ("gemm_dense_bf16_m8192_n8192_k8192.txt", "gemm_dense"),
+    "fp8_gemm_8192": ("gemm_dense_fp8_e4m3_m8192_n8192_k8192.txt", "gemm_dense"),
+    "read_ceiling_31232000": ("probe_read_31232000.txt", "probe_read"),
+    "read_ceiling_470000000": ("probe_read_470000000.txt", "probe_read"),
+    "mfma_fp4_ceiling_8192": ("probe_mfma_fp4_1024x512.txt", "probe_mfma_fp4"),
 }
 
 
@@ -518,7 +523,7 @@ def profile_commands(workload: str) -> list[str]:
     cmds = [f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o run -- {run}",
             f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o run -- {run}",
             f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o run -- {run}"]
-    if "gemm" in workload:
+    if "gemm" in workload or "mfma" in workload:
         cmds.append(f"rocprofv3 --pmc MfmaUtil SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE --output-format csv "
                     f"-d OUT/mfma -o run -- {run}")
     cmds += ["rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/cfetch -o copy -- python3 bench.py "
