@@ -96,7 +96,12 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __res
   // costs a cache-line access per row and step -- as many as the operand panels themselves --
   // and measured half again the panels' load time; batches of four cut that to a quarter.
   // Bytes past the end of a row (K not a multiple of 1024) belong to steps that do not exist.
-  const unsigned vbat = (unsigned)((lane & 1) * 16);
+  // The two 16-byte halves of a row's batch (steps 4b, 4b + 1 and steps 4b + 2, 4b + 3) are
+  // swapped in LDS on rows with bit 3 set.  A step's 8-byte reads of 32 consecutive rows (32
+  // bytes apart) then fall on 16 distinct 8-byte bank pairs of the 64 banks, two rows each,
+  // instead of 8 (rows r and r + 8 share banks).  Lane l writes slot l & 1 of row
+  // 32 g + (l >> 1) and so fetches half (l & 1) ^ ((l >> 4) & 1).
+  const unsigned vbat = (unsigned)(((lane & 1) ^ ((lane >> 4) & 1)) * 16);
   auto issue_batch = [&](int b) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 8 / NW; ++i) {
@@ -139,8 +144,13 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __res
     if (t < FA) f.a[t < FA ? t : 0] = *(const u32x4*)(la + fa_row + col + t * 32 * kRowBytes);
     else f.b[t < FA ? 0 : t - FA] = *(const u32x4*)(la + kPanel + fb_row + col + (t - FA) * 32 * kRowBytes);
   };
+  // Step sn's 8 bytes of row r sit in half ((sn % 4) >> 1) ^ ((r >> 3) & 1) of the row's batch; the
+  // rows a lane reads are 32 t + (l & 31) past a multiple of 32, so (r >> 3) & 1 = (l >> 3) & 1.
+  const int sq = (lane >> 3) & 1;
   auto scale_item = [&](int sn, int t) __attribute__((always_inline)) {  // scales of step sn
-    const unsigned char* ls = lds + 2 * kBuffer + ((sn / kBatchSteps) & 1) * kBatch + (sn % kBatchSteps) * 8;
+    const int st = sn % kBatchSteps;
+    const unsigned char* ls =
+        lds + 2 * kBuffer + ((sn / kBatchSteps) & 1) * kBatch + ((st >> 1) ^ sq) * 16 + (st & 1) * 8;
     if (t < FA) scl_a[t < FA ? t : 0] = *(const u32x2*)(ls + (wm * FA * 32 + t * 32 + (lane & 31)) * kBatchRow);
     else scl_b[t < FA ? 0 : t - FA] =
         *(const u32x2*)(ls + kBM * kBatchRow + (wn * FB * 32 + (t - FA) * 32 + (lane & 31)) * kBatchRow);
