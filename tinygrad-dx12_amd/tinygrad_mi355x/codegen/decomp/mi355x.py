@@ -35,13 +35,15 @@ FP8_CANDIDATES = {
 
 @dataclass(frozen=True)
 class PackedTensor:
-    """A contiguous low-bit tensor stored least-significant payload first in bytes.
+    """Packed low-bit weights on the HIP device (dx12.py:14-47).
 
-    ``shape`` gives logical elements while ``data`` is a flat uint8 tensor.  Six-bit
-    elements may straddle bytes.  FP4 and FP6 use finite OCP payloads.  Optional
-    numeric ``scales`` have shape ``shape[:-1] + (ceil(K/block_size),)``; each scale
-    multiplies one block along the last dimension.  Scales may be any numeric dtype,
-    including ``torch.float8_e8m0fnu`` for OCP MX shared exponents.
+    ``data`` is one flat uint8 device tensor holding every code of the row-major
+    ``shape`` back to back as a bit stream, lowest bits first: two 4-bit codes per byte,
+    four 6-bit codes per three bytes (a 6-bit code can cross a byte boundary).  The FP4
+    and FP6 codes are the OCP formats without infinities or NaNs.  ``scales``, when
+    given, hold one factor per ``block_size`` consecutive codes along the last axis
+    (shape ``shape[:-1] + (ceil(K / block_size),)``), in any numeric dtype; E8M0 bytes
+    (``torch.float8_e8m0fnu``) are OCP MX shared exponents.
     """
 
     data: torch.Tensor
