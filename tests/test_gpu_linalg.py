@@ -28,6 +28,15 @@ def bf16_np(t: torch.Tensor) -> np.ndarray:
     return t.float().cpu().numpy()
 
 
+def host_dequant_rows(p: PackedTensor, rows) -> np.ndarray:
+    """Exact fp64 values of the selected rows of a 2-D MX PackedTensor, decoded by the oracle from
+    the host copy of its packed bytes and E8M0 scale bytes (no device decode involved)."""
+    n, k = p.shape
+    data = p.data.cpu().numpy().reshape(n, -1)[rows].reshape(-1)
+    e = p.scales.view(torch.uint8).cpu().numpy()[rows]
+    return O.dequant_f64(data, p.format, (len(rows), k), O.e8m0_decode(e), p.block_size)
+
+
 # ----------------------------------------------------------------------------- known answers
 def test_scales_stay_with_k_blocks(dev):
     case = GOLDEN["scales_stay_with_k_blocks"]
@@ -439,7 +448,8 @@ def test_gemm_w_one_hot_is_exact(dev, fmt):
 @pytest.mark.parametrize("fmt", ["fp6_e3m2", "fp6_e2m3"])
 def test_gemm_w_fp6_2048x11008x4096_full_size_sampled(dev, fmt):
     """The FP6 prefill GEMM at full size: A bf16 [2048, 4096], W = MX-quantised N(0, 0.02) [11008, 4096]
-    (block-32 E8M0); 64 x 512 sampled outputs against the exact-dequant fp64 oracle."""
+    (block-32 E8M0); 64 x 512 sampled outputs against the fp64 oracle, which decodes the sampled W rows
+    from the host copy of the packed bytes."""
     m, n, k = 2048, 11008, 4096
     g = torch.Generator(device=dev)
     g.manual_seed(3)
@@ -448,7 +458,7 @@ def test_gemm_w_fp6_2048x11008x4096_full_size_sampled(dev, fmt):
     c = matmul_nt(a, w, scope="ThreadGroup", dtype=torch.bfloat16)
     rng = np.random.default_rng(5)
     rows, cols = rng.choice(m, 64, replace=False), rng.choice(n, 512, replace=False)
-    deq = w.unpack(torch.float32)[torch.from_numpy(cols).to(dev)].cpu().numpy().astype(np.float64)
+    deq = host_dequant_rows(w, cols)
     ref = bf16_np(a)[rows] @ deq.T
     assert O.max_rel_err(bf16_np(c)[np.ix_(rows, cols)], ref) <= TOL
 
@@ -592,19 +602,18 @@ def test_gemm_mx_fp4_one_hot_is_exact(dev):
 
 @pytest.mark.parametrize("mnk", [(8192, 8192, 8192), (4096, 14336, 4096)])
 def test_gemm_mx_fp4_full_size_sampled(dev, mnk):
-    """The FP4 x FP4 GEMMs at full size (operands MX-quantised from N(0,1)): 64 sampled rows of C
-    against the exact-dequant fp64 oracle."""
+    """The FP4 x FP4 GEMMs at full size (operands MX-quantised from N(0,1)): 64 x 1024 sampled outputs
+    against the fp64 oracle, which decodes the sampled rows from the host copies of the packed bytes."""
     m, n, k = mnk
     g = torch.Generator(device=dev)
     g.manual_seed(0)
     a = quantize_mx(torch.randn((m, k), device=dev, generator=g), "fp4_e2m1")
     b = quantize_mx(torch.randn((n, k), device=dev, generator=g), "fp4_e2m1")
     c = matmul_nt(a, b, dtype=torch.bfloat16)
-    rows = np.random.default_rng(4).choice(m, 64, replace=False)
-    deq_b = b.unpack(torch.float32).cpu().numpy().astype(np.float64)
-    deq_a = a.unpack(torch.float32).cpu().numpy()[rows].astype(np.float64)
-    ref = deq_a @ deq_b.T
-    assert O.max_rel_err(bf16_np(c)[rows], ref) <= TOL
+    rng = np.random.default_rng(4)
+    rows, cols = rng.choice(m, 64, replace=False), rng.choice(n, 1024, replace=False)
+    ref = host_dequant_rows(a, rows) @ host_dequant_rows(b, cols).T
+    assert O.max_rel_err(bf16_np(c)[np.ix_(rows, cols)], ref) <= TOL
 
 
 MX_PAIRS = [(fa, fb) for fa in ("fp4_e2m1", "fp6_e2m3", "fp6_e3m2") for fb in ("fp4_e2m1", "fp6_e2m3", "fp6_e3m2")]
