@@ -473,8 +473,8 @@ int launch_gemv_rows(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k
   return TGM_E_UNSUPPORTED;
 }
 
-// INT4 waves take 4 rows: twice the VALU work per byte of FP4, so shorter waves overlap
-// better (measured 9.1 vs 9.8 us at 14336 x 4096, 4.4 vs 5.5 us at 4096 x 4096).
+// INT4 waves take 4 rows: with the subnormal decode, 8 rows per wave measured 9.1 against 8.5 us
+// at 14336 x 4096 and 5.7 against 4.7 us at 4096 x 4096 (more waves hide the per-row latency).
 constexpr int kRowsPerWaveInt4 = 4;
 
 template <int IPR, int SDT>
