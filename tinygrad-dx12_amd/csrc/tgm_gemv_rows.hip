@@ -226,22 +226,16 @@ __global__ void __launch_bounds__(256) gemv_rows_fp4(const uint8_t* __restrict__
     const int64_t r = r0 + i / IPR;
     return r < N ? r : N - 1;  // rows past N re-read the last row; they are not stored
   };
-  // Scales: the wave's R rows own R * KB contiguous E8M0 bytes (one byte per lane and load
-  // instruction); they are fetched with 16-byte loads (addresses clamped inside the tensor,
-  // so every load is unconditional), passed through this wave's LDS slice and read back as
-  // the byte each lane needs for each instruction.
-  constexpr int SB = R * KB, SL = (SB + 1023) / 1024;  // scale bytes, 16-byte-per-lane loads
-  __shared__ __attribute__((aligned(16))) unsigned char sl[4][SCALED ? SB : 16];
-  const int wv = threadIdx.x >> 6;
-  u32x4r sraw[SL];
+  // Scales: lane l of instruction i needs the E8M0 byte of block 64 (i % IPR) + l of row
+  // i / IPR.  For each instruction the wave's 64 lanes read 64 consecutive bytes, one byte
+  // load per instruction issued before the weight stream (rows past N re-read the last row).
+  // Loading the wave's scale bytes as 16-byte chunks and handing them out through LDS cost
+  // 0.1 us more at 14336 x 4096 (the LDS round trip and its wave barrier).
+  unsigned sbyte[NI];
   if constexpr (SCALED) {
-    const int64_t limit = N * KB - 16;  // last 16-byte chunk of the scale tensor
 #pragma unroll
-    for (int j = 0; j < SL; ++j) {
-      int64_t off = r0 * KB + 1024 * j + 16 * lane;
-      off = off < limit ? off : limit;
-      sraw[j] = __builtin_nontemporal_load((const u32x4r*)(scales + off));
-    }
+    for (int i = 0; i < NI; ++i)
+      sbyte[i] = __builtin_nontemporal_load(scales + row_of(i) * KB + 64 * (i % IPR) + lane);
   }
   u32x4r codes[D];
   auto load = [&](int i, int slot) __attribute__((always_inline)) {
@@ -251,17 +245,6 @@ __global__ void __launch_bounds__(256) gemv_rows_fp4(const uint8_t* __restrict__
   };
 #pragma unroll
   for (int i = 0; i < D; ++i) load(i, i);
-  unsigned sbyte[NI];
-  if constexpr (SCALED) {
-#pragma unroll
-    for (int j = 0; j < SL; ++j)
-      if (1024 * j + 16 * lane < SB) *(u32x4r*)(&sl[wv][1024 * j + 16 * lane]) = sraw[j];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int i = 0; i < NI; ++i) sbyte[i] = sl[wv][(i / IPR) * KB + 64 * (i % IPR) + lane];
-  }
   if constexpr (NORM) norm_finish<IPR>(nm, nr, xs, red);
   else stage_finish<IPR>(xg, (unsigned char*)xs);
   load_x(xs);
@@ -371,22 +354,15 @@ __global__ void __launch_bounds__(256) gemv_rows_int4(const uint8_t* __restrict_
     const int64_t r = r0 + i / IPR;
     return r < N ? r : N - 1;
   };
-  // Scales: the wave's rows own R * (K >> (5 + GS)) * SSIZE contiguous bytes; staged through
-  // LDS like the FP4 kernel's, then each lane reads its group's scale per instruction.
-  constexpr int SBMAX = R * (K / 32) * SSIZE, SL = (SBMAX + 1023) / 1024;
-  __shared__ __attribute__((aligned(16))) unsigned char sl[4][SCALED ? SBMAX : 16];
-  const int wv = threadIdx.x >> 6;
-  const int ng = (K / 32) >> GS;          // groups per row
-  const int sb = R * ng * SSIZE;          // this wave's scale bytes
-  u32x4r sraw[SL];
+  // Scales: lane l of instruction i needs the scale of group (64 (i % IPR) + l) >> GS of row
+  // i / IPR, read straight from memory before the weight stream (consecutive lanes read
+  // consecutive scales, or the same one for groups of 64 and 128).
+  const int ng = (K / 32) >> GS;  // groups per row
+  float sv[NI];
   if constexpr (SCALED) {
-    const int64_t limit = N * ng * SSIZE - 16;
 #pragma unroll
-    for (int j = 0; j < SL; ++j) {
-      int64_t off = r0 * ng * SSIZE + 1024 * j + 16 * lane;
-      off = off < limit ? off : limit;
-      sraw[j] = __builtin_nontemporal_load((const u32x4r*)(scales + off));
-    }
+    for (int i = 0; i < NI; ++i)
+      sv[i] = int4_scale<SDT>(scales + (row_of(i) * ng + ((64 * (i % IPR) + lane) >> GS)) * SSIZE);
   }
   u32x4r codes[D];
   auto load = [&](int i, int slot) __attribute__((always_inline)) {
@@ -395,18 +371,6 @@ __global__ void __launch_bounds__(256) gemv_rows_int4(const uint8_t* __restrict_
   };
 #pragma unroll
   for (int i = 0; i < D; ++i) load(i, i);
-  float sv[NI];
-  if constexpr (SCALED) {
-#pragma unroll
-    for (int j = 0; j < SL; ++j)
-      if (1024 * j + 16 * lane < sb) *(u32x4r*)(&sl[wv][1024 * j + 16 * lane]) = sraw[j];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-      sv[i] = int4_scale<SDT>(&sl[wv][((i / IPR) * ng + ((64 * (i % IPR) + lane) >> GS)) * SSIZE]);
-  }
   if constexpr (NORM) norm_finish<IPR>(nm, nr, xs, red);
   else stage_finish<IPR>(xg, (unsigned char*)xs);
   load_x(xs);
