@@ -83,6 +83,10 @@ def parse() -> argparse.Namespace:
                    help="run only this workload and print its figures (for profiling)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run --steps device-to-device copies of MIB MiB (reference for HBM byte counters)")
+    p.add_argument("--summarize-decoder", type=Path, default=None, metavar="DIR",
+                   help="summarise the rocprofv3 kernel trace under DIR of a decoder_b1 / decoder_b8 run (--only) "
+                        "per decode step or per prefill (--part)")
+    p.add_argument("--part", choices=("decode", "prefill"), default="decode")
     p.add_argument("--summarize-profile", type=Path, default=None, metavar="DIR",
                    help="summarise the rocprofv3 output folders under DIR for the --only workload")
     return p.parse_args()
@@ -607,9 +611,65 @@ def summarize_profile(folder: Path, workload: str) -> str:
     return "\n".join(lines) + "\n"
 
 
+def _kernel_label(name: str) -> str:
+    return name if len(name) <= 100 else name[:100]
+
+
+def summarize_decoder(folder: Path, workload: str, part: str) -> str:
+    """Per-kernel time of the decoder's timed work in a rocprofv3 kernel trace of
+    ``bench.py --only decoder_bN`` (stdout saved as DIR/bench.json).  Every prefill and every
+    decode step starts with one dec_embed launch; prefills are the segments that run a prompt
+    GEMM or prompt attention.  ``decode``: the last 100 steps (the timed graph replays);
+    ``prefill``: the second of the three timed prefills."""
+    rows = sorted(_csv_rows(folder, "kernel_trace.csv"), key=lambda r: int(r["Start_Timestamp"]))
+    starts = [i for i, r in enumerate(rows) if "dec_embed" in r["Kernel_Name"]]
+    segments = [rows[a:b] for a, b in zip(starts, starts[1:] + [len(rows)])]
+    is_prefill = [any("prefill_attention" in r["Kernel_Name"] or "gemm_w" in r["Kernel_Name"] for r in seg)
+                  for seg in segments]
+    if part == "prefill":
+        chosen = [seg for seg, pf in zip(segments, is_prefill) if pf][-2:-1]
+    else:
+        last = max(i for i, pf in enumerate(is_prefill) if pf)
+        chosen = segments[last + 2:][-100:]  # after the eager first step
+    per: dict[str, list[float]] = {}
+    for seg in chosen:
+        for r in seg:
+            per.setdefault(_kernel_label(r["Kernel_Name"]), []).append(
+                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    n = len(chosen)
+    busy = sum(sum(v) for v in per.values()) / n
+    span = statistics.mean((int(seg[-1]["End_Timestamp"]) - int(seg[0]["Start_Timestamp"])) / 1e3 for seg in chosen)
+    run = json.loads((folder / "bench.json").read_text())[workload]
+    unit = "step" if part == "decode" else "prefill"
+    lines = [f"# {workload}_{part}",
+             "# rocprofv3 kernel trace of the config-5 decoder bench on one MI355X (gfx950); commands, from the "
+             "repository root (OUT = any output folder):",
+             f"#   rocprofv3 --kernel-trace --stats --output-format csv -d OUT -o run -- python3 bench.py --only {workload} "
+             "> OUT/bench.json",
+             f"#   python3 bench.py --summarize-decoder OUT --only {workload} --part {part}",
+             "# Under the tracer every launch is slower (small kernels ~4-5 us each); the untraced step time is the "
+             "bench's decode_ms_per_step.",
+             f"bench line under the tracer: decode {run['decode_ms_per_step']:.3f} ms/step, prefill "
+             f"{run['prefill_ms']:.2f} ms",
+             f"summarised: {n} {unit}{'s' if n != 1 else ''}; kernels per {unit}: "
+             f"{sum(len(v) for v in per.values()) / n:.1f}; "
+             f"busy {busy:.1f} us/{unit}; span {span:.1f} us/{unit}",
+             "",
+             f"{'us/' + unit:>11}  calls   avg us  kernel"]
+    for name, v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"{sum(v) / n:11.2f} {len(v) / n:6.1f} {statistics.mean(v):8.2f}  {name}")
+    return "\n".join(lines) + "\n"
+
+
 # ----------------------------------------------------------------------------- main
 def main() -> int:
     args = parse()
+    if args.summarize_decoder is not None:
+        if not (args.only or "").startswith("decoder"):
+            print("--summarize-decoder needs --only decoder_b1 or decoder_b8", file=sys.stderr)
+            return 2
+        print(summarize_decoder(args.summarize_decoder, args.only, args.part), end="")
+        return 0
     if args.summarize_profile is not None:
         if not args.only:
             print("--summarize-profile needs --only WORKLOAD", file=sys.stderr)

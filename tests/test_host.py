@@ -431,3 +431,40 @@ def test_profile_summary_from_rocprof_csvs(tmp_path):
     assert "GRBM_GUI_ACTIVE / 8 / timed median = 2.000 GHz" in text  # 4.8e6 / 8 cycles in 300 us
     assert f"algorithmic_flops_per_launch={flops}" in text
     assert "--only fp4_gemm_8192" in text and "--pmc MfmaUtil SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE" in text
+
+
+def test_decoder_trace_summary(tmp_path):
+    """bench.py --summarize-decoder: segments start at dec_embed; prefills are the segments with a
+    prompt GEMM; decode summarises the graph replays after the eager first step, prefill the
+    second of the last three prefills."""
+    root = Path(__file__).resolve().parents[1]
+    sys.path.insert(0, str(root))
+    try:
+        import bench
+    finally:
+        sys.path.remove(str(root))
+    trace, t = [], 0
+
+    def launch(name, us):
+        nonlocal t
+        trace.append({"Kernel_Name": name, "Start_Timestamp": t, "End_Timestamp": t + int(us * 1000)})
+        t += int(us * 1000) + 500
+
+    for p in range(5):  # 2 warm-up prefills, then the 3 timed ones
+        launch("tgm::dec_embed", 1)
+        launch("tgm::gemm_w_mx<2, true, true>", 100 + p)
+        launch("tgm::dec_argmax", 2)
+    launch("tgm::dec_embed", 1)  # the eager first decode step: excluded
+    launch("tgm::gemv_rows_fp4<8>", 50)
+    for s in range(3):  # graph replays
+        launch("tgm::dec_embed", 1)
+        launch("tgm::gemv_rows_fp4<8>", 10 + s)
+        launch("tgm::dec_argmax", 2)
+    _write_csv(tmp_path / "run_kernel_trace.csv", trace)
+    (tmp_path / "bench.json").write_text(json.dumps({"decoder_b1": {"decode_ms_per_step": 0.4, "prefill_ms": 3.1}}))
+    dec = bench.summarize_decoder(tmp_path, "decoder_b1", "decode")
+    assert "summarised: 3 steps; kernels per step: 3.0; busy 14.0 us/step" in dec
+    assert "     11.00    1.0    11.00  tgm::gemv_rows_fp4<8>" in dec
+    pre = bench.summarize_decoder(tmp_path, "decoder_b1", "prefill")
+    assert "summarised: 1 prefill; kernels per prefill: 3.0" in pre
+    assert "    103.00    1.0   103.00  tgm::gemm_w_mx<2, true, true>" in pre
