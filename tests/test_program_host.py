@@ -55,6 +55,8 @@ def test_estimates_of_the_measured_gemms():
     dense = P.dense_program("bfloat16", 128, 64, "bfloat16", 256, 64, 64, "float32", 256)
     assert dense.estimates == P.Estimates(2 * 128 * 256 * 64, 128 * 64 * 2 + 256 * 64 * 2 + 128 * 256 * 4)
     assert P.dense_program("float8_e4m3fn", 8, 128, "float8_e5m2", 8, 128, 128, "float32", 8).name == "tgm_gemm_fp8"
+    with pytest.raises(ValueError):  # per-tensor scales belong to FP8 operands only
+        P.dense_program("bfloat16", 8, 64, "bfloat16", 8, 64, 64, "float32", 8, scale_a=4096)
 
 
 def test_program_arguments_follow_the_c_abi():

@@ -203,7 +203,8 @@ extern "C" int tgm_gemm_dense_batched(const void* a, int a_dtype, int64_t m, int
                                       int64_t batch, void* stream) {
   clear_error();
   TGM_CHECK_ARG(a && b && c, "null operand");
-  TGM_CHECK_ARG(m >= 0 && n >= 0 && k >= 0 && batch >= 0 && b_group >= 1 && c_group >= 1,
+  TGM_CHECK_ARG(m >= 0 && n >= 0 && k >= 0 && batch >= 0 && b_group >= 1 && c_group >= 1 && b_group < (1ll << 31) &&
+                    c_group < (1ll << 31),
                 "invalid gemm sizes");
   TGM_CHECK_ARG(m <= 1 || lda >= k, "lda smaller than K");
   TGM_CHECK_ARG(n <= 1 || ldb >= k, "ldb smaller than K");
@@ -254,7 +255,8 @@ extern "C" int tgm_gemm_fp8(const void* a, int a_dtype, int64_t lda, int64_t m, 
   const int64_t lda_eff = m > 1 ? lda : k, ldb_eff = n > 1 ? ldb : k;
   if (lda_eff % 16 || ldb_eff % 16 || (uintptr_t)a % 16 || (uintptr_t)b % 16)
     TGM_UNSUPPORTED("tgm_gemm_fp8: operands and their rows must be 16-byte aligned");
-  if (m >= (1ll << 31) || n >= (1ll << 31) || (m - 1) * lda_eff + k >= (1ll << 32) || (n - 1) * ldb_eff + k >= (1ll << 32))
+  if (m >= (1ll << 31) || n >= (1ll << 31) || k >= (1ll << 31) || (m - 1) * lda_eff + k >= (1ll << 32) ||
+      (n - 1) * ldb_eff + k >= (1ll << 32))
     TGM_UNSUPPORTED("tgm_gemm_fp8: operands must be under 4 GiB (32-bit offsets)");
   const int64_t tiles = ((m + kDM - 1) / kDM) * ((n + kDN - 1) / kDN);
   const hipStream_t st = (hipStream_t)stream;

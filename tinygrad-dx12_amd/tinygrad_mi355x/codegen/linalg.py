@@ -110,6 +110,9 @@ def dense_matmul_nt(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype, sc
     """C[M, N] = a[M, K] @ b[N, K]^T on the ordinary MFMA GEMM (bf16 or f16 operands; FP8
     operands decoded exactly to bf16 in registers); ``scale_a`` / ``scale_b`` are optional fp32
     device scalars (FP8 only) that multiply the fp32 sums before rounding."""
+    for s in (scale_a, scale_b):
+        if s is not None and (s.dtype is not torch.float32 or s.numel() != 1 or s.device != a.device):
+            raise ValueError("scales must be single fp32 values on the operands' device")
     a, b = _k_rows(a), _k_rows(b)
     m, k = a.shape
     n = b.shape[0]

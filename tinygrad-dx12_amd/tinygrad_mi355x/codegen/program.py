@@ -171,6 +171,8 @@ def dense_program(a_dtype: str, m: int, lda: int, b_dtype: str, n: int, ldb: int
         sa, sb = scale_a or None, scale_b or None
         return MatrixProgram(GEMM_FP8, "tgm_gemm_fp8", _tiles(m, n, GEMM_FP8), est,
                              lambda out, x, y, s: (x, adt, lda, m, y, bdt, ldb, n, k, sa, sb, out, cdt, ldc, s))
+    if scale_a or scale_b:
+        raise ValueError("per-tensor scales apply to FP8 operands only")
     return MatrixProgram(GEMM_DENSE, "tgm_gemm_dense", _tiles(m, n, GEMM_DENSE), est,
                          lambda out, x, y, s: (x, adt, m, lda, y, bdt, n, ldb, k, out, cdt, ldc, s))
 
