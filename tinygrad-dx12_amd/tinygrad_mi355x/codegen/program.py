@@ -83,6 +83,9 @@ class MatrixProgram:
         self.global_size = (max(int(groups), 0), 1, 1)
         self.local_size = (kernel.threads, 1, 1)
 
+    def __repr__(self) -> str:
+        return f"MatrixProgram({self.name}, groups={self.global_size[0]})"
+
     def launch(self, out: int, a: int, b: int, stream: int) -> None:
         """Enqueue on ``stream`` with slot addresses (out, a, b); the caller owns ordering."""
         if 0 in self.global_size:
@@ -175,6 +178,18 @@ def dense_program(a_dtype: str, m: int, lda: int, b_dtype: str, n: int, ldb: int
         raise ValueError("per-tensor scales apply to FP8 operands only")
     return MatrixProgram(GEMM_DENSE, "tgm_gemm_dense", _tiles(m, n, GEMM_DENSE), est,
                          lambda out, x, y, s: (x, adt, m, lda, y, bdt, n, ldb, k, out, cdt, ldc, s))
+
+
+def transpose_program(dtype: str, rows: int, cols: int) -> MatrixProgram:
+    """out[cols, rows] = in[rows, cols]^T for 1- or 2-byte elements (slots out, a): the staging
+    copy that puts a GEMM operand K-contiguous."""
+    size = L.DTYPE_SIZES[dtype]
+    if size not in (1, 2):
+        raise ValueError(f"no transpose kernel for {dtype}")
+    name = "tgm_transpose8" if size == 1 else "tgm_transpose16"
+    kernel = MatrixKernel(name, "copy", (64, 64, 1), 256)
+    return MatrixProgram(kernel, name, _tiles(rows, cols, kernel), Estimates(0, 2 * rows * cols * size),
+                         lambda out, a, b, s: (a, rows, cols, cols, out, rows, s))
 
 
 # ----------------------------------------------------------------------------- plugin-buffer path

@@ -5,12 +5,16 @@ src/tinygrad_dx12/renderer/cstyle.py:303-380): it holds the target, the launch l
 and the supported arithmetic dtypes, serialises rendering with a lock, keeps the
 per-renderer matrix rejection cache, and owns the device's compiler.
 
-What it renders is a kernel *description*: a name, typed buffer and scalar parameters and
-a body of HIP C++ statements over the index variables ``gidx0..2`` (workgroup ids) and
-``lidx0..2`` (work-item ids) -- the kernel prologue and signature that tinygrad's C-style
-renderers wrap around rendered UOps (``render_kernel``).  Rendering tinygrad UOps
-themselves is not needed by the packed matmul path, whose kernels are prebuilt in
-libtgm_mi355x.so.
+It renders two things:
+
+* a linear UOp listing (``uop/linearize.py``'s ``LinearKernel``, or a sequence of linear UOps)
+  to a complete kernel, statement by statement (``renderer/uop_hip.py``);
+* a kernel *description* (``KernelSpec``): a name, typed buffer and scalar parameters and a body
+  of HIP C++ statements over the index variables ``gidx0..2`` (workgroup ids) and ``lidx0..2``
+  (work-item ids) -- the prologue and signature tinygrad's C-style renderers wrap around
+  rendered UOps (``render_kernel``), for hand-written bodies.
+
+The packed matmul kernels themselves are prebuilt in libtgm_mi355x.so.
 """
 
 from __future__ import annotations
@@ -18,6 +22,7 @@ from __future__ import annotations
 import threading
 from dataclasses import dataclass, field
 
+from tinygrad_mi355x.renderer.uop_hip import render_uops
 from tinygrad_mi355x.runtime.support.compiler_hip import MI355XCompiler
 
 # dtype name -> HIP C++ element type
@@ -75,8 +80,14 @@ class MI355XRenderer:
         arithmetic)."""
         return set(TYPE_MAP)
 
-    def render(self, spec: KernelSpec) -> str:
-        """Complete ``extern "C" __global__`` source for ``spec``."""
+    def render(self, spec) -> str:
+        """Complete ``extern "C" __global__`` source for a ``KernelSpec``, a ``LinearKernel`` or a
+        sequence of linear UOps."""
+        if not isinstance(spec, KernelSpec):
+            with self._render_lock:
+                if hasattr(spec, "uops") and hasattr(spec, "local_size"):
+                    return render_uops(spec.uops, spec.name, spec.local_size)
+                return render_uops(list(spec))
         if any(dtype_name(b.dtype) not in TYPE_MAP for b in spec.buffers):
             raise ValueError(f"kernel {spec.name}: unsupported buffer dtype")
         if any(kind not in SCALAR_TYPES for _, kind in spec.scalars):

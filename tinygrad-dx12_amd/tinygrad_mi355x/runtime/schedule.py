@@ -1,0 +1,104 @@
+"""Running a schedule (a LINEAR of CALLs) on one MI355X.
+
+The reference leaves execution to tinygrad: each CALL becomes a compiled program launched through
+``DX12Program.__call__`` with the CALL's buffers (alexandreteles/tinygrad-dx12
+src/tinygrad_dx12/runtime/ops_dx12.py:659-744), and native matrix CALLs carry a prebuilt
+PROGRAM (codegen/linalg.py:37-58, codegen/matmul.py:206-218).  ``run_linear`` is that loop for
+the schedules of ``uop/ops.py``:
+
+* a CALL whose body is a kernel SINK is linearized (``uop/linearize.py``), rendered by the
+  device's renderer, compiled by its compiler (both cache by source) and launched as an
+  ``MI355XProgram`` with the CALL's buffers in the kernel's PARAM slot order and the values of
+  its DEFINE_VARs;
+* a CALL whose body is a PROGRAM (a ``MatrixProgram`` of the kernel library, as
+  ``codegen/uop_matmul.py`` makes them) is launched with its (out, a, b) buffers;
+* a BUFFER the caller does not bind is allocated from the device's allocator on first use.
+
+Launches go to the device stream in order under the device lock, as every plugin launch does; the
+returned map holds every buffer of the schedule, so results are read with the allocator's
+``_copyout``.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+from tinygrad_mi355x.codegen.program import MatrixProgram
+from tinygrad_mi355x.uop.linearize import LinearKernel, linearize
+from tinygrad_mi355x.uop.ops import Ops, UOp
+
+
+@dataclass(frozen=True)
+class CompiledKernel:
+    listing: LinearKernel
+    source: str
+    program: object  # MI355XProgram
+
+
+def compile_kernel(dev, sink: UOp) -> CompiledKernel:
+    """Linearize, render and compile ``sink`` for ``dev`` (cached per device by kernel)."""
+    cache = dev.__dict__.setdefault("_uop_kernels", {})
+    found = cache.get(sink)
+    if found is not None:
+        return found
+    listing = linearize(sink)
+    source = dev.renderer.render(listing)
+    program = dev.runtime(listing.name, dev.compiler.compile(source))
+    cache[sink] = compiled = CompiledKernel(listing, source, program)
+    return compiled
+
+
+def _nbytes(u: UOp) -> int:
+    return u.max_numel() * u.dtype.itemsize
+
+
+def run_linear(dev, linear: UOp, buffers: dict | None = None, var_vals: dict[str, int] | None = None,
+               wait: bool = False) -> dict:
+    """Launch every CALL of ``linear`` in order on ``dev``; returns the BUFFER -> MI355XBuffer map
+    (the caller's bindings plus what was allocated here).  With ``wait`` the device is
+    synchronised before returning."""
+    if linear.op is not Ops.LINEAR:
+        raise ValueError("run_linear takes a LINEAR of CALLs")
+    bound = dict(buffers or {})
+    var_vals = var_vals or {}
+
+    def buf(u: UOp):
+        if u.op is not Ops.BUFFER:
+            raise ValueError(f"a CALL argument must be a BUFFER, not {u.op.name}")
+        got = bound.get(u)
+        if got is None:
+            got = bound[u] = dev.allocator.alloc(max(_nbytes(u), 1))
+        elif got.size < _nbytes(u):
+            raise ValueError("a bound buffer is smaller than its BUFFER")
+        return got
+
+    for call in linear.src:
+        if call.op is not Ops.CALL:
+            raise ValueError(f"LINEAR holds CALLs, not {call.op.name}")
+        body, args = call.src[0], call.src[1:]
+        if body.op is Ops.PROGRAM:
+            prog = body.arg
+            if not isinstance(prog, MatrixProgram) or len(args) not in (2, 3):
+                raise ValueError("a PROGRAM call takes a library program and its (out, a[, b]) buffers")
+            prog(*(buf(a) for a in args))
+            continue
+        if body.op is not Ops.SINK:
+            raise ValueError(f"a CALL body is a SINK or a PROGRAM, not {body.op.name}")
+        kernel = compile_kernel(dev, body)
+        bufs = []
+        for p in kernel.listing.params:
+            if p.arg.slot + 1 >= len(call.src):
+                raise ValueError(f"kernel {kernel.listing.name}: no argument for slot {p.arg.slot}")
+            b = buf(args[p.arg.slot])
+            if b.size < _nbytes(p) or args[p.arg.slot].dtype != p.dtype:
+                raise ValueError(f"kernel {kernel.listing.name}: argument for slot {p.arg.slot} does not match")
+            bufs.append(b)
+        vals = tuple(int(var_vals[v.arg[0]]) for v in kernel.listing.variables)
+        for v, x in zip(kernel.listing.variables, vals):
+            if not v.arg[1] <= x <= v.arg[2]:
+                raise ValueError(f"variable {v.arg[0]} = {x} is outside [{v.arg[1]}, {v.arg[2]}]")
+        kernel.program(*bufs, global_size=kernel.listing.global_size, local_size=kernel.listing.local_size,
+                       vals=vals)
+    if wait:
+        dev.synchronize()
+    return bound
