@@ -14,7 +14,7 @@ import pytest
 import packed_oracle as O
 from tinygrad_mi355x.codegen.uop_matmul import lower_matmul
 from tinygrad_mi355x.runtime import ops_mi355x as R
-from tinygrad_mi355x.runtime.schedule import compile_kernel, run_linear
+from tinygrad_mi355x.runtime.schedule import LinearGraph, compile_kernel, run_linear
 from tinygrad_mi355x.uop.ops import AxisType, KernelInfo, Ops, UOp, dtypes
 
 pytestmark = pytest.mark.gpu
@@ -318,3 +318,33 @@ def test_rebindable_inputs_are_staged(device):
 def test_compiled_kernels_are_cached_per_device(device):
     sink = elementwise(dtypes.float32, lambda x, y: x + y, 64, name="cached")
     assert compile_kernel(device, sink) is compile_kernel(device, sink)
+
+
+def test_schedule_graph_replays_match_eager_runs(device):
+    """A lowered schedule (transpose, GEMM, epilogue kernel) captured into one HIP graph: every
+    replay, with new operands written between replays, equals the eager run of the same schedule."""
+    m, n, k = 128, 192, 128
+    sink = matrix_sink(m, n, k, dtypes.bfloat16, activated=True)
+    params = sorted((u for u in sink.toposort() if u.op is Ops.PARAM), key=lambda u: u.arg.slot)
+    bufs = [UOp.new_buffer(DEV, p.max_numel(), p.dtype) for p in params]
+    linear = lower_matmul(UOp.linear(UOp.call(sink, *bufs)))
+    bound = {b: device.allocator.alloc(p.max_numel() * 2) for p, b in zip(params, bufs)}
+    graph = LinearGraph(device, linear, bound)
+    assert len(graph.launches) == 3
+    rng = np.random.default_rng(11)
+    try:
+        for _ in range(3):
+            a, b, av, bv = _operands(rng, m, n, k, dtypes.bfloat16, False, False)
+            device.allocator._copyin(bound[bufs[1]], memoryview(a).cast("B"))
+            device.allocator._copyin(bound[bufs[2]], memoryview(b).cast("B"))
+            graph(wait=True)
+            replayed = np.empty(m * n, np.uint16)
+            device.allocator._copyout(memoryview(replayed).cast("B"), bound[bufs[0]])
+            run_linear(device, linear, graph.buffers, wait=True)
+            eager = np.empty(m * n, np.uint16)
+            device.allocator._copyout(memoryview(eager).cast("B"), bound[bufs[0]])
+            np.testing.assert_array_equal(replayed, eager)
+            want = np.maximum(av @ bv, 0)
+            assert O.max_rel_err(O.bf16_to_f32(replayed).reshape(m, n), want) <= 1e-2
+    finally:
+        graph.close()

@@ -16,7 +16,7 @@ the schedules of ``uop/ops.py``:
 
 Launches go to the device stream in order under the device lock, as every plugin launch does; the
 returned map holds every buffer of the schedule, so results are read with the allocator's
-``_copyout``.
+``_copyout``.  ``LinearGraph`` captures a whole schedule into one HIP graph and replays it.
 """
 
 from __future__ import annotations
@@ -52,11 +52,41 @@ def _nbytes(u: UOp) -> int:
     return u.max_numel() * u.dtype.itemsize
 
 
-def run_linear(dev, linear: UOp, buffers: dict | None = None, var_vals: dict[str, int] | None = None,
-               wait: bool = False) -> dict:
-    """Launch every CALL of ``linear`` in order on ``dev``; returns the BUFFER -> MI355XBuffer map
-    (the caller's bindings plus what was allocated here).  With ``wait`` the device is
-    synchronised before returning."""
+@dataclass(frozen=True)
+class Launch:
+    """One resolved launch of a schedule: a library program with its (out, a[, b]) buffers, or a
+    compiled kernel with its buffers, launch sizes and scalar values."""
+
+    program: object
+    bufs: tuple
+    global_size: tuple[int, int, int] = (1, 1, 1)
+    local_size: tuple[int, int, int] = (1, 1, 1)
+    vals: tuple = ()
+
+    @property
+    def native(self) -> bool:
+        return isinstance(self.program, MatrixProgram)
+
+    def run(self) -> None:
+        """Launch eagerly (under the device lock, recorded for the allocator's deferred frees)."""
+        if self.native:
+            self.program(*self.bufs)
+        else:
+            self.program(*self.bufs, global_size=self.global_size, local_size=self.local_size, vals=self.vals)
+
+    def enqueue(self, stream: int) -> None:
+        """Put the launch on ``stream`` with no locking or bookkeeping (stream capture)."""
+        if self.native:
+            out, a, *b = self.bufs
+            self.program.launch(out.address, a.address, b[0].address if b else 0, stream)
+        else:
+            self.program.enqueue(self.bufs, self.global_size, self.local_size, self.vals)
+
+
+def plan(dev, linear: UOp, buffers: dict | None = None, var_vals: dict[str, int] | None = None
+         ) -> tuple[list[Launch], dict]:
+    """Resolve every CALL of ``linear`` to a ``Launch``: kernels compiled, arguments checked,
+    unbound BUFFERs allocated.  Returns the launches and the BUFFER -> MI355XBuffer map."""
     if linear.op is not Ops.LINEAR:
         raise ValueError("run_linear takes a LINEAR of CALLs")
     bound = dict(buffers or {})
@@ -72,6 +102,7 @@ def run_linear(dev, linear: UOp, buffers: dict | None = None, var_vals: dict[str
             raise ValueError("a bound buffer is smaller than its BUFFER")
         return got
 
+    launches = []
     for call in linear.src:
         if call.op is not Ops.CALL:
             raise ValueError(f"LINEAR holds CALLs, not {call.op.name}")
@@ -80,7 +111,10 @@ def run_linear(dev, linear: UOp, buffers: dict | None = None, var_vals: dict[str
             prog = body.arg
             if not isinstance(prog, MatrixProgram) or len(args) not in (2, 3):
                 raise ValueError("a PROGRAM call takes a library program and its (out, a[, b]) buffers")
-            prog(*(buf(a) for a in args))
+            bufs = tuple(buf(a) for a in args)
+            if any(b.dev is not dev for b in bufs):
+                raise ValueError("MI355X buffer device/signature mismatch")
+            launches.append(Launch(prog, bufs))
             continue
         if body.op is not Ops.SINK:
             raise ValueError(f"a CALL body is a SINK or a PROGRAM, not {body.op.name}")
@@ -97,8 +131,54 @@ def run_linear(dev, linear: UOp, buffers: dict | None = None, var_vals: dict[str
         for v, x in zip(kernel.listing.variables, vals):
             if not v.arg[1] <= x <= v.arg[2]:
                 raise ValueError(f"variable {v.arg[0]} = {x} is outside [{v.arg[1]}, {v.arg[2]}]")
-        kernel.program(*bufs, global_size=kernel.listing.global_size, local_size=kernel.listing.local_size,
-                       vals=vals)
+        launch = Launch(kernel.program, tuple(bufs), kernel.listing.global_size, kernel.listing.local_size, vals)
+        kernel.program.validate(launch.bufs, launch.global_size, launch.local_size, launch.vals)
+        launches.append(launch)
+    return launches, bound
+
+
+def run_linear(dev, linear: UOp, buffers: dict | None = None, var_vals: dict[str, int] | None = None,
+               wait: bool = False) -> dict:
+    """Launch every CALL of ``linear`` in order on ``dev``; returns the BUFFER -> MI355XBuffer map
+    (the caller's bindings plus what was allocated here).  With ``wait`` the device is
+    synchronised before returning."""
+    launches, bound = plan(dev, linear, buffers, var_vals)
+    for launch in launches:
+        launch.run()
     if wait:
         dev.synchronize()
     return bound
+
+
+class LinearGraph:
+    """A schedule captured once into a HIP graph and replayed with one launch (the reference's
+    graph runner, runtime/graph/dx12.py:49-253, for whole schedules): kernels are compiled and
+    buffers resolved before capture; every replay reads the buffers' current contents."""
+
+    def __init__(self, dev, linear: UOp, buffers: dict | None = None, var_vals: dict[str, int] | None = None):
+        from tinygrad_mi355x.runtime.graph import StreamGraph
+
+        self.dev = dev
+        self.launches, self.buffers = plan(dev, linear, buffers, var_vals)
+        if not self.launches:
+            raise ValueError("an empty schedule has nothing to capture")
+
+        def record() -> None:
+            for launch in self.launches:
+                launch.enqueue(dev.stream)
+
+        with dev.lock:
+            dev.select()
+            self.graph = StreamGraph(record, dev.stream)
+        self.owners = tuple({id(b.owner): b.owner for la in self.launches for b in la.bufs}.values())
+
+    def __call__(self, wait: bool = False) -> float | None:
+        """Replay once (asynchronously); GPU seconds when ``wait``."""
+        with self.dev.lock, self.dev.submitting():
+            self.dev.select()
+            seconds = self.graph(wait=wait)
+            self.dev.submitted(self.owners)
+        return seconds
+
+    def close(self) -> None:
+        self.graph.close()
