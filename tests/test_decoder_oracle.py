@@ -118,3 +118,32 @@ def test_generate_feeds_back_the_first_maximum():
 @pytest.mark.parametrize("x", [np.array([1.0, 3.0, 3.0, 2.0]), np.array([-np.inf, 0.5, 0.5])])
 def test_argmax_convention(x):
     assert int(np.argmax(x)) == int(np.flatnonzero(x == x.max())[0])
+
+
+def test_silu_is_x_times_the_logistic_function():
+    """silu against scipy's logistic function and its known values and limits."""
+    from scipy.special import expit
+
+    x = np.linspace(-30, 30, 601)
+    assert np.allclose(D.silu(x), x * expit(x), rtol=1e-13, atol=1e-300)
+    assert D.silu(np.array([1.0]))[0] == pytest.approx(0.7310585786300049, rel=1e-15)
+    assert D.silu(np.array([-1.0]))[0] == pytest.approx(-0.2689414213699951, rel=1e-15)
+    assert D.silu(np.array([0.0]))[0] == 0.0
+    assert D.silu(np.array([-1000.0]))[0] == 0.0 and D.silu(np.array([50.0]))[0] == pytest.approx(50.0)
+
+
+def test_swiglu_gates_with_the_even_rows():
+    """Row 2i of the gate|up weight is gate i (through silu), row 2i + 1 is up i: with gate rows
+    picking x0 and up rows 2 x1, output i is silu(x0) * 2 x1 -- the swapped convention would give
+    silu(2 x1) * x0."""
+    F, d = 3, 4
+    wgu = np.zeros((2 * F, d))
+    wgu[0::2, 0] = 1.0
+    wgu[1::2, 1] = 2.0
+    layer = D.OracleLayer(np.ones(d), np.zeros((1, d)), np.zeros((d, 1)), np.ones(d), wgu, np.zeros((d, F)))
+    dec = D.OracleDecoder(D.OracleWeights(np.zeros((1, d)), [layer], np.ones(d), np.zeros((1, d))), 1, 1, d, F,
+                          1e-5, 1e4, 1, 4)
+    x = np.array([[1.5, -0.75, 3.0, 9.0]])
+    got = dec.swiglu(0, x)
+    assert np.allclose(got, D.silu(np.array(1.5)) * 2 * -0.75)
+    assert not np.allclose(got, D.silu(np.array(2 * -0.75)) * 1.5)
