@@ -136,6 +136,10 @@ def test_lowering_stages_rebindable_inputs():
     assert copy.src[2] is a and staged.src[1].src[2] is copy.src[1]
     # an output that is a rebindable input keeps its ordinary kernel
     assert _kinds(lower_matmul(UOp.linear(call), input_uops=(out,))) == ["kernel"]
+    # so does a call that binds one buffer as both the output and an operand
+    square = _buffers((m * m, dtypes.float16))[0]
+    inplace = UOp.call(matrix_sink(m, m, m, right_nk=True), square, square, b)
+    assert _kinds(lower_matmul(UOp.linear(inplace))) == ["kernel"]
 
 
 # ----------------------------------------------------------------------------- linearizer

@@ -177,6 +177,8 @@ def _lower_call(call: UOp, inputs: set) -> tuple[UOp, ...]:
     if any(s + 1 >= len(call.src) for s in slots):
         return (call,)
     output, left, right = (call.src[s + 1] for s in slots)
+    if output is left or output is right:
+        return (call,)  # the call writes the product over an operand
     if not spec.epilogue and output in inputs:
         return (call,)  # a rebindable output cannot be checked for the GEMM's alignment here
     device = spec.output.arg.device
