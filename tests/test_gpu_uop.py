@@ -348,3 +348,33 @@ def test_schedule_graph_replays_match_eager_runs(device):
             assert O.max_rel_err(O.bf16_to_f32(replayed).reshape(m, n), want) <= 1e-2
     finally:
         graph.close()
+
+
+def test_long_reductions_fold_in_a_workgroup(device):
+    """Row sums and maxima over 4096 points (one workgroup per row, LDS tree) and an RMSNorm
+    whose every output point folds its row."""
+    rows, cols = 97, 4096
+    f32 = dtypes.float32
+    x, o = UOp.param(1, f32, rows * cols, DEV), UOp.param(0, f32, rows, DEV)
+    r, c = UOp.range(rows, 0), UOp.range(cols, 1, AxisType.REDUCE)
+    v = x.index(r * cols + c)
+    sink = o.index(r).store(v.reduce(c, arg=Ops.ADD) + v.reduce(c, arg=Ops.MAX) * 0.5).end(r).sink(
+        arg=KernelInfo(name="rowfold"))
+    assert "BARRIER" in [u.op.name for u in compile_kernel(device, sink).listing.uops]
+    rng = np.random.default_rng(12)
+    xs = rng.integers(-100, 100, rows * cols).astype(np.float32)  # integer-valued: the sums are exact
+    out, _ = run_sink(device, sink, {1: xs})
+    xm = xs.reshape(rows, cols)
+    np.testing.assert_array_equal(out[0], xm.sum(1) + xm.max(1) * np.float32(0.5))
+    # RMSNorm: y[r, k] = x[r, k] / sqrt(sum_j x[r, j]^2 / n + eps)
+    n_rows, n = 8, 1000
+    xx, yy = UOp.param(1, f32, n_rows * n, DEV), UOp.param(0, f32, n_rows * n, DEV)
+    rr, kk, jj = UOp.range(n_rows, 0), UOp.range(n, 1), UOp.range(n, 2, AxisType.REDUCE)
+    sq = xx.index(rr * n + jj)
+    ms = (sq * sq).reduce(jj, arg=Ops.ADD) * (1.0 / n) + 1e-5
+    norm = yy.index(rr * n + kk).store(xx.index(rr * n + kk) * ms.sqrt().reciprocal()).end(rr, kk).sink(
+        arg=KernelInfo(name="rmsnorm"))
+    xr = rng.standard_normal(n_rows * n).astype(np.float32)
+    got, _ = run_sink(device, norm, {1: xr})
+    want = xr.reshape(n_rows, n) / np.sqrt((xr.reshape(n_rows, n).astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-5)
+    assert np.abs(got[0].reshape(n_rows, n) - want).max() <= 1e-5 * np.abs(want).max()

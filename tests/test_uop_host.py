@@ -259,3 +259,34 @@ def test_renderer_takes_tinygrad_spelled_listings():
     st = NS(op=op("STORE"), dtype=None, src=(st_idx, mul), arg=None)
     src = MI355XRenderer().render([g0, g1, n64, lid, ld_idx, ld, two, mul, st_idx, st])
     assert "__launch_bounds__(64)" in src and "float* __restrict__ data0" in src and "0x1.0000000000000p+1f" in src
+
+
+def test_long_reductions_fold_in_a_workgroup():
+    """Reductions of at least 256 points: one workgroup per stored point, work-items striding over
+    the points (the last chunk's surplus folds the identity), then an LDS halving tree."""
+    rows, cols, a, b = 3, 1000, 20, 30
+    x = UOp.param(1, dtypes.int32, rows * cols)
+    y = UOp.param(2, dtypes.int32, rows * a * b)
+    o = UOp.param(0, dtypes.int32, rows)
+    r = UOp.range(rows, 0)
+    c = UOp.range(cols, 1, AxisType.REDUCE)
+    i, j = UOp.range(a, 2, AxisType.REDUCE), UOp.range(b, 3, AxisType.REDUCE)
+    total = x.index(r * cols + c).reduce(c, arg=Ops.ADD)
+    peak = (y.index(r * (a * b) + i * b + j) * (i + 1)).reduce(i, j, arg=Ops.MAX)
+    sink = o.index(r).store(total * 3 + peak).end(r).sink(arg=KernelInfo(name="long"))
+    listing = linearize(sink)
+    assert listing.global_size == (rows, 1, 1) and listing.local_size == (256, 1, 1)
+    names = [u.op.name for u in listing.uops]
+    assert names.count("DEFINE_LOCAL") == 2 and names.count("BARRIER") == 2 * 9
+    rng = np.random.default_rng(3)
+    xs = rng.integers(-1000, 1000, rows * cols).astype(np.int32)
+    ys = rng.integers(-1000, 1000, rows * a * b).astype(np.int32)
+    out = np.zeros(rows, np.int32)
+    uop_interp.run(listing, {0: out, 1: xs, 2: ys})
+    weights = np.arange(1, a + 1, dtype=np.int32)[:, None]
+    want = xs.reshape(rows, cols).sum(1) * 3 + (ys.reshape(rows, a, b) * weights).reshape(rows, -1).max(1)
+    np.testing.assert_array_equal(out, want)
+    # short reductions keep one work-item per stored point
+    short = o.index(r).store(x.index(r * cols + UOp.range(100, 4, AxisType.REDUCE)).reduce(
+        UOp.range(100, 4, AxisType.REDUCE), arg=Ops.ADD)).end(r).sink(arg=KernelInfo(name="short"))
+    assert "BARRIER" not in [u.op.name for u in linearize(short).uops]

@@ -3,7 +3,9 @@
 It executes ``uop/linearize.py``'s listings work-item by work-item over numpy arrays, with
 numpy scalar arithmetic of each dtype (integers wrap, floats round as numpy rounds them), so the
 linearizer's index arithmetic, loops, gates and accumulators are checked on the CPU
-independently of the HIP renderer.  bf16 and FP8 are not interpreted.
+independently of the HIP renderer.  The work-items of a workgroup share its DEFINE_LOCAL arrays
+and run in turns between BARRIERs (each runs until its next barrier, then the next one runs).
+bf16 and FP8 are not interpreted.
 """
 
 from __future__ import annotations
@@ -87,11 +89,22 @@ def run(listing, buffers: dict[int, np.ndarray], var_vals: dict[str, int] | None
     with warnings.catch_warnings():
         warnings.simplefilter("ignore")
         for g in range(groups):
-            for lid in range(local):
-                _item(uops, ends, buffers, var_vals, g, lid)
+            shared: dict[int, np.ndarray] = {}
+            items = [_item(uops, ends, buffers, var_vals, g, lid, shared) for lid in range(local)]
+            while items:  # one turn: every live work-item runs to its next barrier
+                alive = []
+                for it in items:
+                    try:
+                        next(it)
+                        alive.append(it)
+                    except StopIteration:
+                        pass
+                if alive and len(alive) != len(items):
+                    raise AssertionError("work-items of one workgroup reached different barriers")
+                items = alive
 
 
-def _item(uops, ends, buffers, var_vals, gidx, lidx) -> None:
+def _item(uops, ends, buffers, var_vals, gidx, lidx, shared):
     val: dict[int, object] = {}
     ptr: dict[int, tuple] = {}
     regs: dict[int, np.ndarray] = {}
@@ -114,9 +127,13 @@ def _item(uops, ends, buffers, var_vals, gidx, lidx) -> None:
             val[id(u)] = np.int32(gidx if u.arg.startswith("g") else lidx)
         elif op == "DEFINE_REG":
             regs[id(u)] = np.zeros(u.arg[0], NP[dt])
+        elif op == "DEFINE_LOCAL":
+            regs[id(u)] = shared.setdefault(id(u), np.zeros(u.arg[0], NP[dt]))
+        elif op == "BARRIER":
+            yield
         elif op == "INDEX":
             base = u.src[0]
-            arr = regs[id(base)] if base.op.name == "DEFINE_REG" else buffers[base.arg.slot]
+            arr = regs[id(base)] if base.op.name in ("DEFINE_REG", "DEFINE_LOCAL") else buffers[base.arg.slot]
             gate = bool(get(u.src[2])) if len(u.src) > 2 else True
             ptr[id(u)] = (arr, int(get(u.src[1])), gate)
         elif op == "LOAD":

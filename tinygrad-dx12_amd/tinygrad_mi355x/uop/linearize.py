@@ -13,6 +13,13 @@ and turns every REDUCE into a loop over its ranges with a register accumulator:
 * an ``INDEX`` read as a value becomes a ``LOAD`` (a gated index loads 0 where its gate is false);
   an ``INDEX`` a STORE writes through stays an address.
 
+When every REDUCE of the stored values folds at least ``GROUP_MIN`` points over constant bounds
+and none is nested in another, one workgroup computes each stored point instead: work-item
+``lidx0`` folds points ``lidx0, lidx0 + L, ...`` of each reduction into its register accumulator
+(the last chunk's surplus work-items read a valid point and fold the identity), the
+accumulators meet in a ``DEFINE_LOCAL`` array by a halving tree with a ``BARRIER`` after every
+level, and work-item 0 stores.
+
 The listing uses tinygrad's codegen ops (SPECIAL, DEFINE_REG, RANGE/END, IF/ENDIF, LOAD, STORE),
 so ``MI355XRenderer.render`` renders it as it would render a listing made by tinygrad.  The
 reference hands this step to tinygrad (its renderer receives tinygrad's listing,
@@ -29,6 +36,7 @@ from dataclasses import dataclass
 from tinygrad_mi355x.uop.ops import ALU, AxisType, DType, KernelInfo, Ops, UOp, dtypes
 
 LOCAL = 256  # work-items per workgroup
+GROUP_MIN = 256  # reduction length from which a workgroup folds each stored point
 
 
 @dataclass(frozen=True)
@@ -72,12 +80,28 @@ def _items(sink: UOp) -> list[tuple[UOp, tuple[UOp, ...]]]:
     return [(s, order) for s, _ in items]
 
 
+def _grouped(items) -> bool:
+    """Whether the stored values' reductions are long, flat and of constant length."""
+    reduces = [u for store, _ in items for u in store.src[1].toposort() if u.op is Ops.REDUCE]
+    if not reduces:
+        return False
+    for r in reduces:
+        if any(u.op is Ops.REDUCE for u in r.src[0].toposort()):
+            return False
+        if any(x.op is not Ops.RANGE or x.src[0].op is not Ops.CONST for x in r.src[1:]):
+            return False
+        if math.prod(x.src[0].arg for x in r.src[1:]) < GROUP_MIN:
+            return False
+    return True
+
+
 class _Emitter:
     def __init__(self) -> None:
         self.out: list[UOp] = []
         self.scopes: list[dict[UOp, UOp]] = [{}]
         self.regs = self.loops = self.loads = 0
         self.free_cache: dict[UOp, frozenset] = {}
+        self.group: tuple[UOp, int] | None = None  # (lidx0, work-items) when a workgroup folds each point
 
     def put(self, u: UOp) -> UOp:
         self.out.append(u)
@@ -141,7 +165,7 @@ class _Emitter:
             src = (self.address(node.src[0]), *(self.value(s) for s in node.src[1:]))
             return self.bind(node, self.put(UOp(Ops.LOAD, node.dtype, src)))
         if op is Ops.REDUCE:
-            return self.reduce(node)
+            return self.grouped_reduce(node) if self.group is not None else self.reduce(node)
         if op in ALU or op in (Ops.CAST, Ops.BITCAST):
             return self.bind(node, self.put(UOp(op, node.dtype, tuple(self.value(s) for s in node.src), node.arg)))
         raise ValueError(f"{op.name} cannot be a value in a scheduled kernel")
@@ -175,6 +199,70 @@ class _Emitter:
             self.put(UOp(Ops.END, None, (loop,)))
         return self.bind(node, self.put(self.reg_load(slot)))
 
+    def const(self, dt, value) -> UOp:
+        return self.value(UOp.const(dt, value))
+
+    def alu(self, op: Ops, dt, *src: UOp) -> UOp:
+        return self.put(UOp(op, dt, src))
+
+    def grouped_reduce(self, node: UOp) -> UOp:
+        """REDUCE folded by the workgroup (see the module docstring)."""
+        lidx, local = self.group
+        idx = dtypes.index
+        x, ranges = node.src[0], node.src[1:]
+        bounds = [r.src[0].arg for r in ranges]
+        total = math.prod(bounds)
+        ident = _identity(node.arg, node.dtype)
+        acc = self.put(UOp(Ops.DEFINE_REG, node.dtype, (), (1, self.regs)))
+        self.regs += 1
+        slot = self.put(UOp(Ops.INDEX, node.dtype, (acc, UOp.const(idx, 0))))
+        self.put(UOp(Ops.STORE, None, (slot, self.value(ident))))
+        for n in x.toposort():  # loop-invariant parts first
+            if n.op not in (Ops.RANGE, Ops.PARAM, Ops.DEFINE_VAR) and self.in_scope(self.free(n)):
+                self.value(n)
+        loop = self.put(UOp(Ops.RANGE, idx, (self.const(idx, -(-total // local)),), ("group", self.loops)))
+        self.loops += 1
+        self.scopes.append({})
+        p = self.alu(Ops.ADD, idx, self.alu(Ops.MUL, idx, loop, self.const(idx, local)), lidx)
+        gate = None
+        if total % local:
+            gate = self.alu(Ops.CMPLT, dtypes.bool, p, self.const(idx, total))
+            p = self.put(UOp(Ops.WHERE, idx, (gate, p, self.const(idx, total - 1))))  # in-bounds point
+        stride = 1
+        for r, n in reversed(list(zip(ranges, bounds))):
+            v = p if stride == 1 else self.alu(Ops.IDIV, idx, p, self.const(idx, stride))
+            if stride * n < total:
+                v = self.alu(Ops.MOD, idx, v, self.const(idx, n))
+            self.bind(r, v)
+            stride *= n
+        body = self.value(x)
+        if gate is not None:
+            body = self.put(UOp(Ops.WHERE, node.dtype, (gate, body, self.value(ident))))
+        self.put(UOp(Ops.STORE, None, (slot, self.put(UOp(node.arg, node.dtype, (self.put(self.reg_load(slot)), body))))))
+        self.scopes.pop()
+        self.put(UOp(Ops.END, None, (loop,)))
+        # halving tree over the workgroup's accumulators in LDS
+        lds = self.put(UOp(Ops.DEFINE_LOCAL, node.dtype, (), (local, self.regs)))
+        self.regs += 1
+        mine = self.put(UOp(Ops.INDEX, node.dtype, (lds, lidx)))
+        self.put(UOp(Ops.STORE, None, (mine, self.put(self.reg_load(slot)))))
+        self.barrier()
+        half = local // 2
+        while half >= 1:
+            self.put(UOp(Ops.IF, None, (self.alu(Ops.CMPLT, dtypes.bool, lidx, self.const(idx, half)),)))
+            other = self.put(UOp(Ops.INDEX, node.dtype, (lds, self.alu(Ops.ADD, idx, lidx, self.const(idx, half)))))
+            a, b = self.put(self.reg_load(mine)), self.put(self.reg_load(other))
+            self.put(UOp(Ops.STORE, None, (mine, self.put(UOp(node.arg, node.dtype, (a, b))))))
+            self.put(UOp(Ops.ENDIF, None, ()))
+            self.barrier()
+            half //= 2
+        first = self.put(UOp(Ops.INDEX, node.dtype, (lds, UOp.const(idx, 0))))
+        return self.bind(node, self.put(self.reg_load(first)))
+
+    def barrier(self) -> None:
+        self.loads += 1
+        self.put(UOp(Ops.BARRIER, None, (), self.loads))
+
     def reg_load(self, slot: UOp) -> UOp:
         """A read of the accumulator; each is its own UOp (the value changes between reads)."""
         self.loads += 1
@@ -197,12 +285,13 @@ def linearize(sink: UOp, local: int = LOCAL) -> LinearKernel:
         raise ValueError("a kernel stores fewer than 2^31 points")
     if any(p.max_numel() >= 2**31 for p in params):
         raise ValueError("kernel buffers hold fewer than 2^31 elements (32-bit indexing)")
-    local = max(64, min(local, -(-total // 64) * 64))
-    groups = -(-total // local)
-
     e = _Emitter()
     for u in (*params, *variables):
         e.bind(u, e.put(u))
+    if _grouped(items):
+        return _linearize_grouped(sink, items, e, params, variables, order, bounds, total, local)
+    local = max(64, min(local, -(-total // 64) * 64))
+    groups = -(-total // local)
     gidx = e.put(UOp(Ops.SPECIAL, dtypes.index, (UOp.const(dtypes.index, groups),), "gidx0"))
     lidx = e.put(UOp(Ops.SPECIAL, dtypes.index, (UOp.const(dtypes.index, local),), "lidx0"))
     g = e.put(UOp(Ops.ADD, dtypes.index, (e.put(UOp(Ops.MUL, dtypes.index, (gidx, e.value(UOp.const(dtypes.index, local))))), lidx)))
@@ -226,3 +315,26 @@ def linearize(sink: UOp, local: int = LOCAL) -> LinearKernel:
         e.put(UOp(Ops.ENDIF, None, ()))
     name = sink.arg.name if isinstance(sink.arg, KernelInfo) else "kernel"
     return LinearKernel(name, tuple(e.out), tuple(params), tuple(variables), (groups, 1, 1), (local, 1, 1))
+
+
+def _linearize_grouped(sink, items, e: _Emitter, params, variables, order, bounds, total, local) -> LinearKernel:
+    """One workgroup per stored point: the stored ranges are the digits of gidx0."""
+    idx = dtypes.index
+    gidx = e.put(UOp(Ops.SPECIAL, idx, (UOp.const(idx, total),), "gidx0"))
+    lidx = e.put(UOp(Ops.SPECIAL, idx, (UOp.const(idx, local),), "lidx0"))
+    e.group = (lidx, local)
+    stride = 1
+    for r, n in reversed(list(zip(order, bounds))):
+        v = gidx if stride == 1 else e.alu(Ops.IDIV, idx, gidx, e.const(idx, stride))
+        if stride * n < total:
+            v = e.alu(Ops.MOD, idx, v, e.const(idx, n))
+        e.bind(r, v)
+        stride *= n
+    # every work-item takes part in the reductions; work-item 0 stores
+    stores = [(e.address(store.src[0]), e.value(store.src[1])) for store, _ in items]
+    e.put(UOp(Ops.IF, None, (e.alu(Ops.CMPEQ, dtypes.bool, lidx, e.const(idx, 0)),)))
+    for address, value in stores:
+        e.put(UOp(Ops.STORE, None, (address, value)))
+    e.put(UOp(Ops.ENDIF, None, ()))
+    name = sink.arg.name if isinstance(sink.arg, KernelInfo) else "kernel"
+    return LinearKernel(name, tuple(e.out), tuple(params), tuple(variables), (total, 1, 1), (local, 1, 1))
