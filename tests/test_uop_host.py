@@ -290,3 +290,35 @@ def test_long_reductions_fold_in_a_workgroup():
     short = o.index(r).store(x.index(r * cols + UOp.range(100, 4, AxisType.REDUCE)).reduce(
         UOp.range(100, 4, AxisType.REDUCE), arg=Ops.ADD)).end(r).sink(arg=KernelInfo(name="short"))
     assert "BARRIER" not in [u.op.name for u in linearize(short).uops]
+
+
+def test_one_renderer_renders_uop_listings_from_many_threads():
+    """Listings rendered from several threads at once equal their single-threaded renders."""
+    import threading
+
+    r = MI355XRenderer()
+    kinds = (dtypes.float32, dtypes.float64, dtypes.int32, dtypes.float16, dtypes.bfloat16, dtypes.uint8)
+    listings = []
+    for i in range(12):
+        dt = kinds[i % len(kinds)]
+        src, out = UOp.param(1, dt, 4 + i), UOp.param(0, dt, 4 + i)
+        k = UOp.range(4 + i, 0)
+        v = src.index(k)
+        for _ in range(200 * (1 + i % 4)):
+            v = v * src.index(k) + src.index(k)
+        listings.append(linearize(out.index(k).store(v).end(k).sink(arg=KernelInfo(name=f"chain_{i}"))))
+    alone = [r.render(x) for x in listings]
+    start = threading.Event()
+    results: dict[int, list] = {}
+
+    def worker(i: int) -> None:
+        start.wait()
+        results[i] = [r.render(listings[i]) for _ in range(3)]
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(listings))]
+    for t in threads:
+        t.start()
+    start.set()
+    for t in threads:
+        t.join(60)
+    assert all(results[i] == [alone[i]] * 3 for i in range(len(listings)))
