@@ -322,3 +322,23 @@ def test_one_renderer_renders_uop_listings_from_many_threads():
     for t in threads:
         t.join(60)
     assert all(results[i] == [alone[i]] * 3 for i in range(len(listings)))
+
+
+def test_in_place_updates_and_deep_expression_chains():
+    """One INDEX both read and written through (x[i] = x[i] * 3 + 1), and a 5000-deep chain of
+    operations (listed without recursion)."""
+    n = 10
+    x = UOp.param(0, dtypes.int32, n)
+    i = UOp.range(n, 0)
+    buf = np.arange(n, dtype=np.int32)
+    uop_interp.run(linearize(x.index(i).store(x.index(i) * 3 + 1).end(i).sink()), {0: buf})
+    np.testing.assert_array_equal(buf, np.arange(n) * 3 + 1)
+    y, o = UOp.param(1, dtypes.int32, n), UOp.param(0, dtypes.int32, n)
+    v = y.index(i)
+    for _ in range(5000):
+        v = v + 1
+    out = np.zeros(n, np.int32)
+    listing = linearize(o.index(i).store(v).end(i).sink())
+    uop_interp.run(listing, {0: out, 1: np.arange(n, dtype=np.int32)})
+    np.testing.assert_array_equal(out, np.arange(n) + 5000)
+    assert "data0" in MI355XRenderer().render(listing)

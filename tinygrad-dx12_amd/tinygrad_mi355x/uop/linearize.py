@@ -139,36 +139,67 @@ class _Emitter:
         return all(self.find(r) is not None for r in ranges)
 
     def address(self, node: UOp) -> UOp:
-        """An INDEX as an address into its (already listed) buffer."""
-        found = self.find(node)
+        """An INDEX as an address into its (already listed) buffer.  Addresses are bound under
+        their own key: one INDEX can be both read (a LOAD) and written through."""
+        key = ("address", node)
+        found = self.find(key)
         if found is not None:
             return found
         buf = self.find(node.src[0])
         if buf is None:
             raise ValueError(f"INDEX of an unlisted {node.src[0].op.name}")
         src = (buf, *(self.value(s) for s in node.src[1:]))
-        return self.bind(node, self.put(UOp(Ops.INDEX, node.dtype, src)))
+        return self.bind(key, self.put(UOp(Ops.INDEX, node.dtype, src)))
+
+    def _pending(self, root: UOp) -> list[UOp]:
+        """The unlisted nodes ``root`` needs, each after its sources (iterative: expression
+        chains may be thousands deep); a REDUCE is listed with its body by ``reduce``."""
+        order: list[UOp] = []
+        seen: set[int] = set()
+        stack: list[tuple[UOp, bool]] = [(root, False)]
+        while stack:
+            n, done = stack.pop()
+            if done:
+                order.append(n)
+                continue
+            if id(n) in seen or self.find(n) is not None:
+                continue
+            seen.add(id(n))
+            stack.append((n, True))
+            if n.op is not Ops.REDUCE:
+                stack.extend((x, False) for x in reversed(n.src))
+        return order
 
     def value(self, node: UOp) -> UOp:
         found = self.find(node)
         if found is not None:
             return found
+        for n in self._pending(node):
+            if self.find(n) is None:
+                self._emit(n)
+        return self.find(node)
+
+    def _emit(self, node: UOp) -> None:
+        """List one node whose sources are listed."""
         op = node.op
         if op is Ops.CONST:  # constants belong to the outermost scope
             self.scopes[0][node] = node
-            return self.put(node)
-        if op is Ops.RANGE:
+            self.put(node)
+        elif op is Ops.RANGE:
             raise ValueError("a RANGE is used outside its loop")
-        if op is Ops.INDEX:
-            return self.bind(node, self.put(UOp(Ops.LOAD, node.dtype, (self.address(node),))))
-        if op is Ops.LOAD:  # explicit load of an INDEX (with an optional alternative value)
-            src = (self.address(node.src[0]), *(self.value(s) for s in node.src[1:]))
-            return self.bind(node, self.put(UOp(Ops.LOAD, node.dtype, src)))
-        if op is Ops.REDUCE:
-            return self.grouped_reduce(node) if self.group is not None else self.reduce(node)
-        if op in ALU or op in (Ops.CAST, Ops.BITCAST):
-            return self.bind(node, self.put(UOp(op, node.dtype, tuple(self.value(s) for s in node.src), node.arg)))
-        raise ValueError(f"{op.name} cannot be a value in a scheduled kernel")
+        elif op is Ops.INDEX:
+            self.bind(node, self.put(UOp(Ops.LOAD, node.dtype, (self.address(node),))))
+        elif op is Ops.LOAD:  # explicit load of an INDEX (with an optional alternative value)
+            src = (self.address(node.src[0]), *(self.find(s) for s in node.src[1:]))
+            self.bind(node, self.put(UOp(Ops.LOAD, node.dtype, src)))
+        elif op is Ops.REDUCE:
+            self.grouped_reduce(node) if self.group is not None else self.reduce(node)
+        elif op in ALU or op in (Ops.CAST, Ops.BITCAST):
+            self.bind(node, self.put(UOp(op, node.dtype, tuple(self.find(s) for s in node.src), node.arg)))
+        elif op in (Ops.PARAM, Ops.DEFINE_VAR):
+            raise ValueError(f"{op.name} of slot/name {node.arg} is not a kernel parameter")
+        else:
+            raise ValueError(f"{op.name} cannot be a value in a scheduled kernel")
 
     def reduce(self, node: UOp) -> UOp:
         x, ranges = node.src[0], node.src[1:]
