@@ -19,10 +19,12 @@ ROOT = Path(__file__).resolve().parent.parent
 
 
 def test_plugin_path_imports_no_torch():
-    """The runtime, renderer and the plugin-buffer packed path import no torch."""
+    """The runtime, renderer, the plugin-buffer packed path and the UOp layer (IR, linearizer,
+    matmul rewrite, schedule runner) import no torch."""
     code = ("import sys; sys.path.insert(0, 'tinygrad-dx12_amd');"
             "import tinygrad_mi355x.codegen.program, tinygrad_mi355x.runtime.ops_mi355x,"
-            " tinygrad_mi355x.runtime.graph, tinygrad_mi355x.compat;"
+            " tinygrad_mi355x.runtime.graph, tinygrad_mi355x.compat, tinygrad_mi355x.uop.linearize,"
+            " tinygrad_mi355x.codegen.uop_matmul, tinygrad_mi355x.runtime.schedule;"
             "assert 'torch' not in sys.modules, sorted(m for m in sys.modules if 'torch' in m)[:5]")
     subprocess.run([sys.executable, "-c", code], check=True, cwd=ROOT)
 
