@@ -112,8 +112,9 @@ def test_lowering_plans_transposes_product_and_epilogue():
     assert tmp.dtype == dtypes.float32 and act.src[1].src[-1] is tmp    # epilogue reads the fp32 product
     epi = act.src[1].src[0]
     assert not any(u.op is Ops.REDUCE for u in epi.toposort())
+    out32, a8, b8 = _buffers((m * n, dtypes.float32), (m * k, dtypes.fp8e4m3), (k * n, dtypes.fp8e4m3))
     fp8 = lower_matmul(UOp.linear(UOp.call(matrix_sink(m, n, k, dtypes.fp8e4m3, right_nk=True,
-                                                       out_dtype=dtypes.float32), out, a, b)))
+                                                       out_dtype=dtypes.float32), out32, a8, b8)))
     assert _kinds(fp8) == ["tgm_gemm_fp8"]
 
 
@@ -136,6 +137,11 @@ def test_lowering_stages_rebindable_inputs():
     assert copy.src[2] is a and staged.src[1].src[2] is copy.src[1]
     # an output that is a rebindable input keeps its ordinary kernel
     assert _kinds(lower_matmul(UOp.linear(call), input_uops=(out,))) == ["kernel"]
+    # so does a call whose arguments do not hold their parameters (too small, another dtype)
+    small = _buffers((m * k - 1, dtypes.float16))[0]
+    assert _kinds(lower_matmul(UOp.linear(UOp.call(matrix_sink(m, n, k, right_nk=True), out, small, b)))) == ["kernel"]
+    wrong = _buffers((m * k, dtypes.bfloat16))[0]
+    assert _kinds(lower_matmul(UOp.linear(UOp.call(matrix_sink(m, n, k, right_nk=True), out, wrong, b)))) == ["kernel"]
     # so does a call that binds one buffer as both the output and an operand
     square = _buffers((m * m, dtypes.float16))[0]
     inplace = UOp.call(matrix_sink(m, m, m, right_nk=True), square, square, b)

@@ -177,6 +177,11 @@ def _lower_call(call: UOp, inputs: set) -> tuple[UOp, ...]:
     if any(s + 1 >= len(call.src) for s in slots):
         return (call,)
     output, left, right = (call.src[s + 1] for s in slots)
+    for arg, param in ((output, spec.output), (left, spec.left), (right, spec.right)):
+        # the GEMM reads and writes whole matrices: an argument that does not hold its
+        # parameter keeps the ordinary kernel, whose launch rejects it
+        if arg.op is not Ops.BUFFER or arg.dtype != param.dtype or arg.max_numel() < param.max_numel():
+            return (call,)
     if output is left or output is right:
         return (call,)  # the call writes the product over an operand
     if not spec.epilogue and output in inputs:
