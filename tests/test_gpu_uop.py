@@ -284,8 +284,10 @@ def _value(arr, dt):
     dict(m=200, n=136, k=192, dtype=dtypes.float16, transposed=True, right_nk=True, activated=True,
          kinds=["tgm_transpose16", "tgm_gemm_dense", "kernel"]),
     dict(m=96, n=160, k=256, dtype=dtypes.fp8e4m3, right_nk=True, out_dtype=dtypes.float32, kinds=["tgm_gemm_fp8"]),
-    dict(m=64, n=80, k=96, dtype=dtypes.float16, kinds=["kernel"]),
-], ids=["bf16_row_major", "f16_kmajor_relu", "fp8_nk", "f16_k96_rendered"])
+    dict(m=64, n=80, k=96, dtype=dtypes.float16, kinds=["kernel", "kernel", "tgm_gemm_dense"]),
+    dict(m=48, n=72, k=200, dtype=dtypes.fp8e4m3, transposed=True, out_dtype=dtypes.float32,
+         kinds=["kernel", "kernel", "tgm_gemm_fp8"]),
+], ids=["bf16_row_major", "f16_kmajor_relu", "fp8_nk", "f16_k96_padded", "fp8_k200_padded"])
 def test_scheduled_products_lowered_to_the_gemms(device, case):
     case = dict(case)
     kinds = case.pop("kinds")

@@ -118,13 +118,32 @@ def test_lowering_plans_transposes_product_and_epilogue():
     assert _kinds(fp8) == ["tgm_gemm_fp8"]
 
 
-def test_lowering_keeps_products_without_a_native_kernel():
+def test_lowering_pads_k_and_keeps_products_without_a_native_kernel():
     m, n, k = 64, 64, 96
     out, a, b = _buffers((m * n, dtypes.float16), (m * k, dtypes.float16), (k * n, dtypes.float16))
     call = UOp.call(matrix_sink(m, n, k), out, a, b)
-    assert _kinds(lower_matmul(UOp.linear(call))) == ["kernel"]          # K % 64 != 0
-    call32 = UOp.call(matrix_sink(64, 64, 64, dtypes.float32), out, a, b)
+    padded = lower_matmul(UOp.linear(call))                               # K % 64 != 0: zero columns to 128
+    assert _kinds(padded) == ["kernel", "kernel", "tgm_gemm_dense"]
+    assert [c.src[1].max_numel() for c in padded.src[:2]] == [m * 128, n * 128]
+    # the padding kernel: [rows, k] or K-major [k, rows] -> [rows, kp], zero past column k
+    rows, kk, kp = 3, 5, 8
+    src = np.arange(rows * kk, dtype=np.int32) + 1
+    for k_major in (False, True):
+        _, buf = _pad_operand(rows, kk, kp, k_major)
+        dst = np.full(rows * kp, -1, np.int32)
+        uop_interp.run(linearize(buf), {0: dst, 1: src})
+        stored = src.reshape(kk, rows).T if k_major else src.reshape(rows, kk)
+        np.testing.assert_array_equal(dst.reshape(rows, kp), np.pad(stored, ((0, 0), (0, kp - kk))))
+    buffers32 = _buffers((64 * 64, dtypes.float32), (64 * 64, dtypes.float32), (64 * 64, dtypes.float32))
+    call32 = UOp.call(matrix_sink(64, 64, 64, dtypes.float32), *buffers32)
     assert _kinds(lower_matmul(UOp.linear(call32))) == ["kernel"]        # fp32 operands
+
+
+def _pad_operand(rows, k, kp, k_major):
+    from tinygrad_mi355x.codegen.uop_matmul import _pad_call
+
+    call, staged = _pad_call(DEV, UOp.new_buffer(DEV, rows * k, dtypes.int32), dtypes.int32, rows, k, kp, k_major)
+    return staged, call.src[0]
 
 
 def test_lowering_stages_rebindable_inputs():

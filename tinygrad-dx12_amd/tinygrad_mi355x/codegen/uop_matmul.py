@@ -14,13 +14,15 @@ memory planning.  This is that pass over the kernel graphs of ``uop/ops.py``:
   addressing, a second output, aliasing between output and inputs, too-small parameters and
   kernels carrying explicit optimisation options are left alone (matmul.py:51-128).
 * ``lower_matmul(linear, input_uops)`` replaces each matched CALL whose operands have a native
-  kernel -- bf16 x bf16 or f16 x f16 with K a multiple of 64 (``tgm_gemm_dense``), FP8 x FP8
-  with K a multiple of 128 (``tgm_gemm_fp8``), fp32 accumulation -- with: a transpose into a new
-  buffer for each operand not already in the GEMM's K-contiguous layout (A [M, K], B [N, K]),
-  or a copy for one that is a rebindable input (``input_uops``: its storage may change between
-  replays); the product; and, when the kernel has an epilogue, the original kernel with the
-  reduction replaced by a read of the product's fp32 result (matmul.py:152-232: arbitrary
-  post-matrix expressions stay ordinary kernels).  Everything else keeps its CALL.
+  kernel -- bf16 x bf16 or f16 x f16 (``tgm_gemm_dense``, K steps of 64), FP8 x FP8
+  (``tgm_gemm_fp8``, K steps of 128), fp32 accumulation -- with: a transpose into a new buffer
+  for each operand not already in the GEMM's K-contiguous layout (A [M, K], B [N, K]), or a copy
+  for one that is a rebindable input (``input_uops``: its storage may change between replays);
+  when K is not a multiple of the step, a rendered copy of each operand into a K-contiguous
+  buffer padded with zero columns instead; the product; and, when the kernel has an epilogue,
+  the original kernel with the reduction replaced by a read of the product's fp32 result
+  (matmul.py:152-232: arbitrary post-matrix expressions stay ordinary kernels).  Everything
+  else keeps its CALL.
 
 Products of two bf16 / f16 / FP8 values are exact in fp32 on these GEMMs and their sums are
 fp32; a kernel that rounds the product to the operand dtype before the cast (``(a * b).cast``)
@@ -146,11 +148,20 @@ def native_kernel(spec: MatmulSpec) -> str | None:
         return None
     if not spec.epilogue and spec.output.dtype not in OUTPUT_DTYPES:
         return None
-    if a == b and a in (dtypes.bfloat16, dtypes.float16) and spec.k % 64 == 0:
+    if a == b and a in (dtypes.bfloat16, dtypes.float16):
         return "dense"
-    if a in FP8_DTYPES and b in FP8_DTYPES and spec.k % 128 == 0:
+    if a in FP8_DTYPES and b in FP8_DTYPES:
         return "fp8"
     return None
+
+
+def _k_step(kind: str) -> int:
+    return 64 if kind == "dense" else 128  # the GEMMs' K step (tgm_gemm_dense / tgm_gemm_fp8)
+
+
+def _storage(dt: DType) -> DType:
+    """Copies move FP8 elements as their bytes (the renderer decodes FP8 loads but does not encode)."""
+    return dtypes.uint8 if dt in FP8_DTYPES else dt
 
 
 def _program(p) -> UOp:
@@ -161,9 +172,24 @@ def _copy_call(device, arg: UOp, dt: DType, size: int) -> tuple[UOp, UOp]:
     """A rendered element copy of ``arg`` into a new buffer (the reference's staging kernel,
     matmul.py:218-226): (call, new buffer)."""
     staged = UOp.new_buffer(device, size, dt)
-    dest, src = UOp.param(0, dt, size, device), UOp.param(1, dt, size, device)
+    sdt = _storage(dt)
+    dest, src = UOp.param(0, sdt, size, device), UOp.param(1, sdt, size, device)
     axis = UOp.range(size, 0)
     sink = dest.index(axis).store(src.index(axis)).end(axis).sink(arg=KernelInfo(name="mi355x_matrix_input"))
+    return UOp.call(sink, staged, arg), staged
+
+
+def _pad_call(device, arg: UOp, dt: DType, rows: int, k: int, kp: int, k_major: bool) -> tuple[UOp, UOp]:
+    """A rendered copy of an operand into a new K-contiguous [rows, kp] buffer, zero past column k
+    (the reference's tail padding, codegen/linalg.py:61-87): ``arg`` holds [rows, k] or, K-major,
+    [k, rows].  Zero columns add nothing to the product.  (call, new buffer)."""
+    staged = UOp.new_buffer(device, rows * kp, dt)
+    sdt = _storage(dt)
+    dest, src = UOp.param(0, sdt, rows * kp, device), UOp.param(1, sdt, rows * k, device)
+    r, c = UOp.range(rows, 0), UOp.range(kp, 1)
+    value = src.index(c * rows + r if k_major else r * k + c, c < k)  # gated: no read past column k
+    ranges = (c, r) if k_major else (r, c)  # the source's contiguous axis varies fastest
+    sink = dest.index(r * kp + c).store(value).end(*ranges).sink(arg=KernelInfo(name="mi355x_matrix_pad"))
     return UOp.call(sink, staged, arg), staged
 
 
@@ -171,7 +197,8 @@ def _lower_call(call: UOp, inputs: set) -> tuple[UOp, ...]:
     if call.op is not Ops.CALL or call.src[0].op is not Ops.SINK:
         return (call,)
     spec = match_matmul(call.src[0])
-    if spec is None or native_kernel(spec) is None:
+    kind = native_kernel(spec) if spec is not None else None
+    if kind is None:
         return (call,)
     slots = (spec.output.arg.slot, spec.left.arg.slot, spec.right.arg.slot)
     if any(s + 1 >= len(call.src) for s in slots):
@@ -190,27 +217,33 @@ def _lower_call(call: UOp, inputs: set) -> tuple[UOp, ...]:
     m, n, k = spec.m, spec.n, spec.k
     a_dt, b_dt = spec.left.dtype, spec.right.dtype
     calls: list[UOp] = []
-    # A as [M, K] rows, B as [N, K] rows, in fresh buffers where the layout or a rebindable
-    # input requires it
-    if spec.transposed[0]:
-        a_buf = UOp.new_buffer(device, m * k, a_dt)
-        calls.append(UOp.call(_program(P.transpose_program(a_dt.name, k, m)), a_buf, left))
-    elif left in inputs:
-        copy, a_buf = _copy_call(device, left, a_dt, m * k)
-        calls.append(copy)
+    kp = -(-k // _k_step(kind)) * _k_step(kind)
+    if kp != k:  # K padded with zero columns to the GEMM's step, both operands K-contiguous
+        pad_a, a_buf = _pad_call(device, left, a_dt, m, k, kp, spec.transposed[0])
+        pad_b, b_buf = _pad_call(device, right, b_dt, n, k, kp, not spec.transposed[1])
+        calls += [pad_a, pad_b]
     else:
-        a_buf = left
-    if not spec.transposed[1]:
-        b_buf = UOp.new_buffer(device, n * k, b_dt)
-        calls.append(UOp.call(_program(P.transpose_program(b_dt.name, k, n)), b_buf, right))
-    elif right in inputs:
-        copy, b_buf = _copy_call(device, right, b_dt, n * k)
-        calls.append(copy)
-    else:
-        b_buf = right
+        # A as [M, K] rows, B as [N, K] rows, in fresh buffers where the layout or a
+        # rebindable input requires it
+        if spec.transposed[0]:
+            a_buf = UOp.new_buffer(device, m * k, a_dt)
+            calls.append(UOp.call(_program(P.transpose_program(a_dt.name, k, m)), a_buf, left))
+        elif left in inputs:
+            copy, a_buf = _copy_call(device, left, a_dt, m * k)
+            calls.append(copy)
+        else:
+            a_buf = left
+        if not spec.transposed[1]:
+            b_buf = UOp.new_buffer(device, n * k, b_dt)
+            calls.append(UOp.call(_program(P.transpose_program(b_dt.name, k, n)), b_buf, right))
+        elif right in inputs:
+            copy, b_buf = _copy_call(device, right, b_dt, n * k)
+            calls.append(copy)
+        else:
+            b_buf = right
     out_dt = dtypes.float32 if spec.epilogue else spec.output.dtype
     target = UOp.new_buffer(device, m * n, out_dt) if spec.epilogue else output
-    gemm = P.dense_program(a_dt.name, m, k, b_dt.name, n, k, k, out_dt.name, n)
+    gemm = P.dense_program(a_dt.name, m, kp, b_dt.name, n, kp, kp, out_dt.name, n)
     calls.append(UOp.call(_program(gemm), target, a_buf, b_buf))
     if spec.epilogue:
         tmp = UOp.param(len(call.src) - 1, dtypes.float32, m * n, device)

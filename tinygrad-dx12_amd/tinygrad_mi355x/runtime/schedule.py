@@ -25,7 +25,7 @@ from dataclasses import dataclass
 
 from tinygrad_mi355x.codegen.program import MatrixProgram
 from tinygrad_mi355x.uop.linearize import LinearKernel, linearize
-from tinygrad_mi355x.uop.ops import Ops, UOp
+from tinygrad_mi355x.uop.ops import FP8_DTYPES, Ops, UOp, dtypes
 
 
 @dataclass(frozen=True)
@@ -124,7 +124,10 @@ def plan(dev, linear: UOp, buffers: dict | None = None, var_vals: dict[str, int]
             if p.arg.slot + 1 >= len(call.src):
                 raise ValueError(f"kernel {kernel.listing.name}: no argument for slot {p.arg.slot}")
             b = buf(args[p.arg.slot])
-            if b.size < _nbytes(p) or args[p.arg.slot].dtype != p.dtype:
+            arg_dt = args[p.arg.slot].dtype
+            # an FP8 buffer binds a uint8 parameter: copies move FP8 elements as bytes
+            same = arg_dt == p.dtype or (p.dtype == dtypes.uint8 and arg_dt in FP8_DTYPES)
+            if b.size < _nbytes(p) or not same:
                 raise ValueError(f"kernel {kernel.listing.name}: argument for slot {p.arg.slot} does not match")
             bufs.append(b)
         vals = tuple(int(var_vals[v.arg[0]]) for v in kernel.listing.variables)
