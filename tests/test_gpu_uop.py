@@ -380,3 +380,47 @@ def test_long_reductions_fold_in_a_workgroup(device):
     got, _ = run_sink(device, norm, {1: xr})
     want = xr.reshape(n_rows, n) / np.sqrt((xr.reshape(n_rows, n).astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-5)
     assert np.abs(got[0].reshape(n_rows, n) - want).max() <= 1e-5 * np.abs(want).max()
+
+
+def _fp8_probe_values(target):
+    """Every FP8 value, the midpoints between neighbours and the floats next to them, overflow
+    thresholds, a wide random sweep, infinities, NaN and both zeros -- with both signs."""
+    vals = O.fp8_decode(np.arange(256, dtype=np.uint8), target).astype(np.float64)
+    fin = np.unique(vals[np.isfinite(vals) & (vals >= 0)])
+    mids = (fin[1:] + fin[:-1]) / 2
+    top = fin[-1] + (fin[-1] - fin[-2]) / 2  # halfway past the largest value
+    pts = np.concatenate([fin, mids, [top, top * 1.01, 1e9]]).astype(np.float32)
+    near = np.concatenate([np.nextafter(pts, np.float32(np.inf)), np.nextafter(pts, np.float32(0))])
+    rng = np.random.default_rng(13)
+    sweep = (rng.standard_normal(4000) * np.exp2(rng.integers(-24, 20, 4000))).astype(np.float32)
+    pos = np.concatenate([pts, near, np.abs(sweep), np.float32([np.inf, np.nan, 0.0])]).astype(np.float32)
+    return np.concatenate([pos, -pos]).astype(np.float32)
+
+
+@pytest.mark.parametrize("dt,target,torch_name", [(dtypes.fp8e4m3, "fp8e4m3", "float8_e4m3fn"),
+                                                  (dtypes.fp8e5m2, "fp8e5m2", "float8_e5m2")], ids=["e4m3", "e5m2"])
+def test_fp8_casts_stores_and_arithmetic_round_like_torch(device, dt, target, torch_name):
+    """fp32 -> FP8 stores are bit-exact against torch's conversion on the CPU, and FP8 arithmetic
+    is fp32 arithmetic rounded to the format after every operation."""
+    import torch
+
+    x = _fp8_probe_values(target)
+    n = x.size
+    i = UOp.range(n, 0)
+    src, dst = UOp.param(1, dtypes.float32, n, DEV), UOp.param(0, dt, n, DEV)
+    sink = dst.index(i).store(src.index(i).cast(dt)).end(i).sink(arg=KernelInfo(name=f"enc_{target}"))
+    out, _ = run_sink(device, sink, {1: x})
+    want = torch.from_numpy(x).to(getattr(torch, torch_name)).view(torch.uint8).numpy()
+    bad = np.nonzero(out[0] != want)[0]
+    assert bad.size == 0, (x[bad[:8]], out[0][bad[:8]], want[bad[:8]])
+    # a * b + a with every operation rounded to the format
+    rng = np.random.default_rng(14)
+    codes = rng.integers(0, 256, (2, 2048)).astype(np.uint8)
+    codes[(codes & 0x7F) >= (0x7C if target == "fp8e5m2" else 0x7F)] = 0x38  # finite operands
+    sink2 = elementwise(dt, lambda a, b: a * b + a, 2048, name=f"arith_{target}")
+    got, _ = run_sink(device, sink2, {1: codes[0], 2: codes[1]})
+    f8 = getattr(torch, torch_name)
+    a = torch.from_numpy(O.fp8_decode(codes[0], target))
+    b = torch.from_numpy(O.fp8_decode(codes[1], target))
+    ref = ((a * b).to(f8).float() + a).to(f8).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(got[0], ref)

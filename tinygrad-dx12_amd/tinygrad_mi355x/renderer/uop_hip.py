@@ -19,8 +19,10 @@ Arithmetic keeps each dtype's semantics, as the reference's dtype table requires
 negate of signed or narrow types are computed in an unsigned type at least as wide and truncated,
 so overflow is defined); bf16 values are computed in fp32 and rounded to bf16 after every
 operation; f16 uses gfx950's native f16 arithmetic; bool storage is a byte (loads test != 0, stores write 0 / 1);
-FP8 (E4M3FN, E5M2) buffers decode exactly to fp32 on load (FP8 arithmetic and FP8 stores are
-not rendered).  Floating multiply and add are not contracted into FMA (``MULACC`` is the fused
+FP8 (E4M3FN, E5M2) values live in fp32 registers: loads decode exactly, arithmetic and casts
+compute in fp32 and round to the format after every operation, stores encode (round to nearest
+even; E4M3FN turns NaN, infinities and overflow into NaN, E5M2 overflow into infinity, as
+torch's conversions do).  Floating multiply and add are not contracted into FMA (``MULACC`` is the fused
 operation); division and square root are correctly rounded; EXP2 / LOG2 / SIN use the device
 math library.
 """
@@ -65,6 +67,29 @@ __device__ __forceinline__ float tgm_e5m2_f32(unsigned char b) {
   if (e == 31) v = m == 0 ? __builtin_inff() : __builtin_nanf("");
   return (b & 0x80) ? -v : v;
 }
+// fp32 -> FP8, round to nearest even.  E4M3FN: NaN, infinities and magnitudes past 464 (which
+// round beyond 448) give S.1111.111; E5M2: NaN gives S.11111.11, infinities and magnitudes of
+// 61440 and more give S.11111.00.  Normal results round the fp32 significand to 3 (2) bits by
+// integer addition; subnormal ones are rint(|x| * 2^9) (2^16) codes of the smallest step.
+__device__ __forceinline__ unsigned char tgm_f32_e4m3(float f) {
+  const unsigned u = __builtin_bit_cast(unsigned, f) & 0x7FFFFFFFu, s = (__builtin_bit_cast(unsigned, f) >> 24) & 0x80u;
+  if (u > 0x43E80000u) return (unsigned char)(s | 0x7Fu);  // NaN, inf, |f| > 464
+  if (u >= 0x3C800000u) {                                  // |f| >= 2^-6: normal
+    const unsigned r = u + 0x7FFFFu + ((u >> 20) & 1u);
+    return (unsigned char)(s | (((r >> 23) - 120u) << 3) | ((r >> 20) & 7u));
+  }
+  return (unsigned char)(s | (unsigned)__builtin_rintf(__builtin_bit_cast(float, u) * 512.0f));
+}
+__device__ __forceinline__ unsigned char tgm_f32_e5m2(float f) {
+  const unsigned u = __builtin_bit_cast(unsigned, f) & 0x7FFFFFFFu, s = (__builtin_bit_cast(unsigned, f) >> 24) & 0x80u;
+  if (u > 0x7F800000u) return (unsigned char)(s | 0x7Fu);  // NaN
+  if (u >= 0x47700000u) return (unsigned char)(s | 0x7Cu);  // inf, |f| >= 61440
+  if (u >= 0x38800000u) {                                  // |f| >= 2^-14: normal
+    const unsigned r = u + 0xFFFFFu + ((u >> 21) & 1u);
+    return (unsigned char)(s | (((r >> 23) - 112u) << 2) | ((r >> 21) & 3u));
+  }
+  return (unsigned char)(s | (unsigned)__builtin_rintf(__builtin_bit_cast(float, u) * 65536.0f));
+}
 """
 
 
@@ -100,7 +125,15 @@ def _int_literal(v: int, dt: str) -> str:
     return f"(({VALUE_TYPES[dt]}){v})"
 
 
+def fp8_round(expr: str, dt: str) -> str:
+    """``expr`` (an fp32 expression) rounded to FP8 format ``dt``, as the fp32 value of the code."""
+    f = "e4m3" if dt == "float8_e4m3fn" else "e5m2"
+    return f"tgm_{f}_f32(tgm_f32_{f}({expr}))"
+
+
 def literal(value, dt: str) -> str:
+    if dt in FP8:
+        return fp8_round(_float_literal(float(value), "float32"), dt)
     if dt == "bool":
         return "true" if value else "false"
     if dt in FLOATS:
@@ -141,8 +174,6 @@ class _Listing:
     def alu(self, op: str, dt: str, srcs) -> str:
         a = [self.ref(s) for s in srcs]
         sdt = dtype_name(srcs[0].dtype)
-        if sdt in FP8 and op not in ("CMPLT", "CMPNE", "CMPEQ") or dt in FP8:
-            raise ValueError("FP8 values are only loaded and cast")
         if op == "WHERE":
             return f"({a[0]} ? {a[1]} : {a[2]})"
         if op in ("CMPLT", "CMPNE", "CMPEQ"):
@@ -156,6 +187,8 @@ class _Listing:
             if op in bool_ops:
                 return f"({a[0]} {bool_ops[op]} {a[1]})"
             raise ValueError(f"{op} on bool")
+        if dt in FP8:  # fp32 arithmetic on the decoded values, one rounding to the format
+            return fp8_round(self.float_alu(op, "float32", a), dt)
         if dt in FLOATS:
             return self.float_alu(op, dt, a)
         return self.int_alu(op, dt, a)
@@ -209,10 +242,12 @@ class _Listing:
 
     def cast(self, src, dt: str, bit: bool) -> str:
         x, sdt = self.ref(src), dtype_name(src.dtype)
-        if dt in FP8:
-            raise ValueError("FP8 values are only loaded and cast")
         if bit:
+            if dt in FP8 or sdt in FP8:
+                raise ValueError("FP8 values live decoded in fp32 registers: no bit casts")
             return f"__builtin_bit_cast({VALUE_TYPES[dt]}, {x})"
+        if dt in FP8:
+            return fp8_round(f"(float)({x})", dt)
         if dt == "bool":
             return f"((bool)({x}))"
         if sdt == "bfloat16" and dt != "float32":
@@ -239,9 +274,9 @@ class _Listing:
     def store(self, u) -> None:
         idx, val = u.src[0], u.src[1]
         addr, dt, gate = self.ptrs[id(idx)]
-        if dt in FP8:
-            raise ValueError("FP8 stores are not rendered")
         v = self.ref(val)
+        if dt in FP8:
+            v = f"tgm_f32_{'e4m3' if dt == 'float8_e4m3fn' else 'e5m2'}({v})"
         if dt == "bool":
             v = f"(unsigned char)({v} ? 1 : 0)"
         if len(u.src) > 2:  # a separate store gate
