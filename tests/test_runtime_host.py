@@ -60,7 +60,7 @@ def test_renderer_rejects_bad_specs():
         r.render(KernelSpec("k", (BufferParam("x", torch.float32),), local_size=(2048, 1, 1)))
     with pytest.raises(ValueError):
         r.render(KernelSpec("k", (BufferParam("x", torch.float32),), (("n", "i8"),)))
-    assert "bfloat16" in r.supported_dtypes() and r.shared_max == 160 * 1024
+    assert {"bfloat16", "float8_e4m3fn", "float8_e5m2"} <= r.supported_dtypes() and r.shared_max == 160 * 1024
 
 
 class _FakeDev:

@@ -22,6 +22,7 @@ from __future__ import annotations
 import threading
 from dataclasses import dataclass, field
 
+from tinygrad_mi355x.renderer.uop_hip import VALUE_TYPES as UOP_VALUE_TYPES
 from tinygrad_mi355x.renderer.uop_hip import render_uops
 from tinygrad_mi355x.runtime.support.compiler_hip import MI355XCompiler
 
@@ -77,8 +78,9 @@ class MI355XRenderer:
 
     def supported_dtypes(self) -> set[str]:
         """Names of the arithmetic dtypes rendered kernels may use (packed formats are storage, not
-        arithmetic)."""
-        return set(TYPE_MAP)
+        arithmetic): the C++ types of hand-written bodies, and in UOp listings also FP8 E4M3FN /
+        E5M2 (computed in fp32 and rounded to the format after every operation, as bf16 is)."""
+        return set(TYPE_MAP) | set(UOP_VALUE_TYPES)
 
     def render(self, spec) -> str:
         """Complete ``extern "C" __global__`` source for a ``KernelSpec``, a ``LinearKernel`` or a
