@@ -367,3 +367,28 @@ def test_in_place_updates_and_deep_expression_chains():
     uop_interp.run(listing, {0: out, 1: np.arange(n, dtype=np.int32)})
     np.testing.assert_array_equal(out, np.arange(n) + 5000)
     assert "data0" in MI355XRenderer().render(listing)
+
+
+def test_graphs_built_in_many_threads_share_their_nodes():
+    """Hash-consing holds across threads: the same expression built concurrently is one object."""
+    import threading
+
+    results = []
+    start = threading.Event()
+
+    def build() -> None:
+        start.wait()
+        x = UOp.param(3, dtypes.float32, 64)
+        i = UOp.range(64, 7)
+        v = x.index(i)
+        for _ in range(300):
+            v = v * 2.0 + x.index(i)
+        results.append(v)
+
+    threads = [threading.Thread(target=build) for _ in range(8)]
+    for t in threads:
+        t.start()
+    start.set()
+    for t in threads:
+        t.join(60)
+    assert len(results) == 8 and all(r is results[0] for r in results)

@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import itertools
 import math
+import threading
 import weakref
 from dataclasses import dataclass
 from enum import Enum, auto
@@ -166,20 +167,22 @@ _buffer_ids = itertools.count()
 
 
 class _Interned(type):
-    """Hash-consing: one object per (op, dtype, src, arg)."""
+    """Hash-consing: one object per (op, dtype, src, arg), also when threads build graphs at once."""
 
     _cache: weakref.WeakValueDictionary = weakref.WeakValueDictionary()
+    _lock = threading.Lock()
 
     def __call__(cls, op: Ops, dtype: DType | None = None, src: tuple = (), arg: Any = None):
         src = tuple(src)
         # floats key by their bits: -0.0 and 0.0 are distinct constants
         key = (op, dtype, tuple(id(s) for s in src), ("f", arg.hex()) if isinstance(arg, float) else arg)
-        found = cls._cache.get(key)
-        if found is not None:
-            return found
-        obj = super().__call__(op, dtype, src, arg)
-        cls._cache[key] = obj
-        return obj
+        with cls._lock:
+            found = cls._cache.get(key)
+            if found is not None:
+                return found
+            obj = super().__call__(op, dtype, src, arg)
+            cls._cache[key] = obj
+            return obj
 
 
 def _as_uop(x, dtype: DType) -> "UOp":
