@@ -49,7 +49,7 @@ MIN_TRIALS = 5
 EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_n4096", "int4_gemv_n14336", "fp6_e3m2_gemm_m2048",
           "fp6_e2m3_gemm_m2048", "fp4_gemm_8192", "fp4_gemm_4096x14336x4096", "decoder_b1", "decoder_b8",
           "read_ceiling_31232000", "read_ceiling_470000000", "mfma_fp4_ceiling_8192", "bf16_gemm_8192",
-          "fp8_gemm_8192")
+          "fp8_gemm_8192", "uop_rowsum_16384x4096", "uop_gemm_bf16_4096_relu")
 PRIMARY = "fp4_gemv_m1"
 
 # workload -> (committed rocprof summary, substring of the dominant kernel's name)
@@ -66,6 +66,8 @@ PROFILES = {
     "bf16_gemm_8192": ("gemm_dense_bf16_m8192_n8192_k8192.txt", "gemm_dense"),
     "fp8_gemm_8192": ("gemm_dense_fp8_e4m3_m8192_n8192_k8192.txt", "gemm_dense"),
     "read_ceiling_31232000": ("probe_read_31232000.txt", "probe_read"),
+    "uop_rowsum_16384x4096": ("uop_rowsum_f32_16384x4096.txt", "uop_rowsum"),
+    "uop_gemm_bf16_4096_relu": ("uop_schedule_gemm_dense_bf16_4096_relu.txt", "gemm_dense"),
     "read_ceiling_470000000": ("probe_read_470000000.txt", "probe_read"),
     "mfma_fp4_ceiling_8192": ("probe_mfma_fp4_1024x512.txt", "probe_mfma_fp4"),
 }
@@ -313,6 +315,76 @@ def dense_gemm_workload(torch, K, dev, dtype: str, n: int, steps: int, warmup: i
             "TFLOPS": flops / ms / 1e9, "flops": flops, "bytes": nbytes, "timed_dispatches": steps,
             "hipblaslt_ms": lib_ms, "hipblaslt_TFLOPS": flops / lib_ms / 1e9,
             "roofline": mfma_roofline(flops, ms, peak, "dense fp8 MFMA" if fp8 else "dense bf16 MFMA")}
+
+
+def _plugin_graph_ms(graph, steps: int, warmup: int) -> float:
+    """Median GPU ms of one replay of a schedule graph on the plugin device's stream."""
+    for _ in range(max(warmup, 1)):
+        graph()
+    return statistics.median(graph(wait=True) for _ in range(steps)) * 1e3
+
+
+def uop_rowsum_workload(steps: int, warmup: int, rows: int = 16384, cols: int = 4096) -> dict:
+    """A rendered UOp kernel: the row sums of an fp32 [16384, 4096] matrix (a REDUCE of 4096
+    points per row, folded by one workgroup per row: strided register accumulators, then an LDS
+    tree), on the plugin device, as a schedule of two launches over two copies of the matrix
+    (537 MB, past the 256 MB Infinity Cache) replayed as one HIP graph; ms per launch."""
+    from tinygrad_mi355x.runtime import ops_mi355x as R
+    from tinygrad_mi355x.runtime.schedule import LinearGraph
+    from tinygrad_mi355x.uop.ops import AxisType, KernelInfo, Ops, UOp, dtypes
+
+    dev = R.get_device("MI355X")
+    f32 = dtypes.float32
+    x, o = UOp.param(1, f32, rows * cols, "MI355X"), UOp.param(0, f32, rows, "MI355X")
+    r, c = UOp.range(rows, 0), UOp.range(cols, 1, AxisType.REDUCE)
+    sink = o.index(r).store(x.index(r * cols + c).reduce(c, arg=Ops.ADD)).end(r).sink(
+        arg=KernelInfo(name="uop_rowsum"))
+    out, a, b = (UOp.new_buffer("MI355X", n, f32) for n in (rows, rows * cols, rows * cols))
+    bound = {u: dev.allocator.alloc(u.max_numel() * 4) for u in (out, a, b)}
+    graph = LinearGraph(dev, UOp.linear(UOp.call(sink, out, a), UOp.call(sink, out, b)), bound)
+    ms = _plugin_graph_ms(graph, steps, warmup) / 2
+    graph.close()
+    nbytes = rows * cols * 4 + rows * 4
+    return {"workload": f"UOp schedule: rendered row sums of fp32 [{rows}, {cols}] (workgroup-folded REDUCE)",
+            "ms": ms, "bytes": nbytes, "GB/s": nbytes / ms / 1e6, "timed_dispatches": 2 * steps,
+            "roofline": hbm_roofline(nbytes, ms)}
+
+
+def uop_gemm_workload(steps: int, warmup: int, n: int = 4096) -> dict:
+    """A UOp schedule C = relu(A B) (A [n, n], B [n, n] row-major [K, N], bf16, fp32 accumulation,
+    bf16 out) lowered by the matmul rewrite to tgm_transpose16 (B -> [N, K]), tgm_gemm_dense into an
+    fp32 buffer and the rendered ReLU epilogue, replayed as one HIP graph on the plugin device; ms
+    per replay of the whole schedule."""
+    import numpy as np
+
+    from tinygrad_mi355x.codegen.uop_matmul import lower_matmul
+    from tinygrad_mi355x.runtime import ops_mi355x as R
+    from tinygrad_mi355x.runtime.schedule import LinearGraph
+    from tinygrad_mi355x.uop.ops import AxisType, KernelInfo, Ops, UOp, dtypes
+
+    dev = R.get_device("MI355X")
+    bf = dtypes.bfloat16
+    out_p, a_p, b_p = (UOp.param(i, bf, n * n, "MI355X") for i in range(3))
+    row, col, i = UOp.range(n, 1), UOp.range(n, 2), UOp.range(n, 0, AxisType.REDUCE)
+    prod = a_p.index(row * n + i).cast(dtypes.float32) * b_p.index(i * n + col).cast(dtypes.float32)
+    value = prod.reduce(i, arg=Ops.ADD).maximum(0.0).cast(bf)
+    sink = out_p.index(row * n + col).store(value).end(row, col).sink(arg=KernelInfo(name="uop_mm_relu"))
+    bufs = [UOp.new_buffer("MI355X", n * n, bf) for _ in range(3)]
+    linear = lower_matmul(UOp.linear(UOp.call(sink, *bufs)))
+    kinds = [c.src[0].arg.name if c.src[0].op is Ops.PROGRAM else "rendered" for c in linear.src]
+    rng = np.random.default_rng(6)
+    bound = {}
+    for u in bufs:
+        bound[u] = dev.allocator.alloc(n * n * 2)
+        host = (rng.standard_normal(n * n).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        dev.allocator._copyin(bound[u], memoryview(host).cast("B"))
+    graph = LinearGraph(dev, linear, bound)
+    ms = _plugin_graph_ms(graph, steps, max(warmup, 20))
+    graph.close()
+    flops = 2 * n ** 3
+    return {"workload": f"UOp schedule relu(A @ B), bf16 {n}^3, lowered to {' + '.join(kinds)}", "ms": ms,
+            "TFLOPS": flops / ms / 1e9, "flops": flops, "bytes": 3 * n * n * 2, "timed_dispatches": steps,
+            "roofline": mfma_roofline(flops, ms, BF16_PEAK_TFLOPS, "dense bf16 MFMA")}
 
 
 def read_ceiling_workload(torch, K, dev, nbytes: int, steps: int, warmup: int) -> dict:
@@ -708,6 +780,8 @@ def main() -> int:
         "mfma_fp4_ceiling_8192": lambda: mfma_ceiling_workload(torch, K, dev, gemm_steps, 20),
         "bf16_gemm_8192": lambda: dense_gemm_workload(torch, K, dev, "bfloat16", 8192, gemm_steps, 20),
         "fp8_gemm_8192": lambda: dense_gemm_workload(torch, K, dev, "float8_e4m3fn", 8192, gemm_steps, 20),
+        "uop_rowsum_16384x4096": lambda: uop_rowsum_workload(steps, warmup),
+        "uop_gemm_bf16_4096_relu": lambda: uop_gemm_workload(gemm_steps, 20),
     }
     if args.only:
         print(json.dumps({args.only: workloads[args.only]()}))
