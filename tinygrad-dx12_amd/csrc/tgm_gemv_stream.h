@@ -1,5 +1,5 @@
-// Streaming MX GEMV (kernel family 1 fast path) shared by the per-format translation units
-// tgm_gemv_fp4.hip, tgm_gemv_fp6.hip and tgm_gemv_bf6.hip, which instantiate it.
+// Streaming MX GEMV (kernel family 1, M > 1 or shapes the one-row kernels do not take),
+// instantiated for FP4 E2M1, FP6 E2M3 and FP6 E3M2 weights in tgm_gemv_stream.hip.
 #pragma once
 
 #include <stdlib.h>
@@ -439,7 +439,7 @@ int launch_gemv_stream(hipStream_t s, const void* w, int64_t n, int64_t k, const
   return launch_stream_shape<FMT, 1, 8>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
 }
 
-// Instantiated once per format in its own translation unit.
+// Instantiated per format in tgm_gemv_stream.hip.
 int launch_gemv_stream_fp4(hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales, const void* x,
                            int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu = 0);
 int launch_gemv_stream_fp6(hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales, const void* x,
