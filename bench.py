@@ -55,7 +55,7 @@ PRIMARY = "fp4_gemv_m1"
 # workload -> (committed rocprof summary, substring of the dominant kernel's name)
 PROFILES = {
     "fp4_gemv_m1": ("gemv_fp4_e2m1_n14336_k4096_m1.txt", "gemv_rows_fp4"),
-    "fp4_gemv_m4": ("gemv_fp4_e2m1_n14336_k4096_m4.txt", "gemv_stream"),
+    "fp4_gemv_m4": ("gemv_fp4_e2m1_n14336_k4096_m4.txt", "gemv_quads"),
     "fp4_gemv_m16": ("gemv_fp4_e2m1_n14336_k4096_m16.txt", "gemv_stream"),
     "int4_gemv_n4096": ("gemv_int4_g32_n4096_k4096_m1.txt", "gemv_rows_int4"),
     "int4_gemv_n14336": ("gemv_int4_g32_n14336_k4096_m1.txt", "gemv_rows_int4"),

@@ -175,7 +175,8 @@ def test_gemv_fp4_decode_full_shape_against_oracle(dev, fp4_decode_weight_14336x
     """The benchmarked decode GEMV at its own shape: W FP4 E2M1 + E8M0/32 [14336, 4096], X bf16
     [M, 4096] ~ N(0, 1) (drawn after W), bf16 out.  Every one of the M x 14336 outputs is held to
     max relative error 1e-2 against the fp64 product of the host-dequantised weight (M = 1 runs
-    the row-streaming kernel with its full 1792-wave grid, M = 4 and 16 the streaming MFMA GEMV)."""
+    the row-streaming kernel with its full 1792-wave grid, M = 4 the row-quad kernel, M = 16 the
+    streaming MFMA GEMV)."""
     w, deq, state = fp4_decode_weight_14336x4096
     rng = np.random.default_rng(0)
     rng.bit_generator.state = state
@@ -231,6 +232,55 @@ def test_gemv_e8m0_extreme_scales(dev, fmt):
         r = ref[:, row]
         assert np.abs(y[:, row] - r).max() <= 1e-2 * np.abs(r).max()
     assert O.max_rel_err(np.where(ok, y, 0), np.where(ok, ref, 0)) <= TOL
+
+
+@pytest.mark.parametrize("scale_kind", ["e8m0", "none"])
+@pytest.mark.parametrize("nkm", [(37, 2048, 2), (250, 4096, 3), (1000, 6144, 4), (4100, 8192, 4), (1792, 4096, 2),
+                                 (8192, 2048, 3), (14336, 8192, 2)])
+def test_gemv_row_quads(dev, scale_kind, nkm):
+    """2 <= M <= 4 FP4 GEMVs with K a multiple of 2048 up to 8192 run the row-quad kernel (four
+    weight rows and the activation rows share K positions in one bf16 MFMA): ragged N (rows past
+    N are clamped and not stored), every K instantiation, workgroups of 8, 16, 28 and 56 rows
+    (chosen from N and the CU count), scaled and unscaled weights; a second launch on the same
+    inputs is bit-identical."""
+    n, k, m = nkm
+    rng = np.random.default_rng(n + 7 * k + m)
+    w, deq = make_weight(dev, "fp4_e2m1", n, k, scale_kind, rng)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    y = matmul_nt(x, w, dtype=torch.bfloat16)
+    ref = bf16_np(x).astype(np.float64) @ deq.T
+    assert O.max_rel_err(bf16_np(y), ref) <= TOL
+    assert torch.equal(matmul_nt(x, w, dtype=torch.bfloat16), y)
+
+
+def test_gemv_row_quads_one_hot_and_strides(dev):
+    """One-hot activation rows recover columns of deq(W) exactly at the chunk, instruction and
+    K-slice edges of K = 4096; through the C ABI, activations with ldx > K and outputs with
+    ldy > N in f32 and f16 (the columns past N keep their contents)."""
+    from tinygrad_mi355x.runtime import kernels as K
+
+    n, k = 70, 4096
+    rng = np.random.default_rng(3)
+    w, deq = make_weight(dev, "fp4_e2m1", n, k, "e8m0", rng)
+    cols = [0, 31, 32, 511, 512, 1023, 1024, 2047, 2048, 3071, 3072, 4095]
+    for start in range(0, len(cols), 4):
+        sel = cols[start:start + 4]
+        x = torch.zeros((len(sel), k), dtype=torch.bfloat16, device=dev)
+        for i, j in enumerate(sel):
+            x[i, j] = 1.0
+        y = matmul_nt(x, w, dtype=torch.float32).cpu().numpy()
+        assert np.array_equal(y, deq[:, sel].T.astype(np.float32))
+    m, ldx, ldy = 3, k + 64, n + 5
+    xs = torch.from_numpy(rng.standard_normal((m, ldx)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    ref = bf16_np(xs[:, :k]).astype(np.float64) @ deq.T
+    for tdt in (torch.float32, torch.float16):
+        y = torch.full((m, ldy), 7.0, dtype=tdt, device=dev)
+        K.call("tgm_gemv", w.data.data_ptr(), K.FORMAT_IDS["fp4_e2m1"], n, k, K.ptr(w.scales),
+               K.dtype_id(w.scales.dtype), 32, xs.data_ptr(), K.dtype_id(xs.dtype), m, ldx, y.data_ptr(),
+               K.dtype_id(tdt), ldy, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert O.max_rel_err(y[:, :n].float().cpu().numpy(), ref) <= TOL
+        assert bool((y[:, n:] == 7.0).all())
 
 
 @pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e2m3", "fp6_e3m2"])

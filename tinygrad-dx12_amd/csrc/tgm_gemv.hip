@@ -8,7 +8,7 @@
 //
 //   Y[m, n] = sum_k X[m, k] * deq(W)[n, k],   M <= 16
 //
-// Four kernels:
+// Five kernels:
 //  * gemv_rows_fp4 / gemv_rows_int4 -- M = 1 with K a multiple of 2048: FP4 weights with
 //    E8M0 (or no) scales x bf16 activations, or INT4/UINT4 weights with fp16/bf16/f32 group
 //    scales (32, 64, 128) x fp16 activations; each wave streams 8 whole rows in address
@@ -16,6 +16,10 @@
 //  * gemv_int4   -- INT4/UINT4 weights with fp16/bf16/f32/E8M0 group scales (groups of 32,
 //    64 or 128), fp16 activations: one f16 MFMA per 32-element block, scale applied to the
 //    block's exact partial sum (tgm_gemv_int4.hip).
+//  * gemv_quads_fp4 -- 2 <= M <= 4, FP4 weights with E8M0 (or no) scales, bf16 activations,
+//    K = 2048 .. 8192 in steps of 2048: four weight rows and the activation rows share K
+//    positions in one bf16 MFMA, whose 4x4 diagonal blocks are the dot products
+//    (tgm_gemv_quads.hip).
 //  * gemv_stream -- FP4/FP6 weights with E8M0 (or no) scales, bf16 activations.  Each
 //    dequantised weight code*2^(e-127) is exact in bf16, every bf16*bf16 product is
 //    exact in fp32, so v_mfma_f32_16x16x32_bf16 with fp32 accumulation computes the
@@ -25,6 +29,9 @@
 #include "tgm_gemv_stream.h"
 
 namespace tgm {
+// 2 <= M <= 4 FP4 GEMV over row-quads (tgm_gemv_quads.hip).
+int launch_gemv_quads_fp4(hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales, const void* x,
+                          int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy);
 // M = 1 FP4 GEMV streamed row-contiguously (tgm_gemv_rows.hip).
 int launch_gemv_rows(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k, const void* scales, int sdt,
                      int64_t bs, const void* x, int xdt, int64_t m, void* y, int ydt, bool swiglu = false);
@@ -145,6 +152,10 @@ extern "C" int tgm_gemv(const void* w, int fmt, int64_t n, int64_t k, const void
     if (st != TGM_E_UNSUPPORTED) return st;
   }
   if (mfma_gemv_ok(w, fmt, n, k, scales, scale_dtype, block_size, x, x_dtype, m, ldx, y_dtype)) {
+    if (fmt == TGM_FMT_FP4_E2M1) {
+      const int sq = launch_gemv_quads_fp4(s, w, n, k, scales, x, m, ldx, y, y_dtype, ldy);
+      if (sq == TGM_OK) return launch_status("tgm_gemv(quads)");
+    }
     int st;
     switch (fmt) {
       case TGM_FMT_FP4_E2M1: st = launch_gemv_stream_fp4(s, w, n, k, scales, x, m, ldx, y, y_dtype, ldy); break;
