@@ -48,8 +48,8 @@ MIN_TRIALS = 5
 
 EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_n4096", "int4_gemv_n14336", "fp6_e3m2_gemm_m2048",
           "fp6_e2m3_gemm_m2048", "fp4_gemm_8192", "fp4_gemm_4096x14336x4096", "decoder_b1", "decoder_b8",
-          "read_ceiling_31232000", "read_ceiling_470000000", "mfma_fp4_ceiling_8192", "bf16_gemm_8192",
-          "fp8_gemm_8192", "uop_rowsum_16384x4096", "uop_gemm_bf16_4096_relu")
+          "read_ceiling_31232000", "read_ceiling_9453568", "read_ceiling_470000000", "mfma_fp4_ceiling_8192",
+          "bf16_gemm_8192", "fp8_gemm_8192", "uop_rowsum_16384x4096", "uop_gemm_bf16_4096_relu")
 PRIMARY = "fp4_gemv_m1"
 
 # workload -> (committed rocprof summary, substring of the dominant kernel's name)
@@ -66,6 +66,7 @@ PROFILES = {
     "bf16_gemm_8192": ("gemm_dense_bf16_m8192_n8192_k8192.txt", "gemm_dense"),
     "fp8_gemm_8192": ("gemm_dense_fp8_e4m3_m8192_n8192_k8192.txt", "gemm_dense"),
     "read_ceiling_31232000": ("probe_read_31232000.txt", "probe_read"),
+    "read_ceiling_9453568": ("probe_read_9453568.txt", "probe_read"),
     "uop_rowsum_16384x4096": ("uop_rowsum_f32_16384x4096.txt", "uop_rowsum"),
     "uop_gemm_bf16_4096_relu": ("uop_schedule_gemm_dense_bf16_4096_relu.txt", "gemm_dense"),
     "read_ceiling_470000000": ("probe_read_470000000.txt", "probe_read"),
@@ -390,7 +391,8 @@ def uop_gemm_workload(steps: int, warmup: int, n: int = 4096) -> dict:
 def read_ceiling_workload(torch, K, dev, nbytes: int, steps: int, warmup: int) -> dict:
     """tgm_probe_read: ``nbytes`` read with the decode GEMV's access shape and discarded, over a
     rotating copy set timed like the GEMV -- the single-launch read ceiling for that many bytes
-    (31,232,000 B: the FP4 decode GEMV's algorithmic bytes)."""
+    (31,232,000 B: the FP4 decode GEMV's algorithmic bytes; 9,453,568 B: the INT4 g32 4096 x 4096
+    GEMV's)."""
     copies = copies_for(nbytes)
     pool = torch.empty((copies, nbytes), dtype=torch.uint8, device=dev)
     pool.fill_(1)
@@ -776,6 +778,7 @@ def main() -> int:
         "decoder_b1": lambda: decoder_workload(torch, dev, 1),
         "decoder_b8": lambda: decoder_workload(torch, dev, 8),
         "read_ceiling_31232000": lambda: read_ceiling_workload(torch, K, dev, 31_232_000, steps, warmup),
+        "read_ceiling_9453568": lambda: read_ceiling_workload(torch, K, dev, 9_453_568, steps, warmup),
         "read_ceiling_470000000": lambda: read_ceiling_workload(torch, K, dev, 470_000_000, steps, warmup),
         "mfma_fp4_ceiling_8192": lambda: mfma_ceiling_workload(torch, K, dev, gemm_steps, 20),
         "bf16_gemm_8192": lambda: dense_gemm_workload(torch, K, dev, "bfloat16", 8192, gemm_steps, 20),
