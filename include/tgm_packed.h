@@ -175,7 +175,9 @@ int tgm_gemm_w_split(const void* a, int a_dtype, int64_t m, int64_t lda, const v
  * with TGM_E_INVALID.  All calls on one GPU share its array and each call overwrites it, so
  * calls that overlap in time on one GPU (other streams, other threads) race: the caller orders
  * them.  The first call on each device looks up that device's address of the array
- * (hipGetSymbolAddress); make that first call outside graph capture.
+ * (hipGetSymbolAddress); make that first call outside graph capture.  The stream must launch
+ * on the calling thread's current device (the null and legacy / per-thread default streams
+ * do): a stream of another device is rejected with TGM_E_INVALID before any GPU work.
  */
 int64_t tgm_gemm_w_split_noalloc_capacity(void);
 int tgm_gemm_w_split_noalloc(const void* a, int a_dtype, int64_t m, int64_t lda, const void* w, int fmt, int64_t n,

@@ -37,6 +37,23 @@ def host_dequant_rows(p: PackedTensor, rows) -> np.ndarray:
     return O.dequant_f64(data, p.format, (len(rows), k), O.e8m0_decode(e), p.block_size)
 
 
+def stratified(rng, size: int, per_band: int, band: int = 32) -> np.ndarray:
+    """Sorted indices with ``per_band`` distinct random picks in every ``band``-wide band of
+    [0, size) (fewer in a short last band): sampled rows x sampled columns then hold outputs of
+    every 32 x 32 MFMA output tile, so no workgroup, wave or tile-order slot goes unchecked."""
+    picks = [start + rng.choice(min(band, size - start), min(per_band, size - start), replace=False)
+             for start in range(0, size, band)]
+    return np.sort(np.concatenate(picks))
+
+
+def test_stratified_covers_every_band():
+    rng = np.random.default_rng(0)
+    idx = stratified(rng, 14336, 2)
+    assert len(idx) == 2 * 448 and len(np.unique(idx)) == len(idx)
+    assert np.array_equal(np.bincount(idx // 32, minlength=448), np.full(448, 2))
+    assert set(np.unique(stratified(rng, 100, 1) // 32)) == {0, 1, 2, 3}
+
+
 # ----------------------------------------------------------------------------- known answers
 def test_scales_stay_with_k_blocks(dev):
     case = GOLDEN["scales_stay_with_k_blocks"]
@@ -507,7 +524,7 @@ def test_gemm_w_fp6_2048x11008x4096_full_size_sampled(dev, fmt):
     w = quantize_mx(torch.randn((n, k), device=dev, generator=g) * 0.02, fmt)
     c = matmul_nt(a, w, scope="ThreadGroup", dtype=torch.bfloat16)
     rng = np.random.default_rng(5)
-    rows, cols = rng.choice(m, 64, replace=False), rng.choice(n, 512, replace=False)
+    rows, cols = stratified(rng, m, 1), stratified(rng, n, 1)  # one output in every 32 x 32 tile
     deq = host_dequant_rows(w, cols)
     ref = bf16_np(a)[rows] @ deq.T
     assert O.max_rel_err(bf16_np(c)[np.ix_(rows, cols)], ref) <= TOL
@@ -552,7 +569,7 @@ def test_gemm_w_int4_prefill_shape(dev):
     w, deq = int4_weight(dev, "int4", n, k, torch.float16, 128, rng)
     a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float16)).to(dev)
     c = matmul_nt(a, w, scope="ThreadGroup", dtype=torch.float16)
-    rows, cols = rng.choice(m, 64, replace=False), rng.choice(n, 512, replace=False)
+    rows, cols = stratified(rng, m, 4), stratified(rng, n, 1)  # outputs in every 32 x 32 tile
     ref = a.float().cpu().numpy().astype(np.float64)[rows] @ deq[cols].T
     assert O.max_rel_err(c.float().cpu().numpy()[np.ix_(rows, cols)], ref) <= TOL
 
@@ -652,8 +669,10 @@ def test_gemm_mx_fp4_one_hot_is_exact(dev):
 
 @pytest.mark.parametrize("mnk", [(8192, 8192, 8192), (4096, 14336, 4096)])
 def test_gemm_mx_fp4_full_size_sampled(dev, mnk):
-    """The FP4 x FP4 GEMMs at full size (operands MX-quantised from N(0,1)): 64 x 1024 sampled outputs
-    against the fp64 oracle, which decodes the sampled rows from the host copies of the packed bytes."""
+    """The FP4 x FP4 GEMMs at full size (operands MX-quantised from N(0,1)) against the fp64 oracle,
+    which decodes the sampled rows from the host copies of the packed bytes.  Rows are sampled one per
+    32-row band and columns two per 32-column band, so every 32 x 32 MFMA tile of the output -- every
+    workgroup and slot of the XCD-aware tile order -- has sampled outputs."""
     m, n, k = mnk
     g = torch.Generator(device=dev)
     g.manual_seed(0)
@@ -661,7 +680,7 @@ def test_gemm_mx_fp4_full_size_sampled(dev, mnk):
     b = quantize_mx(torch.randn((n, k), device=dev, generator=g), "fp4_e2m1")
     c = matmul_nt(a, b, dtype=torch.bfloat16)
     rng = np.random.default_rng(4)
-    rows, cols = rng.choice(m, 64, replace=False), rng.choice(n, 1024, replace=False)
+    rows, cols = stratified(rng, m, 1), stratified(rng, n, 2)
     ref = host_dequant_rows(a, rows) @ host_dequant_rows(b, cols).T
     assert O.max_rel_err(bf16_np(c)[np.ix_(rows, cols)], ref) <= TOL
 

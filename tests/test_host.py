@@ -283,10 +283,11 @@ def test_matrix_routing_table():
     linalg.py:90-133): every FP4 / FP6 pair, scaled (E8M0 / 32) or not, takes the scaled MFMA;
     integer codes and non-E8M0 scales do not; FP8 tensors take the FP8 GEMM."""
     from tinygrad_mi355x.codegen.linalg import _dense_kernel, choose_matrix
-    from tinygrad_mi355x.renderer.linalg import GEMM_DENSE, GEMM_FP8, GEMM_MX
+    from tinygrad_mi355x.codegen import program as P
+    from tinygrad_mi355x.renderer.linalg import GEMM_DENSE, GEMM_FP8, GEMM_MX, GEMM_MX_GENERAL
 
-    def packed(fmt, scales):
-        n, k = 4, 64
+    def packed(fmt, scales, k=64):
+        n = 4
         data = u8([0] * (n * k * FORMATS[fmt][0] // 8))
         sc = None if scales is None else torch.ones(n, k // 32, dtype=scales)
         return PackedTensor(data, fmt, (n, k), sc, 32)
@@ -296,8 +297,18 @@ def test_matrix_routing_table():
         for fb in ("fp4_e2m1", "fp6_e2m3", "fp6_e3m2"):
             for sa in (None, torch.float8_e8m0fnu):
                 for sb in (None, torch.float8_e8m0fnu):
-                    a, b = packed(fa, sa), packed(fb, sb)
-                    assert choose_matrix(b, a, matrix_intermediate(a, b), f32, 4) is GEMM_MX
+                    for k in (128, 256):
+                        a, b = packed(fa, sa, k), packed(fb, sb, k)
+                        # only FP4 x FP4 with both scales and K % 256 == 0 runs the 256 x 256 kernel
+                        fast = fa == fb == "fp4_e2m1" and sa is not None and sb is not None and k == 256
+                        kernel = choose_matrix(b, a, matrix_intermediate(a, b), f32, 4)
+                        assert kernel is (GEMM_MX if fast else GEMM_MX_GENERAL)
+                        assert choose_matrix(b, a, matrix_intermediate(a, b), f32, 4, tile=kernel.tile) is kernel
+                        prog = P.mx_program(a.desc(), b.desc(), "float32", 4)
+                        assert prog.kernel is kernel and prog.global_size[0] == 1
+    big = P.mx_program(P.PackedDesc("fp4_e2m1", (4096, 8192), 4096 * 4096, 1, "float8_e8m0fnu"),
+                       P.PackedDesc("fp6_e2m3", (1024, 8192), 1024 * 6144, 1, "float8_e8m0fnu"), "bfloat16", 1024)
+    assert big.kernel is GEMM_MX_GENERAL and big.global_size[0] == 16 * 8  # 256 x 128 tiles
     ints = packed("int4", None)
     assert choose_matrix(packed("fp4_e2m1", None), ints, matrix_intermediate(ints, ints), f32, 4) is None
     f16s = packed("fp4_e2m1", torch.float16)
@@ -318,6 +329,16 @@ def test_noalloc_split_k_rejects_oversized_partials_before_any_gpu_call():
     with pytest.raises(ValueError, match="static scratch"):
         K.call("tgm_gemm_w_split_noalloc", None, 12, 4096, 4096, None, 2, 4096, 4096, None, 15, 32, None, 13, 4096, 4,
                None)
+
+
+def test_noalloc_split_k_checks_the_stream_device_before_any_launch():
+    """A product that fits the scratch, on a non-null stream: the entry point settles which device's
+    scratch it may use (the stream's device must be the current one) before it launches anything.
+    Without a usable GPU that check fails with TGM_E_INVALID instead of a launch."""
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present: the GPU tests cover the launch path")
+    with pytest.raises(ValueError, match="current HIP device|hipStreamGetDevice"):
+        K.call("tgm_gemm_w_split_noalloc", 16, 12, 64, 2048, 16, 2, 512, 2048, 16, 15, 32, 16, 13, 512, 4, 0x1000)
 
 
 def test_header_enums_match_binding():

@@ -321,3 +321,25 @@ def test_a_failed_cross_device_transfer_marks_both_devices(monkeypatch):
     for dev in (src, dst):
         with pytest.raises(RuntimeError, match="submission/transfer failed"):
             dev.synchronize()
+
+
+def test_one_hip_runtime_whichever_is_opened_first():
+    """The plugin's HIP binding and kernel library opened before torch is imported must leave one
+    HIP runtime mapped once torch loads its own (torch's libraries ask for libamdhip64.so through
+    their rpath, which the ROCm runtime's soname does not answer)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    pkg = Path(__file__).resolve().parents[1] / "tinygrad-dx12_amd"
+    code = (f"import sys; sys.path.insert(0, {str(pkg)!r})\n"
+            "from tinygrad_mi355x.runtime.support import hip\n"
+            "hip.library()\n"
+            "from tinygrad_mi355x.runtime import library\n"
+            "library.load_library()\n"
+            "import torch\n"
+            "from tinygrad_mi355x.runtime import kernels\n"
+            "print(len(hip._loaded_runtimes()))\n")
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip().splitlines()[-1] == "1"

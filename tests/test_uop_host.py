@@ -118,6 +118,38 @@ def test_lowering_plans_transposes_product_and_epilogue():
     assert _kinds(fp8) == ["tgm_gemm_fp8"]
 
 
+def test_plan_rejects_program_buffers_smaller_than_the_kernel_touches():
+    """A hand-built LINEAR may bind a library PROGRAM's slots to BUFFERs whose own sizes are
+    consistent but smaller than the product the program was built for; plan() must refuse it
+    before anything is launched (the kernel would read and write past those buffers)."""
+    from tinygrad_mi355x.codegen import program as P
+    from tinygrad_mi355x.runtime import ops_mi355x as R
+    from tinygrad_mi355x.runtime.schedule import plan
+
+    class FakeDev:
+        device = DEV
+
+    dev = FakeDev()
+    m, n, k = 128, 256, 128
+    prog = P.dense_program("bfloat16", m, k, "bfloat16", n, k, k, "bfloat16", n)
+    assert prog.slot_bytes == (m * n * 2, m * k * 2, n * k * 2)
+
+    def bound(specs):
+        uops = _buffers(*specs)
+        return uops, {u: R.MI355XBuffer(dev, R._Allocation(0x1000 * (i + 1), nb * 2), nb * 2)
+                      for i, (u, (nb, _)) in enumerate(zip(uops, specs))}
+
+    full, bufs = bound([(m * n, dtypes.bfloat16), (m * k, dtypes.bfloat16), (n * k, dtypes.bfloat16)])
+    launches, _ = plan(dev, UOp.linear(UOp.call(UOp(Ops.PROGRAM, None, (), prog), *full)), bufs)
+    assert len(launches) == 1 and launches[0].native
+    for short in range(3):
+        specs = [(m * n, dtypes.bfloat16), (m * k, dtypes.bfloat16), (n * k, dtypes.bfloat16)]
+        specs[short] = (specs[short][0] // 2, dtypes.bfloat16)
+        small, bufs = bound(specs)
+        with pytest.raises(ValueError, match="the kernel touches"):
+            plan(dev, UOp.linear(UOp.call(UOp(Ops.PROGRAM, None, (), prog), *small)), bufs)
+
+
 def test_lowering_pads_k_and_keeps_products_without_a_native_kernel():
     m, n, k = 64, 64, 96
     out, a, b = _buffers((m * n, dtypes.float16), (m * k, dtypes.float16), (k * n, dtypes.float16))
@@ -203,6 +235,35 @@ def test_linearized_nested_reductions_hoist_and_gates():
     first_range = ops.index("RANGE")
     scale_loads = [i for i, u in enumerate(listing.uops) if u.op is Ops.LOAD and u.src[0].src[0].op is Ops.PARAM and u.src[0].src[0].arg.slot == 2]
     assert len(scale_loads) == 1 and scale_loads[0] < first_range
+
+
+def test_invariant_loads_stay_inside_loops_that_may_not_run():
+    """A REDUCE over a variable bound n >= 0 whose body reads s[n - 1] (loop-invariant): at n = 0
+    the loop runs no iteration and the kernel must not read s[-1]; with a constant bound > 0 the
+    invariant load still moves ahead of the loop."""
+    rows, width = 3, 4
+    x, s, o = UOp.param(1, dtypes.int32, rows * width), UOp.param(2, dtypes.int32, width), UOp.param(0, dtypes.int32, rows)
+    n = UOp.variable("n", 0, width)
+    r, j = UOp.range(rows, 0), UOp.range(n, 1, AxisType.REDUCE)
+    total = (x.index(r * width + j) * s.index(n - 1)).reduce(j, arg=Ops.ADD)
+    listing = linearize(o.index(r).store(total).end(r).sink(arg=KernelInfo(name="tail")))
+    xs, sc = np.arange(rows * width, dtype=np.int32) + 1, np.array([2, 3, 5, 7], np.int32)
+    for nv in range(width + 1):
+        out = np.full(rows, -1, np.int32)
+        uop_interp.run(listing, {0: out, 1: xs, 2: sc}, {"n": nv})
+        want = xs.reshape(rows, width)[:, :nv].sum(1) * (sc[nv - 1] if nv else 0)
+        np.testing.assert_array_equal(out, want)
+    loads = [i for i, u in enumerate(listing.uops) if u.op is Ops.LOAD and u.src[0].src[0].op is Ops.PARAM
+             and u.src[0].src[0].arg.slot == 2]
+    inner = [i for i, u in enumerate(listing.uops) if u.op is Ops.RANGE][-1]
+    assert loads and all(i > inner for i in loads)
+    fixed = (x.index(r * width + UOp.range(width, 1, AxisType.REDUCE)) * s.index(r)).reduce(
+        UOp.range(width, 1, AxisType.REDUCE), arg=Ops.ADD)
+    hoisted = linearize(o.index(r).store(fixed).end(r).sink(arg=KernelInfo(name="fixed")))
+    loads = [i for i, u in enumerate(hoisted.uops) if u.op is Ops.LOAD and u.src[0].src[0].op is Ops.PARAM
+             and u.src[0].src[0].arg.slot == 2]
+    inner = [i for i, u in enumerate(hoisted.uops) if u.op is Ops.RANGE][-1]
+    assert len(loads) == 1 and loads[0] < inner
 
 
 def test_linearizer_rejects_malformed_kernels():

@@ -75,3 +75,30 @@ def test_noalloc_split_k_rejects_partials_beyond_the_capacity(dev):
     c = torch.empty((1024, 4096), dtype=torch.float32, device=dev)
     with pytest.raises(ValueError, match="static scratch"):
         K.call("tgm_gemm_w_split_noalloc", *_args(a, w, c), 4, torch.cuda.current_stream().cuda_stream)
+
+
+def test_noalloc_split_k_on_the_null_stream_and_a_side_stream(dev):
+    """The scratch address is looked up for the device the stream launches on: the null stream (the
+    current device's) and a second stream of the current device give the workspace form's bits."""
+    lib = K.load_library()
+    rng = np.random.default_rng(11)
+    m, n, k, splits = 64, 512, 2048, 4
+    w = _weight(dev, "fp4_e2m1", n, k, rng)
+    a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    ws_bytes = lib.tgm_gemm_w_split_workspace(m, n, splits)
+    ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=dev)
+    want = torch.empty((m, n), dtype=torch.float32, device=dev)
+    K.call("tgm_gemm_w_split", *_args(a, w, want), splits, ws.data_ptr(), ws_bytes,
+           torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    print("noalloc split-K on the null stream", flush=True)
+    got = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+    K.call("tgm_gemm_w_split_noalloc", *_args(a, w, got), splits, None)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    print("noalloc split-K on a side stream", flush=True)
+    side = torch.cuda.Stream(device=dev)
+    got2 = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+    K.call("tgm_gemm_w_split_noalloc", *_args(a, w, got2), splits, side.cuda_stream)
+    side.synchronize()
+    assert torch.equal(got2, want)

@@ -139,12 +139,16 @@ def _item(uops, ends, buffers, var_vals, gidx, lidx, shared):
         elif op == "LOAD":
             arr, i, gate = ptr[id(u.src[0])]
             if gate:
+                if not 0 <= i < len(arr):  # a device would read outside the buffer
+                    raise IndexError(f"load of element {i} of a {len(arr)}-element buffer")
                 val[id(u)] = arr[i]
             else:
                 val[id(u)] = get(u.src[1]) if len(u.src) > 1 else NP[dt](0)
         elif op == "STORE":
             arr, i, gate = ptr[id(u.src[0])]
             if gate:
+                if not 0 <= i < len(arr):
+                    raise IndexError(f"store to element {i} of a {len(arr)}-element buffer")
                 arr[i] = get(u.src[1])
         elif op == "RANGE":
             bound = int(get(u.src[0]))

@@ -621,12 +621,29 @@ static constexpr int kMaxDevices = 64;
 static std::mutex scratch_lock;
 static float* scratch_ptr[kMaxDevices];
 
-// The current device's address of `scratch` (nullptr with the error text set on failure).
-static float* scratch_address() {
+// The address of `scratch` on the device `stream` launches on, which must be the calling
+// thread's current device: hipGetSymbolAddress answers for the current device, so a stream of
+// another device is rejected (TGM_E_INVALID) rather than handed that device's array.  The null
+// stream and the legacy / per-thread default streams launch on the current device.  Returns a
+// TGM_* status; *out is set on success.
+static int scratch_address(hipStream_t stream, float** out) {
   int device = -1;
   if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
     set_error("tgm_gemm_w_split_noalloc: no usable current HIP device (%d)", device);
-    return nullptr;
+    return TGM_E_INVALID;
+  }
+  if (stream != nullptr && stream != hipStreamLegacy && stream != hipStreamPerThread) {
+    hipDevice_t stream_device = -1;
+    const hipError_t err = hipStreamGetDevice(stream, &stream_device);
+    if (err != hipSuccess) {
+      set_error("tgm_gemm_w_split_noalloc: hipStreamGetDevice failed: %s (%d)", hipGetErrorString(err), (int)err);
+      return TGM_E_INVALID;
+    }
+    if ((int)stream_device != device) {
+      set_error("tgm_gemm_w_split_noalloc: the stream belongs to device %d but device %d is current; make the "
+                "stream's device current before the call", (int)stream_device, device);
+      return TGM_E_INVALID;
+    }
   }
   std::lock_guard<std::mutex> guard(scratch_lock);
   if (!scratch_ptr[device]) {
@@ -635,11 +652,12 @@ static float* scratch_address() {
     if (err != hipSuccess || !ptr) {
       set_error("tgm_gemm_w_split_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s (%d)", device,
                 hipGetErrorString(err), (int)err);
-      return nullptr;
+      return (int)(err != hipSuccess ? err : hipErrorInvalidSymbol);
     }
     scratch_ptr[device] = (float*)ptr;
   }
-  return scratch_ptr[device];
+  *out = scratch_ptr[device];
+  return TGM_OK;
 }
 
 extern "C" int64_t tgm_gemm_w_split_noalloc_capacity(void) { return kScratchBytes; }
@@ -658,8 +676,9 @@ extern "C" int tgm_gemm_w_split_noalloc(const void* a, int a_dtype, int64_t m, i
                 "tgm_gemm_w_split_noalloc: %lld split(s) of %lld x %lld fp32 partials need %lld bytes, more than the "
                 "%lld-byte static scratch; use fewer splits or tgm_gemm_w_split with a workspace",
                 (long long)eff, (long long)m, (long long)n, (long long)need, (long long)kScratchBytes);
-  float* part = scratch_address();
-  if (!part) return (int)hipErrorInvalidSymbol;
+  float* part = nullptr;
+  const int rc = scratch_address((hipStream_t)stream, &part);
+  if (rc != TGM_OK) return rc;
   return gemm_w_split_run(a, a_dtype, m, lda, w, fmt, n, k, scales, scale_dtype, block_size, c, c_dtype, ldc, eff,
                           part, stream, "tgm_gemm_w_split_noalloc");
 }

@@ -26,7 +26,7 @@ from dataclasses import dataclass
 from typing import Callable
 
 from tinygrad_mi355x.codegen.decomp.formats import FORMATS, MX_FORMATS, packed_nbytes
-from tinygrad_mi355x.renderer.matrix import GEMM_DENSE, GEMM_FP8, GEMM_MX, GEMM_W, GEMV, GEMV_MAX_ROWS, MatrixKernel
+from tinygrad_mi355x.renderer.matrix import GEMM_DENSE, GEMM_FP8, GEMM_W, GEMV, GEMV_MAX_ROWS, MatrixKernel, mx_kernel
 from tinygrad_mi355x.runtime import library as L
 from tinygrad_mi355x.runtime.support import hip
 
@@ -78,13 +78,24 @@ class MatrixProgram:
     slots = SLOTS
 
     def __init__(self, kernel: MatrixKernel, name: str, groups: int, estimates: Estimates,
-                 args: Callable[[int, int, int, int], tuple]) -> None:
+                 args: Callable[[int, int, int, int], tuple], slot_bytes: tuple[int, ...] = ()) -> None:
         self.kernel, self.name, self.estimates, self._args = kernel, name, estimates, args
         self.global_size = (max(int(groups), 0), 1, 1)
         self.local_size = (kernel.threads, 1, 1)
+        # bytes the kernel reads or writes through each slot (out, a[, b]), from the first
+        # element's address: a buffer bound to a slot must hold at least that many
+        self.slot_bytes = tuple(max(int(x), 0) for x in slot_bytes)
 
     def __repr__(self) -> str:
         return f"MatrixProgram({self.name}, groups={self.global_size[0]})"
+
+    def check_slots(self, sizes: tuple[int, ...]) -> None:
+        """ValueError unless buffers of ``sizes`` bytes (slot order) cover what the kernel touches."""
+        if len(sizes) < len(self.slot_bytes):
+            raise ValueError(f"{self.name}: {len(self.slot_bytes)} slot buffers needed, {len(sizes)} given")
+        for slot, have, need in zip(SLOTS, sizes, self.slot_bytes):
+            if have < need:
+                raise ValueError(f"{self.name}: the {slot} buffer holds {have} bytes; the kernel touches {need}")
 
     def launch(self, out: int, a: int, b: int, stream: int) -> None:
         """Enqueue on ``stream`` with slot addresses (out, a, b); the caller owns ordering."""
@@ -99,6 +110,7 @@ class MatrixProgram:
         dev = out.dev
         if any(x.dev is not dev for x in bufs):
             raise ValueError("MI355X buffer device/signature mismatch")
+        self.check_slots(tuple(x.size for x in bufs))
         if 0 in self.global_size:
             return 0.0 if wait else None
         with dev.lock, dev.submitting():
@@ -120,6 +132,12 @@ class MatrixProgram:
             hip.call("hipEventDestroy", stop)
 
 
+def _extent(rows: int, ld: int, cols: int, dtype: str) -> int:
+    """Bytes from the first element to one past the last of a row-major [rows, cols] matrix with
+    row stride ``ld`` elements."""
+    return 0 if rows <= 0 or cols <= 0 else ((rows - 1) * ld + cols) * L.DTYPE_SIZES[dtype]
+
+
 def _tiles(rows: int, cols: int, kernel: MatrixKernel) -> int:
     return -(-rows // kernel.tile[0]) * -(-cols // kernel.tile[1])
 
@@ -133,7 +151,8 @@ def unpack_program(p: PackedDesc, out_dtype: str) -> MatrixProgram:
     fmt, k, odt = L.FORMAT_IDS[p.format], p.shape[-1], L.DTYPE_IDS[out_dtype]
     kernel = MatrixKernel("tgm_unpack", "elementwise", (256, 1, 1), 256)
     return MatrixProgram(kernel, "tgm_unpack", -(-count // 256), est,
-                         lambda out, a, b, s: (a, p.nbytes, fmt, count, k, scales, sdt, p.block_size, out, odt, s))
+                         lambda out, a, b, s: (a, p.nbytes, fmt, count, k, scales, sdt, p.block_size, out, odt, s),
+                         (count * L.DTYPE_SIZES[out_dtype], packed_nbytes(p.format, count)))
 
 
 def weight_program(w: PackedDesc, m: int, x_dtype: str, ldx: int, y_dtype: str, ldy: int) -> MatrixProgram:
@@ -143,13 +162,14 @@ def weight_program(w: PackedDesc, m: int, x_dtype: str, ldx: int, y_dtype: str, 
     est = Estimates(2 * m * n * k, w.read_bytes + m * k * L.DTYPE_SIZES[x_dtype] + m * n * L.DTYPE_SIZES[y_dtype])
     scales, sdt = w.scale_args()
     fmt, xdt, ydt = L.FORMAT_IDS[w.format], L.DTYPE_IDS[x_dtype], L.DTYPE_IDS[y_dtype]
+    touched = (_extent(m, ldy, n, y_dtype), packed_nbytes(w.format, n * k), _extent(m, ldx, k, x_dtype))
     if m <= GEMV_MAX_ROWS:
         return MatrixProgram(GEMV, "tgm_gemv", _tiles(n, m, GEMV), est,
                              lambda out, a, b, s: (a, fmt, n, k, scales, sdt, w.block_size, b, xdt, m, ldx, out, ydt,
-                                                   ldy, s))
+                                                   ldy, s), touched)
     return MatrixProgram(GEMM_W, "tgm_gemm_w", _tiles(n, m, GEMM_W), est,
                          lambda out, a, b, s: (b, xdt, m, ldx, a, fmt, n, k, scales, sdt, w.block_size, out, ydt, ldy,
-                                               s))
+                                               s), touched)
 
 
 def mx_program(a: PackedDesc, b: PackedDesc, c_dtype: str, ldc: int) -> MatrixProgram:
@@ -159,8 +179,10 @@ def mx_program(a: PackedDesc, b: PackedDesc, c_dtype: str, ldc: int) -> MatrixPr
     est = Estimates(2 * m * n * k, a.read_bytes + b.read_bytes + m * n * L.DTYPE_SIZES[c_dtype])
     sa, sb = a.scales, b.scales
     fa, fb, cdt = L.FORMAT_IDS[a.format], L.FORMAT_IDS[b.format], L.DTYPE_IDS[c_dtype]
-    return MatrixProgram(GEMM_MX, "tgm_gemm_mx", _tiles(m, n, GEMM_MX), est,
-                         lambda out, x, y, s: (x, fa, sa, m, y, fb, sb, n, k, out, cdt, ldc, s))
+    kernel = mx_kernel(a.format, sa is not None, b.format, sb is not None, k)
+    return MatrixProgram(kernel, "tgm_gemm_mx", _tiles(m, n, kernel), est,
+                         lambda out, x, y, s: (x, fa, sa, m, y, fb, sb, n, k, out, cdt, ldc, s),
+                         (_extent(m, ldc, n, c_dtype), packed_nbytes(a.format, m * k), packed_nbytes(b.format, n * k)))
 
 
 def dense_program(a_dtype: str, m: int, lda: int, b_dtype: str, n: int, ldb: int, k: int, c_dtype: str, ldc: int,
@@ -170,14 +192,16 @@ def dense_program(a_dtype: str, m: int, lda: int, b_dtype: str, n: int, ldb: int
     est = Estimates(2 * m * n * k, m * k * L.DTYPE_SIZES[a_dtype] + n * k * L.DTYPE_SIZES[b_dtype]
                     + m * n * L.DTYPE_SIZES[c_dtype])
     adt, bdt, cdt = L.DTYPE_IDS[a_dtype], L.DTYPE_IDS[b_dtype], L.DTYPE_IDS[c_dtype]
+    touched = (_extent(m, ldc, n, c_dtype), _extent(m, lda, k, a_dtype), _extent(n, ldb, k, b_dtype))
     if a_dtype in FP8:
         sa, sb = scale_a or None, scale_b or None
         return MatrixProgram(GEMM_FP8, "tgm_gemm_fp8", _tiles(m, n, GEMM_FP8), est,
-                             lambda out, x, y, s: (x, adt, lda, m, y, bdt, ldb, n, k, sa, sb, out, cdt, ldc, s))
+                             lambda out, x, y, s: (x, adt, lda, m, y, bdt, ldb, n, k, sa, sb, out, cdt, ldc, s),
+                             touched)
     if scale_a or scale_b:
         raise ValueError("per-tensor scales apply to FP8 operands only")
     return MatrixProgram(GEMM_DENSE, "tgm_gemm_dense", _tiles(m, n, GEMM_DENSE), est,
-                         lambda out, x, y, s: (x, adt, m, lda, y, bdt, n, ldb, k, out, cdt, ldc, s))
+                         lambda out, x, y, s: (x, adt, m, lda, y, bdt, n, ldb, k, out, cdt, ldc, s), touched)
 
 
 def transpose_program(dtype: str, rows: int, cols: int) -> MatrixProgram:
@@ -189,7 +213,7 @@ def transpose_program(dtype: str, rows: int, cols: int) -> MatrixProgram:
     name = "tgm_transpose8" if size == 1 else "tgm_transpose16"
     kernel = MatrixKernel(name, "copy", (64, 64, 1), 256)
     return MatrixProgram(kernel, name, _tiles(rows, cols, kernel), Estimates(0, 2 * rows * cols * size),
-                         lambda out, a, b, s: (a, rows, cols, cols, out, rows, s))
+                         lambda out, a, b, s: (a, rows, cols, cols, out, rows, s), (rows * cols * size,) * 2)
 
 
 # ----------------------------------------------------------------------------- plugin-buffer path

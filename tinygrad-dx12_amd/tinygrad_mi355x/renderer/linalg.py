@@ -13,8 +13,8 @@ from __future__ import annotations
 import torch
 
 from tinygrad_mi355x import dtype as D
-from tinygrad_mi355x.renderer.matrix import (GEMM_DENSE, GEMM_FP8, GEMM_MX, GEMM_W, GEMV, GEMV_MAX_ROWS,  # noqa: F401
-                                             PLAIN, MatrixKernel)
+from tinygrad_mi355x.renderer.matrix import (GEMM_DENSE, GEMM_FP8, GEMM_MX, GEMM_MX_GENERAL, GEMM_W, GEMV,  # noqa: F401
+                                             GEMV_MAX_ROWS, PLAIN, MatrixKernel, mx_kernel)
 
 
 def _accumulator(a: torch.dtype, b: torch.dtype) -> torch.dtype:

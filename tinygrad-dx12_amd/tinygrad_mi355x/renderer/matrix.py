@@ -27,9 +27,11 @@ GEMV = MatrixKernel("tgm_gemv", "Wave", (16, 16, 128), 256)
 # Family 2: dequant-to-bf16 MFMA GEMM (replaces linalg_source for one packed operand).
 GEMM_W = MatrixKernel("tgm_gemm_w", "ThreadGroup", (256, 128, 128), 512)
 # Family 2: scaled-MFMA GEMM of two packed FP4 / FP6 operands, each with E8M0 block-32 scales or
-# unscaled (FP4 x FP4 with both scales: 256 x 256 tiles, K steps of 256; every other pair
-# 256 x 128 tiles, K steps of 128).
+# unscaled.  One entry point, two kernels: FP4 x FP4 with both scales and K a multiple of 256
+# runs 256 x 256 tiles with K steps of 256 (GEMM_MX); every other pair, or K a multiple of 128
+# only, runs 256 x 128 tiles with K steps of 128 (GEMM_MX_GENERAL).  ``mx_kernel`` picks.
 GEMM_MX = MatrixKernel("tgm_gemm_mx", "ThreadGroup", (256, 256, 256), 512)
+GEMM_MX_GENERAL = MatrixKernel("tgm_gemm_mx", "ThreadGroup", (256, 128, 128), 512)
 # Family 2: ordinary bf16 x bf16 / f16 x f16 MFMA GEMM (the reference's LinAlg lowering of an
 # ordinary matrix product, codegen/matmul.py:156-246).
 GEMM_DENSE = MatrixKernel("tgm_gemm_dense", "ThreadGroup", (256, 128, 64), 512)
@@ -40,3 +42,9 @@ GEMM_FP8 = MatrixKernel("tgm_gemm_fp8", "ThreadGroup", (256, 128, 128), 512)
 PLAIN = MatrixKernel("tgm_gemm_plain", "tiled", (16, 16, 1), 256)
 
 GEMV_MAX_ROWS = 16
+
+
+def mx_kernel(a_format: str, a_scaled: bool, b_format: str, b_scaled: bool, k: int) -> MatrixKernel:
+    """The kernel tgm_gemm_mx launches for a pair of packed operands (both E8M0/32-scaled or not)."""
+    fp4_pair = a_format == b_format == "fp4_e2m1" and a_scaled and b_scaled
+    return GEMM_MX if fp4_pair and k > 0 and k % GEMM_MX.tile[2] == 0 else GEMM_MX_GENERAL

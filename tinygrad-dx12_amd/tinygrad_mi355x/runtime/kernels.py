@@ -11,9 +11,12 @@ from __future__ import annotations
 import torch
 
 from tinygrad_mi355x.runtime import library as L
+from tinygrad_mi355x.runtime.support import hip as _hip
 from tinygrad_mi355x.runtime.library import (ABI_VERSION, EXPORTS, FORMAT_IDS, LIB_NAME, LIB_PATH, TGM_E_INVALID,  # noqa: F401
                                              TGM_E_UNSUPPORTED, TGM_OK, UnsupportedKernel, check, library_path,
                                              load_library)
+
+_hip.check_single_runtime()  # torch's runtime and the one the plugin opened must be one
 
 _SIGNATURES = L.SIGNATURES
 # enum tgm_dtype by torch dtype

@@ -5,8 +5,9 @@ This is the only route from Python into the packed kernels: the plugin-buffer pa
 (``codegen/program.py``) calls it with plugin buffer addresses and the device stream, the
 torch adapter (``runtime/kernels.py``) with tensor addresses and torch's stream.  There is no
 CPU implementation behind it: when the library is missing or no MI355X is visible, every call
-raises.  The library links the HIP runtime by soname (libamdhip64.so.7), so it shares whatever
-runtime the process already loaded.
+raises.  The library links the HIP runtime by soname (libamdhip64.so.7); the runtime binding
+(``support/hip.py``) is opened first, so the library binds to the one runtime the process
+shares with torch.
 """
 
 from __future__ import annotations
@@ -98,6 +99,9 @@ def load_library() -> ctypes.CDLL:
         path = library_path()
         if not path.exists():
             raise RuntimeError(f"MI355X kernel library {path} is not built; run __graft_entry__.build()")
+        from tinygrad_mi355x.runtime.support import hip
+
+        hip.library()  # the process's one HIP runtime, before the library's soname is resolved
         lib = ctypes.CDLL(str(path))
         lib.tgm_abi_version.restype = ctypes.c_int
         lib.tgm_abi_version.argtypes = ()

@@ -114,6 +114,9 @@ def plan(dev, linear: UOp, buffers: dict | None = None, var_vals: dict[str, int]
             bufs = tuple(buf(a) for a in args)
             if any(b.dev is not dev for b in bufs):
                 raise ValueError("MI355X buffer device/signature mismatch")
+            # the library kernel reads and writes the extents its program records, which the
+            # BUFFER UOps' own sizes need not cover
+            prog.check_slots(tuple(b.size for b in bufs))
             launches.append(Launch(prog, bufs))
             continue
         if body.op is not Ops.SINK:

@@ -6,10 +6,14 @@ plain ``hipError_t`` functions.  Every failure becomes ``RuntimeError("<op> fail
 <code> (<hipGetErrorString>)")``, the shape of the reference's ``check``
 (runtime/support/dx12.py:11-15).
 
-The runtime is opened by its soname (libamdhip64.so.7): a process that already loaded one
-(torch does, and so does libtgm_mi355x.so, which links it) shares that instance, so device
-memory, streams and modules are shared with the kernel library.  Nothing here imports torch
-or touches the GPU at import time.
+One process must hold one HIP runtime, so that device memory, streams and modules are shared
+by torch, this binding and the kernel library.  ``runtime_path`` picks it: an explicit
+``MI355X_HIP_RUNTIME``; else the instance already loaded (opened by its soname,
+libamdhip64.so.7); else, when torch is installed, the copy torch ships and will load -- torch's
+libraries ask for ``libamdhip64.so`` through their own rpath, a name the ROCm runtime's soname
+does not match, so a ROCm runtime opened first would become a second runtime once torch is
+imported; a torch runtime opened first by path is the very file torch later maps, and the
+dynamic loader reuses it.  Nothing here imports torch or touches the GPU at import time.
 """
 
 from __future__ import annotations
@@ -74,14 +78,52 @@ _lib: ctypes.CDLL | None = None
 _initialised = False
 
 
+def _loaded_runtimes() -> set[str]:
+    """Paths of the HIP runtime files mapped into this process."""
+    try:
+        with open("/proc/self/maps") as maps:
+            return {line.split()[-1] for line in maps if "libamdhip64" in line and "/" in line}
+    except OSError:
+        return set()
+
+
+def runtime_path() -> str:
+    """Which HIP runtime file this process should open (see the module docstring)."""
+    explicit = os.environ.get("MI355X_HIP_RUNTIME")
+    if explicit:
+        return explicit
+    if _loaded_runtimes():
+        return "libamdhip64.so.7"
+    import importlib.util
+
+    try:
+        spec = importlib.util.find_spec("torch")
+    except (ImportError, ValueError):
+        spec = None
+    if spec is not None and spec.origin:
+        bundled = os.path.join(os.path.dirname(spec.origin), "lib", "libamdhip64.so")
+        if os.path.exists(bundled):
+            return bundled
+    return "libamdhip64.so.7"
+
+
+def check_single_runtime() -> None:
+    """RuntimeError when two HIP runtime files are mapped (e.g. torch imported after a plugin
+    opened a different runtime with MI355X_HIP_RUNTIME): their devices, streams and memory do
+    not mix."""
+    loaded = _loaded_runtimes()
+    if len(loaded) > 1:
+        raise RuntimeError(f"two HIP runtimes are loaded in this process ({', '.join(sorted(loaded))}); torch and "
+                           "the MI355X plugin must share one: import torch first or unset MI355X_HIP_RUNTIME")
+
+
 def library() -> ctypes.CDLL:
-    """Load and type the HIP runtime once (the instance already in the process, if any)."""
+    """Load and type the HIP runtime once (``runtime_path``)."""
     global _lib
     with _lock:
         if _lib is None:
-            name = os.environ.get("MI355X_HIP_RUNTIME", "libamdhip64.so.7")
             try:
-                lib = ctypes.CDLL(name)
+                lib = ctypes.CDLL(runtime_path())
             except OSError:
                 lib = ctypes.CDLL("/opt/rocm/lib/libamdhip64.so")
             for fn, args in _SIGNATURES.items():

@@ -201,6 +201,12 @@ class _Emitter:
         else:
             raise ValueError(f"{op.name} cannot be a value in a scheduled kernel")
 
+    def hoist_invariants(self, x: UOp) -> None:
+        """List the parts of a REDUCE body that no loop of it changes, before its loops."""
+        for n in x.toposort():
+            if n.op not in (Ops.RANGE, Ops.PARAM, Ops.DEFINE_VAR) and self.in_scope(self.free(n)):
+                self.value(n)
+
     def reduce(self, node: UOp) -> UOp:
         x, ranges = node.src[0], node.src[1:]
         if not ranges or any(r.op is not Ops.RANGE for r in ranges):
@@ -210,10 +216,11 @@ class _Emitter:
         slot = self.put(UOp(Ops.INDEX, node.dtype, (acc, UOp.const(dtypes.index, 0))))
         self.put(UOp(Ops.STORE, None, (slot, self.put(_identity(node.arg, node.dtype)))))
         # loop-invariant parts of the body first, in dependency order (the body stores nothing,
-        # so its loads may move)
-        for n in x.toposort():
-            if n.op not in (Ops.RANGE, Ops.PARAM, Ops.DEFINE_VAR) and self.in_scope(self.free(n)):
-                self.value(n)
+        # so its loads may move) -- but only ahead of loops that surely run: with a variable or
+        # zero bound the loop may run no iteration, and a load hoisted out of it would read an
+        # address the original kernel never touches (e.g. b[n - 1] at n = 0)
+        if all(r.src[0].op is Ops.CONST and r.src[0].arg > 0 for r in ranges):
+            self.hoist_invariants(x)
         loops = []
         for r in ranges:
             bound = self.value(r.src[0])
@@ -248,9 +255,8 @@ class _Emitter:
         self.regs += 1
         slot = self.put(UOp(Ops.INDEX, node.dtype, (acc, UOp.const(idx, 0))))
         self.put(UOp(Ops.STORE, None, (slot, self.value(ident))))
-        for n in x.toposort():  # loop-invariant parts first
-            if n.op not in (Ops.RANGE, Ops.PARAM, Ops.DEFINE_VAR) and self.in_scope(self.free(n)):
-                self.value(n)
+        if total > 0:  # loop-invariant parts first (the loop surely runs)
+            self.hoist_invariants(x)
         loop = self.put(UOp(Ops.RANGE, idx, (self.const(idx, -(-total // local)),), ("group", self.loops)))
         self.loops += 1
         self.scopes.append({})
