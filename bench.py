@@ -248,7 +248,43 @@ def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup:
     flops, nbytes = prog.estimates.ops, prog.estimates.mem
     return {"workload": f"fp4xfp4 e8m0/32 GEMM M={m} N={n} K={k} bf16 out", "ms": ms, "TFLOPS": flops / ms / 1e9,
             "flops": flops, "bytes": nbytes, "GB/s": nbytes / ms / 1e6, "timed_dispatches": steps,
-            "roofline": mfma_roofline(flops, ms, FP4_PEAK_TFLOPS, "dense MXFP4 MFMA")}
+            "roofline": mfma_roofline(flops, ms, FP4_PEAK_TFLOPS, "dense MXFP4 MFMA"),
+            "vendor": vendor_fp4_gemm(m, n, k, steps)}
+
+
+VENDOR_BAR = ROOT / "tinygrad-dx12_amd" / "tinygrad_mi355x" / "_lib" / "ck_mx_gemm_bar"
+
+
+def vendor_fp4_gemm(m: int, n: int, k: int, steps: int) -> dict | None:
+    """The vendor's MXFP4 GEMM on this machine: ROCm's Composable Kernel prebuilt instances
+    (libdevice_gemm_operations.a; this ROCm's hipBLASLt ships no FP4 kernels for gfx950), every
+    instance timed like this benchmark's GEMMs, beside tgm_gemm_mx on the same operands in the same
+    child process (random FP4 codes, every E8M0 scale 2^0 since Composable Kernel reads its scales
+    in its own shuffled order; both outputs checked at 64 sampled elements against exact sums)."""
+    import subprocess
+
+    if not VENDOR_BAR.exists():
+        return None
+    lib = ROOT / "tinygrad-dx12_amd" / "tinygrad_mi355x" / "_lib" / "libtgm_mi355x.so"
+    try:
+        proc = subprocess.run([str(VENDOR_BAR), str(m), str(n), str(k), str(steps), str(lib)], capture_output=True,
+                              text=True, timeout=240)
+    except subprocess.TimeoutExpired:
+        return {"error": "timed out"}
+    lines = [x for x in proc.stdout.splitlines() if x.startswith("{")]
+    if proc.returncode != 0 or not lines:
+        return {"error": (proc.stdout + proc.stderr).strip().splitlines()[-1:] or ["no output"]}
+    r = json.loads(lines[-1])
+    flops = 2 * m * n * k
+    best = min(x for x in (r["ck_best_us"], r["ck_preshuffled_best_us"]) if x > 0)
+    return {"library": "Composable Kernel (ROCm 7.2 libdevice_gemm_operations, MXFP4 instances, fp16 out)",
+            "best_ms": best / 1e3, "TFLOPS": flops / best / 1e6, "frac": round(flops / best / 1e6 / FP4_PEAK_TFLOPS, 4),
+            "best_instance": r["ck_best_instance"] if best == r["ck_best_us"] else r["ck_preshuffled_best_instance"],
+            "natural_layout_best_ms": r["ck_best_us"] / 1e3, "natural_layout_max_rel_err": r["ck_best_err"],
+            "preshuffled_b_best_ms": r["ck_preshuffled_best_us"] / 1e3 if r["ck_preshuffled_best_us"] > 0 else None,
+            "instances": r["ck_instances"], "this_library_same_run_ms": r["tgm_us"] / 1e3,
+            "this_library_max_rel_err": r["tgm_err"],
+            "vendor_ms_over_this_library_ms": round(best / r["tgm_us"], 4) if r["tgm_us"] > 0 else None}
 
 
 def fp6_gemm_workload(torch, K, dev, fmt: str, steps: int, warmup: int, m: int = 2048, n: int = 11008,

@@ -685,6 +685,27 @@ def test_gemm_mx_fp4_full_size_sampled(dev, mnk):
     assert O.max_rel_err(bf16_np(c)[np.ix_(rows, cols)], ref) <= TOL
 
 
+@pytest.mark.parametrize("mnk", [(2100, 1300, 1024), (4352, 4352, 2048), (8192, 8448, 1024)])
+@pytest.mark.parametrize("cdt", [torch.bfloat16, torch.float16, torch.float32])
+def test_gemm_mx_fp4_persistent_stream(dev, mnk, cdt):
+    """FP4 x FP4 with K a multiple of 1024 runs the persistent kernel (one workgroup per CU walking
+    several tiles as one stream of K steps).  The shapes give workgroups 1 to 5 tiles, ragged last
+    tiles, tile counts that are and are not multiples of 8 (54, 289, 1056), and K = 1024, where a
+    workgroup moves to its next tile every four steps; every 32 x 32 output tile is sampled."""
+    m, n, k = mnk
+    print(f"persistent FP4 GEMM {m}x{n}x{k} {cdt}", flush=True)
+    g = torch.Generator(device=dev)
+    g.manual_seed(m + n + k)
+    a = quantize_mx(torch.randn((m, k), device=dev, generator=g), "fp4_e2m1")
+    b = quantize_mx(torch.randn((n, k), device=dev, generator=g), "fp4_e2m1")
+    c = matmul_nt(a, b, dtype=cdt)
+    assert c.dtype is cdt and c.shape == (m, n)
+    rng = np.random.default_rng(7)
+    rows, cols = stratified(rng, m, 1), stratified(rng, n, 1)
+    ref = host_dequant_rows(a, rows) @ host_dequant_rows(b, cols).T
+    assert O.max_rel_err(c.float().cpu().numpy()[np.ix_(rows, cols)], ref) <= TOL
+
+
 MX_PAIRS = [(fa, fb) for fa in ("fp4_e2m1", "fp6_e2m3", "fp6_e3m2") for fb in ("fp4_e2m1", "fp6_e2m3", "fp6_e3m2")]
 
 

@@ -31,6 +31,10 @@ void clear_error();
 // Launch status after an asynchronous kernel launch.
 int launch_status(const char* what);
 
+// Compute units of the device ``stream`` launches on (the current device for the null and
+// legacy / per-thread default streams), looked up once per device; 0 when unknown.
+int stream_cu_count(hipStream_t stream);
+
 __host__ __device__ inline int dtype_size(int dt) {
   switch (dt) {
     case TGM_BOOL: case TGM_I8: case TGM_U8: case TGM_FP8E4M3: case TGM_FP8E5M2: case TGM_E8M0: return 1;

@@ -24,7 +24,9 @@
 // XOR-swizzled so the 32 rows one ds_read_b128 touches fall in distinct banks; the E8M0
 // scales take the same route four steps at a time into their own double buffer (160 KB of
 // LDS in all).  The loads of step s + 2 run while step s + 1's MFMAs do.  Tiles are mapped
-// XCD-aware (tile_of).
+// XCD-aware (tile_of).  For K a multiple of 1024 the same pipeline runs persistently, one
+// workgroup per CU streaming its tiles' steps back to back (gemm_mx_fp4_stream); other K
+// launch one workgroup per tile (gemm_mx_fp4).
 #include "tgm_mfma_common.h"
 
 namespace tgm {
@@ -267,6 +269,274 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __res
 #undef TGM_OUT
 }
 
+// ---------------------------------------------------------------------------------------------
+// Persistent form for K a multiple of 1024 (kBatchSteps steps of 256): one workgroup per CU walks
+// the tiles blockIdx.x, blockIdx.x + G, ... (G = gridDim.x, a multiple of 8, so a workgroup's tiles
+// stay on its XCD's contiguous range of tile_of) as one stream of K steps.  The step pipeline of
+// gemm_mx_fp4 runs across tile boundaries unchanged: the loads of the next tile's first two
+// steps are issued during the current tile's last two, so a tile starts with its operands in LDS
+// instead of waiting for them, and no workgroup is launched per tile.  At a tile's end the
+// accumulators go to C through the idle scale buffer (see the epilogue) with non-temporal
+// stores: a round of tiles writes as much C per XCD (32 x 128 KB) as the XCD's L2 holds, and
+// ordinary stores would evict the operand panels the running tiles share.
+template <int WM, int WN>
+__global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4_stream(const uint8_t* __restrict__ a,
+                                                                   const uint8_t* __restrict__ sa,
+                                                                   const uint8_t* __restrict__ b,
+                                                                   const uint8_t* __restrict__ sb, int M, int N, int K,
+                                                                   void* __restrict__ c, int cdt, int64_t ldc) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  constexpr int NW = WM * WN, FA = 8 / WM, FB = 8 / WN;
+  constexpr int NI = 32 / NW;
+  static_assert(NW == 8, "scale batches are loaded by 8 waves");
+  const int wm = wave / WN, wn = wave % WN;
+  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+  const int ntiles = tiles_m * tiles_n;
+  const int G = gridDim.x;
+  const int my_tiles = (ntiles - (int)blockIdx.x + G - 1) / G;  // >= 1 (the host launches G <= ntiles)
+  const int nsteps = K / kBK;                                    // a multiple of kBatchSteps
+  const int total = my_tiles * nsteps;                           // this workgroup's stream of steps
+
+  const unsigned kb = (unsigned)(K / 2);
+  const unsigned kblk = (unsigned)(K / 32);
+  const i32x4v ra = buffer_rsrc(a, (unsigned)M * kb), rb = buffer_rsrc(b, (unsigned)N * kb);
+  const i32x4v rsa = buffer_rsrc(sa, (unsigned)M * kblk), rsb = buffer_rsrc(sb, (unsigned)N * kblk);
+  const int lrow = wave * (256 / NW) + (lane >> 3);
+  const unsigned lcol = (unsigned)(((lane & 7) ^ (lane >> 4)) * 16);
+  const unsigned lane_a = (unsigned)lrow * kb + lcol;  // + tile row offset, step offset, 8 i kb
+  const unsigned lds_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds;
+  // (first row, first column) of this workgroup's t-th tile
+  auto tile_origin = [&](int t, int& m0, int& n0) __attribute__((always_inline)) {
+    int tm, tn;
+    tile_of((int)blockIdx.x + t * G, tiles_m, tiles_n, kGroupM, tm, tn);
+    m0 = tm * kBM;
+    n0 = tn * kBN;
+  };
+  // Origins of the current tile (t) and the next (t + 1, or t itself for the last), looked up once
+  // per tile: the steps whose loads are issued during tile t belong to one of the two.
+  struct Tiles {
+    int t, base;        // tile index and its first stream step (t * nsteps)
+    int mc, nc, mn, nn;  // (row, column) origins of tiles t and t + 1
+  } tl;
+  auto set_tile = [&](int t) __attribute__((always_inline)) {
+    tl.t = t;
+    tl.base = t * nsteps;
+    tile_origin(t, tl.mc, tl.nc);
+    tile_origin(t + 1 < my_tiles ? t + 1 : t, tl.mn, tl.nn);
+    tl.mc = __builtin_amdgcn_readfirstlane(tl.mc);
+    tl.nc = __builtin_amdgcn_readfirstlane(tl.nc);
+    tl.mn = __builtin_amdgcn_readfirstlane(tl.mn);
+    tl.nn = __builtin_amdgcn_readfirstlane(tl.nn);
+  };
+  // (tile row origin, tile column origin, step within the tile) of stream step gs, clamped to the
+  // stream; gs lies in tile tl.t or tl.t + 1
+  struct StepAt {
+    int m0, n0, st;
+  };
+  auto step_at = [&](int gs) __attribute__((always_inline)) {
+    gs = gs < total ? gs : total - 1;
+    const int local = gs - tl.base;
+    return local < nsteps ? StepAt{tl.mc, tl.nc, local} : StepAt{tl.mn, tl.nn, local - nsteps};
+  };
+  // uniform byte offsets of stream step gs in A and B
+  struct StepOff {
+    unsigned a, b;
+  };
+  auto step_off = [&](int gs) __attribute__((always_inline)) {
+    const StepAt at = step_at(gs);
+    return StepOff{(unsigned)__builtin_amdgcn_readfirstlane((int)((unsigned)at.m0 * kb + (unsigned)(at.st * kRowBytes))),
+                   (unsigned)__builtin_amdgcn_readfirstlane((int)((unsigned)at.n0 * kb + (unsigned)(at.st * kRowBytes)))};
+  };
+  constexpr int NP = 2 * NI;
+  auto dma_piece = [&](const StepOff& o, int buf, int p) __attribute__((always_inline)) {
+    const int i = p >> 1;
+    const unsigned col_flip = (unsigned)((i & 1) * 64);
+    const unsigned la = lds_base + (unsigned)(buf * kBuffer + (p & 1) * kPanel + wave * (2048 / NW) * 16 + i * 1024);
+    const unsigned v = (lane_a ^ col_flip) + (unsigned)(8 * i) * kb + ((p & 1) ? o.b : o.a);
+    lds_dma16((p & 1) ? rb : ra, la, v);
+  };
+  const unsigned vbat = (unsigned)(((lane & 1) ^ ((lane >> 4) & 1)) * 16);
+  // scale batch gb of the stream (steps 4 gb .. 4 gb + 3, all of one tile since nsteps % 4 == 0)
+  auto issue_batch = [&](int gb) __attribute__((always_inline)) {
+    const int gs = gb * kBatchSteps < total ? gb * kBatchSteps : total - kBatchSteps;
+    const StepAt at = step_at(gs);  // the batch's first step; all four are in one tile
+    const int g = wave;             // rows [32 g, 32 g + 32)
+    const int r = 32 * g + (lane >> 1);
+    const unsigned boff = (unsigned)(at.st / kBatchSteps * kBatchRow) + vbat;
+    const unsigned la = lds_base + (unsigned)(2 * kBuffer + (gb & 1) * kBatch + g * 1024);
+    lds_dma16(rsa, la, (unsigned)(at.m0 + r) * kblk + boff);
+    lds_dma16(rsb, la + kBM * kBatchRow, (unsigned)(at.n0 + r) * kblk + boff);
+  };
+  auto dma_pieces = [&](int gs, int buf, int p0, int p1) __attribute__((always_inline)) {
+    const StepOff o = step_off(gs);
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+      if (p >= p0 && p < p1) dma_piece(o, buf, p);
+  };
+  u32x2 scl_a[FA], scl_b[FB];
+  f32x16 acc[FA][FB];
+#pragma unroll
+  for (int i = 0; i < FA; ++i)
+#pragma unroll
+    for (int j = 0; j < FB; ++j) acc[i][j] = f32x16{};
+
+  const int half = lane >> 5;
+  const int sw = (lane >> 1) & 7;
+  const int fa_row = (wm * FA * 32 + (lane & 31)) * kRowBytes;
+  const int fb_row = (wn * FB * 32 + (lane & 31)) * kRowBytes;
+  struct Frags {
+    u32x4 a[FA], b[FB];
+  };
+  auto read_item = [&](Frags& f, int buf, int u, int t) __attribute__((always_inline)) {
+    const unsigned char* la = lds + buf * kBuffer;
+    const int col = ((2 * u + half) ^ sw) * 16;
+    if (t < FA) f.a[t < FA ? t : 0] = *(const u32x4*)(la + fa_row + col + t * 32 * kRowBytes);
+    else f.b[t < FA ? 0 : t - FA] = *(const u32x4*)(la + kPanel + fb_row + col + (t - FA) * 32 * kRowBytes);
+  };
+  const int sq = (lane >> 3) & 1;
+  auto scale_item = [&](int sn, int t) __attribute__((always_inline)) {  // scales of stream step sn
+    const int st = sn % kBatchSteps;
+    const unsigned char* ls =
+        lds + 2 * kBuffer + ((sn / kBatchSteps) & 1) * kBatch + ((st >> 1) ^ sq) * 16 + (st & 1) * 8;
+    if (t < FA) scl_a[t < FA ? t : 0] = *(const u32x2*)(ls + (wm * FA * 32 + t * 32 + (lane & 31)) * kBatchRow);
+    else scl_b[t < FA ? 0 : t - FA] =
+        *(const u32x2*)(ls + kBM * kBatchRow + (wn * FB * 32 + (t - FA) * 32 + (lane & 31)) * kBatchRow);
+  };
+  auto mfmas = [&](const Frags& f, int u, auto&& hook) __attribute__((always_inline)) {
+    const int blk = 2 * u + half;
+    int xa[FA], xb[FB];
+#pragma unroll
+    for (int t = 0; t < FA; ++t) xa[t] = (int)((u < 2 ? scl_a[t][0] : scl_a[t][1]) >> (8 * (blk & 3)));
+#pragma unroll
+    for (int t = 0; t < FB; ++t) xb[t] = (int)((u < 2 ? scl_b[t][0] : scl_b[t][1]) >> (8 * (blk & 3)));
+#pragma unroll
+    for (int i = 0; i < FA; ++i)
+#pragma unroll
+      for (int j = 0; j < FB; ++j) {
+        const i32x8 fa = {(int)f.a[i][0], (int)f.a[i][1], (int)f.a[i][2], (int)f.a[i][3], 0, 0, 0, 0};
+        const i32x8 fb = {(int)f.b[j][0], (int)f.b[j][1], (int)f.b[j][2], (int)f.b[j][3], 0, 0, 0, 0};
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa, fb, acc[i][j], 4, 4, 0, xa[i], 0, xb[j]);
+        hook(i * FB + j);
+      }
+  };
+  constexpr int kMaxItems = 2 * (FA + FB) + NP;
+  auto substep = [&](const Frags& fc, int u, Frags& fn, int rbuf, int ru, bool scales, int sn, const StepOff* lo,
+                     int dbuf, int p0, int p1) __attribute__((always_inline)) {
+    const int nr = (FA + FB) * (scales ? 2 : 1);
+    const int ni = nr + (p1 - p0);
+    mfmas(fc, u, [&](int idx) __attribute__((always_inline)) {
+#pragma unroll
+      for (int it = 0; it < kMaxItems; ++it) {
+        if (it < ni && it * FA * FB / ni == idx) {
+          __builtin_amdgcn_sched_barrier(0);
+          if (it >= nr) dma_piece(*lo, dbuf, p0 + it - nr);
+          else if (!scales) read_item(fn, rbuf, ru, it);
+          else if (it < FA + FB) scale_item(sn, it);
+          else read_item(fn, rbuf, ru, it - (FA + FB));
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    });
+  };
+  set_tile(0);
+  issue_batch(0);
+  dma_pieces(0, 0, 0, NP);
+  dma_pieces(1, 1, 0, NP / 2);
+  wait_lds_dma();
+  __syncthreads();
+  Frags f0, f1;
+#pragma unroll
+  for (int t = 0; t < FA + FB; ++t) {
+    __builtin_amdgcn_sched_barrier(0);
+    scale_item(0, t);
+  }
+#pragma unroll
+  for (int t = 0; t < FA + FB; ++t) {
+    __builtin_amdgcn_sched_barrier(0);
+    read_item(f0, 0, 0, t);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  auto step = [&](int gs, int cur, bool batch) __attribute__((always_inline)) {
+    const StepOff o1 = step_off(gs + 1), o2 = step_off(gs + 2);
+    substep(f0, 0, f1, cur, 1, false, 0, &o1, cur ^ 1, NP / 2, NP);
+    substep(f1, 1, f0, cur, 2, false, 0, &o1, 0, 0, 0);
+    substep(f0, 2, f1, cur, 3, false, 0, &o1, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_lds_dma();
+    __syncthreads();
+    substep(f1, 3, f0, cur ^ 1, 0, true, gs + 1, &o2, cur, 0, NP / 2);
+    __builtin_amdgcn_sched_barrier(0);
+    if (batch) issue_batch(gs / kBatchSteps + 1);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  static_assert(kBatchSteps == 4, "the step loop is unrolled by four");
+  int gs = 0;
+  for (int t = 0; t < my_tiles; ++t) {
+    set_tile(t);
+    for (int s = 0; s < nsteps; s += kBatchSteps, gs += kBatchSteps) {
+      step(gs, 0, true);
+      step(gs + 1, 1, false);
+      step(gs + 2, 0, false);
+      step(gs + 3, 1, false);
+    }
+    // Tile t is complete in the accumulators (MFMA D layout: lane l holds column l % 32 and rows
+    // 8 (v / 4) + 4 (l / 32) + v % 4 of each 32 x 32 tile).  The scale buffer of the tile's last
+    // batch is idle from the last step's barrier until the next tile's first step issues its
+    // second batch into it (after that step's barrier, which every wave reaches only after this
+    // epilogue): each wave turns its 32 x 32 tiles, rounded to 16 bits, into rows through its 2 KB
+    // of that buffer and stores 16-byte row segments.  fp32 output goes out per element.
+    const int col0 = tl.nc + wn * FB * 32;
+    const int row0 = tl.mc + wm * FA * 32;
+    unsigned short* ep = (unsigned short*)(lds + 2 * kBuffer + (((gs - 1) / kBatchSteps) & 1) * kBatch) + wave * 1024;
+#pragma unroll
+    for (int i = 0; i < FA; ++i)
+#pragma unroll
+      for (int j = 0; j < FB; ++j) {
+        if (cdt == TGM_F32) {
+          const int col = col0 + 32 * j + (lane & 31);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int row = row0 + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            if (row < M && col < N) ((float*)c)[(int64_t)row * ldc + col] = acc[i][j][v];
+          }
+        } else {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const float x = acc[i][j][v];
+            const unsigned short h = cdt == TGM_BF16 ? f32_to_bf16(x) : __builtin_bit_cast(unsigned short, (_Float16)x);
+            ep[(8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * 32 + (lane & 31)] = h;
+          }
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {  // lane l: row l / 4 + 16 q, columns 8 (l % 4) .. + 8
+            const int r = (lane >> 2) + 16 * q, cc = 8 * (lane & 3);
+            const u32x4 v = *(const u32x4*)(ep + r * 32 + cc);
+            const int row = row0 + 32 * i + r, col = col0 + 32 * j + cc;
+            const int64_t o = (int64_t)row * ldc + col;
+            if (row < M) {
+              if (col + 7 < N && ((uintptr_t)((uint16_t*)c + o) & 15) == 0) {
+                __builtin_nontemporal_store(v, (u32x4*)((uint16_t*)c + o));
+              } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                  if (col + e < N) ((uint16_t*)c)[o + e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+              }
+            }
+          }
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        acc[i][j] = f32x16{};
+      }
+  }
+  wait_lds_dma();
+}
+
 }  // namespace tgm
 
 using namespace tgm;
@@ -295,6 +565,15 @@ extern "C" int tgm_gemm_mx(const void* a, int a_fmt, const void* a_scales, int64
   if ((uintptr_t)a % 16 || (uintptr_t)b % 16 || (uintptr_t)a_scales % 8 || (uintptr_t)b_scales % 8)
     TGM_UNSUPPORTED("tgm_gemm_mx: operands must be 16-byte and scales 8-byte aligned");
   const int64_t tiles = ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN);
+  const int cus = stream_cu_count((hipStream_t)stream);
+  if (k % (kBK * kBatchSteps) == 0 && cus >= 8 && tiles >= 8) {
+    // persistent: one workgroup per CU (a multiple of 8 of them, so each keeps to its XCD's tiles)
+    const int64_t grid = tiles < cus ? tiles / 8 * 8 : cus / 8 * 8;
+    hipLaunchKernelGGL((gemm_mx_fp4_stream<kWavesM, kWavesN>), dim3((unsigned)grid), dim3(kWavesM * kWavesN * 64), 0,
+                       (hipStream_t)stream, (const uint8_t*)a, (const uint8_t*)a_scales, (const uint8_t*)b,
+                       (const uint8_t*)b_scales, (int)m, (int)n, (int)k, c, c_dtype, ldc);
+    return launch_status("tgm_gemm_mx");
+  }
   // 4 x 2 waves of 64 x 128: two waves per SIMD hide each other's LDS and barrier latency
   hipLaunchKernelGGL((gemm_mx_fp4<kWavesM, kWavesN>), dim3((unsigned)tiles), dim3(kWavesM * kWavesN * 64), 0, (hipStream_t)stream, (const uint8_t*)a,
                      (const uint8_t*)a_scales, (const uint8_t*)b, (const uint8_t*)b_scales, (int)m, (int)n, (int)k, c,

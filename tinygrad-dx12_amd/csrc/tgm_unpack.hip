@@ -5,6 +5,8 @@
 // payload of element i is read straight from the bit stream (two bytes cover any
 // 4- or 6-bit payload), so rows that do not start on a byte boundary (odd K for
 // 4-bit, K % 4 != 0 for 6-bit) decode exactly like the reference's flat word view.
+#include <atomic>
+
 #include "tgm_common.h"
 
 namespace tgm {
@@ -27,6 +29,25 @@ int launch_status(const char* what) {
     return (int)err;
   }
   return TGM_OK;
+}
+
+int stream_cu_count(hipStream_t stream) {
+  static std::atomic<int> counts[64];  // per device, 0 = not looked up yet
+  int device = -1;
+  if (stream != nullptr && stream != hipStreamLegacy && stream != hipStreamPerThread) {
+    hipDevice_t d = -1;
+    if (hipStreamGetDevice(stream, &d) != hipSuccess) return 0;
+    device = (int)d;
+  } else if (hipGetDevice(&device) != hipSuccess) {
+    return 0;
+  }
+  if (device < 0 || device >= 64) return 0;
+  int n = counts[device].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n < 0) return 0;
+    counts[device].store(n, std::memory_order_relaxed);
+  }
+  return n;
 }
 
 // Value of one element in the multiplication type of dx12.py:103 and its final cast.

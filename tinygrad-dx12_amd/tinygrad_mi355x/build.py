@@ -36,6 +36,31 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+VENDOR_SRC = ROOT / "vendor_bar" / "ck_mx_gemm_bar.cpp"
+VENDOR_BIN = PACKAGE / "_lib" / "ck_mx_gemm_bar"
+CK_INSTANCES = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "lib" / "libdevice_gemm_operations.a"
+
+
+def build_vendor_bar(verbose: bool = False) -> Path | None:
+    """The benchmark's vendor comparison for the FP4 GEMM (Composable Kernel's prebuilt MXFP4
+    instances, timed beside tgm_gemm_mx in one process); skipped where ROCm ships no instances."""
+    if not CK_INSTANCES.exists():
+        if verbose:
+            print(f"skipped {VENDOR_BIN.name}: no {CK_INSTANCES}")
+        return None
+    VENDOR_BIN.parent.mkdir(exist_ok=True)
+    tmp = VENDOR_BIN.with_name(VENDOR_BIN.name + ".tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-w", str(VENDOR_SRC), "-o", str(tmp),
+           f"-L{CK_INSTANCES.parent}", "-ldevice_gemm_operations", "-ldl"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {VENDOR_SRC.name}:\n{proc.stderr}")
+    os.replace(tmp, VENDOR_BIN)
+    if verbose:
+        print(f"built {VENDOR_BIN}")
+    return VENDOR_BIN
+
+
 def build_library(verbose: bool = False) -> Path:
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
@@ -43,8 +68,10 @@ def build_library(verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     LIB.parent.mkdir(exist_ok=True)
     workers = min(len(sources), max(1, (os.cpu_count() or 2) // 2), 8)
-    with concurrent.futures.ThreadPoolExecutor(workers) as pool:
+    with concurrent.futures.ThreadPoolExecutor(workers + 1) as pool:
+        vendor = pool.submit(build_vendor_bar, verbose)
         objects = list(pool.map(_compile, sources))
+        vendor.result()
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
