@@ -49,6 +49,7 @@ MIN_TRIALS = 5
 EXTRAS = ("fp4_gemv_m4", "fp4_gemv_m16", "int4_gemv_n4096", "int4_gemv_n14336", "fp6_e3m2_gemm_m2048",
           "fp6_e2m3_gemm_m2048", "fp4_gemm_8192", "fp4_gemm_4096x14336x4096", "decoder_b1", "decoder_b8",
           "read_ceiling_31232000", "read_ceiling_9453568", "read_ceiling_470000000", "mfma_fp4_ceiling_8192",
+          "launch_floor_448", "fp4_gemv_shard_n1792_m1", "fp4_gemv_shard_n1792_m4", "fp4_gemv_shard_n1792_m16",
           "bf16_gemm_8192", "fp8_gemm_8192", "uop_rowsum_16384x4096", "uop_gemm_bf16_4096_relu")
 PRIMARY = "fp4_gemv_m1"
 
@@ -71,6 +72,10 @@ PROFILES = {
     "uop_gemm_bf16_4096_relu": ("uop_schedule_gemm_dense_bf16_4096_relu.txt", "gemm_dense"),
     "read_ceiling_470000000": ("probe_read_470000000.txt", "probe_read"),
     "mfma_fp4_ceiling_8192": ("probe_mfma_fp4_1024x512.txt", "probe_mfma_fp4"),
+    "launch_floor_448": ("probe_launch_448x256.txt", "probe_launch"),
+    "fp4_gemv_shard_n1792_m1": ("gemv_fp4_e2m1_n1792_k4096_m1.txt", "gemv_rows_fp4"),
+    "fp4_gemv_shard_n1792_m4": ("gemv_fp4_e2m1_n1792_k4096_m4.txt", "gemv_quads"),
+    "fp4_gemv_shard_n1792_m16": ("gemv_fp4_e2m1_n1792_k4096_m16.txt", "gemv_stream"),
 }
 
 
@@ -148,10 +153,11 @@ def mfma_roofline(flops: int, ms: float, peak: float, what: str) -> dict:
             "frac": round(achieved / peak, 4), "peak_of": what}
 
 
-def fp4_gemv_workload(torch, K, dev, m: int, steps: int, warmup: int) -> dict:
-    """FP4 E2M1 + E8M0/32 GEMV W [14336, 4096], bf16 X [M, 4096] -> bf16 Y [M, 14336]: codes uniform
-    over the 16 E2M1 values, E8M0 bytes 127 + [-4, 2], X ~ N(0, 1) rounded to bf16."""
-    n, k = 14336, 4096
+def fp4_gemv_workload(torch, K, dev, m: int, steps: int, warmup: int, n: int = 14336) -> dict:
+    """FP4 E2M1 + E8M0/32 GEMV W [N, 4096] (N = 14336; 1792 is one GPU's eighth of it when the rows
+    are split over 8 GPUs), bf16 X [M, 4096] -> bf16 Y [M, N]: codes uniform over the 16 E2M1
+    values, E8M0 bytes 127 + [-4, 2], X ~ N(0, 1) rounded to bf16."""
+    k = 4096
     nbytes = P.weight_program(P.PackedDesc("fp4_e2m1", (n, k), n * k // 2, 1, "float8_e8m0fnu"), m, "bfloat16", k,
                               "bfloat16", n).estimates.mem
     copies = copies_for(nbytes)
@@ -170,7 +176,7 @@ def fp4_gemv_workload(torch, K, dev, m: int, steps: int, warmup: int) -> dict:
         progs[j].launch(y.data_ptr(), ws[j].data_ptr(), x.data_ptr(), K.stream_of(x))
 
     ms, trials, timed = median_trials(torch, launch, steps, warmup, copies)
-    return {"workload": f"fp4_e2m1 e8m0/32 GEMV N=14336 K=4096 M={m}", "ms": ms, "bytes": nbytes,
+    return {"workload": f"fp4_e2m1 e8m0/32 GEMV N={n} K=4096 M={m}", "ms": ms, "bytes": nbytes,
             "GB/s": nbytes / ms / 1e6, "TFLOPS": 2 * m * n * k / ms / 1e9, "copies": copies,
             "copy_set_bytes": copies * nbytes, "trials": trials, "steps_per_trial": steps,
             "timed_dispatches": timed, "roofline": hbm_roofline(nbytes, ms)}
@@ -227,7 +233,7 @@ def median_launch_ms(torch, stream, launch, steps: int) -> float:
     return statistics.median(e0.elapsed_time(e1) for e0, e1 in events)
 
 
-def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup: int) -> dict:
+def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup: int, vendor: bool = False) -> dict:
     """FP4 x FP4 + E8M0/32 GEMM C[M,N] = deq(A) deq(B)^T, bf16 out: A [M, K] and B [N, K] drawn
     N(0, 1) and MX-quantised along K (round to nearest even, shared exponent per 32)."""
     from tinygrad_mi355x.codegen.decomp.mi355x import quantize_mx
@@ -249,7 +255,7 @@ def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup:
     return {"workload": f"fp4xfp4 e8m0/32 GEMM M={m} N={n} K={k} bf16 out", "ms": ms, "TFLOPS": flops / ms / 1e9,
             "flops": flops, "bytes": nbytes, "GB/s": nbytes / ms / 1e6, "timed_dispatches": steps,
             "roofline": mfma_roofline(flops, ms, FP4_PEAK_TFLOPS, "dense MXFP4 MFMA"),
-            "vendor": vendor_fp4_gemm(m, n, k, steps)}
+            "vendor": vendor_fp4_gemm(m, n, k, steps) if vendor else None}
 
 
 VENDOR_BAR = ROOT / "tinygrad-dx12_amd" / "tinygrad_mi355x" / "_lib" / "ck_mx_gemm_bar"
@@ -445,6 +451,26 @@ def read_ceiling_workload(torch, K, dev, nbytes: int, steps: int, warmup: int) -
             "timed_dispatches": timed, "roofline": hbm_roofline(nbytes, ms)}
 
 
+def launch_floor_workload(torch, K, dev, groups: int, steps: int, warmup: int) -> dict:
+    """tgm_probe_launch: an empty kernel of ``groups`` x 256 threads (448: the FP4 decode GEMV's
+    grid at N = 14336), timed exactly like the GEMV (graphs of ``steps`` launches, median trial):
+    the fixed cost every launch pays with no work.  A GEMV of B bytes cannot beat
+    floor + B / 8 TB/s per step; ``ceiling_frac_31232000`` is that bound for the headline GEMV."""
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    lib = K.load_library()
+
+    def launch(i: int) -> None:
+        K.check("tgm_probe_launch", lib.tgm_probe_launch(groups, 256, sink.data_ptr(), K.stream_of(sink)))
+
+    ms, trials, timed = median_trials(torch, launch, steps, warmup, 20)
+    headline = 31_232_000
+    ceiling_ms = ms + headline / (HBM_PEAK_GBS * 1e6)
+    return {"workload": f"empty kernel, {groups} x 256 threads (the launch floor under the decode GEMV)",
+            "ms": ms, "trials": trials, "steps_per_trial": steps, "timed_dispatches": timed,
+            "ceiling_ms_31232000": ceiling_ms,
+            "ceiling_frac_31232000": round(headline / ceiling_ms / 1e6 / HBM_PEAK_GBS, 4)}
+
+
 def mfma_ceiling_workload(torch, K, dev, steps: int, warmup: int) -> dict:
     """tgm_probe_mfma_fp4 on the 8192^3 FP4 GEMM's grid (1024 workgroups of 8 waves, 2^23 FP4
     MFMAs = the GEMM's 1.0995e12 flops), operands from registers changing every round: the FP4
@@ -634,6 +660,8 @@ def measured_traffic(workload: str) -> int | None:
 def profile_commands(workload: str) -> list[str]:
     """The rocprofv3 runs a summary is made from (OUT = the folder given to --summarize-profile)."""
     run = f"python3 bench.py --only {workload} --steps 20 --warmup 5"
+    if workload.startswith("launch_floor"):  # an empty kernel moves no bytes: its trace is the figure
+        return [f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o run -- {run}"]
     cmds = [f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/kt -o run -- {run}",
             f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o run -- {run}",
             f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o run -- {run}"]
@@ -673,6 +701,20 @@ def summarize_profile(folder: Path, workload: str) -> str:
     trace = [r for r in _csv_rows(folder / "kt", "kernel_trace.csv") if pattern in r["Kernel_Name"]]
     durations = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in trace]
     timed = durations[-run["timed_dispatches"]:]
+    if workload.startswith("launch_floor"):
+        starts = sorted(int(r["Start_Timestamp"]) for r in trace)[-run["timed_dispatches"]:]
+        gaps = [b - a for a, b in zip(starts, starts[1:])]
+        return "\n".join([f"# {name[:-4]}", "# rocprofv3 on one MI355X (gfx950); commands run from the repository "
+                          "root, OUT = any output folder:", *[f"#   {c}" for c in profile_commands(workload)],
+                          "#   (the kernel-trace run's stdout saved as OUT/kt/bench.json)",
+                          f"#   python3 bench.py --summarize-profile OUT --only {workload}",
+                          f"workload: {run['workload']}", f"kernel: {trace[-1]['Kernel_Name'][:150]}",
+                          f"kernel_trace: dispatches={len(durations)} timed={len(timed)}",
+                          f"timed dispatch duration: mean_ns={statistics.mean(timed):.0f} "
+                          f"median_ns={statistics.median(timed):.0f}",
+                          f"start-to-start of consecutive timed dispatches: median_ns={statistics.median(gaps):.0f}",
+                          f"bench_ms_per_step_under_trace={run['ms']:.6f} (kernel tracing adds a fixed cost per "
+                          "dispatch; the untraced floor is the bench line's launch_floor_448 ms)"]) + "\n"
     fetch, nf = _counter(folder / "fetch", "FETCH_SIZE", pattern)
     write, nw = _counter(folder / "write", "WRITE_SIZE", pattern)
     cfetch, _ = _counter(folder / "cfetch", "FETCH_SIZE", "copyBuffer")
@@ -809,14 +851,20 @@ def main() -> int:
         "int4_gemv_n14336": lambda: int4_gemv_workload(torch, K, dev, 14336, steps, warmup),
         "fp6_e3m2_gemm_m2048": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e3m2", gemm_steps, 20),
         "fp6_e2m3_gemm_m2048": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e2m3", gemm_steps, 20),
-        "fp4_gemm_8192": lambda: fp4_gemm_workload(torch, K, dev, 8192, 8192, 8192, gemm_steps, 20),
-        "fp4_gemm_4096x14336x4096": lambda: fp4_gemm_workload(torch, K, dev, 4096, 14336, 4096, gemm_steps, 20),
+        # the vendor comparison runs in a child process, so it is left out of --only runs (profiles)
+        "fp4_gemm_8192": lambda: fp4_gemm_workload(torch, K, dev, 8192, 8192, 8192, gemm_steps, 20, not args.only),
+        "fp4_gemm_4096x14336x4096": lambda: fp4_gemm_workload(torch, K, dev, 4096, 14336, 4096, gemm_steps, 20,
+                                                               not args.only),
         "decoder_b1": lambda: decoder_workload(torch, dev, 1),
         "decoder_b8": lambda: decoder_workload(torch, dev, 8),
         "read_ceiling_31232000": lambda: read_ceiling_workload(torch, K, dev, 31_232_000, steps, warmup),
         "read_ceiling_9453568": lambda: read_ceiling_workload(torch, K, dev, 9_453_568, steps, warmup),
         "read_ceiling_470000000": lambda: read_ceiling_workload(torch, K, dev, 470_000_000, steps, warmup),
         "mfma_fp4_ceiling_8192": lambda: mfma_ceiling_workload(torch, K, dev, gemm_steps, 20),
+        "launch_floor_448": lambda: launch_floor_workload(torch, K, dev, 448, steps, warmup),
+        "fp4_gemv_shard_n1792_m1": lambda: fp4_gemv_workload(torch, K, dev, 1, steps, warmup, 1792),
+        "fp4_gemv_shard_n1792_m4": lambda: fp4_gemv_workload(torch, K, dev, 4, steps, warmup, 1792),
+        "fp4_gemv_shard_n1792_m16": lambda: fp4_gemv_workload(torch, K, dev, 16, steps, warmup, 1792),
         "bf16_gemm_8192": lambda: dense_gemm_workload(torch, K, dev, "bfloat16", 8192, gemm_steps, 20),
         "fp8_gemm_8192": lambda: dense_gemm_workload(torch, K, dev, "float8_e4m3fn", 8192, gemm_steps, 20),
         "uop_rowsum_16384x4096": lambda: uop_rowsum_workload(steps, warmup),
@@ -837,9 +885,15 @@ def main() -> int:
         if "int4_gemv_n4096" in extras:
             extras["int4_gemv_n4096"]["cpu_baseline"] = cpu_baseline_int4(args.cpu_seconds)
     for name, w in extras.items():
-        if name in PROFILES:
+        if name in PROFILES and "roofline" in w:
             w["roofline"]["traffic"] = measured_traffic(name)
     roofline = dict(primary["roofline"], traffic=measured_traffic(PRIMARY))
+    floor = extras.get("launch_floor_448")
+    if floor:
+        # what one launch of this many bytes can reach here: the empty kernel's time on the same
+        # grid, in the same graphs, plus the bytes at the HBM peak
+        roofline["launch_floor_ms"] = round(floor["ms"], 6)
+        roofline["single_launch_ceiling_frac"] = floor["ceiling_frac_31232000"]
     line = {
         "metric": "low-bit GEMV GB/s (% HBM peak) + FP4 GEMM TFLOPS (% MFMA peak), 1 GPU",
         "value": roofline["achieved"],

@@ -320,6 +320,9 @@ int tgm_pack_codes(const void* codes, int64_t count, int bits, void* out, void* 
  */
 int tgm_probe_read(const void* p, int64_t nbytes, void* sink, void* stream);
 int tgm_probe_mfma_fp4(int64_t blocks, int64_t iters, void* sink, void* stream);
+/* tgm_probe_launch launches an empty kernel of ``groups`` x ``threads`` (threads <= 1024): the
+ * fixed cost of one launch of that grid with no work, the floor under any kernel's time. */
+int tgm_probe_launch(int64_t groups, int64_t threads, void* sink, void* stream);
 
 #ifdef __cplusplus
 }

@@ -12,6 +12,8 @@
 //    and with it the clock it sustains, depends on operand toggling): the FP4 MFMA throughput
 //    the FP4 GEMM could reach with no data movement at all, on the GEMM's grid (1024
 //    workgroups of 8 waves at 8192^3).
+//  * tgm_probe_launch is an empty kernel: the fixed cost of one launch of a grid, which a
+//    memory-bound kernel of a few microseconds pays in full on top of its transfer time.
 #include "tgm_mfma_common.h"
 
 namespace tgm {
@@ -78,9 +80,24 @@ __global__ void __launch_bounds__(512) probe_mfma_fp4(int iters, unsigned seed, 
   if (s == 1234.5f) sink[0] = s;  // keeps the MFMAs; practically never stores
 }
 
+// An empty kernel: what one launch of a given grid costs with no work at all -- dispatch, the
+// workgroups' start and end, and the launch's completion -- timed like the kernels it bounds.
+__global__ void __launch_bounds__(1024) probe_launch(unsigned* __restrict__ sink, int never) {
+  if ((int)threadIdx.x == never) sink[0] = 1;  // the host passes a thread index past the block
+}
+
 }  // namespace tgm
 
 using namespace tgm;
+
+extern "C" int tgm_probe_launch(int64_t groups, int64_t threads, void* sink, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(sink, "null operand");
+  TGM_CHECK_ARG(groups > 0 && groups < (1ll << 31) && threads > 0 && threads <= 1024, "invalid launch shape");
+  hipLaunchKernelGGL(probe_launch, dim3((unsigned)groups), dim3((unsigned)threads), 0, (hipStream_t)stream,
+                     (unsigned*)sink, (int)threads);
+  return launch_status("tgm_probe_launch");
+}
 
 extern "C" int tgm_probe_read(const void* p, int64_t nbytes, void* sink, void* stream) {
   clear_error();

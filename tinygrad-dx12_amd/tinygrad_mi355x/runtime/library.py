@@ -68,6 +68,7 @@ SIGNATURES = {
     "tgm_device_arch": (_INT, ctypes.c_char_p, _I64),
     "tgm_probe_read": (_P, _I64, _P, _P),
     "tgm_probe_mfma_fp4": (_I64, _I64, _P, _P),
+    "tgm_probe_launch": (_I64, _I64, _P, _P),
     # decoder-step kernels (include/tgm_decoder.h)
     "tgm_dec_embed": (_P, _I64, _I64, _P, _I64, _P, _P),
     "tgm_dec_add_rmsnorm": (_P, _P, _I64, _I64, _P, ctypes.c_float, _P, _INT, _P),
