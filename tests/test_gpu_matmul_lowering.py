@@ -71,7 +71,9 @@ def test_ordinary_matmul_eager_gradient_and_replay(dev):
     assert out.dtype is torch.float16
     np.testing.assert_allclose(f64(out), data_a @ data_b, rtol=3e-3, atol=3e-3)
     ga, gb = a.clone().requires_grad_(), b.clone().requires_grad_()
+    linalg.fallbacks.clear()
     gm(ga, gb).float().sum().backward()
+    assert not linalg.fallbacks  # the gradient products (K = 48 and 16) run zero-padded on the MFMA GEMM
     np.testing.assert_allclose(f64(ga.grad), np.ones((16, 48)) @ data_b.T, rtol=3e-3, atol=3e-3)
     np.testing.assert_allclose(f64(gb.grad), data_a.T @ np.ones((16, 48)), rtol=3e-3, atol=3e-3)
     for step in range(4):
@@ -91,7 +93,9 @@ def test_misaligned_views_are_staged(dev, offset):
         base = torch.tensor(data_a + step, dtype=torch.float16, device=dev)
         a = base[offset:offset + 16 * 64].reshape(16, 64)
         want = np.maximum((data_a[offset:offset + 16 * 64] + step).reshape(16, 64) @ data_b, 0)
+        linalg.fallbacks.clear()
         np.testing.assert_allclose(f64(gm(a, b)), want, rtol=3e-3, atol=3e-3)
+        assert not linalg.fallbacks  # staged zero-padded onto the MFMA GEMM, not the exact-width one
 
 
 def test_packed_weight_product_is_not_materialised(dev):
@@ -126,9 +130,9 @@ def test_packed_weight_product_is_not_materialised(dev):
 
 @pytest.mark.parametrize("k", [256, 96])
 def test_scaled_fp8_product_is_lowered(dev, k):
-    """A traced torch._scaled_mm runs the FP8 GEMM (K = 96 has no 128-element tiling: the
-    exact-width device GEMM, then the scales); both match the exact fp64 product times the
-    per-tensor scales."""
+    """A traced torch._scaled_mm runs the FP8 GEMM (K = 96 is staged zero-padded to the GEMM's
+    128-element step); both match the exact fp64 product times the per-tensor scales, and
+    neither falls back to the exact-width GEMM."""
     g = torch.Generator(device=dev)
     g.manual_seed(k)
     a = (torch.randn((130, k), device=dev, generator=g) * 3).to(torch.float8_e4m3fn)
@@ -141,7 +145,9 @@ def test_scaled_fp8_product_is_lowered(dev, k):
     # shapes are propagated on CPU copies (torch runs _scaled_mm there), the product runs on the GPU
     gm = MM.lower_matmul(MM.trace(f), *(t.cpu() for t in (a, w, sa, sb)))
     assert gm.lowered_matmuls == [(130, 200, k)]
+    linalg.fallbacks.clear()
     out = gm(a, w, sa, sb)
+    assert not linalg.fallbacks
     ref = a.float().cpu().numpy().astype(np.float64) @ w.float().cpu().numpy().astype(np.float64).T * 0.375
     assert out.dtype is torch.float32
     assert O.max_rel_err(out.cpu().numpy(), ref) <= 1e-2

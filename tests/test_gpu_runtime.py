@@ -164,3 +164,57 @@ def test_graph_replays_program_sequence(device):
     with pytest.raises(ValueError):
         graph({0: ((by,), groups, (256, 1, 1), (1.0, n))})  # wrong buffer count, rejected before capture
     graph.close()
+
+
+def test_profiling_publishes_per_kernel_times(device):
+    """Under profiling: an eager launch publishes a ProfileRangeEvent, a library program on
+    plugin buffers one too, and each replay of a three-kernel graph a ProfileGraphEvent whose
+    three entries cover four signals recorded as graph nodes (the reference's kernel_count + 1
+    timestamp queries).  The kernels' times are positive and in launch order, the larger kernel
+    takes longer than the small one after it, and the graph still computes what the eager
+    sequence does."""
+    from tinygrad_mi355x.runtime import profile
+    from tinygrad_mi355x.runtime.graph import MI355XGraph
+
+    src = device.renderer.render(SAXPY)
+    prog = device.runtime("saxpy", device.compiler.compile(src))
+    n_big, n = 8_000_000, 100_003
+    rng = np.random.default_rng(5)
+    x, y0 = rng.standard_normal(n_big).astype(np.float32), rng.standard_normal(n_big).astype(np.float32)
+    bx, by = upload(device, x), upload(device, y0)
+    small, big = (((n + 255) // 256, 1, 1), ((n_big + 255) // 256, 1, 1))
+    profile.set_enabled(True)
+    try:
+        profile.profile_events.clear()
+        print("profiled eager launch", flush=True)
+        prog(by, bx, global_size=small, local_size=(256, 1, 1), vals=(1.0, n))
+        device.synchronize()
+        ranges = [e for e in profile.profile_events if type(e).__name__ == "ProfileRangeEvent"]
+        assert len(ranges) == 1 and ranges[0].name == "saxpy" and ranges[0].en > ranges[0].st
+        print("profiled three-kernel graph", flush=True)
+        calls = [(prog, (by, bx), small, (256, 1, 1), (0.5, n)), (prog, (by, bx), big, (256, 1, 1), (-2.0, n_big)),
+                 (prog, (by, bx), small, (256, 1, 1), (0.25, n))]
+        graph = MI355XGraph(calls)
+        for _ in range(3):
+            graph()
+        device.synchronize()
+        events = [e for e in profile.profile_events if type(e).__name__ == "ProfileGraphEvent"]
+        assert len(events) == 3
+        for ev in events:
+            assert [e.name for e in ev.ents] == ["saxpy"] * 3 and len(ev.sigs) == 4
+            assert all(a < b for a, b in zip(ev.sigs, ev.sigs[1:]))
+            secs = profile.kernel_seconds(ev)
+            # the first interval also holds the replay's start; the 80x larger middle kernel
+            # outlasts the last
+            assert all(0 < s < 0.1 for s in secs) and secs[1] > secs[2]
+        assert events[1].sigs[0] > events[0].sigs[-1]  # replays in stream order
+        graph.close()
+    finally:
+        profile.set_enabled(False)
+    want = y0.astype(np.float64)
+    want[:n] += 1.0 * x[:n]
+    for _ in range(3):
+        want[:n] += 0.5 * x[:n]
+        want += -2.0 * x
+        want[:n] += 0.25 * x[:n]
+    np.testing.assert_allclose(download(device, by, np.float32, n_big), want, rtol=1e-4, atol=1e-4)

@@ -3,6 +3,8 @@ validation (no GPU needed; mirrors the spirit of the reference's test_toolchain.
 the argument checks of ops_dx12.py:659-744)."""
 
 import struct
+import subprocess
+from pathlib import Path
 
 import pytest
 import torch
@@ -343,3 +345,105 @@ def test_one_hip_runtime_whichever_is_opened_first():
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
     assert out.returncode == 0, out.stderr
     assert out.stdout.strip().splitlines()[-1] == "1"
+
+
+def test_dump_src_prints_each_new_source_once(monkeypatch, capsys):
+    """MI355X_DUMP_SRC=1 prints what the compiler compiles (the reference's DX12_DUMP_SHADERS),
+    before invoking the toolchain, once per new source."""
+    from tinygrad_mi355x.runtime.support import compiler_hip as CH
+
+    comp = CH.MI355XCompiler("gfx950")
+    src = MI355XRenderer("gfx950").render(KernelSpec("dumped", (BufferParam("x", torch.float32),),
+                                                     body=("x[0] = 1.0f;",)))
+    monkeypatch.setenv("MI355X_DUMP_SRC", "1")
+    calls = []
+
+    def fake_run(cmd, capture_output, text):
+        calls.append(cmd)
+        Path(cmd[-1]).write_bytes(b"\x7fELF-not-really")
+        return subprocess.CompletedProcess(cmd, 0, "", "")
+
+    monkeypatch.setattr(CH.subprocess, "run", fake_run)
+    comp.compile(src)
+    comp.compile(src)
+    err = capsys.readouterr().err
+    assert err.count("dumped") >= 1 and err.count(src) == 1 and len(calls) == 1
+    monkeypatch.setenv("MI355X_DUMP_SRC", "0")
+    comp2 = CH.MI355XCompiler("gfx950")
+    comp2.compile(src)
+    assert capsys.readouterr().err == ""
+
+
+def test_profile_events_from_eager_graph_and_library_calls_with_stubbed_hip(monkeypatch):
+    """With profiling on, an eager launch publishes a ProfileRangeEvent and a graph replay a
+    ProfileGraphEvent with one entry per kernel over kernel_count + 1 signals, read from the
+    events recorded around them (HIP stubbed: event i completes at 10 * i microseconds)."""
+    import decimal
+
+    from tinygrad_mi355x.runtime import profile
+
+    times: dict[int, float] = {}
+    counter = iter(range(1, 10_000))
+    recorded = []
+
+    class Stub:
+        def __init__(self):
+            self.now = 0.0
+
+    stub = Stub()
+
+    def event_create():
+        e = next(counter)
+        times[e] = 0.0
+        return e
+
+    def call(name, *args):
+        if name in ("hipEventRecord", "hipEventRecordWithFlags"):
+            stub.now += 0.01  # ms
+            times[args[0]] = stub.now
+            recorded.append((name, args[-1] if name == "hipEventRecordWithFlags" else None))
+        return 0
+
+    monkeypatch.setattr(profile.hip, "event_create", event_create)
+    monkeypatch.setattr(profile.hip, "call", call)
+    monkeypatch.setattr(profile.hip, "elapsed_ms", lambda a, b: times[b] - times[a])
+
+    class Dev:
+        device = "MI355X"
+        stream = 7
+
+    dev = Dev()
+    profile.profile_events.clear()
+    rng = profile.RangeTiming(dev, "k_eager")
+    rng.end(dev)
+    rng.publish()
+    timing = profile.GraphTiming(dev, ["k0", "k1", "k2"])
+    for e in timing.events:  # what a replay's event-record nodes do
+        call("hipEventRecord", e, dev.stream)
+    event = timing.publish()
+    kinds = [type(e).__name__ for e in profile.profile_events]
+    assert kinds == ["ProfileDeviceEvent", "ProfileRangeEvent", "ProfileGraphEvent"]
+    r = profile.profile_events[1]
+    assert r.name == "k_eager" and abs(r.en - r.st - decimal.Decimal("10.0")) < decimal.Decimal("1e-9")
+    assert [e.name for e in event.ents] == ["k0", "k1", "k2"] and len(event.sigs) == 4
+    assert [(e.st_id, e.en_id) for e in event.ents] == [(0, 1), (1, 2), (2, 3)]
+    assert event.deps == [[], [0], [1]]
+    assert [round(s, 9) for s in profile.kernel_seconds(event)] == [1e-5, 1e-5, 1e-5]
+
+
+def test_profiled_graph_records_an_event_node_around_every_call(monkeypatch):
+    """StreamGraph.profiled captures the calls once, with an event node before the first call,
+    between calls and after the last (HIP stubbed: the capture-time calls are logged)."""
+    from tinygrad_mi355x.runtime import graph as G
+
+    log = []
+    monkeypatch.setattr(G.hip, "capture_begin", lambda stream: log.append(("begin", stream)))
+    monkeypatch.setattr(G.hip, "capture_end", lambda stream: log.append(("end", stream)) or 7)
+    monkeypatch.setattr(G.hip, "graph_instantiate", lambda graph: 8)
+    monkeypatch.setattr(G.hip, "capture_event", lambda stream, event: log.append(("event", event)))
+    g = G.StreamGraph.profiled([lambda: log.append(("call", 0)), lambda: log.append(("call", 1))], 5, [11, 12, 13])
+    assert log == [("begin", 5), ("event", 11), ("call", 0), ("event", 12), ("call", 1), ("event", 13), ("end", 5)]
+    assert (g._graph, g._exec) == (7, 8)
+    g._graph = g._exec = 0  # nothing real to destroy
+    with pytest.raises(ValueError, match="one event more"):
+        G.StreamGraph.profiled([lambda: None], 5, [1])

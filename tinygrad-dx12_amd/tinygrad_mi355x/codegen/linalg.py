@@ -105,15 +105,34 @@ def _k_rows(x: torch.Tensor) -> torch.Tensor:
     return x if x.stride(1) == 1 or x.shape[1] == 1 else x.contiguous()
 
 
+def _rows_aligned(x: torch.Tensor) -> bool:
+    return x.data_ptr() % 16 == 0 and (x.shape[0] <= 1 or x.stride(0) * x.element_size() % 16 == 0)
+
+
+def _padded_k(x: torch.Tensor, kp: int) -> torch.Tensor:
+    """``x`` [rows, K] as a contiguous [rows, kp] copy with zeros past column K: zero columns on
+    both operands add nothing to any product, so the GEMM's K step and 16-byte row alignment
+    hold for every K (the staging the UOp rewrite does, codegen/uop_matmul.py)."""
+    out = torch.zeros((x.shape[0], kp), dtype=x.dtype, device=x.device)
+    out[:, :x.shape[1]].copy_(x)
+    return out
+
+
 def dense_matmul_nt(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype, scale_a: torch.Tensor | None = None,
                     scale_b: torch.Tensor | None = None) -> torch.Tensor:
     """C[M, N] = a[M, K] @ b[N, K]^T on the ordinary MFMA GEMM (bf16 or f16 operands; FP8
     operands decoded exactly to bf16 in registers); ``scale_a`` / ``scale_b`` are optional fp32
-    device scalars (FP8 only) that multiply the fp32 sums before rounding."""
+    device scalars (FP8 only) that multiply the fp32 sums before rounding.  A K off the GEMM's
+    step (64; 128 for FP8) or rows off 16-byte alignment are staged zero-padded."""
     for s in (scale_a, scale_b):
         if s is not None and (s.dtype is not torch.float32 or s.numel() != 1 or s.device != a.device):
             raise ValueError("scales must be single fp32 values on the operands' device")
     a, b = _k_rows(a), _k_rows(b)
+    step = (GEMM_FP8 if a.dtype in FP8_DTYPES else GEMM_DENSE).tile[2]
+    k0 = a.shape[1]
+    if k0 and (k0 % step or not _rows_aligned(a) or not _rows_aligned(b)):
+        kp = -(-k0 // step) * step
+        a, b = _padded_k(a, kp), _padded_k(b, kp)
     m, k = a.shape
     n = b.shape[0]
     c = torch.empty((m, n), dtype=out_dtype, device=a.device)

@@ -28,6 +28,7 @@ from typing import Callable
 from tinygrad_mi355x.codegen.decomp.formats import FORMATS, MX_FORMATS, packed_nbytes
 from tinygrad_mi355x.renderer.matrix import GEMM_DENSE, GEMM_FP8, GEMM_W, GEMV, GEMV_MAX_ROWS, MatrixKernel, mx_kernel
 from tinygrad_mi355x.runtime import library as L
+from tinygrad_mi355x.runtime import profile
 from tinygrad_mi355x.runtime.support import hip
 
 ACTIVATIONS = ("bfloat16", "float16", "float32")
@@ -116,12 +117,15 @@ class MatrixProgram:
         with dev.lock, dev.submitting():
             dev.select()
             start, stop = (hip.event_create(), hip.event_create()) if wait else (0, 0)
+            ranged = profile.RangeTiming(dev, self.name) if profile.enabled() else None
             if wait:
                 hip.call("hipEventRecord", start, dev.stream)
             self.launch(out.address, a.address, b.address if b is not None else 0, dev.stream)
             if wait:
                 hip.call("hipEventRecord", stop, dev.stream)
-            dev.submitted(tuple(x.owner for x in bufs))
+            if ranged is not None:
+                ranged.end(dev)
+            dev.submitted(tuple(x.owner for x in bufs), ranged.publish if ranged is not None else None)
         if not wait:
             return None
         try:

@@ -18,6 +18,11 @@ the replay object is a hipGraphExec:
 Replays are ordered on the stream like any other work, so a graph needs no ring of slots:
 the GPU runs replay n + 1 after replay n.  Captured work must not allocate, synchronise or
 issue memsets; the kernels of this package do none of those.
+
+Under profiling (``runtime/profile.py``) a graph is captured with a timestamp event before its
+first kernel and after each kernel, as graph nodes, and every replay waits for completion and
+publishes a ``ProfileGraphEvent`` of per-kernel times (the reference's ``kernel_count + 1``
+queries, runtime/graph/dx12.py:224, :249-253).
 """
 
 from __future__ import annotations
@@ -25,6 +30,7 @@ from __future__ import annotations
 import threading
 from typing import Callable, Sequence
 
+from tinygrad_mi355x.runtime import profile
 from tinygrad_mi355x.runtime.support import hip
 
 
@@ -46,6 +52,22 @@ class StreamGraph:
             raise
         self._graph = hip.capture_end(stream)
         self._exec = hip.graph_instantiate(self._graph)
+
+    @classmethod
+    def profiled(cls, records: list[Callable[[], None]], stream: int, events: list[int]) -> "StreamGraph":
+        """One capture of ``records`` with an event-record node before the first call, between
+        consecutive calls and after the last (``events``, one more than calls): every replay
+        writes each call's start and end."""
+        if len(events) != len(records) + 1:
+            raise ValueError("a profiled graph needs one event more than it has calls")
+
+        def record() -> None:
+            hip.capture_event(stream, events[0])
+            for rec, event in zip(records, events[1:]):
+                rec()
+                hip.capture_event(stream, event)
+
+        return cls(record, stream)
 
     def launch(self) -> None:
         """Enqueue one replay on the stream (asynchronous)."""
@@ -102,6 +124,7 @@ class MI355XGraph:
         self.calls = [self._normalise(c) for c in calls]
         self._graph: StreamGraph | None = None
         self._recorded: list[tuple] | None = None
+        self._timing: profile.GraphTiming | None = None
 
     @staticmethod
     def _normalise(call: tuple) -> tuple:
@@ -109,22 +132,33 @@ class MI355XGraph:
         return program, tuple(bufs), tuple(global_size), tuple(local_size), tuple(vals)
 
     def _key(self, calls: list[tuple]) -> list[tuple]:
-        return [(id(p), tuple(id(b) for b in bufs), g, l, v) for p, bufs, g, l, v in calls]
+        # a graph captured with timestamp nodes is re-recorded when profiling is switched
+        return [profile.enabled()] + [(id(p), tuple(id(b) for b in bufs), g, l, v) for p, bufs, g, l, v in calls]
 
     def _record(self, calls: list[tuple]) -> None:
         # validate every call exactly as an eager launch would, before capturing anything
         for program, bufs, global_size, local_size, vals in calls:
             program.validate(bufs, global_size, local_size, vals)
 
-        def record() -> None:
-            for program, bufs, global_size, local_size, vals in calls:
-                program.enqueue(bufs, global_size, local_size, vals)
-
-        if self._graph is not None:
-            self._graph.close()
+        if self._timing is not None:
+            self._timing.close()
+            self._timing = None
         with self.dev.lock:
             self.dev.select()
-            self._graph = StreamGraph(record, self.dev.stream)
+            timing = profile.GraphTiming(self.dev, [c[0].name for c in calls]) if profile.enabled() else None
+
+            def record() -> None:
+                for program, bufs, global_size, local_size, vals in calls:
+                    program.enqueue(bufs, global_size, local_size, vals)
+
+            if self._graph is not None:
+                self._graph.close()
+            if timing is None:
+                self._graph = StreamGraph(record, self.dev.stream)
+            else:
+                one = [lambda c=c: c[0].enqueue(*c[1:]) for c in calls]
+                self._graph = StreamGraph.profiled(one, self.dev.stream, timing.events)
+            self._timing = timing
         self._recorded = self._key(calls)
 
     def __call__(self, updates: dict[int, tuple] | None = None, wait: bool = False) -> float | None:
@@ -141,15 +175,20 @@ class MI355XGraph:
                 self.calls = calls
             with self.dev.lock, self.dev.submitting():
                 owners = tuple(b.owner for _, bufs, *_ in calls for b in bufs)
-                if not wait:
+                if not wait and self._timing is None:
                     self._graph.launch()
                     self.dev.submitted(owners)
                     return None
                 seconds = self._graph(wait=True)
                 self.dev.submitted(owners)
-                return seconds
+                if self._timing is not None:  # this replay's signals, before another overwrites them
+                    self._timing.publish()
+                return seconds if wait else None
 
     def close(self) -> None:
         if self._graph is not None:
             self._graph.close()
             self._graph = None
+        if self._timing is not None:
+            self._timing.close()
+            self._timing = None

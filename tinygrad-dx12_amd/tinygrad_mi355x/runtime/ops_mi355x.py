@@ -38,6 +38,7 @@ from typing import Callable
 
 from tinygrad_mi355x.compat import DEVICE
 from tinygrad_mi355x.renderer.cstyle import MI355XRenderer
+from tinygrad_mi355x.runtime import profile
 from tinygrad_mi355x.runtime.support import hip
 from tinygrad_mi355x.runtime.support.compiler_hip import CompileError, unpack_object
 
@@ -288,12 +289,15 @@ class MI355XProgram:
             self.dev.select()
             # timing events belong to this call only (the device retires and destroys its own)
             start, stop = (hip.event_create(), hip.event_create()) if wait else (0, 0)
+            ranged = profile.RangeTiming(self.dev, self.name) if profile.enabled() else None
             if wait:
                 hip.call("hipEventRecord", start, self.dev.stream)
             self.enqueue(bufs, global_size, local_size, vals)
             if wait:
                 hip.call("hipEventRecord", stop, self.dev.stream)
-            self.dev.submitted(tuple(b.owner for b in bufs))
+            if ranged is not None:
+                ranged.end(self.dev)
+            self.dev.submitted(tuple(b.owner for b in bufs), ranged.publish if ranged is not None else None)
         if not wait:
             return None
         try:

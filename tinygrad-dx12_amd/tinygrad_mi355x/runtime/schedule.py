@@ -24,6 +24,7 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 from tinygrad_mi355x.codegen.program import MatrixProgram
+from tinygrad_mi355x.runtime import profile
 from tinygrad_mi355x.uop.linearize import LinearKernel, linearize
 from tinygrad_mi355x.uop.ops import FP8_DTYPES, Ops, UOp, dtypes
 
@@ -168,23 +169,36 @@ class LinearGraph:
         self.launches, self.buffers = plan(dev, linear, buffers, var_vals)
         if not self.launches:
             raise ValueError("an empty schedule has nothing to capture")
-
-        def record() -> None:
-            for launch in self.launches:
-                launch.enqueue(dev.stream)
-
         with dev.lock:
             dev.select()
-            self.graph = StreamGraph(record, dev.stream)
+            # under profiling: a timestamp node before the first kernel and after each
+            self.timing = profile.GraphTiming(dev, [la.program.name for la in self.launches]) \
+                if profile.enabled() else None
+
+            def record() -> None:
+                for launch in self.launches:
+                    launch.enqueue(dev.stream)
+
+            if self.timing is None:
+                self.graph = StreamGraph(record, dev.stream)
+            else:
+                one = [lambda la=la: la.enqueue(dev.stream) for la in self.launches]
+                self.graph = StreamGraph.profiled(one, dev.stream, self.timing.events)
         self.owners = tuple({id(b.owner): b.owner for la in self.launches for b in la.bufs}.values())
 
     def __call__(self, wait: bool = False) -> float | None:
-        """Replay once (asynchronously); GPU seconds when ``wait``."""
+        """Replay once (asynchronously); GPU seconds when ``wait``.  A graph captured under
+        profiling waits for each replay and publishes its per-kernel times."""
         with self.dev.lock, self.dev.submitting():
             self.dev.select()
-            seconds = self.graph(wait=wait)
+            seconds = self.graph(wait=wait or self.timing is not None)
             self.dev.submitted(self.owners)
-        return seconds
+            if self.timing is not None:
+                self.timing.publish()
+        return seconds if wait else None
 
     def close(self) -> None:
         self.graph.close()
+        if self.timing is not None:
+            self.timing.close()
+            self.timing = None

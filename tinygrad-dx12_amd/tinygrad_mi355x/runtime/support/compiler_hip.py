@@ -11,6 +11,10 @@ one ``amdclang++ -x hip --cuda-device-only`` invocation producing an AMDGPU code
 The compiled object keeps its source and kernel signature in front of the code object
 (as the reference keeps HLSL beside DXIL, compiler_dx12.py:122-123), so a Program can
 validate buffer and scalar counts without parsing machine code.
+
+With ``MI355X_DUMP_SRC=1`` every source the compiler compiles (each new source, once) is
+printed to stderr first, as the reference's ``DX12_DUMP_SHADERS=1`` prints its HLSL
+(compiler_dx12.py:81-82).
 """
 
 from __future__ import annotations
@@ -20,6 +24,7 @@ import json
 import os
 import re
 import subprocess
+import sys
 import tempfile
 import threading
 from dataclasses import dataclass
@@ -127,6 +132,8 @@ class MI355XCompiler:
         with self.lock:
             if key in self._cache:
                 return self._cache[key]
+            if os.environ.get("MI355X_DUMP_SRC", "0") == "1":  # the reference's DX12_DUMP_SHADERS
+                print(src, file=sys.stderr)
             with tempfile.TemporaryDirectory(prefix="mi355x_cc_") as tmp:
                 path = Path(tmp) / "kernel.hip"
                 out = Path(tmp) / "kernel.hsaco"

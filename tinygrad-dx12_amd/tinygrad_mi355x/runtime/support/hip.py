@@ -69,7 +69,12 @@ _SIGNATURES = {
     "hipGraphLaunch": (_P, _P),
     "hipGraphExecDestroy": (_P,),
     "hipGraphDestroy": (_P,),
+    "hipGraphAddEventRecordNode": (ctypes.POINTER(_P), _P, ctypes.POINTER(_P), _SZ, _P),
+    "hipStreamGetCaptureInfo_v2": (_P, ctypes.POINTER(_INT), ctypes.POINTER(ctypes.c_ulonglong), ctypes.POINTER(_P),
+                                   ctypes.POINTER(ctypes.POINTER(_P)), ctypes.POINTER(_SZ)),
+    "hipStreamUpdateCaptureDependencies": (_P, ctypes.POINTER(_P), _SZ, _U32),
 }
+CAPTURE_SET_DEPENDENCIES = 1  # hipStreamSetCaptureDependencies
 # hipStreamCaptureMode: only this thread's HIP calls are checked against the capture
 CAPTURE_THREAD_LOCAL = 1
 
@@ -258,6 +263,21 @@ def capture_end(stream: int) -> int:
     g = ctypes.c_void_p()
     call("hipStreamEndCapture", stream, ctypes.byref(g))
     return g.value or 0
+
+
+def capture_event(stream: int, event: int) -> None:
+    """While ``stream`` is being captured: add a node that records ``event`` after everything
+    captured so far, and make it what the next captured work depends on.  (hipEventRecord under
+    capture becomes no graph node on this runtime, so the node is added to the capture graph.)"""
+    status = ctypes.c_int(0)
+    graph = ctypes.c_void_p()
+    deps = ctypes.POINTER(ctypes.c_void_p)()
+    count = ctypes.c_size_t(0)
+    call("hipStreamGetCaptureInfo_v2", stream, ctypes.byref(status), None, ctypes.byref(graph), ctypes.byref(deps),
+         ctypes.byref(count))
+    node = ctypes.c_void_p()
+    call("hipGraphAddEventRecordNode", ctypes.byref(node), graph, deps if count.value else None, count.value, event)
+    call("hipStreamUpdateCaptureDependencies", stream, ctypes.byref(node), 1, CAPTURE_SET_DEPENDENCIES)
 
 
 def graph_instantiate(graph: int) -> int:
