@@ -323,6 +323,12 @@ int tgm_probe_mfma_fp4(int64_t blocks, int64_t iters, void* sink, void* stream);
 /* tgm_probe_launch launches an empty kernel of ``groups`` x ``threads`` (threads <= 1024): the
  * fixed cost of one launch of that grid with no work, the floor under any kernel's time. */
 int tgm_probe_launch(int64_t groups, int64_t threads, void* sink, void* stream);
+/* tgm_probe_bf16_rounding converts the fp32 bit patterns first .. first + count - 1 (both even,
+ * first + count <= 2^32) to bf16 with the instruction the bf16 epilogues use, in both halves of a
+ * packed pair, and compares each with integer round-to-nearest-even (NaN -> quiet NaN).  ``bad``
+ * (2 x uint32, set by the caller to 0 and 0xFFFFFFFF) receives the mismatch count and the
+ * smallest mismatching pattern; ``bits`` (nullable, count x uint16) the converted patterns. */
+int tgm_probe_bf16_rounding(uint32_t first, int64_t count, void* bits, void* bad, void* stream);
 
 #ifdef __cplusplus
 }

@@ -162,3 +162,33 @@ def test_quantize_mx_device(dev, fmt, xdt):
     codes, e = O.quantize_mx(xt.float().cpu().numpy(), fmt, 32)
     assert np.array_equal(q.scales.view(torch.uint8).cpu().numpy(), e)
     assert np.array_equal(q.data.cpu().numpy(), O.pack_codes(codes, FORMATS[fmt][0]))
+
+
+def test_bf16_rounding_instruction_on_every_fp32_pattern(dev):
+    """The bf16 epilogues round with one v_cvt_pk_bf16_f32 per pair; it must equal integer
+    round-to-nearest-even (NaN -> quiet NaN) on all 2^32 patterns, in both halves of the pair."""
+    from tinygrad_mi355x.runtime import kernels as K
+
+    lib = K.load_library()
+    bad = torch.tensor([0, -1], dtype=torch.int32, device=dev)
+    K.check("tgm_probe_bf16_rounding", lib.tgm_probe_bf16_rounding(0, 1 << 32, None, bad.data_ptr(), K.stream_of(bad)))
+    n, low = bad.cpu().numpy().view(np.uint32)
+    assert n == 0, f"{n} mismatches, first at {low:#010x}"
+
+
+@pytest.mark.parametrize("first", [0x00000000, 0x007F0000, 0x3F7F0000, 0x7F7F0000, 0x7F800000, 0x7FBE0000,
+                                   0x80000000, 0xFF7F0000, 0xFFFE0000])
+def test_bf16_rounding_instruction_against_the_oracle(dev, first):
+    """Zeros and subnormals, the 1.0 boundary, overflow to infinity, infinities, signalling and
+    quiet NaNs of both signs: the written bf16 bits equal the oracle's rounding bit for bit."""
+    from tinygrad_mi355x.runtime import kernels as K
+
+    count = 1 << 17
+    lib = K.load_library()
+    bits = torch.empty(count, dtype=torch.int16, device=dev)
+    bad = torch.tensor([0, -1], dtype=torch.int32, device=dev)
+    K.check("tgm_probe_bf16_rounding", lib.tgm_probe_bf16_rounding(first, count, bits.data_ptr(), bad.data_ptr(),
+                                                                   K.stream_of(bits)))
+    x = np.arange(first, first + count, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    assert np.array_equal(bits_of(bits), O.bf16_round(x))
+    assert bad.cpu().numpy().view(np.uint32).tolist() == [0, 0xFFFFFFFF]

@@ -102,12 +102,25 @@ TGM_HD uint32_t f32_bits(float x) { union { float f; uint32_t u; } v; v.f = x; r
 TGM_HD float bits_f32(uint32_t x) { union { uint32_t u; float f; } v; v.u = x; return v.f; }
 TGM_HD uint64_t f64_bits(double x) { union { double f; uint64_t u; } v; v.f = x; return v.u; }
 
-// fp32 -> bf16 round-to-nearest-even; NaN stays a quiet NaN.
-TGM_HD uint16_t f32_to_bf16(float x) {
+// fp32 -> bf16 round-to-nearest-even in integer arithmetic; NaN stays a quiet NaN (payload's
+// upper bits kept, bit 6 set).
+TGM_HD uint16_t f32_to_bf16_int(float x) {
   const uint32_t u = f32_bits(x);
   if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
   return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
+#if defined(__HIPCC__)
+// On the device the same rounding is one v_cvt_pk_bf16_f32 (gfx950), which rounds a pair at once;
+// tgm_probe_bf16_rounding compares it with f32_to_bf16_int over every fp32 bit pattern.
+typedef __bf16 tgm_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16x2_bits(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, tgm_bf16x2{(__bf16)lo, (__bf16)hi});
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) { return (uint16_t)(bf16x2_bits(x, 0.0f) & 0xFFFFu); }
+__host__ inline uint16_t f32_to_bf16(float x) { return f32_to_bf16_int(x); }
+#else
+static inline uint16_t f32_to_bf16(float x) { return f32_to_bf16_int(x); }
+#endif
 TGM_HD float bf16_to_f32(uint16_t h) { return bits_f32((uint32_t)h << 16); }
 
 // Generic IEEE-style narrowing of a double to a small float format with RNE.

@@ -503,10 +503,14 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4_stream(const uint8_t
           }
         } else {
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const float x = acc[i][j][v];
-            const unsigned short h = cdt == TGM_BF16 ? f32_to_bf16(x) : __builtin_bit_cast(unsigned short, (_Float16)x);
-            ep[(8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * 32 + (lane & 31)] = h;
+          for (int v = 0; v < 16; v += 2) {  // rows v and v + 1 of the lane's column, one rounding instruction
+            const float x0 = acc[i][j][v], x1 = acc[i][j][v + 1];
+            const unsigned h = cdt == TGM_BF16 ? bf16x2_bits(x0, x1)
+                                               : __builtin_bit_cast(unsigned short, (_Float16)x0) |
+                                                     ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)x1) << 16);
+            const int r = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            ep[r * 32 + (lane & 31)] = (unsigned short)h;
+            ep[(r + 1) * 32 + (lane & 31)] = (unsigned short)(h >> 16);
           }
           __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
           __builtin_amdgcn_wave_barrier();
@@ -514,16 +518,14 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4_stream(const uint8_t
 #pragma unroll
           for (int q = 0; q < 2; ++q) {  // lane l: row l / 4 + 16 q, columns 8 (l % 4) .. + 8
             const int r = (lane >> 2) + 16 * q, cc = 8 * (lane & 3);
-            const u32x4 v = *(const u32x4*)(ep + r * 32 + cc);
             const int row = row0 + 32 * i + r, col = col0 + 32 * j + cc;
-            const int64_t o = (int64_t)row * ldc + col;
+            uint16_t* out = (uint16_t*)c + (int64_t)row * ldc + col;
             if (row < M) {
-              if (col + 7 < N && ((uintptr_t)((uint16_t*)c + o) & 15) == 0) {
-                __builtin_nontemporal_store(v, (u32x4*)((uint16_t*)c + o));
-              } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                  if (col + e < N) ((uint16_t*)c)[o + e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+              if (col + 7 < N && ((uintptr_t)out & 15) == 0) {
+                __builtin_nontemporal_store(*(const u32x4*)(ep + r * 32 + cc), (u32x4*)out);
+              } else {  // the ragged edge, element by element from LDS (a rolled loop holds no row in VGPRs)
+#pragma unroll 1
+                for (int e = 0; e < 8 && col + e < N; ++e) out[e] = ep[r * 32 + cc + e];
               }
             }
           }

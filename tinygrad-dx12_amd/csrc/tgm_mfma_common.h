@@ -94,7 +94,7 @@ __device__ __forceinline__ void store_tile32(const f32x16& t, float* ep, int lan
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       if (cdt == TGM_BF16)
-        pk[q] = f32_to_bf16(vals[2 * q]) | ((unsigned)f32_to_bf16(vals[2 * q + 1]) << 16);
+        pk[q] = bf16x2_bits(vals[2 * q], vals[2 * q + 1]);
       else
         pk[q] = __builtin_bit_cast(unsigned short, (_Float16)vals[2 * q]) |
                 ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)vals[2 * q + 1]) << 16);
@@ -135,7 +135,7 @@ __device__ __forceinline__ void store_tile32_swiglu(const f32x16& t, float* ep, 
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       if (cdt == TGM_BF16)
-        pk[q] = f32_to_bf16(y[2 * q]) | ((unsigned)f32_to_bf16(y[2 * q + 1]) << 16);
+        pk[q] = bf16x2_bits(y[2 * q], y[2 * q + 1]);
       else
         pk[q] = __builtin_bit_cast(unsigned short, (_Float16)y[2 * q]) |
                 ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)y[2 * q + 1]) << 16);

@@ -14,6 +14,10 @@
 //    workgroups of 8 waves at 8192^3).
 //  * tgm_probe_launch is an empty kernel: the fixed cost of one launch of a grid, which a
 //    memory-bound kernel of a few microseconds pays in full on top of its transfer time.
+//  * tgm_probe_bf16_rounding checks the hardware fp32 -> bf16 conversion every bf16 epilogue
+//    uses (v_cvt_pk_bf16_f32 via bf16x2_bits) against the integer round-to-nearest-even formula,
+//    in both halves of the packed pair, over any range of fp32 bit patterns (all 2^32 in one
+//    launch), and can write the converted bits out for comparison on the host.
 #include "tgm_mfma_common.h"
 
 namespace tgm {
@@ -86,9 +90,52 @@ __global__ void __launch_bounds__(1024) probe_launch(unsigned* __restrict__ sink
   if ((int)threadIdx.x == never) sink[0] = 1;  // the host passes a thread index past the block
 }
 
+// Inputs first + i for i < count (count even, at most 2^32); each thread takes 64 consecutive
+// patterns as 32 pairs and converts each pair in both orders.  bad[0] counts mismatches, bad[1]
+// receives the smallest mismatching pattern (the host starts them at 0 and 0xFFFFFFFF).
+constexpr int kRoundRun = 64;
+
+__global__ void __launch_bounds__(256) probe_bf16_rounding(uint32_t first, int64_t count,
+                                                           uint16_t* __restrict__ bits, unsigned* __restrict__ bad) {
+  const int64_t base = ((int64_t)blockIdx.x * 256 + threadIdx.x) * kRoundRun;
+  unsigned n = 0, low = 0xFFFFFFFFu;
+  for (int i = 0; i < kRoundRun && base + i < count; i += 2) {
+    const uint32_t u0 = first + (uint32_t)(base + i), u1 = u0 + 1u;
+    const float x0 = bits_f32(u0), x1 = bits_f32(u1);
+    const uint32_t w0 = f32_to_bf16_int(x0), w1 = f32_to_bf16_int(x1);
+    const uint32_t ab = bf16x2_bits(x0, x1), ba = bf16x2_bits(x1, x0);
+    const bool bad0 = (ab & 0xFFFFu) != w0 || (ba >> 16) != w0;
+    const bool bad1 = (ab >> 16) != w1 || (ba & 0xFFFFu) != w1;
+    n += bad0 + bad1;
+    if (bad0) low = min(low, u0);
+    if (bad1) low = min(low, u1);
+    if (bits) {
+      bits[base + i] = (uint16_t)(ab & 0xFFFFu);
+      bits[base + i + 1] = (uint16_t)(ab >> 16);
+    }
+  }
+  if (n) {
+    atomicAdd(&bad[0], n);
+    atomicMin(&bad[1], low);
+  }
+}
+
 }  // namespace tgm
 
 using namespace tgm;
+
+extern "C" int tgm_probe_bf16_rounding(uint32_t first, int64_t count, void* bits, void* bad, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(bad, "null operand");
+  TGM_CHECK_ARG(count > 0 && count % 2 == 0 && count <= (1ll << 32) && first % 2 == 0 &&
+                    (int64_t)first + count <= (1ll << 32),
+                "invalid range (first and count even, first + count <= 2^32)");
+  const int64_t per_block = 256 * kRoundRun;
+  const int64_t grid = (count + per_block - 1) / per_block;
+  hipLaunchKernelGGL(probe_bf16_rounding, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, first, count,
+                     (uint16_t*)bits, (unsigned*)bad);
+  return launch_status("tgm_probe_bf16_rounding");
+}
 
 extern "C" int tgm_probe_launch(int64_t groups, int64_t threads, void* sink, void* stream) {
   clear_error();

@@ -69,6 +69,7 @@ SIGNATURES = {
     "tgm_probe_read": (_P, _I64, _P, _P),
     "tgm_probe_mfma_fp4": (_I64, _I64, _P, _P),
     "tgm_probe_launch": (_I64, _I64, _P, _P),
+    "tgm_probe_bf16_rounding": (ctypes.c_uint32, _I64, _P, _P, _P),
     # decoder-step kernels (include/tgm_decoder.h)
     "tgm_dec_embed": (_P, _I64, _I64, _P, _I64, _P, _P),
     "tgm_dec_add_rmsnorm": (_P, _P, _I64, _I64, _P, ctypes.c_float, _P, _INT, _P),
