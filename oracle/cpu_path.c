@@ -28,34 +28,63 @@ static float decode_one(uint32_t p, int fmt) {
   return (p >> (bits - 1)) & 1u ? -v : v;
 }
 
-/* deq[i] for the flattened [rows, k] array: code * scale in fp32 (dx12.py:101-106). */
+/* deq[i] for the flattened [rows, k] array: code * scale in fp32 (dx12.py:101-106).  Codes decode
+ * through a table of every code's value (decode_one), as a vectorising CPU compiler would; byte-
+ * aligned rows of 4-bit codes take two codes per byte, low nibble first. */
 void oracle_dequant_f32(const uint8_t* data, int64_t nbytes, int fmt, int64_t rows, int64_t k,
                         const float* scales, int64_t block, float* out) {
   const int bits = FMT[fmt][0];
   const int64_t nblk = (k + block - 1) / block;
+  float lut[64];
+  for (uint32_t p = 0; p < (1u << bits); ++p) lut[p] = decode_one(p, fmt);
+  if (bits == 4 && k % 2 == 0 && block % 2 == 0 && nbytes >= rows * k / 2) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+      const uint8_t* src = data + r * k / 2;
+      float* dst = out + r * k;
+      for (int64_t b = 0; b < nblk; ++b) {
+        const float sc = scales ? scales[r * nblk + b] : 1.0f;
+        const int64_t c1 = (b + 1) * block < k ? (b + 1) * block : k;
+        for (int64_t c = b * block; c < c1; c += 2) {
+          const uint8_t v = src[c / 2];
+          dst[c] = lut[v & 15u] * sc;
+          dst[c + 1] = lut[v >> 4] * sc;
+        }
+      }
+    }
+    return;
+  }
 #pragma omp parallel for schedule(static)
   for (int64_t r = 0; r < rows; ++r) {
     for (int64_t c = 0; c < k; ++c) {
       const int64_t i = r * k + c, bit = i * bits, byte = bit >> 3;
       const uint32_t lo = byte < nbytes ? data[byte] : 0u, hi = byte + 1 < nbytes ? data[byte + 1] : 0u;
       const uint32_t p = ((lo | (hi << 8)) >> (bit & 7)) & ((1u << bits) - 1u);
-      float v = decode_one(p, fmt);
+      float v = lut[p];
       if (scales) v = v * scales[r * nblk + c / block];
       out[i] = v;
     }
   }
 }
 
-/* y[m, n] = sum_k x[m, k] * w[n, k], fp32 accumulation in k order. */
+/* y[m, n] = sum_k x[m, k] * w[n, k] in fp32: 16 interleaved partial sums per output (lane l
+ * takes k = l mod 16), added pairwise at the end -- the split-accumulator order a vectorising
+ * CPU compiler gives a long dot product. */
+#define ACC_LANES 16
 void oracle_linear_f32(const float* w, const float* x, int64_t m, int64_t n, int64_t k, float* y) {
 #pragma omp parallel for schedule(static) collapse(2)
   for (int64_t i = 0; i < m; ++i) {
     for (int64_t j = 0; j < n; ++j) {
       const float* wr = w + j * k;
       const float* xr = x + i * k;
-      float acc = 0.f;
-      for (int64_t t = 0; t < k; ++t) acc += xr[t] * wr[t];
-      y[i * n + j] = acc;
+      float acc[ACC_LANES] = {0.f};
+      int64_t t = 0;
+      for (; t + ACC_LANES <= k; t += ACC_LANES)
+        for (int l = 0; l < ACC_LANES; ++l) acc[l] += xr[t + l] * wr[t + l];
+      for (int l = 0; t < k; ++t, ++l) acc[l] += xr[t] * wr[t];
+      for (int h = ACC_LANES / 2; h > 0; h /= 2)
+        for (int l = 0; l < h; ++l) acc[l] += acc[l + h];
+      y[i * n + j] = acc[0];
     }
   }
 }

@@ -218,9 +218,10 @@ def _p(a):
 
 
 @pytest.mark.parametrize("fmt", list(O.FORMATS))
-def test_c_dequant_matches_numpy_oracle(oracle_lib, fmt):
+@pytest.mark.parametrize("k", [70, 71])  # 4-bit codes: the two-per-byte path, then the bit-addressed one
+def test_c_dequant_matches_numpy_oracle(oracle_lib, fmt, k):
     rng = np.random.default_rng(7)
-    n, k, bs = 5, 70, 32
+    n, bs = 5, 32
     bits = O.bits_of(fmt)
     data = rng.integers(0, 256, (n * k * bits + 7) // 8).astype(np.uint8)
     scales = rng.uniform(0.005, 0.02, (n, 3)).astype(np.float16).astype(np.float32)
@@ -231,9 +232,10 @@ def test_c_dequant_matches_numpy_oracle(oracle_lib, fmt):
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
 
 
-def test_c_linear_and_rounding(oracle_lib):
+@pytest.mark.parametrize("k", [5, 300])  # shorter than the 16 partial sums; 18 full rounds and a tail
+def test_c_linear_and_rounding(oracle_lib, k):
     rng = np.random.default_rng(8)
-    m, n, k = 3, 17, 300
+    m, n = 3, 17
     w = rng.standard_normal((n, k)).astype(np.float32)
     x = rng.standard_normal((m, k)).astype(np.float32)
     y = np.empty((m, n), np.float32)
