@@ -470,6 +470,31 @@ def test_graph_replay_matches_eager_decode(dev):
     assert torch.equal(eager2, dec.generate(prompts.flip(1), 5, graph=True))
 
 
+@pytest.mark.parametrize("batch,max_seq", [(1, 160), (3, 700), (8, 160)])
+def test_decode_attention_one_pass_and_position_splits_agree(dev, batch, max_seq):
+    """The decoder's two forms of decode attention (one pass per (token, q head), and positions
+    split over workgroups then merged) give the same greedy tokens and logits within fp32
+    summation-order noise, against the oracle as well; the split form runs through a captured
+    graph, the one-pass form eagerly."""
+    cfg = SMALL
+    w = random_weights(cfg, dev, seed=7 + batch)
+    prompts = np.random.default_rng(batch).integers(0, cfg.vocab, (batch, 9))
+    logits, tokens = [], []
+    for form in ("one", "split"):
+        dec = Decoder(w, cfg, batch, max_seq, 9)
+        dec.splits = 1 if form == "one" else dec.position_splits
+        assert dec.splits > 1 or form == "one"
+        tokens.append(dec.generate(torch.from_numpy(prompts).to(dev), 6, graph=form == "split"))
+        logits.append(np64(dec.logits))
+    assert torch.equal(tokens[0], tokens[1])
+    # relative to the largest logit: an f16 rounding of the attention output may fall either way
+    assert O.max_rel_err(logits[0], logits[1], 1.0) <= 2e-3
+    oracle = oracle_for(w, cfg, batch, max_seq)
+    seq = np.concatenate([prompts, tokens[0].cpu().numpy()[:, :-1]], axis=1)
+    ref = oracle.forward(seq, 0)[:, -1]
+    assert O.max_rel_err(logits[0], ref, 1.0) <= 2e-3
+
+
 @pytest.mark.parametrize("batch", [1, 8])
 def test_decoder_full_size_prefill_and_graph_decode(dev, batch):
     """8 layers, hidden 4096, 32/8 heads, SwiGLU 14336, vocab 32000: 512-token prefill at batch

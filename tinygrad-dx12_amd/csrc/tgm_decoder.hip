@@ -499,6 +499,193 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
   }
 }
 
+// One pass, no partials: grid (rows, kv_heads * hs), 1024 threads (16 waves).  Workgroup (r, y)
+// takes kv head j = y % HK and the GW q heads j * G + (y / HK) * GW + [0, GW) of it (G = H / HK,
+// GW = G / hs).  Workgroup ids r + rows (s HK + j) put every sub-group of kv head j on the same
+// XCD (ids are dealt to the 8 XCDs round robin), and a row's kv heads on one XCD when rows is a
+// multiple of 8, so the sub-groups' re-reads of a kv head hit that XCD's L2.  Wave w takes the
+// chunks of 16 positions w, w + 16, ... of [0, len):
+//   lanes 4 i .. 4 i + 3 hold a quarter of head_dim of position c0 + i's k each; their dot
+//   products with the GW scaled q's (read from LDS per chunk) are combined by two lane swaps;
+//   the wave folds the chunk into its own running max / sum per q head (online softmax);
+//   lane l accumulates dims (2 l, 2 l + 1) of p . v, each probability read from the lane that
+//   holds it.
+// The first chunk's loads are issued before q is staged; later chunks' k loads as soon as the
+// previous chunk's scores are done and their v loads as soon as its p . v is, so a wave's next
+// chunk is in flight while it computes.  At the end the 16 waves' (o, m, l) meet in LDS and are
+// merged with weights exp(m_w - M).  Loads use positions clamped into the valid range (their
+// probabilities are zero).  With ``own`` the kernel does tgm_dec_rope_kv's work for the token as
+// dec_attention does: sub-group 0 stores the rotated k and v, and every workgroup takes the
+// token's own position from LDS.
+constexpr int kOneWaves = 16, kOneChunk = 16;
+
+template <int GW, int HD>
+__global__ void __launch_bounds__(kOneWaves * 64) dec_attention_one(const float* __restrict__ qkv, int T, int H, int HK,
+                                                                    const int32_t* __restrict__ pos,
+                                                                    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                                    int max_seq, float scale, int own, double log2_base,
+                                                                    void* __restrict__ out, int odt) {
+  constexpr int NP = HD / 2;  // rotation pairs; lanes [0, NP) hold two dims of v each
+  constexpr int QD = HD / 4;  // dims of k per lane (four lanes per position)
+  constexpr int KL = QD / 8;  // 16-byte k loads per lane and chunk
+  const int r = blockIdx.x, y = blockIdx.y, j = y % HK, sub = y / HK;
+  const int hq0 = j * (H / HK) + sub * GW;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = r / T, t = r % T;
+  const int p = pos[b] + t;
+  const int len = p + 1 < max_seq ? p + 1 : max_seq;
+  const int64_t ld = (int64_t)(H + 2 * HK) * HD;
+  const int64_t kvbase = ((int64_t)b * HK + j) * max_seq;
+  __shared__ __attribute__((aligned(16))) float qs[GW][HD];
+  __shared__ __attribute__((aligned(16))) uint16_t kp[HD], vp[HD];  // the token's own k, v (bf16 bits)
+  __shared__ float mw[kOneWaves][GW], lw[kOneWaves][GW];
+  __shared__ float ow[kOneWaves][GW][HD];
+  const float* qrow = qkv + (int64_t)r * ld + (int64_t)hq0 * HD;
+  const int pi = lane >> 2, qd = lane & 3;
+  dec_u32x4 kreg[KL];
+  unsigned vreg[kOneChunk];
+  auto load_k = [&](int c0) __attribute__((always_inline)) {
+    const int tk = c0 + pi < len ? c0 + pi : len - 1;
+    const uint16_t* kr = kc + (kvbase + tk) * HD + qd * QD;
+#pragma unroll
+    for (int e = 0; e < KL; ++e) kreg[e] = *(const dec_u32x4*)(kr + 8 * e);
+  };
+  auto load_v = [&](int c0) __attribute__((always_inline)) {
+    const int dl = lane < NP ? lane : 0;  // lanes past NP read (and ignore) dims 0, 1
+#pragma unroll
+    for (int i = 0; i < kOneChunk; ++i) {
+      const int tt = c0 + i < len ? c0 + i : len - 1;
+      vreg[i] = *(const unsigned*)(vc + (kvbase + tt) * HD + 2 * dl);
+    }
+  };
+  const int c_first = wave * kOneChunk;
+  constexpr int c_step = kOneWaves * kOneChunk;
+  if (c_first < len) {
+    load_k(c_first);
+    load_v(c_first);
+  }
+  if (own) {
+    for (int i = tid; i < GW * NP; i += kOneWaves * 64) {
+      const int g = i / NP, e = i % NP;
+      float y1, y2;
+      rope_pair(qrow[g * HD + e], qrow[g * HD + e + NP], p, e, HD, log2_base, y1, y2);
+      qs[g][e] = y1 * scale;
+      qs[g][e + NP] = y2 * scale;
+    }
+    if (tid < NP) {
+      const float* kx = qkv + (int64_t)r * ld + (int64_t)(H + j) * HD;
+      const float* vx = qkv + (int64_t)r * ld + (int64_t)(H + HK + j) * HD;
+      float y1, y2;
+      rope_pair(kx[tid], kx[tid + NP], p, tid, HD, log2_base, y1, y2);
+      const uint16_t k1 = f32_to_bf16(y1), k2 = f32_to_bf16(y2);
+      const uint16_t v1 = f32_to_bf16(vx[tid]), v2 = f32_to_bf16(vx[tid + NP]);
+      if (sub == 0 && p < max_seq) {  // one sub-group stores; every workgroup uses the values from LDS
+        const int64_t o = (kvbase + p) * HD;
+        kc[o + tid] = k1;
+        kc[o + tid + NP] = k2;
+        vc[o + tid] = v1;
+        vc[o + tid + NP] = v2;
+      }
+      kp[tid] = k1;
+      kp[tid + NP] = k2;
+      vp[tid] = v1;
+      vp[tid + NP] = v2;
+    }
+  } else {
+    for (int i = tid; i < GW * HD; i += kOneWaves * 64) qs[i / HD][i % HD] = qrow[i] * scale;
+  }
+  __syncthreads();
+  float m[GW], l[GW], oa[GW][2];
+#pragma unroll
+  for (int g = 0; g < GW; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+    oa[g][0] = oa[g][1] = 0.f;
+  }
+  for (int c0 = c_first; c0 < len; c0 += c_step) {
+    const int cn = c0 + c_step;  // this wave's next chunk
+    if (own && c0 + pi == p)  // the token's own position (the loads may predate its store): from LDS
+#pragma unroll
+      for (int e = 0; e < KL; ++e) kreg[e] = *(const dec_u32x4*)(kp + qd * QD + 8 * e);
+    // q is re-read from LDS for every chunk: an opaque zero offset keeps the compiler from holding
+    // the lane's GW * QD q values in registers across the loop
+    int zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    const float* qb = &qs[0][0] + qd * QD + zero;
+    float s[GW];
+#pragma unroll
+    for (int g = 0; g < GW; ++g) s[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < KL; ++e) {
+      const dec_u32x4 kv = kreg[e];
+#pragma unroll
+      for (int g = 0; g < GW; ++g) {
+        const dec_f32x4 qa = *(const dec_f32x4*)(qb + g * HD + 8 * e), qb4 = *(const dec_f32x4*)(qb + g * HD + 8 * e + 4);
+        s[g] += qa[0] * lo_bf16(kv[0]) + qa[1] * hi_bf16(kv[0]) + qa[2] * lo_bf16(kv[1]) + qa[3] * hi_bf16(kv[1]) +
+                qb4[0] * lo_bf16(kv[2]) + qb4[1] * hi_bf16(kv[2]) + qb4[2] * lo_bf16(kv[3]) + qb4[3] * hi_bf16(kv[3]);
+      }
+    }
+    if (cn < len) load_k(cn);
+    const bool valid = c0 + pi < len;
+    float pe[GW];
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+      float sv = s[g] + __shfl_xor(s[g], 1, 64);
+      sv = valid ? sv + __shfl_xor(sv, 2, 64) : -INFINITY;
+      const float m_new = fmaxf(m[g], wave_max(sv));  // position c0 is valid
+      pe[g] = valid ? expf(sv - m_new) : 0.f;
+      const float alpha = m[g] == -INFINITY ? 0.f : expf(m[g] - m_new);
+      l[g] = l[g] * alpha + wave_sum(qd == 0 ? pe[g] : 0.f);
+      m[g] = m_new;
+      oa[g][0] *= alpha;
+      oa[g][1] *= alpha;
+    }
+    if (own && lane < NP) {
+      const unsigned own_v = *(const unsigned*)(vp + 2 * lane);
+#pragma unroll
+      for (int i = 0; i < kOneChunk; ++i) vreg[i] = c0 + i == p ? own_v : vreg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kOneChunk; ++i) {
+      const float v0 = lo_bf16(vreg[i]), v1 = hi_bf16(vreg[i]);
+#pragma unroll
+      for (int g = 0; g < GW; ++g) {
+        const float pg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pe[g]), 4 * i));
+        oa[g][0] += pg * v0;
+        oa[g][1] += pg * v1;
+      }
+    }
+    if (cn < len) load_v(cn);
+  }
+  if (lane == 0)
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+      mw[wave][g] = m[g];
+      lw[wave][g] = l[g];
+    }
+  if (lane < NP)
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+      ow[wave][g][2 * lane] = oa[g][0];
+      ow[wave][g][2 * lane + 1] = oa[g][1];
+    }
+  __syncthreads();
+  for (int i = tid; i < GW * HD; i += kOneWaves * 64) {
+    const int g = i / HD, d = i % HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kOneWaves; ++w) M = fmaxf(M, mw[w][g]);
+    float L = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kOneWaves; ++w) {
+      const float wgt = mw[w][g] == -INFINITY ? 0.f : expf(mw[w][g] - M);
+      L += lw[w][g] * wgt;
+      o += ow[w][g][d] * wgt;
+    }
+    store_from_f32(out, odt, (int64_t)r * H * HD + (int64_t)(hq0 + g) * HD + d, L > 0.f ? o / L : 0.f);
+  }
+}
+
 // Grid (rows, heads), head_dim threads: combine the splits' (o, m, l) partials.  The (m, l) of
 // every split go to LDS and become merge weights exp(m_s - M); each thread issues the loads of
 // its S partial sums at once.  (The kernel boundary publishes the partials; merging in the last
@@ -764,6 +951,23 @@ extern "C" int tgm_dec_attention(const float* qkv, int64_t rows, int64_t seq_row
   if (G != 1 && G != 2 && G != 4 && G != 8) TGM_UNSUPPORTED("tgm_dec_attention: heads / kv_heads must be 1, 2, 4 or 8");
   if ((uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 4) TGM_UNSUPPORTED("tgm_dec_attention: caches must be 16-byte aligned");
   if (rows == 0) return TGM_OK;
+  const hipStream_t st = (hipStream_t)stream;
+  const int own = rope_base > 0.0;
+  const float scale = (float)(1.0 / sqrt((double)head_dim));
+  if (splits == 1 && rows * heads <= stream_cu_count(st)) {
+    // few (token, q head) pairs: one workgroup of 16 waves per pair, one pass over the cache (the
+    // grid stays within one round of CUs, and each workgroup's q head fits the wave's registers)
+    const dim3 g1((unsigned)rows, (unsigned)heads);
+    if (head_dim == 64)
+      hipLaunchKernelGGL((dec_attention_one<1, 64>), g1, dim3(kOneWaves * 64), 0, st, qkv, (int)seq_rows, (int)heads,
+                         (int)kv_heads, pos, (uint16_t*)k_cache, (uint16_t*)v_cache, (int)max_seq, scale, own,
+                         own ? log2(rope_base) : 0.0, out, out_dtype);
+    else
+      hipLaunchKernelGGL((dec_attention_one<1, 128>), g1, dim3(kOneWaves * 64), 0, st, qkv, (int)seq_rows, (int)heads,
+                         (int)kv_heads, pos, (uint16_t*)k_cache, (uint16_t*)v_cache, (int)max_seq, scale, own,
+                         own ? log2(rope_base) : 0.0, out, out_dtype);
+    return launch_status("tgm_dec_attention");
+  }
   const int cps = (int)((chunks + splits - 1) / splits);
   // few (token, kv head, split) workgroups leave most CUs idle: then the q heads of a kv head
   // are spread over hs workgroups (each re-reads the kv head's chunk, mostly from cache)
@@ -771,10 +975,7 @@ extern "C" int tgm_dec_attention(const float* qkv, int64_t rows, int64_t seq_row
   while (hs < G && rows * kv_heads * splits * hs * 2 <= 512) hs *= 2;
   const int64_t Gw = G / hs;
   const dim3 grid((unsigned)rows, (unsigned)(kv_heads * hs), (unsigned)splits);
-  const hipStream_t st = (hipStream_t)stream;
   float* part = splits > 1 ? workspace : nullptr;
-  const int own = rope_base > 0.0;
-  const float scale = (float)(1.0 / sqrt((double)head_dim));
 #define TGM_ATT(GG, HDD)                                                                                            \
   if (Gw == GG && head_dim == HDD)                                                                                  \
     launch_attention<GG, HDD>(grid, st, qkv, (int)seq_rows, (int)heads, (int)kv_heads, pos, k_cache, v_cache,        \

@@ -35,6 +35,15 @@ from tinygrad_mi355x.runtime.graph import StreamGraph
 
 F16, BF16, F32 = K.DTYPE_IDS[torch.float16], K.DTYPE_IDS[torch.bfloat16], K.DTYPE_IDS[torch.float32]
 GEMV_MAX_ROWS = 16
+# Decode attention takes one of two forms (tgm_dec_attention):
+#   one pass (splits = 1): a 16-wave workgroup per (token, q head) streams its kv head's cache,
+#     about 8-9 ns per position per workgroup on top of ~5 us (one CU per q head bounds it);
+#   position splits: the positions spread over workgroups and a second launch merges them,
+#     ~8 us at batch 1 almost independent of the length (~9-11 us at batch 8, 100-600 positions).
+# One pass is taken when its grid fits one round of CUs and either fills at least half of them or
+# the mean decode length is short; never beyond ONE_PASS_MAX_LEN.
+ONE_PASS_SHORT_LEN = 384
+ONE_PASS_MAX_LEN = 1024
 
 
 @dataclass(frozen=True)
@@ -233,7 +242,14 @@ class Decoder:
         cache = (cfg.layers, batch, cfg.kv_heads, max_seq, cfg.head_dim)
         self.k_cache = torch.zeros(cache, dtype=torch.bfloat16, device=dev)
         self.v_cache = torch.zeros(cache, dtype=torch.bfloat16, device=dev)
-        self.splits = min(max(1, math.ceil(max_seq / 64)), 32)
+        # decode attention: one pass or position splits (ONE_PASS_SHORT_LEN)
+        self.position_splits = min(max(1, math.ceil(max_seq / 64)), 32)
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        mean_len = (max_prompt + max_seq) / 2
+        grid = batch * cfg.heads
+        one_pass = (grid <= cus and mean_len <= ONE_PASS_MAX_LEN
+                    and (2 * grid >= cus or mean_len <= ONE_PASS_SHORT_LEN))
+        self.splits = 1 if one_pass else self.position_splits
         self.fuse_rope = True
         # attention of prompts of several tokens:
         #   "fused": one flash-attention kernel on MFMA (scores stay on chip);
@@ -254,7 +270,7 @@ class Decoder:
                           and all(_norm_gemv_fits(L.wqkv, False) and _norm_gemv_fits(L.w_gate_up, True)
                                   for L in weights.layers))
         self.h_alt = torch.empty((batch, d), **f32) if self.fuse_norm else None
-        ws = K.load_library().tgm_dec_attention_workspace(batch, cfg.heads, cfg.head_dim, self.splits)
+        ws = K.load_library().tgm_dec_attention_workspace(batch, cfg.heads, cfg.head_dim, self.position_splits)
         self.workspace = torch.empty(max(ws // 4, 1), **f32)
         self.workspace_bytes = ws
         self.tokens = torch.zeros(rows, dtype=torch.int32, device=dev)
