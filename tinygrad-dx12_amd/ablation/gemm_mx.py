@@ -1,0 +1,128 @@
+"""Ablations of the FP4 x FP4 GEMM (csrc/tgm_gemm_mx.hip): where its time goes.
+
+Each variant is the committed kernel source with one literal edit, built into a library of its
+own under _build/ablation/<variant>/ (linked with the other objects of the last build_library()
+run) and timed by bench.py in a child process pointed at that library (MI355X_KERNEL_LIB), all
+in one call so that every variant runs on the same GPU:
+
+    python tinygrad-dx12_amd/ablation/gemm_mx.py build          # here (hipcc cross-compiles)
+    python tinygrad-dx12_amd/ablation/gemm_mx.py run [--rounds 2] [--steps 50]   # on the GPU
+
+Variants that remove work compute wrong products by design: they exist to be timed.  No edit
+changes an address, a loop bound or a wait count, so every variant reads and writes exactly
+the memory the committed kernel does and every wait ends.
+
+    baseline                the committed kernel
+    l2_hot_panels           every K step of a tile loads the tile's first two steps' panels
+                            again (a working set that stays in L2): the cost of global-load
+                            latency and L2 misses
+    no_step_barrier         the persistent kernel's barrier between steps removed (LDS races)
+    quarter_fragment_reads  three of four substeps skip their LDS fragment reads and reuse
+                            registers: the cost of the LDS operand traffic
+    launch_per_tile         the launch-per-tile kernel instead of the persistent one
+    waves_2x2               launch per tile, 4 waves of 128 x 128 (one wave per SIMD)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parents[1]
+ROOT = PKG.parent
+sys.path.insert(0, str(PKG))
+
+from tinygrad_mi355x.build import ARCH, BUILD, FLAGS, HIPCC, LIB, build_library  # noqa: E402
+
+SRC = PKG / "csrc" / "tgm_gemm_mx.hip"
+OUT = BUILD / "ablation"
+WORKLOADS = ("fp4_gemm_8192", "fp4_gemm_4096x14336x4096")
+
+STREAM = "gemm_mx_fp4_stream(const uint8_t"
+PERSISTENT = "if (k % (kBK * kBatchSteps) == 0 && cus >= 8 && tiles >= 8) {"
+# (anchor that must precede the edit, old text, new text)
+VARIANTS: dict[str, list[tuple[str, str, str]]] = {
+    "baseline": [],
+    "l2_hot_panels": [(STREAM, "(unsigned)at.m0 * kb + (unsigned)(at.st * kRowBytes)",
+                       "(unsigned)at.m0 * kb + (unsigned)((at.st & 1) * kRowBytes)"),
+                      (STREAM, "(unsigned)at.n0 * kb + (unsigned)(at.st * kRowBytes)",
+                       "(unsigned)at.n0 * kb + (unsigned)((at.st & 1) * kRowBytes)")],
+    "no_step_barrier": [(STREAM, "    wait_lds_dma();\n    __syncthreads();\n    substep(f1, 3,",
+                         "    wait_lds_dma();\n    __builtin_amdgcn_sched_barrier(0);\n    substep(f1, 3,")],
+    "quarter_fragment_reads": [(STREAM, "else if (!scales) read_item(fn, rbuf, ru, it);",
+                                "else if (!scales) { if (ru == 0) read_item(fn, rbuf, ru, it); }")],
+    "launch_per_tile": [("extern \"C\"", PERSISTENT, "if (false) {")],
+    "waves_2x2": [("extern \"C\"", PERSISTENT, "if (false) {"),
+                  ("extern \"C\"", "hipLaunchKernelGGL((gemm_mx_fp4<kWavesM, kWavesN>), dim3((unsigned)tiles), "
+                                   "dim3(kWavesM * kWavesN * 64)",
+                   "hipLaunchKernelGGL((gemm_mx_fp4<2, 2>), dim3((unsigned)tiles), dim3(256)")],
+}
+
+
+def patched(name: str) -> str:
+    src = SRC.read_text()
+    for anchor, old, new in VARIANTS[name]:
+        start = src.index(anchor)
+        at = src.find(old, start)
+        if at < 0:
+            raise SystemExit(f"{name}: {old!r} not found after {anchor!r}: the kernel changed, update the ablation")
+        src = src[:at] + new + src[at + len(old):]
+    return src
+
+
+def build() -> None:
+    build_library()
+    others = [p for p in sorted(BUILD.glob("*.o")) if p.name != "tgm_gemm_mx.o"]
+    for name in VARIANTS:
+        d = OUT / name
+        d.mkdir(parents=True, exist_ok=True)
+        src = d / "tgm_gemm_mx.hip"
+        src.write_text(patched(name))
+        obj, lib = d / "tgm_gemm_mx.o", d / LIB.name
+        for cmd in ([HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)],
+                    [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, others), str(obj), "-o", str(lib)]):
+            proc = subprocess.run(cmd, capture_output=True, text=True)
+            if proc.returncode != 0:
+                raise SystemExit(f"{name}: {proc.stderr}")
+        print(f"built {lib}", flush=True)
+
+
+def time_variant(name: str, workload: str, steps: int) -> float:
+    env = dict(os.environ, MI355X_KERNEL_LIB=str(OUT / name / LIB.name))
+    cmd = [sys.executable, str(ROOT / "bench.py"), "--only", workload, "--steps", str(steps), "--warmup", "10",
+           "--no-cpu-baseline"]
+    proc = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=240)
+    if proc.returncode != 0:
+        raise SystemExit(f"{name} {workload}: {proc.stderr[-2000:]}")
+    return json.loads(proc.stdout.strip().splitlines()[-1])[workload]["ms"] * 1e3
+
+
+def run(rounds: int, steps: int) -> None:
+    times: dict[tuple[str, str], list[float]] = {}
+    for r in range(rounds):
+        for name in VARIANTS:
+            for w in WORKLOADS:
+                us = time_variant(name, w, steps)
+                times.setdefault((name, w), []).append(us)
+                print(f"round {r} {name} {w}: {us:.1f} us", flush=True)
+    print("\n| variant | " + " | ".join(WORKLOADS) + " |")
+    print("| --- |" + " --- |" * len(WORKLOADS))
+    for name in VARIANTS:
+        cells = []
+        for w in WORKLOADS:
+            med, base = statistics.median(times[(name, w)]), statistics.median(times[("baseline", w)])
+            cells.append(f"{med:.1f} us ({med / base:.3f})")
+        print(f"| {name} | " + " | ".join(cells) + " |")
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("action", choices=("build", "run"))
+    ap.add_argument("--rounds", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=50)
+    a = ap.parse_args()
+    build() if a.action == "build" else run(a.rounds, a.steps)
