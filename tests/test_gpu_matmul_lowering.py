@@ -151,3 +151,50 @@ def test_scaled_fp8_product_is_lowered(dev, k):
     ref = a.float().cpu().numpy().astype(np.float64) @ w.float().cpu().numpy().astype(np.float64).T * 0.375
     assert out.dtype is torch.float32
     assert O.max_rel_err(out.cpu().numpy(), ref) <= 1e-2
+
+
+# Products with at least one round of 256 x 256 tiles (256 CUs) and K a multiple of 128 run the
+# persistent dense kernel (gemm_dense_stream): one workgroup per CU walking its tiles.
+STREAM_SHAPES = [(4096, 4096, 256), (4000, 4200, 384), (8192, 4352, 128)]
+
+
+@pytest.mark.parametrize("mnk", STREAM_SHAPES)
+def test_dense_stream_one_hot_is_exact(dev, mnk):
+    """One-hot rows of A pick rows of B exactly in every output tile of the persistent kernel
+    (ragged edges, several tiles per workgroup, bf16 and f32 outputs): operand layout, swizzle,
+    K order, tile walk and epilogue line up."""
+    from tinygrad_mi355x.renderer.matrix import GEMM_DENSE_STREAM, dense_kernel
+
+    m, n, k = mnk
+    assert dense_kernel(m, n, k) is GEMM_DENSE_STREAM
+    rng = np.random.default_rng(m + k)
+    b = torch.from_numpy(rng.standard_normal((n, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    cols = torch.from_numpy(rng.integers(0, k, m)).to(dev)
+    a = torch.zeros((m, k), dtype=torch.bfloat16, device=dev)
+    a[torch.arange(m, device=dev), cols] = 1.0
+    want = b.t()[cols]  # [m, n]: row i of C is column cols[i] of B^T
+    for out in (torch.float32, torch.bfloat16):
+        c = linalg.dense_matmul_nt(a, b, out)
+        assert torch.equal(c, want.to(out)), out
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mnk", STREAM_SHAPES[:2])
+def test_dense_stream_parity(dev, dtype, mnk):
+    """Random operands against the fp64 product (bf16 / f16 products are exact in fp32; only the
+    summation order differs), A as a strided view (row stride > K), three output dtypes."""
+    m, n, k = mnk
+    rng = np.random.default_rng(n + k)
+    a_full = torch.from_numpy(rng.standard_normal((m, k + 64)).astype(np.float32)).to(dev).to(dtype)
+    a = a_full[:, 32:32 + k]
+    b = torch.from_numpy(rng.standard_normal((n, k)).astype(np.float32)).to(dev).to(dtype)
+    rows = torch.from_numpy(rng.choice(m, 256, replace=False)).to(dev)
+    a_rows, b64 = f64(a[rows]), f64(b)
+    ref = a_rows @ b64.T
+    bound = k * 2.0 ** -23 * (np.abs(a_rows) @ np.abs(b64).T)  # fp32 sums of exact products
+    for out in (torch.float32, torch.bfloat16, torch.float16):
+        c = linalg.dense_matmul_nt(a, b, out)
+        got = f64(c[rows])
+        assert O.max_rel_err(got, ref) <= 1e-2, out
+        if out is torch.float32:
+            assert bool((np.abs(got - ref) <= bound).all())

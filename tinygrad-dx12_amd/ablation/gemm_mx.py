@@ -19,6 +19,15 @@ the memory the committed kernel does and every wait ends.
     no_step_barrier         the persistent kernel's barrier between steps removed (LDS races)
     quarter_fragment_reads  three of four substeps skip their LDS fragment reads and reuse
                             registers: the cost of the LDS operand traffic
+    reads_in_use_order      each substep's fragment reads issued in the order the next
+                            substep's MFMAs consume them (A0, B0 .. B3, A1)
+    front_loaded_reads      fragment and scale reads spread over the first half of a substep's
+                            MFMAs, the panel loads over the second half
+    front_loaded_in_use_order   both
+    no_c_stores             the epilogue's C stores left out (no output): the cost of the
+                            tile switch's store drain (every step waits on vmcnt(0), which
+                            counts stores as well as loads)
+    plain_c_stores          ordinary instead of non-temporal C stores
     launch_per_tile         the launch-per-tile kernel instead of the persistent one
     waves_2x2               launch per tile, 4 waves of 128 x 128 (one wave per SIMD)
 """
@@ -44,6 +53,14 @@ WORKLOADS = ("fp4_gemm_8192", "fp4_gemm_4096x14336x4096")
 
 STREAM = "gemm_mx_fp4_stream(const uint8_t"
 PERSISTENT = "if (k % (kBK * kBatchSteps) == 0 && cus >= 8 && tiles >= 8) {"
+# fragment reads in the order the next substep's MFMAs consume them: A0, B0 .. B3, A1 (FA = 2)
+READ_IN_USE_ORDER = "else if (!scales) read_item(fn, rbuf, ru, it == 0 ? 0 : it == FA + FB - 1 ? 1 : it + 1);"
+READ_IN_USE_ORDER_S = ("else read_item(fn, rbuf, ru, it - (FA + FB) == 0 ? 0 : it - (FA + FB) == FA + FB - 1 ? 1 "
+                       ": it - (FA + FB) + 1);")
+# fragment and scale reads spread over the first half of a substep's MFMAs, panel loads over the second
+FRONT_LOADED = ("(it < nr ? it * (FA * FB / 2) / nr : FA * FB / 2 + (it - nr) * (FA * FB / 2) / (ni - nr + 1)) "
+                "== idx")
+C_STORE = "__builtin_nontemporal_store(*(const u32x4*)(ep + r * 32 + cc), (u32x4*)out);"
 # (anchor that must precede the edit, old text, new text)
 VARIANTS: dict[str, list[tuple[str, str, str]]] = {
     "baseline": [],
@@ -55,6 +72,14 @@ VARIANTS: dict[str, list[tuple[str, str, str]]] = {
                          "    wait_lds_dma();\n    __builtin_amdgcn_sched_barrier(0);\n    substep(f1, 3,")],
     "quarter_fragment_reads": [(STREAM, "else if (!scales) read_item(fn, rbuf, ru, it);",
                                 "else if (!scales) { if (ru == 0) read_item(fn, rbuf, ru, it); }")],
+    "reads_in_use_order": [(STREAM, "else if (!scales) read_item(fn, rbuf, ru, it);", READ_IN_USE_ORDER),
+                           (STREAM, "else read_item(fn, rbuf, ru, it - (FA + FB));", READ_IN_USE_ORDER_S)],
+    "front_loaded_reads": [(STREAM, "it * FA * FB / ni == idx", FRONT_LOADED)],
+    "front_loaded_in_use_order": [(STREAM, "it * FA * FB / ni == idx", FRONT_LOADED),
+                                  (STREAM, "else if (!scales) read_item(fn, rbuf, ru, it);", READ_IN_USE_ORDER),
+                                  (STREAM, "else read_item(fn, rbuf, ru, it - (FA + FB));", READ_IN_USE_ORDER_S)],
+    "no_c_stores": [(STREAM, C_STORE, "(void)out;")],
+    "plain_c_stores": [(STREAM, C_STORE, "*(u32x4*)out = *(const u32x4*)(ep + r * 32 + cc);")],
     "launch_per_tile": [("extern \"C\"", PERSISTENT, "if (false) {")],
     "waves_2x2": [("extern \"C\"", PERSISTENT, "if (false) {"),
                   ("extern \"C\"", "hipLaunchKernelGGL((gemm_mx_fp4<kWavesM, kWavesN>), dim3((unsigned)tiles), "
@@ -74,10 +99,10 @@ def patched(name: str) -> str:
     return src
 
 
-def build() -> None:
+def build(names: list[str]) -> None:
     build_library()
     others = [p for p in sorted(BUILD.glob("*.o")) if p.name != "tgm_gemm_mx.o"]
-    for name in VARIANTS:
+    for name in names:
         d = OUT / name
         d.mkdir(parents=True, exist_ok=True)
         src = d / "tgm_gemm_mx.hip"
@@ -101,17 +126,17 @@ def time_variant(name: str, workload: str, steps: int) -> float:
     return json.loads(proc.stdout.strip().splitlines()[-1])[workload]["ms"] * 1e3
 
 
-def run(rounds: int, steps: int) -> None:
+def run(names: list[str], rounds: int, steps: int) -> None:
     times: dict[tuple[str, str], list[float]] = {}
     for r in range(rounds):
-        for name in VARIANTS:
+        for name in names:
             for w in WORKLOADS:
                 us = time_variant(name, w, steps)
                 times.setdefault((name, w), []).append(us)
                 print(f"round {r} {name} {w}: {us:.1f} us", flush=True)
     print("\n| variant | " + " | ".join(WORKLOADS) + " |")
     print("| --- |" + " --- |" * len(WORKLOADS))
-    for name in VARIANTS:
+    for name in names:
         cells = []
         for w in WORKLOADS:
             med, base = statistics.median(times[(name, w)]), statistics.median(times[("baseline", w)])
@@ -124,5 +149,8 @@ if __name__ == "__main__":
     ap.add_argument("action", choices=("build", "run"))
     ap.add_argument("--rounds", type=int, default=2)
     ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--variants", nargs="+", choices=sorted(VARIANTS), default=list(VARIANTS),
+                    help="variants to build or time (baseline is always included)")
     a = ap.parse_args()
-    build() if a.action == "build" else run(a.rounds, a.steps)
+    names = ["baseline"] + [v for v in a.variants if v != "baseline"]
+    build(names) if a.action == "build" else run(names, a.rounds, a.steps)

@@ -174,6 +174,246 @@ __global__ void __launch_bounds__(512) gemm_dense(const uint8_t* __restrict__ a,
       store_tile32(acc[i][j], ep, lane, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, M, N, c, cdt, ldc);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Persistent form for one large bf16 / f16 product (K a multiple of 128, at least one round of
+// 256 x 256 tiles): the FP4 GEMM's persistent schedule (tgm_gemm_mx.hip, gemm_mx_fp4_stream) on
+// the 16-bit MFMA.  A K step of 64 elements is 128 bytes of a row -- the FP4 kernel's step width
+// -- so panels, swizzle, load pieces and fragment reads are laid out exactly as there:
+//
+//  * one workgroup per CU (G, a multiple of 8, so a workgroup keeps to its XCD's tile range)
+//    walks tiles blockIdx.x, blockIdx.x + G, ... of 256 x 256 as one stream of K steps;
+//  * eight waves in 4 x 2, each 64 x 128 = 2 x 4 MFMA tiles of v_mfma_f32_32x32x16_{bf16,f16}
+//    (128 fp32 accumulators per lane, two waves per SIMD): 0.75 KB of LDS fragment reads per
+//    MFMA, against 1 KB for gemm_dense's 64 x 64 wave tiles;
+//  * a step's A and B panels (256 rows x 128 B each) go straight from global memory into one of
+//    two 64 KB LDS buffers (buffer_load ... lds), 16-byte columns XOR-swizzled by (row / 2) % 8;
+//    the loads of step s + 2 are issued during step s + 1's MFMAs, half in its first substep and
+//    half in its last, across tile boundaries (the next tile's first steps load during the
+//    current tile's last);
+//  * substep u of a step takes K [16 u + 8 h, + 8) for lane half h (16-byte column 2 u + h); after
+//    every MFMA the wave issues an even share of the next substep's fragment reads and of the
+//    panel loads, fenced by scheduling barriers;
+//  * at a tile's end each wave rounds its 32 x 32 tiles to 16 bits through its own 2 KB LDS slice
+//    and writes 16-byte row segments with non-temporal stores (fp32 output goes out per element).
+constexpr int kSB = 256;                 // output tile edge
+constexpr int kSRow = 128;               // bytes per panel row and step
+constexpr int kSPanel = kSB * kSRow;     // 32 KB
+constexpr int kSBuffer = 2 * kSPanel;    // A and B panels of one step
+constexpr int kSEpi = 8 * 2048;          // one 2 KB epilogue slice per wave
+constexpr int kSLds = 2 * kSBuffer + kSEpi;
+
+template <int T>
+__global__ void __launch_bounds__(512) gemm_dense_stream(const uint8_t* __restrict__ a, unsigned lda_bytes,
+                                                         const uint8_t* __restrict__ b, unsigned ldb_bytes, int M,
+                                                         int N, int K, void* __restrict__ c, int cdt, int64_t ldc) {
+  using V = typename std::conditional<T == TGM_F16, dn_f16x8, dn_bf16x8>::type;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kSLds];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  constexpr int WN = 2, FA = 2, FB = 4;  // 4 x 2 waves of 64 x 128
+  constexpr int NI = 4, NP = 2 * NI;     // panel loads per wave, operand and step; pieces per step
+  const int wm = wave / WN, wn = wave % WN;
+  const int tiles_m = (M + kSB - 1) / kSB, tiles_n = (N + kSB - 1) / kSB;
+  const int ntiles = tiles_m * tiles_n;
+  const int G = gridDim.x;
+  const int my_tiles = (ntiles - (int)blockIdx.x + G - 1) / G;  // >= 1 (the host launches G <= ntiles)
+  const int nsteps = K / 64;                                     // even (K % 128 == 0)
+  const int total = my_tiles * nsteps;
+
+  const i32x4v ra = buffer_rsrc(a, (unsigned)(M - 1) * lda_bytes + (unsigned)K * 2u);
+  const i32x4v rb = buffer_rsrc(b, (unsigned)(N - 1) * ldb_bytes + (unsigned)K * 2u);
+  // Load instruction i of a wave fills rows 32 wave + 8 i .. + 7 of a panel: lane l writes slot
+  // l % 8 of row 32 wave + 8 i + l / 8, which holds logical column (l % 8) ^ ((row >> 1) & 7) =
+  // (l % 8) ^ (l >> 4), flipped by 4 for odd i.  Rows past M or N read zeros (buffer bounds).
+  const int lrow = wave * 32 + (lane >> 3);
+  const unsigned lcol = (unsigned)(((lane & 7) ^ (lane >> 4)) * 16);
+  const unsigned la0 = (unsigned)lrow * lda_bytes, lb0 = (unsigned)lrow * ldb_bytes;
+  const unsigned lds_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds;
+  struct Tiles {
+    int base, mc, nc, mn, nn;  // first stream step of the tile; origins of this tile and the next
+  } tl;
+  auto tile_origin = [&](int t, int& m0, int& n0) __attribute__((always_inline)) {
+    int tm, tn;
+    tile_of((int)blockIdx.x + t * G, tiles_m, tiles_n, kDGroupM, tm, tn);
+    m0 = tm * kSB;
+    n0 = tn * kSB;
+  };
+  auto set_tile = [&](int t) __attribute__((always_inline)) {
+    tl.base = t * nsteps;
+    tile_origin(t, tl.mc, tl.nc);
+    tile_origin(t + 1 < my_tiles ? t + 1 : t, tl.mn, tl.nn);
+    tl.mc = __builtin_amdgcn_readfirstlane(tl.mc);
+    tl.nc = __builtin_amdgcn_readfirstlane(tl.nc);
+    tl.mn = __builtin_amdgcn_readfirstlane(tl.mn);
+    tl.nn = __builtin_amdgcn_readfirstlane(tl.nn);
+  };
+  struct StepOff {
+    unsigned a, b;  // uniform byte offsets of a stream step in A and B
+  };
+  // stream step gs (clamped to the stream) lies in the current tile or the next
+  auto step_off = [&](int gs) __attribute__((always_inline)) {
+    gs = gs < total ? gs : total - 1;
+    const int local = gs - tl.base;
+    const bool cur = local < nsteps;
+    const int m0 = cur ? tl.mc : tl.mn, n0 = cur ? tl.nc : tl.nn, st = cur ? local : local - nsteps;
+    return StepOff{(unsigned)__builtin_amdgcn_readfirstlane((int)((unsigned)m0 * lda_bytes + (unsigned)(st * kSRow))),
+                   (unsigned)__builtin_amdgcn_readfirstlane((int)((unsigned)n0 * ldb_bytes + (unsigned)(st * kSRow)))};
+  };
+  auto dma_piece = [&](const StepOff& o, int buf, int p) __attribute__((always_inline)) {
+    const int i = p >> 1;
+    const unsigned col = lcol ^ (unsigned)((i & 1) * 64);
+    const unsigned la = lds_base + (unsigned)(buf * kSBuffer + (p & 1) * kSPanel + wave * 4096 + i * 1024);
+    if (p & 1) lds_dma16(rb, la, lb0 + (unsigned)(8 * i) * ldb_bytes + col + o.b);
+    else lds_dma16(ra, la, la0 + (unsigned)(8 * i) * lda_bytes + col + o.a);
+  };
+  auto dma_pieces = [&](int gs, int buf, int p0, int p1) __attribute__((always_inline)) {
+    const StepOff o = step_off(gs);
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+      if (p >= p0 && p < p1) dma_piece(o, buf, p);
+  };
+  f32x16 acc[FA][FB];
+#pragma unroll
+  for (int i = 0; i < FA; ++i)
+#pragma unroll
+    for (int j = 0; j < FB; ++j) acc[i][j] = f32x16{};
+
+  const int half = lane >> 5;
+  const int sw = (lane >> 1) & 7;  // (row >> 1) & 7 of every row this lane reads
+  const int fa_row = (wm * FA * 32 + (lane & 31)) * kSRow;
+  const int fb_row = (wn * FB * 32 + (lane & 31)) * kSRow;
+  struct Frags {
+    u32x4 a[FA], b[FB];
+  };
+  // fragment t (A 0..FA-1, then B) of substep u from buffer buf
+  auto read_item = [&](Frags& f, int buf, int u, int t) __attribute__((always_inline)) {
+    const unsigned char* la = lds + buf * kSBuffer;
+    const int col = ((2 * u + half) ^ sw) * 16;
+    if (t < FA) f.a[t < FA ? t : 0] = *(const u32x4*)(la + fa_row + col + t * 32 * kSRow);
+    else f.b[t < FA ? 0 : t - FA] = *(const u32x4*)(la + kSPanel + fb_row + col + (t - FA) * 32 * kSRow);
+  };
+  auto mfmas = [&](const Frags& f, auto&& hook) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < FA; ++i)
+#pragma unroll
+      for (int j = 0; j < FB; ++j) {
+        const V va = __builtin_bit_cast(V, f.a[i]), vb = __builtin_bit_cast(V, f.b[j]);
+        if constexpr (T == TGM_F16) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, vb, acc[i][j], 0, 0, 0);
+        else acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, vb, acc[i][j], 0, 0, 0);
+        hook(i * FB + j);
+      }
+  };
+  // One substep: the MFMAs of fragments fc, with the reads of fn (substep ru of buffer rbuf) and
+  // load pieces [p0, p1) of offsets lo into buffer dbuf spread over them, one item after each
+  // MFMA share (reads first).
+  constexpr int kMaxItems = (FA + FB) + NP;
+  auto substep = [&](const Frags& fc, Frags& fn, int rbuf, int ru, const StepOff* lo, int dbuf, int p0,
+                     int p1) __attribute__((always_inline)) {
+    constexpr int nr = FA + FB;
+    const int ni = nr + (p1 - p0);
+    mfmas(fc, [&](int idx) __attribute__((always_inline)) {
+#pragma unroll
+      for (int it = 0; it < kMaxItems; ++it) {
+        if (it < ni && it * FA * FB / ni == idx) {
+          __builtin_amdgcn_sched_barrier(0);
+          if (it >= nr) dma_piece(*lo, dbuf, p0 + it - nr);
+          else read_item(fn, rbuf, ru, it);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    });
+  };
+  set_tile(0);
+  dma_pieces(0, 0, 0, NP);
+  dma_pieces(1, 1, 0, NP / 2);
+  wait_lds_dma();
+  __syncthreads();
+  Frags f0, f1;
+#pragma unroll
+  for (int t = 0; t < FA + FB; ++t) {
+    __builtin_amdgcn_sched_barrier(0);
+    read_item(f0, 0, 0, t);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // Step gs from buffer cur:
+  //   u0 (f0): read f1 <- u1; second half of step gs + 1's loads (into the other buffer)
+  //   u1 (f1): read f0 <- u2
+  //   u2 (f0): read f1 <- u3
+  //   wait for this wave's loads of step gs + 1, barrier: step gs + 1 is complete in the other
+  //       buffer and every read of this buffer has been issued and completed
+  //   u3 (f1): read f0 <- u0 of step gs + 1; first half of step gs + 2's loads (into this buffer)
+  auto step = [&](int gs, int cur) __attribute__((always_inline)) {
+    const StepOff o1 = step_off(gs + 1), o2 = step_off(gs + 2);
+    substep(f0, f1, cur, 1, &o1, cur ^ 1, NP / 2, NP);
+    substep(f1, f0, cur, 2, &o1, 0, 0, 0);
+    substep(f0, f1, cur, 3, &o1, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_lds_dma();
+    __syncthreads();
+    substep(f1, f0, cur ^ 1, 0, &o2, cur, 0, NP / 2);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  uint16_t* ep = (uint16_t*)(lds + 2 * kSBuffer) + wave * 1024;
+  int gs = 0;
+  for (int t = 0; t < my_tiles; ++t) {
+    set_tile(t);
+    for (int s = 0; s < nsteps; s += 2, gs += 2) {
+      step(gs, 0);
+      step(gs + 1, 1);
+    }
+    // Tile t is complete (MFMA D layout: lane l holds column l % 32 and rows 8 (v / 4) + 4 (l / 32)
+    // + v % 4 of each 32 x 32 tile); the wave's epilogue slice is its own.
+    const int col0 = tl.nc + wn * FB * 32;
+    const int row0 = tl.mc + wm * FA * 32;
+#pragma unroll
+    for (int i = 0; i < FA; ++i)
+#pragma unroll
+      for (int j = 0; j < FB; ++j) {
+        if (cdt == TGM_F32) {
+          const int col = col0 + 32 * j + (lane & 31);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int row = row0 + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            if (row < M && col < N) ((float*)c)[(int64_t)row * ldc + col] = acc[i][j][v];
+          }
+        } else {
+#pragma unroll
+          for (int v = 0; v < 16; v += 2) {  // rows v and v + 1 of the lane's column, one rounding instruction
+            const float x0 = acc[i][j][v], x1 = acc[i][j][v + 1];
+            const unsigned h = cdt == TGM_BF16 ? bf16x2_bits(x0, x1)
+                                               : __builtin_bit_cast(unsigned short, (_Float16)x0) |
+                                                     ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)x1) << 16);
+            const int r = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            ep[r * 32 + (lane & 31)] = (unsigned short)h;
+            ep[(r + 1) * 32 + (lane & 31)] = (unsigned short)(h >> 16);
+          }
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {  // lane l: row l / 4 + 16 q, columns 8 (l % 4) .. + 8
+            const int r = (lane >> 2) + 16 * q, cc = 8 * (lane & 3);
+            const int row = row0 + 32 * i + r, col = col0 + 32 * j + cc;
+            uint16_t* out = (uint16_t*)c + (int64_t)row * ldc + col;
+            if (row < M) {
+              if (col + 7 < N && ((uintptr_t)out & 15) == 0) {
+                __builtin_nontemporal_store(*(const u32x4*)(ep + r * 32 + cc), (u32x4*)out);
+              } else {  // the ragged edge, element by element from LDS
+#pragma unroll 1
+                for (int e = 0; e < 8 && col + e < N; ++e) out[e] = ep[r * 32 + cc + e];
+              }
+            }
+          }
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        acc[i][j] = f32x16{};
+      }
+  }
+  wait_lds_dma();
+}
+
 // out[j, i] = in[i, j] through padded 64 x 64 LDS tiles; T = uint16_t (bf16 / f16) or uint8_t (fp8).
 template <typename T>
 __global__ void __launch_bounds__(256) transpose_t(const T* __restrict__ in, int rows, int cols, int64_t ld_in,
@@ -222,8 +462,21 @@ extern "C" int tgm_gemm_dense_batched(const void* a, int a_dtype, int64_t m, int
   if (m >= (1ll << 31) || n >= (1ll << 31) || (m - 1) * lda_eff * 2 + k * 2 >= (1ll << 32) ||
       (n - 1) * ldb_eff * 2 + k * 2 >= (1ll << 32) || batch > 65535)
     TGM_UNSUPPORTED("tgm_gemm_dense: operands must be under 4 GiB (32-bit offsets), at most 65535 batches");
-  const int64_t tiles = ((m + kDM - 1) / kDM) * ((n + kDN - 1) / kDN);
   const hipStream_t st = (hipStream_t)stream;
+  const int64_t tiles_s = ((m + kSB - 1) / kSB) * ((n + kSB - 1) / kSB);
+  const int cus = stream_cu_count(st);
+  if (batch == 1 && k % 128 == 0 && cus >= 8 && tiles_s >= cus) {
+    // one large product: persistent, one workgroup per CU (a multiple of 8 of them)
+    const dim3 g((unsigned)(cus / 8 * 8));
+    if (a_dtype == TGM_BF16)
+      hipLaunchKernelGGL((gemm_dense_stream<TGM_BF16>), g, dim3(512), 0, st, (const uint8_t*)a, (unsigned)(lda_eff * 2),
+                         (const uint8_t*)b, (unsigned)(ldb_eff * 2), (int)m, (int)n, (int)k, c, c_dtype, ldc);
+    else
+      hipLaunchKernelGGL((gemm_dense_stream<TGM_F16>), g, dim3(512), 0, st, (const uint8_t*)a, (unsigned)(lda_eff * 2),
+                         (const uint8_t*)b, (unsigned)(ldb_eff * 2), (int)m, (int)n, (int)k, c, c_dtype, ldc);
+    return launch_status("tgm_gemm_dense");
+  }
+  const int64_t tiles = ((m + kDM - 1) / kDM) * ((n + kDN - 1) / kDN);
   const dim3 grid((unsigned)tiles, (unsigned)batch);
   if (a_dtype == TGM_BF16)
     hipLaunchKernelGGL((gemm_dense<TGM_BF16, TGM_BF16>), grid, dim3(512), 0, st, (const uint8_t*)a,

@@ -26,7 +26,8 @@ from dataclasses import dataclass
 from typing import Callable
 
 from tinygrad_mi355x.codegen.decomp.formats import FORMATS, MX_FORMATS, packed_nbytes
-from tinygrad_mi355x.renderer.matrix import GEMM_DENSE, GEMM_FP8, GEMM_W, GEMV, GEMV_MAX_ROWS, MatrixKernel, mx_kernel
+from tinygrad_mi355x.renderer.matrix import (GEMM_FP8, GEMM_W, GEMV, GEMV_MAX_ROWS, MatrixKernel, dense_kernel,
+                                            mx_kernel)
 from tinygrad_mi355x.runtime import library as L
 from tinygrad_mi355x.runtime import profile
 from tinygrad_mi355x.runtime.support import hip
@@ -204,7 +205,8 @@ def dense_program(a_dtype: str, m: int, lda: int, b_dtype: str, n: int, ldb: int
                              touched)
     if scale_a or scale_b:
         raise ValueError("per-tensor scales apply to FP8 operands only")
-    return MatrixProgram(GEMM_DENSE, "tgm_gemm_dense", _tiles(m, n, GEMM_DENSE), est,
+    kernel = dense_kernel(m, n, k)
+    return MatrixProgram(kernel, "tgm_gemm_dense", _tiles(m, n, kernel), est,
                          lambda out, x, y, s: (x, adt, m, lda, y, bdt, n, ldb, k, out, cdt, ldc, s), touched)
 
 

@@ -35,6 +35,10 @@ GEMM_MX_GENERAL = MatrixKernel("tgm_gemm_mx", "ThreadGroup", (256, 128, 128), 51
 # Family 2: ordinary bf16 x bf16 / f16 x f16 MFMA GEMM (the reference's LinAlg lowering of an
 # ordinary matrix product, codegen/matmul.py:156-246).
 GEMM_DENSE = MatrixKernel("tgm_gemm_dense", "ThreadGroup", (256, 128, 64), 512)
+# The same entry point's persistent kernel for one large product (K a multiple of 128 and at least
+# one round of 256 x 256 tiles on the device's CUs): 256 x 256 tiles, K steps of 64, one workgroup
+# per CU walking its tiles.  ``dense_kernel`` picks.
+GEMM_DENSE_STREAM = MatrixKernel("tgm_gemm_dense", "ThreadGroup", (256, 256, 64), 512)
 # Family 2: ordinary FP8 x FP8 GEMM, the FP8 values decoded exactly to bf16 in registers for the
 # dense GEMM's MFMA (the reference's LinAlg takes FP8 operands as they are, renderer/linalg.py:12-13).
 GEMM_FP8 = MatrixKernel("tgm_gemm_fp8", "ThreadGroup", (256, 128, 128), 512)
@@ -42,6 +46,14 @@ GEMM_FP8 = MatrixKernel("tgm_gemm_fp8", "ThreadGroup", (256, 128, 128), 512)
 PLAIN = MatrixKernel("tgm_gemm_plain", "tiled", (16, 16, 1), 256)
 
 GEMV_MAX_ROWS = 16
+MI355X_CUS = 256  # compute units of one MI355X
+
+
+def dense_kernel(m: int, n: int, k: int, batch: int = 1, cus: int = MI355X_CUS) -> MatrixKernel:
+    """The kernel tgm_gemm_dense launches for a bf16 / f16 product (tgm_gemm_dense.hip's choice)."""
+    tiles = -(-m // GEMM_DENSE_STREAM.tile[0]) * -(-n // GEMM_DENSE_STREAM.tile[1])
+    stream = batch == 1 and k > 0 and k % 128 == 0 and cus >= 8 and tiles >= cus
+    return GEMM_DENSE_STREAM if stream else GEMM_DENSE
 
 
 def mx_kernel(a_format: str, a_scaled: bool, b_format: str, b_scaled: bool, k: int) -> MatrixKernel:
