@@ -872,3 +872,39 @@ def test_concurrent_callers_get_their_sequential_results(dev):
     for got, want in zip(results, expected):
         assert all(torch.equal(g, want) for g in got)
 
+
+
+# At least one round of 128 x 256 tiles (256 CUs) with K a multiple of 512 runs the persistent weight
+# GEMM (gemm_w_stream): 1000 x 8200 is 8 x 33 = 264 tiles, so some workgroups take two tiles.
+@pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e2m3", "fp6_e3m2"])
+@pytest.mark.parametrize("scale_kind", ["e8m0", "none"])
+def test_gemm_w_stream_one_hot_is_exact(dev, fmt, scale_kind):
+    """One-hot activation rows recover deq(W)[:, j] exactly (fp32 and bf16 outputs) in every tile of the
+    persistent kernel, ragged edges included: code order, the two MX blocks a lane decodes per step,
+    their scale bytes, the MFMA K order, the tile walk and the epilogue all line up."""
+    m, n, k = 1000, 8200, 512
+    rng = np.random.default_rng(17)
+    w, deq = make_weight(dev, fmt, n, k, scale_kind, rng)
+    cols = rng.choice(k, m, replace=True)
+    a = torch.zeros((m, k), dtype=torch.bfloat16, device=dev)
+    a[torch.arange(m), torch.from_numpy(cols)] = 1.0
+    want = deq[:, cols].T.astype(np.float32)
+    for cdt in (torch.float32, torch.bfloat16):
+        c = matmul_nt(a, w, scope="ThreadGroup", dtype=cdt).float().cpu().numpy()
+        assert np.array_equal(c, want), cdt
+
+
+@pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e3m2"])
+def test_gemm_w_stream_parity(dev, fmt):
+    """Random bf16 activations (a strided view) against the fp64 oracle on rows sampled in every
+    32-row band, three output dtypes, K = 1024 (two scale batches per tile)."""
+    m, n, k = 1000, 8200, 1024
+    rng = np.random.default_rng(23)
+    w, deq = make_weight(dev, fmt, n, k, "e8m0", rng)
+    big = torch.from_numpy(rng.standard_normal((m, k + 64)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    a = big[:, 32:32 + k]
+    rows = stratified(rng, m, 2)
+    ref = bf16_np(a)[rows].astype(np.float64) @ deq.T
+    for cdt in (torch.float32, torch.bfloat16, torch.float16):
+        c = matmul_nt(a, w, scope="ThreadGroup", dtype=cdt)
+        assert O.max_rel_err(bf16_np(c)[rows], ref) <= TOL, cdt

@@ -246,6 +246,423 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
         store_tile32(acc[i][j], ep, lane, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, M, N, c, cdt, ldc);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Persistent form for K a multiple of 512 and at least one round of 128 x 256 tiles
+// (gemm_w_stream): the same tile, waves, panels, K order and decode as gemm_w_mx, on the step
+// pipeline of the persistent FP4 GEMM (tgm_gemm_mx.hip) --
+//
+//  * one workgroup per CU (G, a multiple of 8) walks tiles blockIdx.x, blockIdx.x + G, ... as one
+//    stream of K steps; the loads of the next tile's first steps are issued during the current
+//    tile's last, so no tile waits for its operands and no workgroup is launched per tile;
+//  * a step is eight substeps of 16 K (MFMA j takes K [64 h + 8 j, + 8) for lane half h); after
+//    each MFMA the wave issues an even share of the work placed on its substep, fenced by
+//    scheduling barriers: the next substep's A fragments, the panel loads (the rest of step
+//    s + 1's in substeps 0 and 1, the first of step s + 2's in substep 7) and the weight decode;
+//  * the step barrier sits before substep 7: there the next step's A fragments, packed weights
+//    and E8M0 words are read from the other buffer, and the first of the two MX blocks each lane
+//    owns per weight fragment is decoded; the second block is decoded under the next step's
+//    first substep.  So no step begins with an LDS round trip and a full decode;
+//  * at a tile's end each wave rounds its 32 x 32 tiles to 16 bits through its own 2 KB LDS slice
+//    and writes 16-byte row segments with non-temporal stores (the SwiGLU form pairs gate and up
+//    columns across neighbouring lanes first).
+constexpr int kVEpi = 8 * 2048;                                    // one 2 KB epilogue slice per wave
+constexpr int kVLds = 2 * kWStage + 2 * kWBatch + kVEpi;           // 136 KB
+constexpr int kVKMultiple = kWK * kWBatchSteps;                     // K = 512: whole scale batches per tile
+
+// MX block ``blk`` (0 or 1) of the 64 codes a lane owns in one step (raw: 12 dwords FP6 / 8
+// dwords FP4, block 1 from dword 6 / 4) to the operands of MFMAs 4 blk .. 4 blk + 3; its E8M0
+// byte is byte ``sbyte`` of ``sword`` (the shift happens here, at the decode, not where the word
+// is read from LDS).
+template <int FMT>
+__device__ __forceinline__ void decode_block(const unsigned* raw, int blk, unsigned sword, int sbyte, bf16x8 out[4]) {
+  const float s = __builtin_bit_cast(float, ((sword >> (8 * sbyte)) & 0xFFu) << 23);
+  if constexpr (FMT == TGM_FMT_FP4_E2M1) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const unsigned v = raw[4 * blk + d];
+      const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, s, 0);
+      const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, s, 1);
+      const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, s, 2);
+      const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, s, 3);
+      out[d] = bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+    }
+  } else {
+    i32x6 v;
+#pragma unroll
+    for (int q = 0; q < 6; ++q) v[q] = (int)raw[6 * blk + q];
+    bf16x32 d;
+    if constexpr (FMT == TGM_FMT_FP6_E2M3) d = __builtin_amdgcn_cvt_scalef32_pk32_bf16_fp6(v, s);
+    else d = __builtin_amdgcn_cvt_scalef32_pk32_bf16_bf6(v, s);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      out[j] = bf16x8{d[8 * j], d[8 * j + 1], d[8 * j + 2], d[8 * j + 3], d[8 * j + 4], d[8 * j + 5], d[8 * j + 6],
+                      d[8 * j + 7]};
+  }
+}
+
+template <int FMT, bool SCALED, bool SWIGLU>
+__global__ void __launch_bounds__(512) gemm_w_stream(const uint8_t* __restrict__ a, unsigned lda_bytes,
+                                                     const uint8_t* __restrict__ w, const uint8_t* __restrict__ sw,
+                                                     int M, int N, int K, void* __restrict__ c, int cdt, int64_t ldc) {
+  using T = GemmWTraits<FMT>;
+  constexpr bool FP4 = FMT == TGM_FMT_FP4_E2M1;
+  constexpr int R = T::kRow;            // packed weight bytes per row and step
+  constexpr int FA = 2, FB = 2;
+  constexpr int NPA = 4;                // A panel: 32 instructions of 4 rows, 4 per wave
+  constexpr int NPW = T::kPanelLoads / 8;  // W panel: 16 (FP4) or 24 (FP6) instructions, 2 or 3 per wave
+  constexpr int NP = NPA + NPW;         // load pieces per wave and step
+  constexpr int NP0 = NP / 2;           // pieces of step s + 2 issued in step s's last substep
+  constexpr int NRB = FP4 ? 1 : 2;      // LDS reads of one MX block of a weight fragment
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kVLds];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
+  const int tiles_m = (M + kWM - 1) / kWM, tiles_n = (N + kWN - 1) / kWN;
+  const int ntiles = tiles_m * tiles_n;
+  const int G = gridDim.x;
+  const int my_tiles = (ntiles - (int)blockIdx.x + G - 1) / G;  // >= 1 (the host launches G <= ntiles)
+  const int nsteps = K / kWK;                                    // a multiple of kWBatchSteps
+  const int total = my_tiles * nsteps;
+  const unsigned kbw = (unsigned)K / 8u * (FP4 ? 4u : 6u);       // packed bytes per weight row
+  const unsigned kblk = (unsigned)K / 32u;
+  const i32x4v ra = buffer_rsrc(a, (unsigned)(M - 1) * lda_bytes + (unsigned)K * 2u);
+  const i32x4v rw = buffer_rsrc(w, (unsigned)N * kbw);
+  const i32x4v rs = buffer_rsrc(sw, SCALED ? (unsigned)N * kblk : 0u);
+  const unsigned lds_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds;
+
+  // Per-lane load offsets within a tile's step (the uniform tile and step parts come from step_off).
+  // A: instruction 4 wave + q covers rows 16 wave + 4 q .. + 3; lane l fills slot l % 16 of row
+  // 16 wave + 4 q + l / 16, which holds logical 16-byte column (l % 16) ^ (row % 16).
+  unsigned voa[NPA];
+#pragma unroll
+  for (int q = 0; q < NPA; ++q) {
+    const int row = 16 * wave + 4 * q + (lane >> 4);
+    voa[q] = (unsigned)row * lda_bytes + (unsigned)(((lane & 15) ^ (row & 15)) * 16);
+  }
+  // W: instruction wave + 8 q fills bytes [1024 i, + 1024) of the panel: FP6 rows are 96 bytes
+  // stored densely; FP4 rows are 64 bytes with 16-byte chunks swizzled by (row / 4) % 4.
+  unsigned vow[NPW];
+#pragma unroll
+  for (int q = 0; q < NPW; ++q) {
+    const int i = wave + 8 * q;
+    if constexpr (FP4) {
+      const int row = 16 * i + (lane >> 2);
+      vow[q] = (unsigned)row * kbw + (unsigned)(((lane & 3) ^ ((row >> 2) & 3)) * 16);
+    } else {
+      const int f = 1024 * i + 16 * lane;
+      vow[q] = (unsigned)(f / 96) * kbw + (unsigned)(f % 96);
+    }
+  }
+  struct Tiles {
+    int base, mc, nc, mn, nn;  // first stream step of the tile; origins of this tile and the next
+  } tl;
+  auto tile_origin = [&](int t, int& m0, int& n0) __attribute__((always_inline)) {
+    int tm, tn;
+    tile_of((int)blockIdx.x + t * G, tiles_m, tiles_n, kWGroupM, tm, tn);
+    m0 = tm * kWM;
+    n0 = tn * kWN;
+  };
+  auto set_tile = [&](int t) __attribute__((always_inline)) {
+    tl.base = t * nsteps;
+    tile_origin(t, tl.mc, tl.nc);
+    tile_origin(t + 1 < my_tiles ? t + 1 : t, tl.mn, tl.nn);
+    tl.mc = __builtin_amdgcn_readfirstlane(tl.mc);
+    tl.nc = __builtin_amdgcn_readfirstlane(tl.nc);
+    tl.mn = __builtin_amdgcn_readfirstlane(tl.mn);
+    tl.nn = __builtin_amdgcn_readfirstlane(tl.nn);
+  };
+  struct StepAt {
+    int m0, n0, st;
+  };
+  // (tile origins, step within the tile) of stream step gs, clamped to the stream; gs lies in the
+  // current tile or the next
+  auto step_at = [&](int gs) __attribute__((always_inline)) {
+    gs = gs < total ? gs : total - 1;
+    const int local = gs - tl.base;
+    return local < nsteps ? StepAt{tl.mc, tl.nc, local} : StepAt{tl.mn, tl.nn, local - nsteps};
+  };
+  struct StepOff {
+    unsigned a, w;
+  };
+  auto step_off = [&](int gs) __attribute__((always_inline)) {
+    const StepAt at = step_at(gs);
+    return StepOff{
+        (unsigned)__builtin_amdgcn_readfirstlane((int)((unsigned)at.m0 * lda_bytes + (unsigned)(at.st * kWK * 2))),
+        (unsigned)__builtin_amdgcn_readfirstlane((int)((unsigned)at.n0 * kbw + (unsigned)(at.st * R)))};
+  };
+  auto dma_piece = [&](const StepOff& o, int buf, int p) __attribute__((always_inline)) {
+    const unsigned st = lds_base + (unsigned)(buf * kWStage);
+    if (p < NPA) lds_dma16(ra, st + (unsigned)(4 * wave + p) * 1024u, voa[p < NPA ? p : 0] + o.a);
+    else {
+      const int q = p - NPA;
+      lds_dma16(rw, st + (unsigned)kAPanel + (unsigned)(wave + 8 * q) * 1024u, vow[q < NPW ? q : 0] + o.w);
+    }
+  };
+  auto dma_pieces = [&](int gs, int buf, int p0, int p1) __attribute__((always_inline)) {
+    const StepOff o = step_off(gs);
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+      if (p >= p0 && p < p1) dma_piece(o, buf, p);
+  };
+  // E8M0 scales arrive four steps at a time: batch gb of the stream (steps 4 gb .. 4 gb + 3, one
+  // tile) puts the 16 bytes of W row r at byte 16 r of scale buffer gb & 1; waves 0..3 load 64
+  // rows each.
+  auto issue_batch = [&](int gb) __attribute__((always_inline)) {
+    if (SCALED && wave < 4) {
+      const int gs = gb * kWBatchSteps < total ? gb * kWBatchSteps : total - kWBatchSteps;
+      const StepAt at = step_at(gs);
+      lds_dma16(rs, lds_base + (unsigned)(2 * kWStage + (gb & 1) * kWBatch + wave * 1024),
+                (unsigned)(at.n0 + 64 * wave + lane) * kblk + (unsigned)at.st * 4u);
+    }
+  };
+
+  f32x16 acc[FA][FB];
+#pragma unroll
+  for (int i = 0; i < FA; ++i)
+#pragma unroll
+    for (int j = 0; j < FB; ++j) acc[i][j] = f32x16{};
+
+  const int half = lane >> 5;
+  const int a_row = (wm * 64 + (lane & 31)) * 256;  // + 32 t rows
+  const int w_row = wn * 64 + (lane & 31);          // + 32 t
+  bf16x8 fa[2][FA];                                 // A fragments of substeps j (slot j & 1)
+  bf16x8 wd[FB][8];                                 // decoded weights of the step (MFMA j: wd[t][j])
+  unsigned raw[FB][FP4 ? 8 : 12];                  // packed codes of the step's weight fragments
+  unsigned sword[FB];                               // E8M0 word of the step (blocks 2 h, 2 h + 1: bytes 2 h, 2 h + 1)
+  auto read_a = [&](int buf, int j, int t) __attribute__((always_inline)) {
+    const int col = (8 * half + j) ^ (lane & 15);
+    fa[j & 1][t] = *(const bf16x8*)(lds + buf * kWStage + a_row + t * 32 * 256 + col * 16);
+  };
+  // read q (< NRB) of MX block blk of weight fragment t: FP4 one 16-byte chunk; FP6 the block's 24
+  // bytes as 16 + 8 (block 0) or 8 + 16 (block 1) at 8-byte aligned offsets of the lane's 48
+  auto read_raw = [&](int buf, int t, int blk, int q) __attribute__((always_inline)) {
+    const unsigned char* pw = lds + buf * kWStage + kAPanel;
+    const int row = w_row + 32 * t;
+    if constexpr (FP4) {
+      const u32x4 v = *(const u32x4*)(pw + row * 64 + ((2 * half + blk) ^ ((row >> 2) & 3)) * 16);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) raw[t][4 * blk + e] = v[e];
+    } else {
+      const unsigned char* p = pw + row * 96 + 48 * half + 24 * blk;
+      if ((blk == 0) == (q == 0)) {  // the 16-byte piece: block 0 at +0, block 1 at +8
+        const u32x4 v = *(const u32x4*)(p + (blk ? 8 : 0));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) raw[t][6 * blk + (blk ? 2 : 0) + e] = v[e];
+      } else {                       // the 8-byte piece: block 0 at +16, block 1 at +0
+        const u32x2 v = *(const u32x2*)(p + (blk ? 0 : 16));
+#pragma unroll
+        for (int e = 0; e < 2; ++e) raw[t][6 * blk + (blk ? 0 : 4) + e] = v[e];
+      }
+    }
+  };
+  auto read_scale = [&](int gs, int t) __attribute__((always_inline)) {  // scales of stream step gs
+    if constexpr (SCALED) {
+      const unsigned* ps = (const unsigned*)(lds + 2 * kWStage + ((gs / kWBatchSteps) & 1) * kWBatch);
+      sword[t] = ps[4 * (w_row + 32 * t) + gs % kWBatchSteps];
+    } else {
+      sword[t] = 0x7F7F7F7Fu;  // 2^0
+    }
+  };
+  auto decode = [&](int t, int blk) __attribute__((always_inline)) {
+    decode_block<FMT>(raw[t], blk, sword[t], 2 * half + blk, &wd[t][4 * blk]);
+  };
+  auto mfmas = [&](int j, auto&& hook) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ta = 0; ta < FA; ++ta)
+#pragma unroll
+      for (int tb = 0; tb < FB; ++tb) {
+        acc[ta][tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[j & 1][ta], wd[tb][j], acc[ta][tb], 0, 0, 0);
+        hook(ta * FB + tb);
+      }
+  };
+  // Items of a substep, spread over its FA * FB MFMAs in order: it < n_items.
+  constexpr int kMaxItems = FA + 2 * FB + FB * NRB + NP;
+  auto run_items = [&](int j, int n_items, auto&& item) __attribute__((always_inline)) {
+    mfmas(j, [&](int idx) __attribute__((always_inline)) {
+#pragma unroll
+      for (int it = 0; it < kMaxItems; ++it) {
+        if (it < n_items && it * FA * FB / n_items == idx) {
+          __builtin_amdgcn_sched_barrier(0);
+          item(it);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    });
+  };
+  // Step gs from buffer cur (fa[0] and wd[.][0..3] hold substep 0's operands on entry, raw and sword
+  // the step's block-0 codes and E8M0 words):
+  //   j = 0: A of j = 1; block 1 of the packed weights; pieces [NP0, NP1) of step gs + 1
+  //   j = 1: A of j = 2; the remaining pieces of step gs + 1
+  //   j = 2: A of j = 3; decode block 1 (MFMAs 4 .. 7)
+  //   j = 3 .. 6: A of j + 1
+  //   wait for this wave's loads of step gs + 1, barrier
+  //   j = 7: A of step gs + 1's j = 0, its E8M0 words and block 0 of its packed weights (other
+  //          buffer); pieces [0, NP0) of step gs + 2 (into this buffer); decode block 0
+  constexpr int NP1 = NP0 + (NP - NP0 + 1) / 2;
+  auto step = [&](int gs, int cur, bool batch) __attribute__((always_inline)) {
+    const StepOff o1 = step_off(gs + 1), o2 = step_off(gs + 2);
+    run_items(0, FA + FB * NRB + (NP1 - NP0), [&](int it) __attribute__((always_inline)) {
+      if (it < FA) read_a(cur, 1, it);
+      else if (it < FA + FB * NRB) read_raw(cur, (it - FA) / NRB, 1, (it - FA) % NRB);
+      else dma_piece(o1, cur ^ 1, NP0 + it - FA - FB * NRB);
+    });
+    run_items(1, FA + (NP - NP1), [&](int it) __attribute__((always_inline)) {
+      if (it < FA) read_a(cur, 2, it);
+      else dma_piece(o1, cur ^ 1, NP1 + it - FA);
+    });
+    run_items(2, FA + FB, [&](int it) __attribute__((always_inline)) {
+      if (it < FA) read_a(cur, 3, it);
+      else decode(it - FA, 1);
+    });
+#pragma unroll
+    for (int j = 3; j < 7; ++j)
+      run_items(j, FA, [&](int it) __attribute__((always_inline)) { read_a(cur, j + 1, it); });
+    __builtin_amdgcn_sched_barrier(0);
+    wait_lds_dma();  // this wave's loads of step gs + 1 (and of a scale batch issued at step gs - 3)
+    __syncthreads();
+    run_items(7, FA + FB + FB * NRB + NP0 + FB, [&](int it) __attribute__((always_inline)) {
+      if (it < FA) read_a(cur ^ 1, 0, it);
+      else if (it < FA + FB) read_scale(gs + 1, it - FA);
+      else if (it < FA + FB + FB * NRB) read_raw(cur ^ 1, (it - FA - FB) / NRB, 0, (it - FA - FB) % NRB);
+      else if (it < FA + FB + FB * NRB + NP0) dma_piece(o2, cur, it - FA - FB - FB * NRB);
+      else decode(it - FA - FB - FB * NRB - NP0, 0);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+    // Batch b + 1 goes to the buffer batch b - 1 used; its last reads (step 4 b - 1's words, in
+    // step 4 b - 2) are behind this step's barrier; it is complete after step 4 b + 3's wait.
+    if (batch) issue_batch(gs / kWBatchSteps + 1);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  set_tile(0);
+  issue_batch(0);
+  dma_pieces(0, 0, 0, NP);
+  dma_pieces(1, 1, 0, NP0);
+  wait_lds_dma();
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < FB; ++t) {
+    read_scale(0, t);
+#pragma unroll
+    for (int q = 0; q < NRB; ++q) read_raw(0, t, 0, q);
+  }
+#pragma unroll
+  for (int t = 0; t < FA; ++t) read_a(0, 0, t);
+#pragma unroll
+  for (int t = 0; t < FB; ++t) decode(t, 0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  unsigned char* ep = lds + 2 * kWStage + 2 * kWBatch + wave * 2048;  // this wave's epilogue slice
+  static_assert(kWBatchSteps == 4, "the step loop is unrolled by four");
+  int gs = 0;
+  for (int t = 0; t < my_tiles; ++t) {
+    set_tile(t);
+    for (int s = 0; s < nsteps; s += kWBatchSteps, gs += kWBatchSteps) {
+      step(gs, 0, true);
+      step(gs + 1, 1, false);
+      step(gs + 2, 0, false);
+      step(gs + 3, 1, false);
+    }
+    // Tile t is complete (MFMA D layout: lane l holds column l % 32 and rows 8 (v / 4) + 4 (l / 32)
+    // + v % 4 of each 32 x 32 tile: columns are weight rows, rows are activation rows).
+    const int row0 = tl.mc + wm * 64;
+    const int col0 = tl.nc + wn * 64;
+#pragma unroll
+    for (int i = 0; i < FA; ++i)
+#pragma unroll
+      for (int j = 0; j < FB; ++j) {
+        if constexpr (SWIGLU) {
+          // columns 2 q, 2 q + 1 (lanes l, l ^ 1) are the gate and up rows of output column q
+          const int oc = (col0 + 32 * j) / 2 + (lane & 31) / 2;
+          float y[16];
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const float g = acc[i][j][v], u = __shfl_xor(acc[i][j][v], 1, 64);
+            y[v] = g / (1.0f + expf(-g)) * u;
+          }
+          if (cdt == TGM_F32) {
+            if ((lane & 1) == 0 && oc < N / 2)
+#pragma unroll
+              for (int v = 0; v < 16; ++v) {
+                const int row = row0 + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                if (row < M) ((float*)c)[(int64_t)row * ldc + oc] = y[v];
+              }
+          } else {
+            unsigned short* e16 = (unsigned short*)ep;  // 32 rows x 16 output columns
+            if ((lane & 1) == 0)
+#pragma unroll
+              for (int v = 0; v < 16; v += 2) {
+                const unsigned h = cdt == TGM_BF16 ? bf16x2_bits(y[v], y[v + 1])
+                                                   : __builtin_bit_cast(unsigned short, (_Float16)y[v]) |
+                                                         ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)y[v + 1]) << 16);
+                const int r = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                e16[r * 16 + (lane & 31) / 2] = (unsigned short)h;
+                e16[(r + 1) * 16 + (lane & 31) / 2] = (unsigned short)(h >> 16);
+              }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const int r = lane >> 1, cc = 8 * (lane & 1);  // lane l: row l / 2, output columns 8 (l % 2) .. + 8
+            const int row = row0 + 32 * i + r, col = (col0 + 32 * j) / 2 + cc;
+            uint16_t* out = (uint16_t*)c + (int64_t)row * ldc + col;
+            if (row < M) {
+              if (col + 7 < N / 2 && ((uintptr_t)out & 15) == 0) {
+                __builtin_nontemporal_store(*(const u32x4*)(e16 + r * 16 + cc), (u32x4*)out);
+              } else {
+#pragma unroll 1
+                for (int e = 0; e < 8 && col + e < N / 2; ++e) out[e] = e16[r * 16 + cc + e];
+              }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          }
+        } else if (cdt == TGM_F32) {
+          const int col = col0 + 32 * j + (lane & 31);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int row = row0 + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            if (row < M && col < N) ((float*)c)[(int64_t)row * ldc + col] = acc[i][j][v];
+          }
+        } else {
+          unsigned short* e16 = (unsigned short*)ep;  // 32 rows x 32 columns
+#pragma unroll
+          for (int v = 0; v < 16; v += 2) {
+            const float x0 = acc[i][j][v], x1 = acc[i][j][v + 1];
+            const unsigned h = cdt == TGM_BF16 ? bf16x2_bits(x0, x1)
+                                               : __builtin_bit_cast(unsigned short, (_Float16)x0) |
+                                                     ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)x1) << 16);
+            const int r = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            e16[r * 32 + (lane & 31)] = (unsigned short)h;
+            e16[(r + 1) * 32 + (lane & 31)] = (unsigned short)(h >> 16);
+          }
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {  // lane l: row l / 4 + 16 q, columns 8 (l % 4) .. + 8
+            const int r = (lane >> 2) + 16 * q, cc = 8 * (lane & 3);
+            const int row = row0 + 32 * i + r, col = col0 + 32 * j + cc;
+            uint16_t* out = (uint16_t*)c + (int64_t)row * ldc + col;
+            if (row < M) {
+              if (col + 7 < N && ((uintptr_t)out & 15) == 0) {
+                __builtin_nontemporal_store(*(const u32x4*)(e16 + r * 32 + cc), (u32x4*)out);
+              } else {
+#pragma unroll 1
+                for (int e = 0; e < 8 && col + e < N; ++e) out[e] = e16[r * 32 + cc + e];
+              }
+            }
+          }
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        acc[i][j] = f32x16{};
+      }
+  }
+  wait_lds_dma();
+}
+
 // Sum of the split-K partial products [splits][M][N] (fp32) in split order, rounded once to
 // C; 4 consecutive elements of a row per thread and pass (N % 4 == 0).
 __global__ void __launch_bounds__(256) gemm_split_reduce(const float* __restrict__ part, int splits, int64_t M,
@@ -498,6 +915,14 @@ template <int FMT, bool SCALED, bool SWIGLU = false>
 int launch_gemm_w(const void* a, int64_t lda, const void* w, const void* scales, int64_t m, int64_t n, int64_t k,
                   void* c, int cdt, int64_t ldc, hipStream_t stream, int splits = 1, float* part = nullptr) {
   const int64_t tiles = ((m + kWM - 1) / kWM) * ((n + kWN - 1) / kWN);
+  const int cus = stream_cu_count(stream);
+  if (splits == 1 && !part && k % kVKMultiple == 0 && cus >= 8 && tiles >= cus) {
+    // at least one round of tiles: persistent, one workgroup per CU (a multiple of 8 of them)
+    hipLaunchKernelGGL((gemm_w_stream<FMT, SCALED, SWIGLU>), dim3((unsigned)(cus / 8 * 8)), dim3(512), 0, stream,
+                       (const uint8_t*)a, (unsigned)(lda * 2), (const uint8_t*)w, (const uint8_t*)scales, (int)m,
+                       (int)n, (int)k, c, cdt, ldc);
+    return launch_status(SWIGLU ? "tgm_gemm_w_swiglu" : "tgm_gemm_w");
+  }
   const int kps = (int)((k / kWK + splits - 1) / splits);
   hipLaunchKernelGGL((gemm_w_mx<FMT, SCALED, SWIGLU>), dim3((unsigned)tiles, (unsigned)splits), dim3(512), 0, stream,
                      (const uint8_t*)a, (unsigned)(lda * 2), (const uint8_t*)w, (const uint8_t*)scales, (int)m, (int)n,
