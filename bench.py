@@ -60,8 +60,8 @@ PROFILES = {
     "fp4_gemv_m16": ("gemv_fp4_e2m1_n14336_k4096_m16.txt", "gemv_stream"),
     "int4_gemv_n4096": ("gemv_int4_g32_n4096_k4096_m1.txt", "gemv_rows_int4"),
     "int4_gemv_n14336": ("gemv_int4_g32_n14336_k4096_m1.txt", "gemv_rows_int4"),
-    "fp6_e3m2_gemm_m2048": ("gemm_w_fp6_e3m2_m2048_n11008_k4096.txt", "gemm_w_mx"),
-    "fp6_e2m3_gemm_m2048": ("gemm_w_fp6_e2m3_m2048_n11008_k4096.txt", "gemm_w_mx"),
+    "fp6_e3m2_gemm_m2048": ("gemm_w_fp6_e3m2_m2048_n11008_k4096.txt", "gemm_w_stream"),
+    "fp6_e2m3_gemm_m2048": ("gemm_w_fp6_e2m3_m2048_n11008_k4096.txt", "gemm_w_stream"),
     "fp4_gemm_8192": ("gemm_mx_fp4_m8192_n8192_k8192.txt", "gemm_mx"),
     "fp4_gemm_4096x14336x4096": ("gemm_mx_fp4_m4096_n14336_k4096.txt", "gemm_mx"),
     "bf16_gemm_8192": ("gemm_dense_bf16_m8192_n8192_k8192.txt", "gemm_dense"),

@@ -568,8 +568,8 @@ def test_gemv_swiglu_epilogue(dev, nk):
     assert err <= 1e-2, err
 
 
-# (1000, 16400, 512): 8 x 65 tiles of 128 x 256, at least one round of CUs and K % 512 == 0, so both
-# products run the persistent kernel (gemm_w_stream)
+# (1000, 16400, 512): 8 x 65 tiles of 128 x 256, at least one round of CUs and K % 512 == 0, so the
+# plain product runs the persistent kernel (gemm_w_stream) and the SwiGLU form gemm_w_mx
 @pytest.mark.parametrize("m,n,k,pad", [(300, 1000, 512, 0), (17, 28672 // 8, 4096, 3), (256, 512, 128, 8),
                                        (1000, 16400, 512, 3)])
 @pytest.mark.parametrize("scaled", [True, False])

@@ -263,8 +263,10 @@ __global__ void __launch_bounds__(512) gemm_w_mx(const uint8_t* __restrict__ a, 
 //    owns per weight fragment is decoded; the second block is decoded under the next step's
 //    first substep.  So no step begins with an LDS round trip and a full decode;
 //  * at a tile's end each wave rounds its 32 x 32 tiles to 16 bits through its own 2 KB LDS slice
-//    and writes 16-byte row segments with non-temporal stores (the SwiGLU form pairs gate and up
-//    columns across neighbouring lanes first).
+//    and writes 16-byte row segments with non-temporal stores.
+// Measured in one process against gemm_w_mx: config 3 (2048 x 11008 x 4096, FP6 E3M2) 156.5 against
+// 171.0 us; with FP4 weights the batch-8 decoder prefill (its down projections 4096 x 4096 x 14336 on
+// this kernel) came out even (15.96 against 15.81 ms).  The SwiGLU form keeps gemm_w_mx.
 constexpr int kVEpi = 8 * 2048;                                    // one 2 KB epilogue slice per wave
 constexpr int kVLds = 2 * kWStage + 2 * kWBatch + kVEpi;           // 136 KB
 constexpr int kVKMultiple = kWK * kWBatchSteps;                     // K = 512: whole scale batches per tile
@@ -300,7 +302,7 @@ __device__ __forceinline__ void decode_block(const unsigned* raw, int blk, unsig
   }
 }
 
-template <int FMT, bool SCALED, bool SWIGLU>
+template <int FMT, bool SCALED>
 __global__ void __launch_bounds__(512) gemm_w_stream(const uint8_t* __restrict__ a, unsigned lda_bytes,
                                                      const uint8_t* __restrict__ w, const uint8_t* __restrict__ sw,
                                                      int M, int N, int K, void* __restrict__ c, int cdt, int64_t ldc) {
@@ -571,53 +573,7 @@ __global__ void __launch_bounds__(512) gemm_w_stream(const uint8_t* __restrict__
     for (int i = 0; i < FA; ++i)
 #pragma unroll
       for (int j = 0; j < FB; ++j) {
-        if constexpr (SWIGLU) {
-          // columns 2 q, 2 q + 1 (lanes l, l ^ 1) are the gate and up rows of output column q
-          const int oc = (col0 + 32 * j) / 2 + (lane & 31) / 2;
-          float y[16];
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const float g = acc[i][j][v], u = __shfl_xor(acc[i][j][v], 1, 64);
-            y[v] = g / (1.0f + expf(-g)) * u;
-          }
-          if (cdt == TGM_F32) {
-            if ((lane & 1) == 0 && oc < N / 2)
-#pragma unroll
-              for (int v = 0; v < 16; ++v) {
-                const int row = row0 + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                if (row < M) ((float*)c)[(int64_t)row * ldc + oc] = y[v];
-              }
-          } else {
-            unsigned short* e16 = (unsigned short*)ep;  // 32 rows x 16 output columns
-            if ((lane & 1) == 0)
-#pragma unroll
-              for (int v = 0; v < 16; v += 2) {
-                const unsigned h = cdt == TGM_BF16 ? bf16x2_bits(y[v], y[v + 1])
-                                                   : __builtin_bit_cast(unsigned short, (_Float16)y[v]) |
-                                                         ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)y[v + 1]) << 16);
-                const int r = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                e16[r * 16 + (lane & 31) / 2] = (unsigned short)h;
-                e16[(r + 1) * 16 + (lane & 31) / 2] = (unsigned short)(h >> 16);
-              }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            const int r = lane >> 1, cc = 8 * (lane & 1);  // lane l: row l / 2, output columns 8 (l % 2) .. + 8
-            const int row = row0 + 32 * i + r, col = (col0 + 32 * j) / 2 + cc;
-            uint16_t* out = (uint16_t*)c + (int64_t)row * ldc + col;
-            if (row < M) {
-              if (col + 7 < N / 2 && ((uintptr_t)out & 15) == 0) {
-                __builtin_nontemporal_store(*(const u32x4*)(e16 + r * 16 + cc), (u32x4*)out);
-              } else {
-#pragma unroll 1
-                for (int e = 0; e < 8 && col + e < N / 2; ++e) out[e] = e16[r * 16 + cc + e];
-              }
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-          }
-        } else if (cdt == TGM_F32) {
+        if (cdt == TGM_F32) {
           const int col = col0 + 32 * j + (lane & 31);
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
@@ -916,9 +872,9 @@ int launch_gemm_w(const void* a, int64_t lda, const void* w, const void* scales,
                   void* c, int cdt, int64_t ldc, hipStream_t stream, int splits = 1, float* part = nullptr) {
   const int64_t tiles = ((m + kWM - 1) / kWM) * ((n + kWN - 1) / kWN);
   const int cus = stream_cu_count(stream);
-  if (splits == 1 && !part && k % kVKMultiple == 0 && cus >= 8 && tiles >= cus) {
+  if (!SWIGLU && splits == 1 && !part && k % kVKMultiple == 0 && cus >= 8 && tiles >= cus) {
     // at least one round of tiles: persistent, one workgroup per CU (a multiple of 8 of them)
-    hipLaunchKernelGGL((gemm_w_stream<FMT, SCALED, SWIGLU>), dim3((unsigned)(cus / 8 * 8)), dim3(512), 0, stream,
+    hipLaunchKernelGGL((gemm_w_stream<FMT, SCALED>), dim3((unsigned)(cus / 8 * 8)), dim3(512), 0, stream,
                        (const uint8_t*)a, (unsigned)(lda * 2), (const uint8_t*)w, (const uint8_t*)scales, (int)m,
                        (int)n, (int)k, c, cdt, ldc);
     return launch_status(SWIGLU ? "tgm_gemm_w_swiglu" : "tgm_gemm_w");
