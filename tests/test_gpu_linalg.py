@@ -667,6 +667,25 @@ def test_gemm_mx_fp4_one_hot_is_exact(dev):
     assert np.array_equal(c, deq_b[:, cols].T.astype(np.float32))
 
 
+def test_gemm_mx_fp4_stream_one_hot_is_exact(dev):
+    """The persistent FP4 x FP4 kernel (K a multiple of 1024, 289 tiles: workgroups walk two tiles)
+    with one-hot A rows whose E8M0 scales vary per block: C is deq(B)[:, j] times A's scale of block
+    j / 32, exactly, in every output element -- the scale byte of every block, A's and B's, reaches
+    its MFMA (the per-half scale words and the byte each substep's MFMA selects)."""
+    m, n, k = 4352, 4352, 1024
+    rng = np.random.default_rng(12)
+    b, deq_b = make_weight(dev, "fp4_e2m1", n, k, "e8m0", rng)
+    cols = rng.choice(k, m, replace=True)
+    codes = np.zeros((m, k), np.uint8)
+    codes[np.arange(m), cols] = 2  # E2M1 code 2 = 1.0
+    e = (127 + rng.integers(-3, 4, (m, k // 32))).astype(np.uint8)
+    a = PackedTensor(torch.from_numpy(O.pack_codes(codes, 4)).to(dev), "fp4_e2m1", (m, k),
+                     torch.from_numpy(e).to(dev).view(torch.float8_e8m0fnu), 32)
+    c = matmul_nt(a, b, dtype=torch.float32).cpu().numpy()
+    scale_a = np.exp2(e[np.arange(m), cols // 32].astype(np.float64) - 127)
+    assert np.array_equal(c, (deq_b[:, cols].T * scale_a[:, None]).astype(np.float32))
+
+
 @pytest.mark.parametrize("mnk", [(8192, 8192, 8192), (4096, 14336, 4096)])
 def test_gemm_mx_fp4_full_size_sampled(dev, mnk):
     """The FP4 x FP4 GEMMs at full size (operands MX-quantised from N(0,1)) against the fp64 oracle,

@@ -28,6 +28,11 @@ the memory the committed kernel does and every wait ends.
                             tile switch's store drain (every step waits on vmcnt(0), which
                             counts stores as well as loads)
     plain_c_stores          ordinary instead of non-temporal C stores
+    no_scale_reads          the E8M0 words are never read from LDS (each substep keeps the
+                            prologue's): the cost of the scale reads
+    no_scale_batches        the E8M0 batches are never loaded into LDS: the cost of their loads
+    bf16_mfma               the bf16 MFMA (same cycles per instruction) on the same fragments
+                            instead of the scaled FP4 MFMA: the cost of the instruction itself
     launch_per_tile         the launch-per-tile kernel instead of the persistent one
     waves_2x2               launch per tile, 4 waves of 128 x 128 (one wave per SIMD)
 """
@@ -61,6 +66,13 @@ READ_IN_USE_ORDER_S = ("else read_item(fn, rbuf, ru, it - (FA + FB) == 0 ? 0 : i
 FRONT_LOADED = ("(it < nr ? it * (FA * FB / 2) / nr : FA * FB / 2 + (it - nr) * (FA * FB / 2) / (ni - nr + 1)) "
                 "== idx")
 C_STORE = "__builtin_nontemporal_store(*(const u32x4*)(ep + r * 32 + cc), (u32x4*)out);"
+SCALE_READ_A = "if (t < FA) sraw_a[t < FA ? t : 0] = *(const u32x2*)(ls + (wm * FA * 32 + t * 32 + (lane & 31)) * kBatchRow);"
+SCALE_READ_B = ("else sraw_b[t < FA ? 0 : t - FA] =\n"
+                "        *(const u32x2*)(ls + kBM * kBatchRow + (wn * FB * 32 + (t - FA) * 32 + (lane & 31)) * kBatchRow);")
+MX_MFMA = ("acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa, fb, acc[i][j], 4, 4, u, (int)xa[i], u,\n"
+           "                                                                    (int)xb[j]);")
+BF16_MFMA = ("acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(__attribute__((__vector_size__(16))) __bf16, f.a[i]),\n"
+             "            __builtin_bit_cast(__attribute__((__vector_size__(16))) __bf16, f.b[j]), acc[i][j], 0, 0, 0); (void)fa; (void)fb; (void)xa; (void)xb;")
 # (anchor that must precede the edit, old text, new text)
 VARIANTS: dict[str, list[tuple[str, str, str]]] = {
     "baseline": [],
@@ -68,8 +80,8 @@ VARIANTS: dict[str, list[tuple[str, str, str]]] = {
                        "(unsigned)at.m0 * kb + (unsigned)((at.st & 1) * kRowBytes)"),
                       (STREAM, "(unsigned)at.n0 * kb + (unsigned)(at.st * kRowBytes)",
                        "(unsigned)at.n0 * kb + (unsigned)((at.st & 1) * kRowBytes)")],
-    "no_step_barrier": [(STREAM, "    wait_lds_dma();\n    __syncthreads();\n    substep(f1, 3,",
-                         "    wait_lds_dma();\n    __builtin_amdgcn_sched_barrier(0);\n    substep(f1, 3,")],
+    "no_step_barrier": [(STREAM, "    wait_lds_dma();\n    __syncthreads();\n    substep(f1, U3{},",
+                         "    wait_lds_dma();\n    __builtin_amdgcn_sched_barrier(0);\n    substep(f1, U3{},")],
     "quarter_fragment_reads": [(STREAM, "else if (!scales) read_item(fn, rbuf, ru, it);",
                                 "else if (!scales) { if (ru == 0) read_item(fn, rbuf, ru, it); }")],
     "reads_in_use_order": [(STREAM, "else if (!scales) read_item(fn, rbuf, ru, it);", READ_IN_USE_ORDER),
@@ -79,6 +91,11 @@ VARIANTS: dict[str, list[tuple[str, str, str]]] = {
                                   (STREAM, "else if (!scales) read_item(fn, rbuf, ru, it);", READ_IN_USE_ORDER),
                                   (STREAM, "else read_item(fn, rbuf, ru, it - (FA + FB));", READ_IN_USE_ORDER_S)],
     "no_c_stores": [(STREAM, C_STORE, "(void)out;")],
+    "no_scale_reads": [(STREAM, SCALE_READ_A, "if (t < FA) { }"), (STREAM, SCALE_READ_B, "else { }")],
+    "no_scale_batches": [(STREAM, "    lds_dma16(rsa, la, (unsigned)(at.m0 + r) * kblk + boff);\n"
+                                  "    lds_dma16(rsb, la + kBM * kBatchRow, (unsigned)(at.n0 + r) * kblk + boff);",
+                          "    (void)la; (void)r; (void)boff;")],
+    "bf16_mfma": [(STREAM, MX_MFMA, BF16_MFMA)],
     "plain_c_stores": [(STREAM, C_STORE, "*(u32x4*)out = *(const u32x4*)(ep + r * 32 + cc);")],
     "launch_per_tile": [("extern \"C\"", PERSISTENT, "if (false) {")],
     "waves_2x2": [("extern \"C\"", PERSISTENT, "if (false) {"),

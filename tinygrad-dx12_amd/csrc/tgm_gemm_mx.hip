@@ -27,6 +27,8 @@
 // XCD-aware (tile_of).  For K a multiple of 1024 the same pipeline runs persistently, one
 // workgroup per CU streaming its tiles' steps back to back (gemm_mx_fp4_stream); other K
 // launch one workgroup per tile (gemm_mx_fp4).
+#include <type_traits>
+
 #include "tgm_mfma_common.h"
 
 namespace tgm {
@@ -375,7 +377,11 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4_stream(const uint8_t
     for (int p = 0; p < NP; ++p)
       if (p >= p0 && p < p1) dma_piece(o, buf, p);
   };
-  u32x2 scl_a[FA], scl_b[FB];
+  // E8M0 bytes of the lane's row for one step: the 8 blocks as read from LDS (raw), then the four
+  // blocks 2 u + half (u = 0 .. 3) of the lane's K half packed into one word per fragment, whose byte
+  // u the MFMA of substep u selects itself (op_sel), so no instruction sits between a scale and its use
+  u32x2 sraw_a[FA], sraw_b[FB];
+  unsigned sw_a[FA], sw_b[FB];
   f32x16 acc[FA][FB];
 #pragma unroll
   for (int i = 0; i < FA; ++i)
@@ -396,42 +402,54 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4_stream(const uint8_t
     else f.b[t < FA ? 0 : t - FA] = *(const u32x4*)(la + kPanel + fb_row + col + (t - FA) * 32 * kRowBytes);
   };
   const int sq = (lane >> 3) & 1;
-  auto scale_item = [&](int sn, int t) __attribute__((always_inline)) {  // scales of stream step sn
+  auto scale_item = [&](int sn, int t) __attribute__((always_inline)) {  // raw scales of stream step sn
     const int st = sn % kBatchSteps;
     const unsigned char* ls =
         lds + 2 * kBuffer + ((sn / kBatchSteps) & 1) * kBatch + ((st >> 1) ^ sq) * 16 + (st & 1) * 8;
-    if (t < FA) scl_a[t < FA ? t : 0] = *(const u32x2*)(ls + (wm * FA * 32 + t * 32 + (lane & 31)) * kBatchRow);
-    else scl_b[t < FA ? 0 : t - FA] =
+    if (t < FA) sraw_a[t < FA ? t : 0] = *(const u32x2*)(ls + (wm * FA * 32 + t * 32 + (lane & 31)) * kBatchRow);
+    else sraw_b[t < FA ? 0 : t - FA] =
         *(const u32x2*)(ls + kBM * kBatchRow + (wn * FB * 32 + (t - FA) * 32 + (lane & 31)) * kBatchRow);
   };
-  auto mfmas = [&](const Frags& f, int u, auto&& hook) __attribute__((always_inline)) {
-    const int blk = 2 * u + half;
-    int xa[FA], xb[FB];
+  // bytes half, 2 + half (word 0) and half, 2 + half (word 1) of the raw pair: blocks 2 u + half
+  const unsigned ssel = half ? 0x07050301u : 0x06040200u;
+  auto scale_word = [&](int t) __attribute__((always_inline)) {
+    if (t < FA) sw_a[t < FA ? t : 0] = __builtin_amdgcn_perm(sraw_a[t < FA ? t : 0][1], sraw_a[t < FA ? t : 0][0], ssel);
+    else sw_b[t < FA ? 0 : t - FA] = __builtin_amdgcn_perm(sraw_b[t < FA ? 0 : t - FA][1], sraw_b[t < FA ? 0 : t - FA][0], ssel);
+  };
+  auto mfmas = [&](const Frags& f, auto uc, auto&& hook) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;  // the MFMA's scale byte select
+    unsigned xa[FA], xb[FB];                // this substep's words (the hook may write the next step's)
 #pragma unroll
-    for (int t = 0; t < FA; ++t) xa[t] = (int)((u < 2 ? scl_a[t][0] : scl_a[t][1]) >> (8 * (blk & 3)));
+    for (int t = 0; t < FA; ++t) xa[t] = sw_a[t];
 #pragma unroll
-    for (int t = 0; t < FB; ++t) xb[t] = (int)((u < 2 ? scl_b[t][0] : scl_b[t][1]) >> (8 * (blk & 3)));
+    for (int t = 0; t < FB; ++t) xb[t] = sw_b[t];
 #pragma unroll
     for (int i = 0; i < FA; ++i)
 #pragma unroll
       for (int j = 0; j < FB; ++j) {
         const i32x8 fa = {(int)f.a[i][0], (int)f.a[i][1], (int)f.a[i][2], (int)f.a[i][3], 0, 0, 0, 0};
         const i32x8 fb = {(int)f.b[j][0], (int)f.b[j][1], (int)f.b[j][2], (int)f.b[j][3], 0, 0, 0, 0};
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa, fb, acc[i][j], 4, 4, 0, xa[i], 0, xb[j]);
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa, fb, acc[i][j], 4, 4, u, (int)xa[i], u,
+                                                                    (int)xb[j]);
         hook(i * FB + j);
       }
   };
-  constexpr int kMaxItems = 2 * (FA + FB) + NP;
-  auto substep = [&](const Frags& fc, int u, Frags& fn, int rbuf, int ru, bool scales, int sn, const StepOff* lo,
+  // Substep u's items, one after each MFMA share: the fragment reads of the next substep, or (the
+  // scales substep) the next step's raw scales and fragments, then load pieces, then (scales) the
+  // next step's scale words.
+  constexpr int kMaxItems = 3 * (FA + FB) + NP;
+  auto substep = [&](const Frags& fc, auto uc, Frags& fn, int rbuf, int ru, bool scales, int sn, const StepOff* lo,
                      int dbuf, int p0, int p1) __attribute__((always_inline)) {
     const int nr = (FA + FB) * (scales ? 2 : 1);
-    const int ni = nr + (p1 - p0);
-    mfmas(fc, u, [&](int idx) __attribute__((always_inline)) {
+    const int nd = nr + (p1 - p0);
+    const int ni = nd + (scales ? FA + FB : 0);
+    mfmas(fc, uc, [&](int idx) __attribute__((always_inline)) {
 #pragma unroll
       for (int it = 0; it < kMaxItems; ++it) {
         if (it < ni && it * FA * FB / ni == idx) {
           __builtin_amdgcn_sched_barrier(0);
-          if (it >= nr) dma_piece(*lo, dbuf, p0 + it - nr);
+          if (it >= nd) scale_word(it - nd);
+          else if (it >= nr) dma_piece(*lo, dbuf, p0 + it - nr);
           else if (!scales) read_item(fn, rbuf, ru, it);
           else if (it < FA + FB) scale_item(sn, it);
           else read_item(fn, rbuf, ru, it - (FA + FB));
@@ -440,6 +458,10 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4_stream(const uint8_t
       }
     });
   };
+  using U0 = std::integral_constant<int, 0>;
+  using U1 = std::integral_constant<int, 1>;
+  using U2 = std::integral_constant<int, 2>;
+  using U3 = std::integral_constant<int, 3>;
   set_tile(0);
   issue_batch(0);
   dma_pieces(0, 0, 0, NP);
@@ -457,16 +479,18 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4_stream(const uint8_t
     __builtin_amdgcn_sched_barrier(0);
     read_item(f0, 0, 0, t);
   }
+#pragma unroll
+  for (int t = 0; t < FA + FB; ++t) scale_word(t);
   __builtin_amdgcn_sched_barrier(0);
   auto step = [&](int gs, int cur, bool batch) __attribute__((always_inline)) {
     const StepOff o1 = step_off(gs + 1), o2 = step_off(gs + 2);
-    substep(f0, 0, f1, cur, 1, false, 0, &o1, cur ^ 1, NP / 2, NP);
-    substep(f1, 1, f0, cur, 2, false, 0, &o1, 0, 0, 0);
-    substep(f0, 2, f1, cur, 3, false, 0, &o1, 0, 0, 0);
+    substep(f0, U0{}, f1, cur, 1, false, 0, &o1, cur ^ 1, NP / 2, NP);
+    substep(f1, U1{}, f0, cur, 2, false, 0, &o1, 0, 0, 0);
+    substep(f0, U2{}, f1, cur, 3, false, 0, &o1, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     wait_lds_dma();
     __syncthreads();
-    substep(f1, 3, f0, cur ^ 1, 0, true, gs + 1, &o2, cur, 0, NP / 2);
+    substep(f1, U3{}, f0, cur ^ 1, 0, true, gs + 1, &o2, cur, 0, NP / 2);
     __builtin_amdgcn_sched_barrier(0);
     if (batch) issue_batch(gs / kBatchSteps + 1);
     __builtin_amdgcn_sched_barrier(0);
