@@ -251,11 +251,27 @@ def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup:
 
     settle(torch, stream, launch, warmup)
     ms = median_launch_ms(torch, stream, launch, steps)
+    zero_ms = zero_operand_ms(torch, stream, prog, c, a.data, b.data, steps, warmup)
     flops, nbytes = prog.estimates.ops, prog.estimates.mem
     return {"workload": f"fp4xfp4 e8m0/32 GEMM M={m} N={n} K={k} bf16 out", "ms": ms, "TFLOPS": flops / ms / 1e9,
             "flops": flops, "bytes": nbytes, "GB/s": nbytes / ms / 1e6, "timed_dispatches": steps,
+            "zero_operands_ms": zero_ms, "zero_operands_TFLOPS": flops / zero_ms / 1e9,
             "roofline": mfma_roofline(flops, ms, FP4_PEAK_TFLOPS, "dense MXFP4 MFMA"),
             "vendor": vendor_fp4_gemm(m, n, k, steps) if vendor else None}
+
+
+def zero_operand_ms(torch, stream, prog, c, a, b, steps: int, warmup: int) -> float:
+    """The same kernel program on all-zero operand bytes of the same sizes (same scales, same
+    launch): the instruction stream, memory traffic and stalls are those of the real product, only
+    the operand bits stop toggling.  The difference to the real time is what the MFMAs' switching
+    power costs through the clock the chip can hold (not part of any workload's value)."""
+    za, zb = torch.zeros_like(a), torch.zeros_like(b)
+
+    def launch() -> None:
+        prog.launch(c.data_ptr(), za.data_ptr(), zb.data_ptr(), stream.cuda_stream)
+
+    settle(torch, stream, launch, warmup)
+    return median_launch_ms(torch, stream, launch, steps)
 
 
 VENDOR_BAR = ROOT / "tinygrad-dx12_amd" / "tinygrad_mi355x" / "_lib" / "ck_mx_gemm_bar"
@@ -341,6 +357,7 @@ def dense_gemm_workload(torch, K, dev, dtype: str, n: int, steps: int, warmup: i
 
     settle(torch, stream, launch, warmup)
     ms = median_launch_ms(torch, stream, launch, steps)
+    zero_ms = zero_operand_ms(torch, stream, prog, c, a, b, steps, warmup)
     bt = b.t()  # column-major [K, N] view: hipBLASLt's natural B layout for C = A B^T
     if fp8:
         def library() -> None:
@@ -357,6 +374,7 @@ def dense_gemm_workload(torch, K, dev, dtype: str, n: int, steps: int, warmup: i
     return {"workload": f"{dtype} x {dtype} GEMM M=N=K={n} bf16 out ({prog.name})", "ms": ms,
             "TFLOPS": flops / ms / 1e9, "flops": flops, "bytes": nbytes, "timed_dispatches": steps,
             "hipblaslt_ms": lib_ms, "hipblaslt_TFLOPS": flops / lib_ms / 1e9,
+            "zero_operands_ms": zero_ms, "zero_operands_TFLOPS": flops / zero_ms / 1e9,
             "roofline": mfma_roofline(flops, ms, peak, "dense fp8 MFMA" if fp8 else "dense bf16 MFMA")}
 
 

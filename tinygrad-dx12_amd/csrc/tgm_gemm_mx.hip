@@ -278,9 +278,10 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4(const uint8_t* __res
 // gemm_mx_fp4 runs across tile boundaries unchanged: the loads of the next tile's first two
 // steps are issued during the current tile's last two, so a tile starts with its operands in LDS
 // instead of waiting for them, and no workgroup is launched per tile.  At a tile's end the
-// accumulators go to C through the idle scale buffer (see the epilogue) with non-temporal
-// stores: a round of tiles writes as much C per XCD (32 x 128 KB) as the XCD's L2 holds, and
-// ordinary stores would evict the operand panels the running tiles share.
+// accumulators go to C through the idle scale buffer (see the epilogue) with ordinary stores (in
+// one process against non-temporal ones: 251.4 against 253.0 us at 8192^3, 134.0 against 137.4 us
+// at 4096 x 14336 x 4096; a round of tiles writes as much C per XCD, 32 x 128 KB, as its L2 holds,
+// but a store that completes in L2 holds up the next step's load wait for less time).
 template <int WM, int WN>
 __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4_stream(const uint8_t* __restrict__ a,
                                                                    const uint8_t* __restrict__ sa,
@@ -434,15 +435,16 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4_stream(const uint8_t
         hook(i * FB + j);
       }
   };
-  // Substep u's items, one after each MFMA share: the fragment reads of the next substep, or (the
-  // scales substep) the next step's raw scales and fragments, then load pieces, then (scales) the
-  // next step's scale words.
+  // Substep u's items, one after each MFMA share, in this order: the fragment reads of the next
+  // substep (from buffer rbuf), then with ``rs`` the raw E8M0 bytes of stream step sn, then load
+  // pieces [p0, p1) into buffer dbuf, then with ``words`` the scale words of the step just read.
   constexpr int kMaxItems = 3 * (FA + FB) + NP;
-  auto substep = [&](const Frags& fc, auto uc, Frags& fn, int rbuf, int ru, bool scales, int sn, const StepOff* lo,
-                     int dbuf, int p0, int p1) __attribute__((always_inline)) {
-    const int nr = (FA + FB) * (scales ? 2 : 1);
+  auto substep = [&](const Frags& fc, auto uc, Frags& fn, int rbuf, int ru, bool rs, int sn, bool words,
+                     const StepOff* lo, int dbuf, int p0, int p1) __attribute__((always_inline)) {
+    const int nf = FA + FB;
+    const int nr = nf + (rs ? FA + FB : 0);
     const int nd = nr + (p1 - p0);
-    const int ni = nd + (scales ? FA + FB : 0);
+    const int ni = nd + (words ? FA + FB : 0);
     mfmas(fc, uc, [&](int idx) __attribute__((always_inline)) {
 #pragma unroll
       for (int it = 0; it < kMaxItems; ++it) {
@@ -450,9 +452,8 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4_stream(const uint8_t
           __builtin_amdgcn_sched_barrier(0);
           if (it >= nd) scale_word(it - nd);
           else if (it >= nr) dma_piece(*lo, dbuf, p0 + it - nr);
-          else if (!scales) read_item(fn, rbuf, ru, it);
-          else if (it < FA + FB) scale_item(sn, it);
-          else read_item(fn, rbuf, ru, it - (FA + FB));
+          else if (it >= nf) scale_item(sn, it - nf);
+          else read_item(fn, rbuf, ru, it);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -482,15 +483,26 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4_stream(const uint8_t
 #pragma unroll
   for (int t = 0; t < FA + FB; ++t) scale_word(t);
   __builtin_amdgcn_sched_barrier(0);
+  // Step gs from buffer cur:
+  //   u0 (f0): read f1 <- u1; second half of step gs + 1's loads (into the other buffer)
+  //   u1 (f1): read f0 <- u2; the raw E8M0 bytes of step gs + 1.  Its batch is complete (a batch is
+  //       issued four steps ahead of its first step and waited for by the step after that), and
+  //       the batch that will overwrite a buffer is issued only after the barrier of the step whose
+  //       scales it last held were read two steps before, so the reads need no barrier of their own
+  //       and stay out of the burst of reads that follows the step barrier
+  //   u2 (f0): read f1 <- u3
+  //   wait for this wave's loads of step gs + 1, barrier
+  //   u3 (f1): read f0 <- u0 of step gs + 1 (other buffer); first half of step gs + 2's loads (into
+  //       this buffer); the scale words of step gs + 1
   auto step = [&](int gs, int cur, bool batch) __attribute__((always_inline)) {
     const StepOff o1 = step_off(gs + 1), o2 = step_off(gs + 2);
-    substep(f0, U0{}, f1, cur, 1, false, 0, &o1, cur ^ 1, NP / 2, NP);
-    substep(f1, U1{}, f0, cur, 2, false, 0, &o1, 0, 0, 0);
-    substep(f0, U2{}, f1, cur, 3, false, 0, &o1, 0, 0, 0);
+    substep(f0, U0{}, f1, cur, 1, false, 0, false, &o1, cur ^ 1, NP / 2, NP);
+    substep(f1, U1{}, f0, cur, 2, true, gs + 1, false, &o1, 0, 0, 0);
+    substep(f0, U2{}, f1, cur, 3, false, 0, false, &o1, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     wait_lds_dma();
     __syncthreads();
-    substep(f1, U3{}, f0, cur ^ 1, 0, true, gs + 1, &o2, cur, 0, NP / 2);
+    substep(f1, U3{}, f0, cur ^ 1, 0, false, 0, true, &o2, cur, 0, NP / 2);
     __builtin_amdgcn_sched_barrier(0);
     if (batch) issue_batch(gs / kBatchSteps + 1);
     __builtin_amdgcn_sched_barrier(0);
@@ -546,7 +558,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mx_fp4_stream(const uint8_t
             uint16_t* out = (uint16_t*)c + (int64_t)row * ldc + col;
             if (row < M) {
               if (col + 7 < N && ((uintptr_t)out & 15) == 0) {
-                __builtin_nontemporal_store(*(const u32x4*)(ep + r * 32 + cc), (u32x4*)out);
+                *(u32x4*)out = *(const u32x4*)(ep + r * 32 + cc);
               } else {  // the ragged edge, element by element from LDS (a rolled loop holds no row in VGPRs)
 #pragma unroll 1
                 for (int e = 0; e < 8 && col + e < N; ++e) out[e] = ep[r * 32 + cc + e];
