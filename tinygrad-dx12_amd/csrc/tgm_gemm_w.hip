@@ -496,10 +496,14 @@ __global__ void __launch_bounds__(512) gemm_w_stream(const uint8_t* __restrict__
   //   j = 0: A of j = 1; block 1 of the packed weights; pieces [NP0, NP1) of step gs + 1
   //   j = 1: A of j = 2; the remaining pieces of step gs + 1
   //   j = 2: A of j = 3; decode block 1 (MFMAs 4 .. 7)
-  //   j = 3 .. 6: A of j + 1
+  //   j = 3: A of j = 4; the E8M0 words of step gs + 1.  Their batch is complete (a batch is issued
+  //          four steps ahead of its first step and waited for by the step after that), and the batch
+  //          that overwrites a buffer is issued only after the barrier of the step whose words it
+  //          last held were read two steps before, so the reads need no barrier of their own
+  //   j = 4 .. 6: A of j + 1
   //   wait for this wave's loads of step gs + 1, barrier
-  //   j = 7: A of step gs + 1's j = 0, its E8M0 words and block 0 of its packed weights (other
-  //          buffer); pieces [0, NP0) of step gs + 2 (into this buffer); decode block 0
+  //   j = 7: A of step gs + 1's j = 0 and block 0 of its packed weights (other buffer); pieces
+  //          [0, NP0) of step gs + 2 (into this buffer); decode block 0
   constexpr int NP1 = NP0 + (NP - NP0 + 1) / 2;
   auto step = [&](int gs, int cur, bool batch) __attribute__((always_inline)) {
     const StepOff o1 = step_off(gs + 1), o2 = step_off(gs + 2);
@@ -516,18 +520,21 @@ __global__ void __launch_bounds__(512) gemm_w_stream(const uint8_t* __restrict__
       if (it < FA) read_a(cur, 3, it);
       else decode(it - FA, 1);
     });
+    run_items(3, FA + FB, [&](int it) __attribute__((always_inline)) {
+      if (it < FA) read_a(cur, 4, it);
+      else read_scale(gs + 1, it - FA);  // its batch is complete (see below): no barrier needed
+    });
 #pragma unroll
-    for (int j = 3; j < 7; ++j)
+    for (int j = 4; j < 7; ++j)
       run_items(j, FA, [&](int it) __attribute__((always_inline)) { read_a(cur, j + 1, it); });
     __builtin_amdgcn_sched_barrier(0);
     wait_lds_dma();  // this wave's loads of step gs + 1 (and of a scale batch issued at step gs - 3)
     __syncthreads();
-    run_items(7, FA + FB + FB * NRB + NP0 + FB, [&](int it) __attribute__((always_inline)) {
+    run_items(7, FA + FB * NRB + NP0 + FB, [&](int it) __attribute__((always_inline)) {
       if (it < FA) read_a(cur ^ 1, 0, it);
-      else if (it < FA + FB) read_scale(gs + 1, it - FA);
-      else if (it < FA + FB + FB * NRB) read_raw(cur ^ 1, (it - FA - FB) / NRB, 0, (it - FA - FB) % NRB);
-      else if (it < FA + FB + FB * NRB + NP0) dma_piece(o2, cur, it - FA - FB - FB * NRB);
-      else decode(it - FA - FB - FB * NRB - NP0, 0);
+      else if (it < FA + FB * NRB) read_raw(cur ^ 1, (it - FA) / NRB, 0, (it - FA) % NRB);
+      else if (it < FA + FB * NRB + NP0) dma_piece(o2, cur, it - FA - FB * NRB);
+      else decode(it - FA - FB * NRB - NP0, 0);
     });
     __builtin_amdgcn_sched_barrier(0);
     // Batch b + 1 goes to the buffer batch b - 1 used; its last reads (step 4 b - 1's words, in
