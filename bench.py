@@ -233,7 +233,8 @@ def median_launch_ms(torch, stream, launch, steps: int) -> float:
     return statistics.median(e0.elapsed_time(e1) for e0, e1 in events)
 
 
-def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup: int, vendor: bool = False) -> dict:
+def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup: int, vendor: bool = False,
+                      zero: bool = False) -> dict:
     """FP4 x FP4 + E8M0/32 GEMM C[M,N] = deq(A) deq(B)^T, bf16 out: A [M, K] and B [N, K] drawn
     N(0, 1) and MX-quantised along K (round to nearest even, shared exponent per 32)."""
     from tinygrad_mi355x.codegen.decomp.mi355x import quantize_mx
@@ -251,11 +252,11 @@ def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup:
 
     settle(torch, stream, launch, warmup)
     ms = median_launch_ms(torch, stream, launch, steps)
-    zero_ms = zero_operand_ms(torch, stream, prog, c, a.data, b.data, steps, warmup)
+    zero_ms = zero_operand_ms(torch, stream, prog, c, a.data, b.data, steps, warmup) if zero else None
     flops, nbytes = prog.estimates.ops, prog.estimates.mem
     return {"workload": f"fp4xfp4 e8m0/32 GEMM M={m} N={n} K={k} bf16 out", "ms": ms, "TFLOPS": flops / ms / 1e9,
             "flops": flops, "bytes": nbytes, "GB/s": nbytes / ms / 1e6, "timed_dispatches": steps,
-            "zero_operands_ms": zero_ms, "zero_operands_TFLOPS": flops / zero_ms / 1e9,
+            "zero_operands_ms": zero_ms, "zero_operands_TFLOPS": flops / zero_ms / 1e9 if zero_ms else None,
             "roofline": mfma_roofline(flops, ms, FP4_PEAK_TFLOPS, "dense MXFP4 MFMA"),
             "vendor": vendor_fp4_gemm(m, n, k, steps) if vendor else None}
 
@@ -263,8 +264,10 @@ def fp4_gemm_workload(torch, K, dev, m: int, n: int, k: int, steps: int, warmup:
 def zero_operand_ms(torch, stream, prog, c, a, b, steps: int, warmup: int) -> float:
     """The same kernel program on all-zero operand bytes of the same sizes (same scales, same
     launch): the instruction stream, memory traffic and stalls are those of the real product, only
-    the operand bits stop toggling.  The difference to the real time is what the MFMAs' switching
-    power costs through the clock the chip can hold (not part of any workload's value)."""
+    the operand bits stop toggling.  The difference to the real time is what the operands'
+    switching power costs through the clock the chip can hold (not part of any workload's value).
+    Run in the full bench line only: its launches follow the timed ones, and a profile of a single
+    workload takes its last launches as the timed ones."""
     za, zb = torch.zeros_like(a), torch.zeros_like(b)
 
     def launch() -> None:
@@ -335,7 +338,7 @@ def fp6_gemm_workload(torch, K, dev, fmt: str, steps: int, warmup: int, m: int =
             "roofline": mfma_roofline(flops, ms, BF16_PEAK_TFLOPS, "dense bf16 MFMA (the activations stay bf16)")}
 
 
-def dense_gemm_workload(torch, K, dev, dtype: str, n: int, steps: int, warmup: int) -> dict:
+def dense_gemm_workload(torch, K, dev, dtype: str, n: int, steps: int, warmup: int, zero: bool = False) -> dict:
     """Ordinary product C[N,N] = A B^T (A, B [N, N], K-contiguous) on this library's kernel
     (tgm_gemm_dense for bf16, tgm_gemm_fp8 for float8_e4m3fn with per-tensor scales 1), bf16 out,
     with hipBLASLt timed on the same operands in the same run for comparison (torch.matmul for
@@ -357,7 +360,7 @@ def dense_gemm_workload(torch, K, dev, dtype: str, n: int, steps: int, warmup: i
 
     settle(torch, stream, launch, warmup)
     ms = median_launch_ms(torch, stream, launch, steps)
-    zero_ms = zero_operand_ms(torch, stream, prog, c, a, b, steps, warmup)
+    zero_ms = zero_operand_ms(torch, stream, prog, c, a, b, steps, warmup) if zero else None
     bt = b.t()  # column-major [K, N] view: hipBLASLt's natural B layout for C = A B^T
     if fp8:
         def library() -> None:
@@ -374,7 +377,7 @@ def dense_gemm_workload(torch, K, dev, dtype: str, n: int, steps: int, warmup: i
     return {"workload": f"{dtype} x {dtype} GEMM M=N=K={n} bf16 out ({prog.name})", "ms": ms,
             "TFLOPS": flops / ms / 1e9, "flops": flops, "bytes": nbytes, "timed_dispatches": steps,
             "hipblaslt_ms": lib_ms, "hipblaslt_TFLOPS": flops / lib_ms / 1e9,
-            "zero_operands_ms": zero_ms, "zero_operands_TFLOPS": flops / zero_ms / 1e9,
+            "zero_operands_ms": zero_ms, "zero_operands_TFLOPS": flops / zero_ms / 1e9 if zero_ms else None,
             "roofline": mfma_roofline(flops, ms, peak, "dense fp8 MFMA" if fp8 else "dense bf16 MFMA")}
 
 
@@ -869,8 +872,10 @@ def main() -> int:
         "int4_gemv_n14336": lambda: int4_gemv_workload(torch, K, dev, 14336, steps, warmup),
         "fp6_e3m2_gemm_m2048": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e3m2", gemm_steps, 20),
         "fp6_e2m3_gemm_m2048": lambda: fp6_gemm_workload(torch, K, dev, "fp6_e2m3", gemm_steps, 20),
-        # the vendor comparison runs in a child process, so it is left out of --only runs (profiles)
-        "fp4_gemm_8192": lambda: fp4_gemm_workload(torch, K, dev, 8192, 8192, 8192, gemm_steps, 20, not args.only),
+        # the vendor comparison (a child process) and the zero-operand timing are left out of --only runs
+        # (profiles take a run's last launches as its timed ones)
+        "fp4_gemm_8192": lambda: fp4_gemm_workload(torch, K, dev, 8192, 8192, 8192, gemm_steps, 20, not args.only,
+                                                   not args.only),
         "fp4_gemm_4096x14336x4096": lambda: fp4_gemm_workload(torch, K, dev, 4096, 14336, 4096, gemm_steps, 20,
                                                                not args.only),
         "decoder_b1": lambda: decoder_workload(torch, dev, 1),
@@ -883,7 +888,7 @@ def main() -> int:
         "fp4_gemv_shard_n1792_m1": lambda: fp4_gemv_workload(torch, K, dev, 1, steps, warmup, 1792),
         "fp4_gemv_shard_n1792_m4": lambda: fp4_gemv_workload(torch, K, dev, 4, steps, warmup, 1792),
         "fp4_gemv_shard_n1792_m16": lambda: fp4_gemv_workload(torch, K, dev, 16, steps, warmup, 1792),
-        "bf16_gemm_8192": lambda: dense_gemm_workload(torch, K, dev, "bfloat16", 8192, gemm_steps, 20),
+        "bf16_gemm_8192": lambda: dense_gemm_workload(torch, K, dev, "bfloat16", 8192, gemm_steps, 20, not args.only),
         "fp8_gemm_8192": lambda: dense_gemm_workload(torch, K, dev, "float8_e4m3fn", 8192, gemm_steps, 20),
         "uop_rowsum_16384x4096": lambda: uop_rowsum_workload(steps, warmup),
         "uop_gemm_bf16_4096_relu": lambda: uop_gemm_workload(gemm_steps, 20),
