@@ -381,6 +381,41 @@ def test_gemv_int4_mfma_parity(dev, fmt, sdt, bs, m):
 
 
 @pytest.mark.parametrize("fmt", ["int4", "uint4"])
+@pytest.mark.parametrize("sdt,bs", [(torch.float16, 32), (torch.bfloat16, 64), (torch.float32, 32),
+                                    (torch.float16, 128), (None, 32)])
+@pytest.mark.parametrize("nkm", [(1000, 1024, 2), (6144, 4096, 8), (300, 2048, 16), (4100, 2048, 5),
+                                 (14336, 1024, 3), (300, 3072, 16)])
+def test_gemv_int4_xr_parity(dev, fmt, sdt, bs, nkm):
+    """INT4/UINT4 x fp16 GEMV with the activations in registers (K = 1024, 2048, 4096 and
+    2 <= M <= 16): 1 row tile per workgroup (1000, 300 rows: 4- and 8-row workgroups), 2 (6144,
+    4100 rows: 24 and 20) and 4 (14336 rows: 56), every scale type and group size, one, two and
+    four K super-steps per wave.  K = 3072 (slices of 6-48 scale bytes) takes the LDS-staging
+    kernel."""
+    n, k, m = nkm
+    rng = np.random.default_rng(n + k + m + bs)
+    w, deq = int4_weight(dev, fmt, n, k, sdt, bs, rng)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float16)).to(dev)
+    y = matmul_nt(x, w, dtype=torch.float32)
+    assert O.max_rel_err(y.cpu().numpy(), x.float().cpu().numpy().astype(np.float64) @ deq.T) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["int4", "uint4"])
+@pytest.mark.parametrize("bs", [32, 128])
+def test_gemv_int4_xr_one_hot_is_exact(dev, fmt, bs):
+    """Register-activation INT4 GEMV (6144 x 4096, M = 8: two row tiles per workgroup, four
+    super-steps per wave): one-hot rows recover code * scale exactly for columns in every
+    wave's K slice, block, lane group and code position."""
+    n, k, m = 6144, 4096, 8
+    rng = np.random.default_rng(40 + bs)
+    w, deq = int4_weight(dev, fmt, n, k, torch.float16, bs, rng)
+    for cols in ([0, 1, 7, 8, 31, 32, 127, 128], [511, 512, 1000, 2047, 2048, 3000, 4094, 4095]):
+        x = torch.zeros((m, k), dtype=torch.float16, device=dev)
+        x[torch.arange(m), torch.tensor(cols)] = 1.0
+        y = matmul_nt(x, w, dtype=torch.float32).cpu().numpy()
+        assert np.array_equal(y, deq[:, cols].T.astype(np.float32)), cols
+
+
+@pytest.mark.parametrize("fmt", ["int4", "uint4"])
 def test_gemv_int4_one_hot_is_exact(dev, fmt):
     """One-hot fp16 activation rows recover code * scale exactly (fp32 out): nibble order,
     block K order and the per-block scale FMA line up."""

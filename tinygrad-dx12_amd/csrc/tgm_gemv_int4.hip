@@ -64,10 +64,12 @@ __device__ __forceinline__ void transpose4(unsigned& r0, unsigned& r1, unsigned&
   swap16(r2, r3);
 }
 
-// A workgroup holds NT x NK waves: wave (ti, ki) owns weight tile blockIdx.x * NT + ti (16
-// rows) and the ki-th of NK contiguous slices of its 128-element super-steps (at most
-// SMAX).  Each super-step lane (c, q) loads 16 bytes of row c -- block q of the four -- and
-// the row's scales of the super-step's blocks (4 / G groups, one vector load); a lane-row
+// A workgroup owns rpw consecutive weight rows (rpw <= 16 NT) and holds NT x NK waves: wave
+// (ti, ki) owns the 16-row tile starting at row blockIdx.x * rpw + 16 ti (rows past the
+// workgroup's range are clamped to its last row and not stored) and the ki-th of NK
+// contiguous slices of its 128-element super-steps (at most SMAX).  Each super-step lane
+// (c, q) loads 16 bytes of row c -- block q of the four -- and the row's scales of the
+// super-step's blocks (4 / G groups, one vector load); a lane-row
 // transpose hands each MFMA u the dword q of block u.  D super-steps are in flight;
 // refills past the slice re-read its last super-step, so every load is unconditional.  The
 // activations are copied to LDS once ([M][K + 8] fp16) and each step's operands are read
@@ -76,7 +78,8 @@ template <int NT, int NK, int SMAX, int G, int SDT, int XP>
 __global__ void __launch_bounds__(NT * NK * 64) gemv_int4(const uint8_t* __restrict__ w, int64_t N, int64_t K,
                                                         const uint8_t* __restrict__ scales, int64_t ngroups,
                                                         unsigned flip, float bias, const _Float16* __restrict__ x,
-                                                        int M, int64_t ldx, void* __restrict__ y, int ydt, int64_t ldy) {
+                                                        int M, int64_t ldx, void* __restrict__ y, int ydt, int64_t ldy,
+                                                        int rpw) {
   constexpr int D = SMAX < 8 ? SMAX : 8;
   constexpr bool SCALED = SDT >= 0;
   constexpr int SSIZE = SDT == TGM_F32 ? 4 : 2;
@@ -90,8 +93,10 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_int4(const uint8_t* __restr
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ti = wave % NT, ki = wave / NT;
   const int c = lane & 15, q = lane >> 4;
-  const int64_t n0 = ((int64_t)blockIdx.x * NT + ti) * 16;
-  const int64_t row = n0 + c < N ? n0 + c : N - 1;  // clamped: rows >= N are computed, not stored
+  const int64_t wg0 = (int64_t)blockIdx.x * rpw;
+  const int64_t wg_end = wg0 + rpw < N ? wg0 + rpw : N;  // rows of this workgroup: [wg0, wg_end)
+  const int64_t n0 = wg0 + 16 * ti;
+  const int64_t row = n0 + c < wg_end ? n0 + c : wg_end - 1;  // clamped rows are computed, not stored
   const int S = (int)(K / 128);
   const int per = (S + NK - 1) / NK;
   const int t_begin = ki * per < S ? ki * per : S;
@@ -209,7 +214,7 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_int4(const uint8_t* __restr
       for (int v = 0; v < 4; ++v) acc[v] += partial[((kk * NT + ti) * 64 + lane) * 4 + v];
   }
   // Lane (c, q) holds Y[4 q + v][n0 + c].
-  if (n0 + c < N) {
+  if (n0 + c < wg_end) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int m = 4 * q + v;
@@ -218,10 +223,179 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_int4(const uint8_t* __restr
   }
 }
 
+// Activations in registers, for K = 1024 KS (KS = 1, 2, 4) and 2 <= M <= 16 (the decoder's
+// projections at batch 2-16).  A workgroup owns rpw <= 16 T consecutive weight rows as T
+// 16-row tiles (rows past its range clamped to its last row, computed and not stored) and
+// holds 8 waves; wave ki owns K super-steps [ki KS, ki KS + KS) of every tile.  Its MFMA A
+// operands -- X rows c < M at the 16 blocks of its slice (zero for c >= M, whose D rows are
+// never stored) -- are loaded once into 16 KS registers straight from global memory, so no
+// workgroup stages X through LDS and no barrier precedes the first MFMA.  Then, for every
+// tile, the slice's codes (one 16-byte load per lane and super-step, transposed across lane
+// rows as in gemv_int4) and the row's scale groups of the slice (one vector load) are all
+// issued before the first MFMA.  The 8 waves' partial tiles meet in LDS; wave t < T sums
+// tile t and stores it.  Exactness and nibble order as in gemv_int4.
+template <int T, int KS, int G, int SDT>
+__global__ void __launch_bounds__(512) gemv_int4_xr(const uint8_t* __restrict__ w, int64_t N, int64_t K,
+                                                   const uint8_t* __restrict__ scales, int64_t ngroups,
+                                                   unsigned flip, float bias, const _Float16* __restrict__ x,
+                                                   int M, int64_t ldx, void* __restrict__ y, int ydt, int64_t ldy,
+                                                   int rpw) {
+  constexpr bool SCALED = SDT >= 0;
+  constexpr int SSIZE = SDT == TGM_F32 ? 4 : 2;
+  constexpr int GPS = 4 / G;              // scale groups per super-step
+  constexpr int SB = KS * GPS * SSIZE;    // scale bytes per row and slice: 2 .. 64
+  constexpr int SW = SB < 4 ? 1 : SB / 4;
+  __shared__ __attribute__((aligned(16))) float partial[8][T][64][4];
+  const int lane = threadIdx.x & 63;
+  const int ki = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, q = lane >> 4;
+  const int64_t wg0 = (int64_t)blockIdx.x * rpw;
+  const int64_t wg_end = wg0 + rpw < N ? wg0 + rpw : N;  // rows of this workgroup: [wg0, wg_end)
+  const int t0 = ki * KS;                                 // first super-step of the slice
+  const half2v hbias = {(_Float16)bias, (_Float16)bias};
+
+  // lanes of rows c >= M load nothing (their D rows are never stored): M x 1 KB per super-step
+  // of requests instead of 16 x 1 KB
+  half8 xa[KS][4];
+  {
+    const _Float16* xp = x + (int64_t)(c < M ? c : 0) * ldx + t0 * 128 + 8 * q;
+#pragma unroll
+    for (int j = 0; j < KS; ++j)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) xa[j][u] = c < M ? *(const half8*)(xp + j * 128 + 32 * u) : half8{};
+  }
+  u32x4 codes[T][KS];
+  unsigned sraw[T][SW];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t n0 = wg0 + 16 * t;
+    const int64_t row = n0 + c < wg_end ? n0 + c : wg_end - 1;
+    const uint8_t* wrow = w + row * (K / 2) + t0 * 64 + 16 * q;
+#pragma unroll
+    for (int j = 0; j < KS; ++j) codes[t][j] = __builtin_nontemporal_load((const u32x4*)(wrow + 64 * j));
+    if constexpr (SCALED) {
+      const uint8_t* p = scales + row * ngroups * SSIZE + t0 * GPS * SSIZE;  // SB-aligned (host)
+      if constexpr (SB == 2) {
+        sraw[t][0] = *(const uint16_t*)p;
+      } else if constexpr (SB == 4) {
+        sraw[t][0] = *(const unsigned*)p;
+      } else if constexpr (SB == 8) {
+        const u32x2 v = *(const u32x2*)p;
+        sraw[t][0] = v[0]; sraw[t][1] = v[1];
+      } else {
+#pragma unroll
+        for (int i = 0; i < SB / 16; ++i) {
+          const u32x4 v = *(const u32x4*)(p + 16 * i);
+          sraw[t][4 * i] = v[0]; sraw[t][4 * i + 1] = v[1]; sraw[t][4 * i + 2] = v[2]; sraw[t][4 * i + 3] = v[3];
+        }
+      }
+    }
+  }
+  // Every load is issued before any of them is used: without this barrier the scheduler pulls
+  // the first transpose's register copies up behind the first code load, and its wait for
+  // that load holds back every load after it.
+  __builtin_amdgcn_sched_barrier(0);
+  // scale of group g (0 .. KS GPS - 1) of the slice from tile t's raw words
+  auto scale_of = [&](int t, int g) __attribute__((always_inline)) {
+    if constexpr (SSIZE == 4) {
+      return __builtin_bit_cast(float, sraw[t][g]);
+    } else {
+      const unsigned h = (sraw[t][g >> 1] >> (16 * (g & 1))) & 0xFFFFu;
+      if constexpr (SDT == TGM_F16) return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
+      else return __builtin_bit_cast(float, h << 16);
+    }
+  };
+  f32x4v acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    acc[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+      unsigned d[4] = {codes[t][j][0], codes[t][j][1], codes[t][j][2], codes[t][j][3]};
+      transpose4(d[0], d[1], d[2], d[3]);
+      f32x4v part = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const half8 wb = int4_to_half8(d[u], flip, hbias);
+        part = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j][u], wb, part, 0, 0, 0);
+        if ((u + 1) % G == 0) {  // end of a scale group
+          const float s = SCALED ? scale_of(t, j * GPS + u / G) : 1.0f;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(s, part[v], acc[t][v]);
+          part = f32x4v{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) *(f32x4v*)partial[ki][t][lane] = acc[t];
+  __syncthreads();
+  if (ki >= T) return;
+  const int t = ki;  // this wave sums and stores tile t
+  f32x4v sum = *(const f32x4v*)partial[0][t][lane];
+#pragma unroll
+  for (int kk = 1; kk < 8; ++kk) {
+    const f32x4v p = *(const f32x4v*)partial[kk][t][lane];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) sum[v] += p[v];
+  }
+  // Lane (c, q) holds Y[4 q + v][n0 + c].
+  const int64_t n0 = wg0 + 16 * t;
+  if (n0 + c < wg_end) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = 4 * q + v;
+      if (m < M) store_from_f32(y, ydt, (int64_t)m * ldy + n0 + c, sum[v]);
+    }
+  }
+}
+
+template <int T, int KS, int G, int SDT>
+int launch_int4_xr_t(unsigned grid, hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales,
+                     int64_t ngroups, bool sgn, const void* x, int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy,
+                     int rpw) {
+  hipLaunchKernelGGL((gemv_int4_xr<T, KS, G, SDT>), dim3(grid), dim3(512), 0, s, (const uint8_t*)w, n, k,
+                     (const uint8_t*)scales, ngroups, sgn ? 0x88888888u : 0u, sgn ? 1032.0f : 1024.0f,
+                     (const _Float16*)x, (int)m, ldx, y, ydt, ldy, rpw);
+  return TGM_OK;
+}
+
+// gemv_int4_xr for K = 1024 KS (KS = 1, 2, 4: a slice's scale bytes are then a power of two,
+// and so is their alignment): T tiles per workgroup so that one round of CUs covers the rows
+// when it can (at most 4 tiles), spread evenly over whole rounds.
+template <int G, int SDT>
+int launch_int4_xr(bool sgn, hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales, int64_t ngroups,
+                   const void* x, int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy) {
+  const int ks = (int)(k / 1024);
+  const int64_t tiles = (n + 15) / 16;
+  const int cus = stream_cu_count(s);
+  const int64_t per_cu = cus > 0 ? (tiles + cus - 1) / cus : 4;
+  const int tt = per_cu <= 1 ? 1 : per_cu <= 2 ? 2 : 4;
+  int rpw = 16 * tt;
+  int64_t wgs = (n + rpw - 1) / rpw;
+  if (cus > 0 && wgs % cus != 0) {
+    const int64_t rounds = (wgs + cus - 1) / cus;
+    const int64_t even = ((n + rounds * cus - 1) / (rounds * cus) + 3) / 4 * 4;
+    if (even > 16 * (tt - 1) && even < rpw) {
+      rpw = (int)even;
+      wgs = (n + rpw - 1) / rpw;
+    }
+  }
+  const unsigned grid = (unsigned)wgs;
+#define TGM_XR(TT, KK)                                                                                              \
+  if (tt == TT && ks == KK)                                                                                         \
+    return launch_int4_xr_t<TT, KK, G, SDT>(grid, s, w, n, k, scales, ngroups, sgn, x, m, ldx, y, ydt, ldy, rpw);
+  TGM_XR(1, 1) TGM_XR(1, 2) TGM_XR(1, 4)
+  TGM_XR(2, 1) TGM_XR(2, 2) TGM_XR(2, 4)
+  TGM_XR(4, 1) TGM_XR(4, 2) TGM_XR(4, 4)
+#undef TGM_XR
+  return TGM_E_UNSUPPORTED;
+}
+
 template <int NT, int NK, int G, int SDT>
 int launch_int4_shape(unsigned grid, hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales,
                       int64_t ngroups, bool sgn, const void* x, int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy,
-                      int per) {
+                      int per, int rpw) {
   const size_t lds = (NK > 1 ? NT * NK * 64 * 16 : 0) + (size_t)m * (size_t)(k + 8) * 2;
   if (lds > kInt4MaxLds) return TGM_E_UNSUPPORTED;
   const int64_t passes = (m * (k / 8) + NT * NK * 64 - 1) / (NT * NK * 64);  // staging passes
@@ -244,7 +418,7 @@ int launch_int4_shape(unsigned grid, hipStream_t s, const void* w, int64_t n, in
     }                                                                                                               \
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(NT * NK * 64), lds, s,                                              \
                        (const uint8_t*)w, n, k, (const uint8_t*)scales, ngroups, sgn ? 0x88888888u : 0u,            \
-                       sgn ? 1032.0f : 1024.0f, (const _Float16*)x, (int)m, ldx, y, ydt, ldy);                      \
+                       sgn ? 1032.0f : 1024.0f, (const _Float16*)x, (int)m, ldx, y, ydt, ldy, rpw);                 \
     return TGM_OK;                                                                                                  \
   }
   TGM_INT4(4) TGM_INT4(8) TGM_INT4(16)
@@ -256,19 +430,38 @@ template <int G, int SDT>
 int launch_int4_g(bool sgn, hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales, int64_t ngroups,
                   const void* x, int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy) {
   const int64_t tiles = (n + 15) / 16, S = k / 128;
-  // Split K until about 2048 waves are in flight (or a slice is 2 super-steps): 8 waves per
-  // workgroup as NT tiles x NK slices.
-  int nk = 1;
-  while (nk < 8 && tiles * nk < 2048 && (S + 2 * nk - 1) / (2 * nk) >= 2) nk *= 2;
-  const int per = (int)((S + nk - 1) / nk);
-  if (per > 16) return TGM_E_UNSUPPORTED;
-  const int nt = 8 / nk;
-  const unsigned grid = (unsigned)((tiles + nt - 1) / nt);
+  // 8 waves per workgroup as NT tiles x NK slices of K.  Every workgroup stages all of X, so
+  // the more tiles there are, the more of them a workgroup takes (NT) before K is split
+  // (NK): 6144 x 4096 at M = 8 took 9.4 us with one tile and 8 slices per workgroup.
+  static const int order_big[3][2] = {{4, 2}, {2, 4}, {1, 8}};
+  static const int order_mid[3][2] = {{2, 4}, {1, 8}, {4, 2}};
+  static const int order_small[3][2] = {{1, 8}, {2, 4}, {4, 2}};
+  const int(*order)[2] = tiles >= 768 ? order_big : tiles >= 384 ? order_mid : order_small;
+  int nt = 0, nk = 0, per = 0;
+  for (int i = 0; i < 3 && nt == 0; ++i) {
+    const int p = (int)((S + order[i][1] - 1) / order[i][1]);
+    if (p <= 16) nt = order[i][0], nk = order[i][1], per = p;
+  }
+  if (nt == 0) return TGM_E_UNSUPPORTED;
+  // Rows per workgroup: 16 NT, unless the workgroups would leave part of the last round of
+  // CUs idle; then the rows are spread evenly over whole rounds (a multiple of 4 rows each,
+  // every tile of the shape keeping rows).
+  int rpw = 16 * nt;
+  int64_t wgs = (n + rpw - 1) / rpw;
+  const int cus = stream_cu_count(s);
+  if (cus > 0 && wgs % cus != 0) {
+    const int64_t rounds = (wgs + cus - 1) / cus;
+    const int64_t even = ((n + rounds * cus - 1) / (rounds * cus) + 3) / 4 * 4;
+    if (even > 16 * (nt - 1) && even < rpw) {
+      rpw = (int)even;
+      wgs = (n + rpw - 1) / rpw;
+    }
+  }
+  const unsigned grid = (unsigned)wgs;
   switch (nk) {
-    case 1: return launch_int4_shape<8, 1, G, SDT>(grid, s, w, n, k, scales, ngroups, sgn, x, m, ldx, y, ydt, ldy, per);
-    case 2: return launch_int4_shape<4, 2, G, SDT>(grid, s, w, n, k, scales, ngroups, sgn, x, m, ldx, y, ydt, ldy, per);
-    case 4: return launch_int4_shape<2, 4, G, SDT>(grid, s, w, n, k, scales, ngroups, sgn, x, m, ldx, y, ydt, ldy, per);
-    default: return launch_int4_shape<1, 8, G, SDT>(grid, s, w, n, k, scales, ngroups, sgn, x, m, ldx, y, ydt, ldy, per);
+    case 2: return launch_int4_shape<4, 2, G, SDT>(grid, s, w, n, k, scales, ngroups, sgn, x, m, ldx, y, ydt, ldy, per, rpw);
+    case 4: return launch_int4_shape<2, 4, G, SDT>(grid, s, w, n, k, scales, ngroups, sgn, x, m, ldx, y, ydt, ldy, per, rpw);
+    default: return launch_int4_shape<1, 8, G, SDT>(grid, s, w, n, k, scales, ngroups, sgn, x, m, ldx, y, ydt, ldy, per, rpw);
   }
 }
 
@@ -284,7 +477,16 @@ int launch_gemv_int4(hipStream_t s, const void* w, int fmt, int64_t n, int64_t k
   if (scales && (uintptr_t)scales % (4 / g * dtype_size(sdt))) return TGM_E_UNSUPPORTED;  // one vector load per step
   const int64_t ngroups = scales ? k / bs : 0;
   const bool sg = fmt == TGM_FMT_INT4;
+  // K = 1024, 2048 or 4096: activations in registers (gemv_int4_xr), whose scale loads take a
+  // row's groups of a K slice at once (aligned to their size, at most 16 bytes)
+  const int64_t slice_bytes = scales ? k / 1024 * (4 / g) * dtype_size(sdt) : 0;
+  const bool xr = m >= 2 && (k == 1024 || k == 2048 || k == 4096) &&
+                  (!scales || (uintptr_t)scales % (slice_bytes < 16 ? slice_bytes : 16) == 0);
 #define TGM_SDT(SDT)                                                                                                 \
+  if (xr)                                                                                                            \
+    return g == 1   ? launch_int4_xr<1, SDT>(sg, s, w, n, k, scales, ngroups, x, m, ldx, y, ydt, ldy)               \
+           : g == 2 ? launch_int4_xr<2, SDT>(sg, s, w, n, k, scales, ngroups, x, m, ldx, y, ydt, ldy)               \
+                    : launch_int4_xr<4, SDT>(sg, s, w, n, k, scales, ngroups, x, m, ldx, y, ydt, ldy);              \
   return g == 1   ? launch_int4_g<1, SDT>(sg, s, w, n, k, scales, ngroups, x, m, ldx, y, ydt, ldy)                 \
          : g == 2 ? launch_int4_g<2, SDT>(sg, s, w, n, k, scales, ngroups, x, m, ldx, y, ydt, ldy)                 \
                   : launch_int4_g<4, SDT>(sg, s, w, n, k, scales, ngroups, x, m, ldx, y, ydt, ldy)
