@@ -46,6 +46,26 @@ int tgm_dec_embed(const void* table, int64_t vocab, int64_t d, const int32_t* to
 int tgm_dec_add_rmsnorm(float* h, const float* delta, int64_t rows, int64_t d, const void* weight, float eps,
                         void* out, int out_dtype, void* stream);
 
+/* tgm_dec_add_rmsnorm with the residual update given as nparts fp32 parts (part p at
+ * parts + p * part_stride floats, each [rows, d]; 1 <= nparts <= 64, part_stride a multiple of 4
+ * and at least rows * d): h[r] += parts_0[r] + parts_1[r] + ... (summed in part order), then the
+ * same norm.  The parts are what tgm_dec_gemv_parts writes.  The reference has no model code
+ * (decoder harness). */
+int tgm_dec_add_rmsnorm_parts(float* h, const float* parts, int64_t nparts, int64_t part_stride, int64_t rows,
+                              int64_t d, const void* weight, float eps, void* out, int out_dtype, void* stream);
+
+/* A packed GEMV with its K sum cut into `slices` equal slices K_z (k a multiple of 128 * slices,
+ * 1 <= slices <= 64): parts + z * m * ldp receives the fp32 [m, ldp] product x[:, K_z] .
+ * deq(w[:, K_z])^T, for a consumer that adds the parts (tgm_dec_add_rmsnorm_parts).  FP4 / FP6
+ * weights with E8M0/32 (or no) scales, bf16 x [m, ldx], 1 <= m <= 16, operands aligned as for
+ * tgm_gemv; otherwise TGM_E_UNSUPPORTED.  For a projection with few output rows and a long K
+ * (a decoder's down projection, 4096 x 14336, at 2-16 tokens) each workgroup then stages one
+ * slice of x for 64 rows instead of all of x for 16.  The reference has no model code (decoder
+ * harness). */
+int tgm_dec_gemv_parts(const void* w, int fmt, int64_t n, int64_t k, const void* scales, int scale_dtype,
+                       int64_t block_size, const void* x, int x_dtype, int64_t m, int64_t ldx, float* parts,
+                       int64_t ldp, int64_t slices, void* stream);
+
 /* Rotary position embedding (rotate-half pairs (i, i + head_dim / 2), angle p * base^(-2 i /
  * head_dim)) applied in place to the q and k heads of qkv; the rotated k heads and the v heads
  * are stored as bf16 into the caches at each token's position.  For the prefill GEMMs it can

@@ -1,5 +1,7 @@
 """Decoder-step kernels and the Llama-style decoder on gfx950 against the decoder oracle."""
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -58,6 +60,27 @@ def test_add_rmsnorm(dev):
         assert np.allclose(np64(hh), ref_h, rtol=0, atol=1e-6)
         ref = D.rmsnorm(ref_h, np64(w), 1e-5)
         assert O.max_rel_err(np64(out), cast(ref)) <= (1e-5 if dt == F32 else 1e-2)
+
+
+def test_add_rmsnorm_parts_sums_parts_in_order(dev):
+    """tgm_dec_add_rmsnorm_parts is tgm_dec_add_rmsnorm given the parts summed in order
+    (p_0 + p_1 + ... in fp32), bit for bit, for the residual and the normed output."""
+    rng = np.random.default_rng(3)
+    rows, d, nparts = 7, 4096, 7
+    h = torch.from_numpy(rng.standard_normal((rows, d)).astype(np.float32)).to(dev)
+    parts = torch.from_numpy(rng.standard_normal((nparts, rows, d)).astype(np.float32)).to(dev)
+    w = torch.from_numpy(1 + 0.1 * rng.standard_normal(d)).to(dev).to(torch.bfloat16)
+    delta = parts[0].clone()
+    for p in range(1, nparts):
+        delta += parts[p]
+    for dt, tdt in ((F32, torch.float32), (BF16, torch.bfloat16)):
+        h1, h2 = h.clone(), h.clone()
+        o1, o2 = torch.empty((rows, d), dtype=tdt, device=dev), torch.empty((rows, d), dtype=tdt, device=dev)
+        K.call("tgm_dec_add_rmsnorm", h1.data_ptr(), delta.data_ptr(), rows, d, w.data_ptr(), 1e-5, o1.data_ptr(), dt,
+               stream())
+        K.call("tgm_dec_add_rmsnorm_parts", h2.data_ptr(), parts.data_ptr(), nparts, rows * d, rows, d, w.data_ptr(),
+               1e-5, o2.data_ptr(), dt, stream())
+        assert torch.equal(h1, h2) and torch.equal(o1, o2)
 
 
 def test_rope_kv_rotates_and_stores_at_each_position(dev):
@@ -364,8 +387,8 @@ F16_ROUNDING, BF16_ROUNDING = 2.0 ** -10, 2.0 ** -7
 
 
 @pytest.mark.parametrize("attention", ["fused", "gemm", "split"])
-@pytest.mark.parametrize("batch,prompt", [(8, 6), (1, 9), (3, 40)])
-def test_decoder_layers_match_oracle_elementwise(dev, batch, prompt, attention):
+@pytest.mark.parametrize("batch,prompt,ffn", [(8, 6, 512), (1, 9, 512), (3, 40, 512), (8, 6, 4096), (5, 7, 4096)])
+def test_decoder_layers_match_oracle_elementwise(dev, batch, prompt, ffn, attention):
     """Teacher-forced parity of every operation of every layer, elementwise.  Each operation is
     recomputed by the oracle from the device's own input to it (the device's residual, normed
     activations, KV cache, attention output and SwiGLU output of that layer), so an activation
@@ -378,8 +401,10 @@ def test_decoder_layers_match_oracle_elementwise(dev, batch, prompt, attention):
     * the logits of the device's last residual: 1e-2.
 
     Prefill (GEMM path at 48 and 120 rows, GEMV path at 9), then three cached decode steps
-    (batch 8: eight sequences per multi-row GEMV, SwiGLU GEMV and decode attention launch)."""
-    cfg, max_seq = SMALL, 64
+    (batch 8: eight sequences per multi-row GEMV, SwiGLU GEMV and decode attention launch).  With
+    a feed-forward width of 4096 the decode steps at 5 and 8 tokens run the down projection as
+    two K-slice parts that the next norm adds."""
+    cfg, max_seq = dataclasses.replace(SMALL, ffn=ffn), 64
     w = random_weights(cfg, dev, seed=batch + 20)
     prompts = np.random.default_rng(prompt).integers(0, cfg.vocab, (batch, prompt))
     dec = Decoder(w, cfg, batch, max_seq, prompt)

@@ -153,6 +153,51 @@ def make_weight(dev, fmt, n, k, scale_kind, rng, bs=32):
     return w, deq
 
 
+@pytest.mark.parametrize("fmt,scale_kind", [("fp4_e2m1", "e8m0"), ("fp6_e2m3", "e8m0"), ("fp4_e2m1", None)])
+@pytest.mark.parametrize("nkm,slices", [((1000, 4096, 8), 2), ((4096, 14336, 8), 7), ((300, 14336, 16), 7),
+                                        ((4100, 2048, 5), 4), ((64, 1024, 1), 8)])
+def test_dec_gemv_parts(dev, fmt, scale_kind, nkm, slices):
+    """K-slice partial GEMV (tgm_dec_gemv_parts): part z is x[:, K_z] . deq(W[:, K_z])^T over the
+    z-th of ``slices`` equal K slices, each within the GEMV tolerance of the oracle's product over
+    that slice, and their sum within it of the whole product (exact-shape and guarded kernels,
+    ragged N, 1-16 activation rows)."""
+    from tinygrad_mi355x.runtime import kernels as K
+    n, k, m = nkm
+    rng = np.random.default_rng(n + k + m + slices)
+    w, deq = make_weight(dev, fmt, n, k, scale_kind, rng)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    parts = torch.full((slices, m, n), float("nan"), dtype=torch.float32, device=dev)
+    K.call("tgm_dec_gemv_parts", w.data.data_ptr(), K.FORMAT_IDS[fmt], n, k, K.ptr(w.scales),
+           K.dtype_id(w.scales.dtype) if w.scales is not None else -1, w.block_size, x.data_ptr(),
+           K.dtype_id(torch.bfloat16), m, k, parts.data_ptr(), n, slices, torch.cuda.current_stream().cuda_stream)
+    xs = x.float().cpu().numpy().astype(np.float64)
+    got = parts.cpu().numpy().astype(np.float64)
+    ks = k // slices
+    for z in range(slices):
+        ref = xs[:, z * ks:(z + 1) * ks] @ deq[:, z * ks:(z + 1) * ks].T
+        assert O.max_rel_err(got[z], ref) <= TOL, z
+    assert O.max_rel_err(got.sum(0), xs @ deq.T) <= TOL
+
+
+def test_dec_gemv_parts_rejects_bad_slices(dev):
+    """K must split into slices of whole 128-element super-steps; INT4 weights are not taken."""
+    from tinygrad_mi355x.runtime import kernels as K
+    rng = np.random.default_rng(5)
+    w, _ = make_weight(dev, "fp4_e2m1", 64, 1024, "e8m0", rng)
+    x = torch.zeros((2, 1024), dtype=torch.bfloat16, device=dev)
+    parts = torch.empty((3, 2, 64), dtype=torch.float32, device=dev)
+    args = (w.data.data_ptr(), K.FORMAT_IDS["fp4_e2m1"], 64, 1024, w.scales.data_ptr(), K.dtype_id(w.scales.dtype), 32,
+            x.data_ptr(), K.dtype_id(torch.bfloat16), 2, 1024, parts.data_ptr(), 64)
+    with pytest.raises(ValueError):
+        K.call("tgm_dec_gemv_parts", *args, 3, torch.cuda.current_stream().cuda_stream)
+    wi, _ = int4_weight(dev, "int4", 64, 1024, torch.float16, 32, rng)
+    xi = torch.zeros((2, 1024), dtype=torch.float16, device=dev)
+    with pytest.raises(K.UnsupportedKernel):
+        K.call("tgm_dec_gemv_parts", wi.data.data_ptr(), K.FORMAT_IDS["int4"], 64, 1024, wi.scales.data_ptr(),
+               K.dtype_id(torch.float16), 32, xi.data_ptr(), K.dtype_id(torch.float16), 2, 1024, parts.data_ptr(), 64,
+               2, torch.cuda.current_stream().cuda_stream)
+
+
 @pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e2m3", "fp6_e3m2"])
 @pytest.mark.parametrize("m", [1, 4, 16])
 @pytest.mark.parametrize("nk", [(256, 512), (200, 384), (14336 // 8, 4096)])

@@ -68,8 +68,10 @@ __device__ __forceinline__ void store4(void* out, int odt, int64_t i, dec_f32x4 
   }
 }
 
+// h += the nparts deltas (part p at delta + p part_stride), then RMSNorm(h) * w -> out.
 __global__ void __launch_bounds__(kNormThreads) dec_add_rmsnorm(float* __restrict__ h, const float* __restrict__ delta,
-                                                                int d, const uint16_t* __restrict__ w, float eps,
+                                                                int nparts, int64_t part_stride, int d,
+                                                                const uint16_t* __restrict__ w, float eps,
                                                                 void* __restrict__ out, int odt) {
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -77,14 +79,26 @@ __global__ void __launch_bounds__(kNormThreads) dec_add_rmsnorm(float* __restric
   dec_f32x4* hr = (dec_f32x4*)(h + r * d);
   const dec_f32x4* dr = delta ? (const dec_f32x4*)(delta + r * d) : nullptr;
   dec_f32x4 v[4];
+  // the norm weights are loaded with the row, not after the reduction: one memory round trip
+  const uint2* w4 = (const uint2*)w;
+  uint2 wv[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int i = tid + q * kNormThreads;
+    if (i < d4) wv[q] = w4[i];
+  }
   float ss = 0.f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int i = tid + q * kNormThreads;
     if (i < d4) {
       dec_f32x4 x = hr[i];
-      if (dr) {
-        const dec_f32x4 y = dr[i];
+      if (nparts > 0) {
+        dec_f32x4 y = dr[i];
+        for (int p = 1; p < nparts; ++p) {  // parts summed in order, then added to h
+          const dec_f32x4 z = dr[(int64_t)p * (part_stride / 4) + i];
+          y = dec_f32x4{y[0] + z[0], y[1] + z[1], y[2] + z[2], y[3] + z[3]};
+        }
         x = dec_f32x4{x[0] + y[0], x[1] + y[1], x[2] + y[2], x[3] + y[3]};
         hr[i] = x;
       }
@@ -100,12 +114,11 @@ __global__ void __launch_bounds__(kNormThreads) dec_add_rmsnorm(float* __restric
 #pragma unroll
   for (int i = 0; i < kNormThreads / 64; ++i) tot += part[i];
   const float inv = 1.0f / sqrtf(tot / (float)d + eps);
-  const uint2* w4 = (const uint2*)w;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int i = tid + q * kNormThreads;
     if (i < d4) {
-      const uint2 ww = w4[i];
+      const uint2 ww = wv[q];
       const dec_f32x4 x = v[q];
       store4(out, odt, r * d + 4 * i,
              dec_f32x4{x[0] * inv * lo_bf16(ww.x), x[1] * inv * hi_bf16(ww.x), x[2] * inv * lo_bf16(ww.y),
@@ -885,9 +898,28 @@ extern "C" int tgm_dec_add_rmsnorm(float* h, const float* delta, int64_t rows, i
       (uintptr_t)weight % 8)
     TGM_UNSUPPORTED("tgm_dec_add_rmsnorm: d must be a multiple of 4 and at most %d, rows 16-byte aligned", kNormMaxD);
   if (rows == 0) return TGM_OK;
-  hipLaunchKernelGGL(dec_add_rmsnorm, dim3((unsigned)rows), dim3(kNormThreads), 0, (hipStream_t)stream, h, delta, (int)d,
-                     (const uint16_t*)weight, eps, out, out_dtype);
+  hipLaunchKernelGGL(dec_add_rmsnorm, dim3((unsigned)rows), dim3(kNormThreads), 0, (hipStream_t)stream, h, delta,
+                     delta ? 1 : 0, (int64_t)0, (int)d, (const uint16_t*)weight, eps, out, out_dtype);
   return launch_status("tgm_dec_add_rmsnorm");
+}
+
+extern "C" int tgm_dec_add_rmsnorm_parts(float* h, const float* parts, int64_t nparts, int64_t part_stride, int64_t rows,
+                                         int64_t d, const void* weight, float eps, void* out, int out_dtype,
+                                         void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(h && parts && weight && out, "null operand");
+  TGM_CHECK_ARG(rows >= 0 && d > 0 && d < (1ll << 31) && rows < (1ll << 31), "invalid norm sizes");
+  TGM_CHECK_ARG(nparts >= 1 && nparts <= 64 && part_stride >= rows * d, "1 .. 64 parts of at least rows x d floats each");
+  TGM_CHECK_ARG(out_dtype_ok(out_dtype), "output must be f16, bf16 or f32");
+  TGM_CHECK_ARG(eps >= 0.f, "eps must be non-negative");
+  if (d % 4 || d > kNormMaxD || part_stride % 4 || (uintptr_t)h % 16 || (uintptr_t)out % 16 || (uintptr_t)parts % 16 ||
+      (uintptr_t)weight % 8)
+    TGM_UNSUPPORTED("tgm_dec_add_rmsnorm_parts: d and the part stride must be multiples of 4, d at most %d, rows "
+                    "16-byte aligned", kNormMaxD);
+  if (rows == 0) return TGM_OK;
+  hipLaunchKernelGGL(dec_add_rmsnorm, dim3((unsigned)rows), dim3(kNormThreads), 0, (hipStream_t)stream, h, parts,
+                     (int)nparts, part_stride, (int)d, (const uint16_t*)weight, eps, out, out_dtype);
+  return launch_status("tgm_dec_add_rmsnorm_parts");
 }
 
 extern "C" int tgm_dec_rope_kv(float* qkv, int64_t rows, int64_t seq_rows, int64_t heads, int64_t kv_heads,
@@ -904,7 +936,7 @@ extern "C" int tgm_dec_rope_kv(float* qkv, int64_t rows, int64_t seq_rows, int64
   TGM_CHECK_ARG(!(q_out || k_out || vt_out) || (parts >= 1 && parts <= 3), "parts must be 1, 2 or 3");
   TGM_CHECK_ARG(!vt_out || (ld_vt % parts == 0 && ld_vt / parts >= seq_rows && (ld_vt / parts) % 8 == 0 &&
                              head_dim % 8 == 0 && (uintptr_t)vt_out % 16 == 0 && (uintptr_t)v_cache % 16 == 0),
-                "vt_out needs ld_vt / parts >= seq_rows and a multiple of 8, head_dim % 8 == 0, 16-byte alignment");
+                "vt_out needs ld_vt / parts >= seq_rows and a multiple of 8, head_dim %% 8 == 0, 16-byte alignment");
   TGM_CHECK_ARG(!vt_out || rows / seq_rows * kv_heads <= 65535, "too many sequences for vt_out");
   if (rows == 0) return TGM_OK;
   hipLaunchKernelGGL(dec_rope_kv, dim3((unsigned)rows, (unsigned)(heads + kv_heads)), dim3((unsigned)(head_dim / 2)), 0,

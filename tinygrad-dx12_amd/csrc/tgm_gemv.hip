@@ -111,7 +111,7 @@ extern "C" int tgm_gemv_swiglu(const void* w, int fmt, int64_t n, int64_t k, con
     return st == TGM_OK ? launch_status("tgm_gemv_swiglu") : st;
   }
   if (!mfma_gemv_ok(w, fmt, n, k, scales, scale_dtype, block_size, x, x_dtype, m, ldx, y_dtype))
-    TGM_UNSUPPORTED("tgm_gemv_swiglu: 2-16 rows need FP4/FP6 weights with E8M0/32 (or no) scales, bf16 x, K % 128 == 0");
+    TGM_UNSUPPORTED("tgm_gemv_swiglu: 2-16 rows need FP4/FP6 weights with E8M0/32 (or no) scales, bf16 x, K %% 128 == 0");
   int st;
   switch (fmt) {
     case TGM_FMT_FP4_E2M1: st = launch_gemv_stream_fp4(s, w, n, k, scales, x, m, ldx, y, y_dtype, ldy, 1); break;
@@ -120,6 +120,31 @@ extern "C" int tgm_gemv_swiglu(const void* w, int fmt, int64_t n, int64_t k, con
   }
   if (st == TGM_E_UNSUPPORTED) TGM_UNSUPPORTED("tgm_gemv_swiglu: no streaming shape for K = %lld", (long long)k);
   return st == TGM_OK ? launch_status("tgm_gemv_swiglu") : st;
+}
+
+extern "C" int tgm_dec_gemv_parts(const void* w, int fmt, int64_t n, int64_t k, const void* scales, int scale_dtype,
+                                  int64_t block_size, const void* x, int x_dtype, int64_t m, int64_t ldx, float* parts,
+                                  int64_t ldp, int64_t slices, void* stream) {
+  clear_error();
+  TGM_CHECK_ARG(valid_format(fmt), "unknown packed format %d", fmt);
+  TGM_CHECK_ARG(w && x && parts, "null operand");
+  TGM_CHECK_ARG(n >= 0 && k >= 0 && block_size >= 1 && m >= 1 && m <= 16, "invalid gemv sizes (1 <= M <= 16)");
+  TGM_CHECK_ARG(slices >= 1 && slices <= 64 && k % (128 * slices) == 0, "K must be a multiple of 128 x slices (1 .. 64)");
+  TGM_CHECK_ARG(ldx >= k && ldp >= n, "ldx smaller than K or ldp smaller than N");
+  if (n == 0) return TGM_OK;
+  // (a slice is a multiple of 128 elements, so its scale bytes start dword-aligned)
+  if (!mfma_gemv_ok(w, fmt, n, k, scales, scale_dtype, block_size, x, x_dtype, m, ldx, TGM_F32) || (uintptr_t)parts % 4)
+    TGM_UNSUPPORTED("tgm_dec_gemv_parts: FP4/FP6 weights with E8M0/32 (or no) scales, bf16 x, K %% 128 == 0");
+  const hipStream_t s = (hipStream_t)stream;
+  const int64_t stride = m * ldp;  // floats per part
+  int st;
+  switch (fmt) {
+    case TGM_FMT_FP4_E2M1: st = launch_gemv_stream_fp4(s, w, n, k, scales, x, m, ldx, parts, TGM_F32, ldp, 0, (int)slices, stride); break;
+    case TGM_FMT_FP6_E2M3: st = launch_gemv_stream_fp6(s, w, n, k, scales, x, m, ldx, parts, TGM_F32, ldp, 0, (int)slices, stride); break;
+    default: st = launch_gemv_stream_bf6(s, w, n, k, scales, x, m, ldx, parts, TGM_F32, ldp, 0, (int)slices, stride); break;
+  }
+  if (st == TGM_E_UNSUPPORTED) TGM_UNSUPPORTED("tgm_dec_gemv_parts: no streaming shape for K / slices = %lld", (long long)(k / slices));
+  return st == TGM_OK ? launch_status("tgm_dec_gemv_parts") : st;
 }
 
 extern "C" int tgm_gemv(const void* w, int fmt, int64_t n, int64_t k, const void* scales, int scale_dtype,

@@ -110,12 +110,16 @@ __device__ __forceinline__ void load_codes(const uint8_t* p, unsigned out[6]) {
 // column c >= M read activation row 0: those D columns are never stored and MFMA columns
 // do not mix, so they need no zeroing.  The NK partial tiles of a weight tile are summed
 // through LDS.
+// K slices (gridDim.y > 1): workgroup row blockIdx.y takes K elements [blockIdx.y K, + K) of
+// rows whose packed bytes are row_bytes apart (the scale rows nblk blocks apart, the
+// activation rows ldx elements apart) and writes its partial product to y + blockIdx.y
+// part_stride; one slice (gridDim.y = 1) is the whole product.
 template <int FMT, int NT, int NK, int RING, int SMAX, bool EXACT, int XV, int SC>
 __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __restrict__ w, int64_t N, int64_t K,
                                                           const uint8_t* __restrict__ scales, int64_t nblk,
                                                           const __bf16* __restrict__ x, int M, int64_t ldx,
                                                           void* __restrict__ y, int ydt, int64_t ldy, int swiglu,
-                                                          int rpw) {
+                                                          int rpw, int64_t row_bytes, int64_t part_stride) {
   static_assert(SMAX % 4 == 0, "scale groups");
   constexpr int D = RING < SMAX ? RING : SMAX;  // ring depth
   constexpr bool SCALED = SC != kScaleNone, SG4 = SC == kScaleGroup4, XLDS = XV > 0;
@@ -132,7 +136,12 @@ __global__ void __launch_bounds__(NT * NK * 64) gemv_stream(const uint8_t* __res
   const int64_t wg_end = wg0 + rpw < N ? wg0 + rpw : N;  // rows of this workgroup: [wg0, wg_end)
   const int64_t n0 = wg0 + 16 * ti;
   const int64_t row = n0 + r < wg_end ? n0 + r : wg_end - 1;  // clamped rows are computed but not stored
-  const int64_t row_bytes = K * format_info(FMT).bits / 8;
+  if (gridDim.y > 1) {  // this workgroup's K slice (uniform offsets)
+    w += (int64_t)blockIdx.y * (K * format_info(FMT).bits / 8);
+    scales += (int64_t)blockIdx.y * (K / 32);
+    x += (int64_t)blockIdx.y * K;
+    y = (char*)y + (int64_t)blockIdx.y * part_stride * dtype_size(ydt);
+  }
   const unsigned* srow = (const unsigned*)(scales + row * nblk);  // dereferenced only when SCALED
   const int S = (int)(K / 128);
   const int per = SG4 ? ((S + NK - 1) / NK + 3) / 4 * 4 : (S + NK - 1) / NK;  // <= SMAX (host)
@@ -356,8 +365,14 @@ inline GemvShape gemv_shape(int64_t tiles, int64_t S, bool sg4) {
   return GemvShape{0, 0, 0, false};
 }
 
+// The launch description of one streaming GEMV: grid.x row groups x grid.y K slices.
+struct StreamLaunch {
+  unsigned grid, slices;
+  int64_t row_bytes, part_stride;
+};
+
 template <int FMT, int NT, int NK, int SMAX, bool EXACT, int XV, int SC>
-int launch_stream(unsigned grid, size_t lds, hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales,
+int launch_stream(const StreamLaunch& L, size_t lds, hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales,
                   int64_t nblk, const void* x, int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu, int rpw) {
   auto kernel = gemv_stream<FMT, NT, NK, (XV > 0 ? kGemvRing : kGemvRingX), SMAX, EXACT, XV, SC>;
   if (lds > 64 * 1024) {
@@ -371,60 +386,68 @@ int launch_stream(unsigned grid, size_t lds, hipStream_t s, const void* w, int64
       raised = true;
     }
   }
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(NT * NK * 64), lds, s, (const uint8_t*)w, n, k, (const uint8_t*)scales,
-                     nblk, (const __bf16*)x, (int)m, ldx, y, ydt, ldy, swiglu, rpw);
+  hipLaunchKernelGGL(kernel, dim3(L.grid, L.slices), dim3(NT * NK * 64), lds, s, (const uint8_t*)w, n, k,
+                     (const uint8_t*)scales, nblk, (const __bf16*)x, (int)m, ldx, y, ydt, ldy, swiglu, rpw, L.row_bytes,
+                     L.part_stride);
   return TGM_OK;
 }
 
 // xv: 2, 8 or 16 straight-line activation passes, 0 for activations in the load ring.
 template <int FMT, int NT, int NK, int SMAX, bool EXACT, int SC>
-int launch_stream_xv(int xv, unsigned grid, size_t lds, hipStream_t s, const void* w, int64_t n, int64_t k,
+int launch_stream_xv(int xv, const StreamLaunch& L, size_t lds, hipStream_t s, const void* w, int64_t n, int64_t k,
                      const void* scales, int64_t nblk, const void* x, int64_t m, int64_t ldx, void* y, int ydt,
                      int64_t ldy, int swiglu, int rpw) {
-  if (xv == 2) return launch_stream<FMT, NT, NK, SMAX, EXACT, 2, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
-  if (xv == 8) return launch_stream<FMT, NT, NK, SMAX, EXACT, 8, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
-  if (xv == 16) return launch_stream<FMT, NT, NK, SMAX, EXACT, 16, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
-  return launch_stream<FMT, NT, NK, SMAX, EXACT, 0, SC>(grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  if (xv == 2) return launch_stream<FMT, NT, NK, SMAX, EXACT, 2, SC>(L, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  if (xv == 8) return launch_stream<FMT, NT, NK, SMAX, EXACT, 8, SC>(L, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  if (xv == 16) return launch_stream<FMT, NT, NK, SMAX, EXACT, 16, SC>(L, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  return launch_stream<FMT, NT, NK, SMAX, EXACT, 0, SC>(L, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
 }
 
 template <int FMT, int NT, int NK>
-int launch_stream_shape(const GemvShape& g, int sc, int xv, unsigned grid, size_t lds, hipStream_t s, const void* w,
+int launch_stream_shape(const GemvShape& g, int sc, int xv, const StreamLaunch& L, size_t lds, hipStream_t s, const void* w,
                         int64_t n, int64_t k, const void* scales, int64_t nblk, const void* x, int64_t m, int64_t ldx,
                         void* y, int ydt, int64_t ldy, int swiglu, int rpw) {
   if (g.exact) {  // block-32 E8M0 scales in groups of four, slices of exactly SMAX super-steps
 #define TGM_EXACT(SMAX) \
-    if (g.smax == SMAX) return launch_stream_xv<FMT, NT, NK, SMAX, true, kScaleGroup4>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+    if (g.smax == SMAX) return launch_stream_xv<FMT, NT, NK, SMAX, true, kScaleGroup4>(xv, L, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
     TGM_EXACT(4) TGM_EXACT(8) TGM_EXACT(16) TGM_EXACT(28) TGM_EXACT(32)
 #undef TGM_EXACT
     return TGM_E_UNSUPPORTED;
   }
-  if (sc == kScaleGroup4) return launch_stream_xv<FMT, NT, NK, 32, false, kScaleGroup4>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
-  if (sc == kScaleDword) return launch_stream_xv<FMT, NT, NK, 32, false, kScaleDword>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
-  return launch_stream_xv<FMT, NT, NK, 32, false, kScaleNone>(xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  if (sc == kScaleGroup4) return launch_stream_xv<FMT, NT, NK, 32, false, kScaleGroup4>(xv, L, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  if (sc == kScaleDword) return launch_stream_xv<FMT, NT, NK, 32, false, kScaleDword>(xv, L, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  return launch_stream_xv<FMT, NT, NK, 32, false, kScaleNone>(xv, L, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
 }
 
 // swiglu: the weight rows interleave gate and up rows; y gets silu(gate) * up (N / 2 columns).
+// slices > 1: K is cut into ``slices`` equal parts (k a multiple of 128 slices) and the product
+// over part z goes to y + z part_stride (the caller sums the parts); the workgroups then take
+// the widest row groups, so that each stages its slice of X for as many rows as it can.
 template <int FMT>
 int launch_gemv_stream(hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales, const void* x,
-                       int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu = 0) {
+                       int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu = 0, int slices = 1,
+                       int64_t part_stride = 0) {
+  if (slices < 1 || k % (128 * (int64_t)slices) != 0) return TGM_E_UNSUPPORTED;
+  const int64_t ks = k / slices;  // K of one slice
   const int64_t tiles = (n + 15) / 16;
-  const int sc = scales == nullptr ? kScaleNone : (k % 512 == 0 ? kScaleGroup4 : kScaleDword);
-  const GemvShape g = gemv_shape(tiles, k / 128, sc == kScaleGroup4);
+  const int sc = scales == nullptr ? kScaleNone : (ks % 512 == 0 ? kScaleGroup4 : kScaleDword);
+  const GemvShape g = gemv_shape(slices > 1 && tiles < 768 ? 768 : tiles, ks / 128, sc == kScaleGroup4);
   if (g.nt == 0) return TGM_E_UNSUPPORTED;
   const size_t part = (size_t)g.nt * g.nk * 64 * 16;
-  const size_t xbytes = (size_t)m * (size_t)(k + 8) * 2;
+  const size_t xbytes = (size_t)m * (size_t)(ks + 8) * 2;
   const bool xlds = part + xbytes <= kMaxLds;
-  const int64_t passes = (m * k + 8 * 64 * 8 - 1) / (8 * 64 * 8);  // XSTEP of an 8-wave workgroup
+  const int64_t passes = (m * ks + 8 * 64 * 8 - 1) / (8 * 64 * 8);  // XSTEP of an 8-wave workgroup
   // every staging load is issued before the weight ring up to 16 passes: a load in the
   // staging loop after it waits for the whole ring (the vector memory counter retires in order)
   const int xv = !xlds ? 0 : passes <= 2 ? 2 : passes <= 8 ? 8 : 16;
   const size_t lds = part + (xlds ? xbytes : 0);
-  const int64_t nblk = k / 32;
+  const int64_t nblk = k / 32;  // scale row stride (blocks of the whole row)
   // Rows per workgroup: 16 NT, unless the workgroups would leave part of the last round of
   // CUs idle; then the rows are spread evenly over whole rounds (a multiple of 4 rows each).
+  // With K slices each slice counts on its share of the CUs.
   int rpw = 16 * g.nt;
   int64_t wgs = (n + rpw - 1) / rpw;
-  const int cus = device_cus();
+  const int cus = device_cus() / slices;
   if (cus > 0 && wgs % cus != 0) {
     const int64_t rounds = (wgs + cus - 1) / cus;
     const int64_t even = ((n + rounds * cus - 1) / (rounds * cus) + 3) / 4 * 4;
@@ -433,18 +456,21 @@ int launch_gemv_stream(hipStream_t s, const void* w, int64_t n, int64_t k, const
       wgs = (n + rpw - 1) / rpw;
     }
   }
-  const unsigned grid = (unsigned)wgs;
-  if (g.nt == 4) return launch_stream_shape<FMT, 4, 2>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
-  if (g.nt == 2) return launch_stream_shape<FMT, 2, 4>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
-  return launch_stream_shape<FMT, 1, 8>(g, sc, xv, grid, lds, s, w, n, k, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  const StreamLaunch L{(unsigned)wgs, (unsigned)slices, k * format_info(FMT).bits / 8, part_stride};
+  if (g.nt == 4) return launch_stream_shape<FMT, 4, 2>(g, sc, xv, L, lds, s, w, n, ks, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  if (g.nt == 2) return launch_stream_shape<FMT, 2, 4>(g, sc, xv, L, lds, s, w, n, ks, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
+  return launch_stream_shape<FMT, 1, 8>(g, sc, xv, L, lds, s, w, n, ks, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
 }
 
 // Instantiated per format in tgm_gemv_stream.hip.
 int launch_gemv_stream_fp4(hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales, const void* x,
-                           int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu = 0);
+                           int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu = 0, int slices = 1,
+                           int64_t part_stride = 0);
 int launch_gemv_stream_fp6(hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales, const void* x,
-                           int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu = 0);
+                           int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu = 0, int slices = 1,
+                           int64_t part_stride = 0);
 int launch_gemv_stream_bf6(hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales, const void* x,
-                           int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu = 0);
+                           int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu = 0, int slices = 1,
+                           int64_t part_stride = 0);
 
 }  // namespace tgm

@@ -270,6 +270,15 @@ class Decoder:
                           and all(_norm_gemv_fits(L.wqkv, False) and _norm_gemv_fits(L.w_gate_up, True)
                                   for L in weights.layers))
         self.h_alt = torch.empty((batch, d), **f32) if self.fuse_norm else None
+        # 5-8 tokens: the down projection's K is cut into slices of 2048 (tgm_dec_gemv_parts) and
+        # the next add + RMSNorm sums the parts: a workgroup then stages one slice of the
+        # activations for 64 weight rows instead of all 14336 columns for 16 rows
+        # (4096 x 14336 at 8 tokens: 13.7 -> 10.8 us)
+        wd = weights.layers[0].w_down
+        self.down_slices = cfg.ffn // 2048 if (batch >= 5 and cfg.ffn % 2048 == 0 and 2 <= cfg.ffn // 2048 <= 16
+                                               and wd.format in ("fp4_e2m1", "fp6_e2m3", "fp6_e3m2")
+                                               and (wd.scales is None or wd.block_size == 32)) else 1
+        self.delta_parts = torch.empty((self.down_slices, batch, d), **f32) if self.down_slices > 1 else None
         ws = K.load_library().tgm_dec_attention_workspace(batch, cfg.heads, cfg.head_dim, self.position_splits)
         self.workspace = torch.empty(max(ws // 4, 1), **f32)
         self.workspace_bytes = ws
@@ -287,10 +296,35 @@ class Decoder:
         self.layer_trace: list[dict[str, torch.Tensor | None]] | None = None
 
     # ---------------------------------------------------------------- building blocks
+    def _add_norm(self, rows: int, parts: int, first: bool, weight: torch.Tensor, out: torch.Tensor, odt: int,
+                  stream: int) -> None:
+        """h += delta (or the ``parts`` down-projection parts; nothing before the first layer),
+        then RMSNorm(h) * weight -> out."""
+        d = self.cfg.hidden
+        if parts:
+            K.call("tgm_dec_add_rmsnorm_parts", self.h.data_ptr(), self.delta_parts.data_ptr(), parts, rows * d, rows, d,
+                   weight.data_ptr(), self.cfg.eps, out.data_ptr(), odt, stream)
+        else:
+            K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), None if first else self.delta.data_ptr(), rows, d,
+                   weight.data_ptr(), self.cfg.eps, out.data_ptr(), odt, stream)
+
+    def _down(self, rows: int, L: LayerWeights, stream: int) -> int:
+        """The down projection of ``act``: into ``delta``, or as K-slice parts (returns their count)."""
+        cfg = self.cfg
+        if self.down_slices > 1 and 5 <= rows <= GEMV_MAX_ROWS:
+            w = L.w_down
+            K.call("tgm_dec_gemv_parts", w.data.data_ptr(), K.FORMAT_IDS[w.format], cfg.hidden, cfg.ffn, K.ptr(w.scales),
+                   K.dtype_id(w.scales.dtype) if w.scales is not None else -1, w.block_size, self.act.data_ptr(), BF16,
+                   rows, cfg.ffn, self.delta_parts.data_ptr(), cfg.hidden, self.down_slices, stream)
+            return self.down_slices
+        _packed_product(self.act, rows, cfg.ffn, L.w_down, self.delta, cfg.hidden, stream, self._split_ws)
+        return 0
+
     def _layers(self, rows: int, seq_rows: int, splits: int, stream: int) -> None:
         cfg = self.cfg
         d = cfg.hidden
         fuse_norm = rows == 1 and self.fuse_norm
+        parts = 0  # down-projection parts the next norm adds (0: the output is in delta)
         for li, L in enumerate(self.w.layers):
             if fuse_norm:  # h + delta -> h_alt, RMSNorm and the QKV projection in one launch
                 w = L.wqkv
@@ -300,8 +334,7 @@ class Decoder:
                        K.dtype_id(w.scales.dtype) if w.scales is not None else -1, w.block_size, self.qkv.data_ptr(),
                        F32, 0, stream)
             else:
-                K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr() if li else None, rows, d,
-                       L.attn_norm.data_ptr(), cfg.eps, self.xn16.data_ptr(), F16, stream)
+                self._add_norm(rows, parts, li == 0, L.attn_norm, self.xn16, F16, stream)
                 _packed_product(self.xn16, rows, d, L.wqkv, self.qkv, cfg.qkv_rows, stream, self._split_ws)
             kc, vc = self.k_cache[li], self.v_cache[li]
             fused = seq_rows == 1 and self.fuse_rope  # one new token per sequence: RoPE + cache store in attention
@@ -348,15 +381,19 @@ class Decoder:
             else:
                 _packed_product(self.xnb, rows, d, L.w_gate_up, self.gu, 2 * cfg.ffn, stream, self._split_ws)
                 K.call("tgm_dec_silu_mul", self.gu.data_ptr(), rows, cfg.ffn, self.act.data_ptr(), BF16, stream)
-            _packed_product(self.act, rows, cfg.ffn, L.w_down, self.delta, d, stream, self._split_ws)
-            self._trace(rows)
-        K.call("tgm_dec_add_rmsnorm", self.h.data_ptr(), self.delta.data_ptr(), rows, d, self.w.final_norm.data_ptr(),
-               cfg.eps, self.xnb.data_ptr(), BF16, stream)
+            parts = self._down(rows, L, stream)
+            self._trace(rows, parts=parts)
+        self._add_norm(rows, parts, False, self.w.final_norm, self.xnb, BF16, stream)
 
-    def _trace(self, rows: int, fused_norm: bool = False) -> None:
+    def _trace(self, rows: int, fused_norm: bool = False, parts: int = 0) -> None:
         if self.layer_trace is not None:
+            delta = self.delta[:rows].clone()
+            if parts:  # the parts summed in the order the next norm adds them
+                delta = self.delta_parts[0, :rows].clone()
+                for p in range(1, parts):
+                    delta += self.delta_parts[p, :rows]
             self.layer_trace.append({
-                "h": self.h[:rows].clone(), "delta": self.delta[:rows].clone(), "attn": self.attn[:rows].clone(),
+                "h": self.h[:rows].clone(), "delta": delta, "attn": self.attn[:rows].clone(),
                 "act": self.act[:rows].clone(), "x16": None if fused_norm else self.xn16[:rows].clone(),
                 "xb": None if fused_norm else self.xnb[:rows].clone()})
 
