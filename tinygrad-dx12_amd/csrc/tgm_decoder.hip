@@ -12,6 +12,7 @@
 
 #include "../../include/tgm_decoder.h"
 #include "tgm_common.h"
+#include "tgm_lanes.h"
 
 namespace tgm {
 
@@ -19,15 +20,32 @@ typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 dec_bf16x2;
 typedef unsigned dec_u32x4 __attribute__((ext_vector_type(4)));
 typedef float dec_f32x4 __attribute__((ext_vector_type(4)));
 
+// Whole-wave reductions without LDS: DPP exchanges inside the 16-lane rows, then the gfx950
+// row swaps (every lane ends with the result).  A __shfl_xor butterfly is six dependent
+// ds_bpermute round trips through LDS.  All 64 lanes must be active.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += xor1(v);
+  v += xor2(v);
+  v += xor4(v);
+  v += xor8(v);
+  float a = v, b = v;
+  swap16(a, b);  // lane l: a + b = v[l] + v[l ^ 16]
+  v = a + b;
+  a = v, b = v;
+  swap32(a, b);  // lane l: a + b = v[l] + v[l ^ 32]
+  return a + b;
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, xor1(v));
+  v = fmaxf(v, xor2(v));
+  v = fmaxf(v, xor4(v));
+  v = fmaxf(v, xor8(v));
+  float a = v, b = v;
+  swap16(a, b);
+  v = fmaxf(a, b);
+  a = v, b = v;
+  swap32(a, b);
+  return fmaxf(a, b);
 }
 __device__ __forceinline__ float lo_bf16(unsigned w) { return __builtin_bit_cast(float, w << 16); }
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) { return __builtin_bit_cast(float, (unsigned)h << 16); }
@@ -359,6 +377,9 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
   const int pi = tid >> 2, qd = tid & 3;
   dec_u32x4 kreg[QD / 8];
   unsigned vreg[CH / 4];
+  // lane l's dims 2 l, 2 l + 1 of the wave's first cache row; the wave's positions are uniform,
+  // so a whole chunk inside the split is one base and constant offsets
+  const uint16_t* vlane = vc + (kvbase + wave) * HD + 2 * lane;
   auto load_chunk = [&](int c0) __attribute__((always_inline)) {
     const int last = c_end - 1;
     const int tk = c0 + pi;
@@ -366,10 +387,16 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
 #pragma unroll
     for (int e = 0; e < QD / 8; ++e) kreg[e] = *(const dec_u32x4*)(kr + 8 * e);
     if (lane < NP) {
+      if (c0 + CH <= c_end) {
+        const uint16_t* vb = vlane + (int64_t)c0 * HD;
 #pragma unroll
-      for (int i = 0; i < CH / 4; ++i) {
-        const int tt = c0 + wave + 4 * i;
-        vreg[i] = *(const unsigned*)(vc + (kvbase + (tt < last ? tt : last)) * HD + 2 * lane);
+        for (int i = 0; i < CH / 4; ++i) vreg[i] = *(const unsigned*)(vb + 4 * i * HD);
+      } else {  // the split's last chunk: positions clamped to its last one
+#pragma unroll
+        for (int i = 0; i < CH / 4; ++i) {
+          const int tt = c0 + wave + 4 * i;
+          vreg[i] = *(const unsigned*)(vlane + (int64_t)((tt < last ? tt : last) - wave) * HD);
+        }
       }
     }
   };
@@ -443,8 +470,8 @@ __global__ void __launch_bounds__(256) dec_attention(const float* __restrict__ q
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        s[g] += __shfl_xor(s[g], 1, 64);
-        s[g] += __shfl_xor(s[g], 2, 64);
+        s[g] += xor1(s[g]);
+        s[g] += xor2(s[g]);
       }
       if (qd == 0)
 #pragma unroll
@@ -563,12 +590,20 @@ __global__ void __launch_bounds__(kOneWaves * 64) dec_attention_one(const float*
 #pragma unroll
     for (int e = 0; e < KL; ++e) kreg[e] = *(const dec_u32x4*)(kr + 8 * e);
   };
+  // lane l's dims 2 l, 2 l + 1 of cache row 0 (lanes past NP read, and ignore, dims 0, 1); a
+  // chunk's positions are wave-uniform, so a whole chunk is one base and immediate offsets
+  const uint16_t* vlane = vc + kvbase * HD + 2 * (lane < NP ? lane : 0);
   auto load_v = [&](int c0) __attribute__((always_inline)) {
-    const int dl = lane < NP ? lane : 0;  // lanes past NP read (and ignore) dims 0, 1
+    if (c0 + kOneChunk <= len) {
+      const uint16_t* vb = vlane + (int64_t)c0 * HD;
 #pragma unroll
-    for (int i = 0; i < kOneChunk; ++i) {
-      const int tt = c0 + i < len ? c0 + i : len - 1;
-      vreg[i] = *(const unsigned*)(vc + (kvbase + tt) * HD + 2 * dl);
+      for (int i = 0; i < kOneChunk; ++i) vreg[i] = *(const unsigned*)(vb + i * HD);
+    } else {  // the last chunk: positions clamped to the last one
+#pragma unroll
+      for (int i = 0; i < kOneChunk; ++i) {
+        const int tt = c0 + i < len ? c0 + i : len - 1;
+        vreg[i] = *(const unsigned*)(vlane + (int64_t)tt * HD);
+      }
     }
   };
   const int c_first = wave * kOneChunk;
@@ -643,8 +678,8 @@ __global__ void __launch_bounds__(kOneWaves * 64) dec_attention_one(const float*
     float pe[GW];
 #pragma unroll
     for (int g = 0; g < GW; ++g) {
-      float sv = s[g] + __shfl_xor(s[g], 1, 64);
-      sv = valid ? sv + __shfl_xor(sv, 2, 64) : -INFINITY;
+      float sv = s[g] + xor1(s[g]);
+      sv = valid ? sv + xor2(sv) : -INFINITY;
       const float m_new = fmaxf(m[g], wave_max(sv));  // position c0 is valid
       pe[g] = valid ? expf(sv - m_new) : 0.f;
       const float alpha = m[g] == -INFINITY ? 0.f : expf(m[g] - m_new);
@@ -653,7 +688,7 @@ __global__ void __launch_bounds__(kOneWaves * 64) dec_attention_one(const float*
       oa[g][0] *= alpha;
       oa[g][1] *= alpha;
     }
-    if (own && lane < NP) {
+    if (own && p >= c0 && p < c0 + kOneChunk && lane < NP) {  // the chunk holding the token's position
       const unsigned own_v = *(const unsigned*)(vp + 2 * lane);
 #pragma unroll
       for (int i = 0; i < kOneChunk; ++i) vreg[i] = c0 + i == p ? own_v : vreg[i];
