@@ -54,6 +54,32 @@ __device__ __forceinline__ half8 int4_to_half8(unsigned d, unsigned flip, half2v
   return out;
 }
 
+// 8 codes (one dword, low nibble first) -> 8 exact fp16 values in the order [0, 4, 1, 5, 2, 6,
+// 3, 7], 9 VALU instructions: one AND + XOR places two nibbles under the fp16 pattern 0x6400
+// (1024 + v for the low nibble of a byte, 1024 + 16 v for the high one, v = u ^ 8 for int4: the
+// sign flip is the XOR's 0x0008 / 0x0080 bits), and one packed f16 add (or multiply by 1/16 and
+// add) removes the offset.  klo / khi are 0x64006400 with the flip bits, bias 1032 or 1024,
+// bias16 72 or 64.  The activation operand is permuted to the same order (permute_x8).
+__device__ __forceinline__ half8 int4_to_half8_pairs(unsigned d, unsigned klo, unsigned khi, half2v bias,
+                                                     half2v bias16) {
+  const unsigned d8 = d >> 8;
+  const half2v a = __builtin_bit_cast(half2v, (d & 0x000F000Fu) ^ klo);   // codes 0, 4
+  const half2v b = __builtin_bit_cast(half2v, (d & 0x00F000F0u) ^ khi);   // codes 1, 5 (x 16)
+  const half2v c = __builtin_bit_cast(half2v, (d8 & 0x000F000Fu) ^ klo);  // codes 2, 6
+  const half2v e = __builtin_bit_cast(half2v, (d8 & 0x00F000F0u) ^ khi);  // codes 3, 7 (x 16)
+  const half2v inv16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const half2v h0 = a - bias, h1 = b * inv16 - bias16, h2 = c - bias, h3 = e * inv16 - bias16;
+  return half8{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+}
+
+// x0 .. x7 -> x0, x4, x1, x5, x2, x6, x3, x7 (the order int4_to_half8_pairs produces codes in)
+__device__ __forceinline__ half8 permute_x8(half8 x) {
+  const u32x4 w = __builtin_bit_cast(u32x4, x);
+  const u32x4 o = {__builtin_amdgcn_perm(w[2], w[0], 0x05040100u), __builtin_amdgcn_perm(w[2], w[0], 0x07060302u),
+                   __builtin_amdgcn_perm(w[3], w[1], 0x05040100u), __builtin_amdgcn_perm(w[3], w[1], 0x07060302u)};
+  return __builtin_bit_cast(half8, o);
+}
+
 // Transpose 4 x 4 dwords across the four 16-lane rows of a wave: on return register r of
 // lane row g holds what register g of lane row r held.  A lane that loaded 16 bytes (block
 // g = its row, dwords 0..3) then holds dword g of blocks 0..3, one per MFMA.
@@ -253,16 +279,24 @@ __global__ void __launch_bounds__(512) gemv_int4_xr(const uint8_t* __restrict__ 
   const int64_t wg_end = wg0 + rpw < N ? wg0 + rpw : N;  // rows of this workgroup: [wg0, wg_end)
   const int t0 = ki * KS;                                 // first super-step of the slice
   const half2v hbias = {(_Float16)bias, (_Float16)bias};
+  const half2v hbias16 = {(_Float16)(bias - 960.f), (_Float16)(bias - 960.f)};
+  const unsigned klo = 0x64006400u ^ (flip & 0x00080008u), khi = 0x64006400u ^ (flip & 0x00800080u);
 
-  // lanes of rows c >= M load nothing (their D rows are never stored): M x 1 KB per super-step
-  // of requests instead of 16 x 1 KB
+  // MFMA u of a super-step takes the lane's K elements 32 u + 8 q .. + 8 (the codes transposed
+  // across lane rows), or with one scale group per super-step (G = 4) 32 q + 8 u .. + 8 (the
+  // lane's own codes, no transpose).  Lanes of rows c >= M load nothing (their D rows are never
+  // stored): M x 1 KB per super-step of requests instead of 16 x 1 KB.
+  constexpr bool TRANSPOSE = G < 4;
   half8 xa[KS][4];
   {
-    const _Float16* xp = x + (int64_t)(c < M ? c : 0) * ldx + t0 * 128 + 8 * q;
+    const _Float16* xp = x + (int64_t)(c < M ? c : 0) * ldx + t0 * 128;
 #pragma unroll
     for (int j = 0; j < KS; ++j)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) xa[j][u] = c < M ? *(const half8*)(xp + j * 128 + 32 * u) : half8{};
+      for (int u = 0; u < 4; ++u) {
+        const int k = TRANSPOSE ? 32 * u + 8 * q : 32 * q + 8 * u;
+        xa[j][u] = c < M ? permute_x8(*(const half8*)(xp + j * 128 + k)) : half8{};
+      }
   }
   u32x4 codes[T][KS];
   unsigned sraw[T][SW];
@@ -312,11 +346,11 @@ __global__ void __launch_bounds__(512) gemv_int4_xr(const uint8_t* __restrict__ 
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
       unsigned d[4] = {codes[t][j][0], codes[t][j][1], codes[t][j][2], codes[t][j][3]};
-      transpose4(d[0], d[1], d[2], d[3]);
+      if constexpr (TRANSPOSE) transpose4(d[0], d[1], d[2], d[3]);
       f32x4v part = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const half8 wb = int4_to_half8(d[u], flip, hbias);
+        const half8 wb = int4_to_half8_pairs(d[u], klo, khi, hbias, hbias16);
         part = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j][u], wb, part, 0, 0, 0);
         if ((u + 1) % G == 0) {  // end of a scale group
           const float s = SCALED ? scale_of(t, j * GPS + u / G) : 1.0f;
