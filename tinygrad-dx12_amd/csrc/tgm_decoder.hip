@@ -839,6 +839,70 @@ __global__ void __launch_bounds__(256) dec_gemv_bf16(const uint16_t* __restrict_
   }
 }
 
+// The same product for 2 <= M <= 8 rows on bf16 MFMA (K a multiple of 128, M x K <= 32768):
+// each weight pair meets every x row in its own dot2 above, which makes that form VALU-bound at
+// 8 rows.  x is staged in LDS once per workgroup (16-byte chunk c of row m at c ^ m, so that
+// the 8 rows' reads of one chunk fall in different banks); each wave streams 16-row tiles of W.
+// In a 128-element step lane (r, q) loads 16 bytes of weight row r at K 32 s + 8 q for s = 0..3
+// (each load instruction reads 64 contiguous bytes of 16 rows; a ring of kHeadRing steps in
+// flight), and MFMA s (v_mfma_f32_16x16x32_bf16, A = those weights, B = x) takes load s against
+// x at the same K, so lane l ends with Y[m = l & 15][n0 + 4 (l / 16) + i] (rows m >= M read x
+// row 0 and are not stored).
+// Products of bf16 values are exact in the fp32 accumulator, as in the dot2 form.
+constexpr int kHeadRing = 4;
+__global__ void __launch_bounds__(256) dec_gemv_bf16_mfma(const uint16_t* __restrict__ w, int N, int K,
+                                                          const uint16_t* __restrict__ x, int64_t ldx, int M,
+                                                          float* __restrict__ y, int64_t ldy) {
+  typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+  __shared__ dec_u32x4 xs[32768 / 8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kc = K / 8;  // 16-byte chunks per row (a multiple of 16)
+  for (int i = tid; i < M * kc; i += 256) {
+    const int m = i / kc, c = i % kc;
+    xs[m * kc + (c ^ m)] = *(const dec_u32x4*)(x + (int64_t)m * ldx + (int64_t)c * 8);
+  }
+  __syncthreads();
+  const int r = lane & 15, q = lane >> 4;
+  const int xr = r < M ? r : 0;
+  const dec_u32x4* xrow = xs + xr * kc;
+  const int S = K / 128;
+  const int ntiles = (N + 15) / 16;
+  for (int tile = blockIdx.x * 4 + wave; tile < ntiles; tile += gridDim.x * 4) {  // uniform per wave
+    const int n0 = tile * 16;
+    const uint16_t* wrow = w + (int64_t)(n0 + r < N ? n0 + r : N - 1) * K + 8 * q;  // rows past N: not stored
+    dec_u32x4 ring[kHeadRing][4];
+    auto load = [&](int t, int slot) __attribute__((always_inline)) {
+      const uint16_t* p = wrow + 128 * (t < S ? t : S - 1);  // past the end: the last step
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ring[slot][e] = __builtin_nontemporal_load((const dec_u32x4*)(p + 32 * e));
+    };
+#pragma unroll
+    for (int j = 0; j < kHeadRing; ++j) load(j, j);
+    dec_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int t0 = 0; t0 < S; t0 += kHeadRing) {
+#pragma unroll
+      for (int jj = 0; jj < kHeadRing; ++jj) {
+        const int t = t0 + jj;
+        if (t < S) {
+#pragma unroll
+          for (int s2 = 0; s2 < 4; ++s2) {
+            const int chunk = 16 * t + 4 * s2 + q;
+            const dec_u32x4 xv = xrow[chunk ^ xr];
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ring[jj][s2]),
+                                                          __builtin_bit_cast(bf16x8_t, xv), acc, 0, 0, 0);
+          }
+        }
+        load(t + kHeadRing, jj);
+        __builtin_amdgcn_sched_barrier(0);  // each refill right after its slot's MFMAs
+      }
+    }
+    if (r < M)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (n0 + 4 * q + i < N) y[(int64_t)r * ldy + n0 + 4 * q + i] = acc[i];
+  }
+}
+
 // ------------------------------------------------------------------ greedy argmax
 __global__ void __launch_bounds__(1024) dec_argmax(const float* __restrict__ logits, int n, int64_t ld,
                                                    int32_t* __restrict__ tokens, int32_t* __restrict__ pos,
@@ -1102,6 +1166,13 @@ extern "C" int tgm_dec_gemv_bf16(const void* w, int64_t n, int64_t k, const void
     TGM_UNSUPPORTED("tgm_dec_gemv_bf16: k must be a multiple of 8 with m * k <= 32768");
   if ((uintptr_t)w % 16 || (uintptr_t)x % 16 || (m > 1 && (ldx * 2) % 16))
     TGM_UNSUPPORTED("tgm_dec_gemv_bf16: operands and x rows must be 16-byte aligned");
+  if (m >= 2 && k % 128 == 0) {  // bf16 MFMA (x staged as for the dot2 form: m * k <= 32768)
+    const int64_t tiles = (n + 15) / 16;
+    const unsigned g = (unsigned)((tiles + 3) / 4 < 1024 ? (tiles + 3) / 4 : 1024);
+    hipLaunchKernelGGL(dec_gemv_bf16_mfma, dim3(g), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)w, (int)n,
+                       (int)k, (const uint16_t*)x, ldx, (int)m, y, ldy);
+    return launch_status("tgm_dec_gemv_bf16");
+  }
   const int rows_per_wave = m == 1 ? 1 : 4;
   const int64_t waves = (n + rows_per_wave - 1) / rows_per_wave;
   const unsigned blocks = (unsigned)((waves + 3) / 4 < 512 ? (waves + 3) / 4 : 512);
