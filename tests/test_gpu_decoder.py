@@ -625,7 +625,8 @@ def test_gemm_swiglu_epilogue(dev, m, n, k, pad, scaled):
     assert err <= 1e-2, err
 
 
-@pytest.mark.parametrize("m,n,k", [(8, 28672 // 4, 4096), (2, 1000, 512), (16, 4096, 14336 // 4), (5, 12288, 2048)])
+@pytest.mark.parametrize("m,n,k", [(8, 28672 // 4, 4096), (2, 1000, 512), (16, 4096, 14336 // 4), (5, 12288, 2048),
+                                   (8, 28672, 1024)])
 def test_gemv_swiglu_epilogue_rows(dev, m, n, k):
     """2 to 16 activation rows: the streaming MFMA GEMV with the SwiGLU epilogue equals the plain
     GEMV (fp32 out) followed by tgm_dec_silu_mul bit for bit, and the oracle within 1e-2."""

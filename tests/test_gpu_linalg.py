@@ -155,7 +155,7 @@ def make_weight(dev, fmt, n, k, scale_kind, rng, bs=32):
 
 @pytest.mark.parametrize("fmt,scale_kind", [("fp4_e2m1", "e8m0"), ("fp6_e2m3", "e8m0"), ("fp4_e2m1", None)])
 @pytest.mark.parametrize("nkm,slices", [((1000, 4096, 8), 2), ((4096, 14336, 8), 7), ((300, 14336, 16), 7),
-                                        ((4100, 2048, 5), 4), ((64, 1024, 1), 8)])
+                                        ((4100, 2048, 5), 4), ((64, 1024, 1), 8), ((28672, 2048, 8), 2)])
 def test_dec_gemv_parts(dev, fmt, scale_kind, nkm, slices):
     """K-slice partial GEMV (tgm_dec_gemv_parts): part z is x[:, K_z] . deq(W[:, K_z])^T over the
     z-th of ``slices`` equal K slices, each within the GEMV tolerance of the oracle's product over
@@ -255,12 +255,13 @@ def test_gemv_fp4_decode_full_shape_against_oracle(dev, fp4_decode_weight_14336x
 @pytest.mark.parametrize("fmt", ["fp4_e2m1", "fp6_e3m2"])
 @pytest.mark.parametrize("nkm", [(12288, 2048, 1), (6144, 4096, 4), (4096, 14336, 1), (2048, 3584, 2),
                                  (256, 14336, 16), (1000, 4096, 16), (64, 1536, 7), (4096, 14336, 8),
-                                 (512, 12160, 12), (12288, 4096, 5), (13000, 2048, 9), (14336, 4096, 12)])
+                                 (512, 12160, 12), (12288, 4096, 5), (13000, 2048, 9), (14336, 4096, 12),
+                                 (28700, 1024, 16), (28672, 2048, 8)])
 def test_gemv_mx_launch_shapes(dev, fmt, nkm):
-    """Every workgroup shape of the streaming GEMV (4x2, 2x4, 1x8 tiles x K slices), exact and
-    guarded slices, activations staged in LDS up front, loaded with the weight ring and shared
-    through LDS (4x2 tiles, 5+ rows, ragged N), and in the load ring (M x K too large for LDS:
-    the decoder's down projection at 8 rows, and per-dword scales with guarded slices)."""
+    """Every workgroup shape of the streaming GEMV (8x1 from 1792 tiles on, 4x2, 2x4, 1x8 tiles x
+    K slices), exact and guarded slices, ragged N, activations staged in LDS and in the load ring
+    (M x K too large for LDS: the decoder's down projection at 8 rows, and per-dword scales with
+    guarded slices)."""
     n, k, m = nkm
     rng = np.random.default_rng(n + k + m)
     w, deq = make_weight(dev, fmt, n, k, "e8m0", rng)

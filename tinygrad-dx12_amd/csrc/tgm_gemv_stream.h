@@ -348,12 +348,20 @@ struct GemvShape {
   bool exact;
 };
 
+// From kGemvWideTiles tiles (28672 rows) up, eight tiles x the whole K per workgroup: every
+// workgroup stages X once for 128 rows, one round of 224 workgroups instead of two rounds of
+// 512 with 56 rows each (at 8-16 activation rows the staging traffic, each workgroup reading
+// all of X from its XCD's L2, is what grows with M).
+constexpr int64_t kGemvWideTiles = 1792;
+
 inline GemvShape gemv_shape(int64_t tiles, int64_t S, bool sg4) {
-  static const int order_big[3][2] = {{4, 2}, {2, 4}, {1, 8}};
-  static const int order_mid[3][2] = {{2, 4}, {1, 8}, {4, 2}};
-  static const int order_small[3][2] = {{1, 8}, {2, 4}, {4, 2}};
-  const int(*order)[2] = tiles >= 768 ? order_big : tiles >= 384 ? order_mid : order_small;
-  for (int i = 0; i < 3; ++i) {
+  static const int order_wide[4][2] = {{8, 1}, {4, 2}, {2, 4}, {1, 8}};
+  static const int order_big[4][2] = {{4, 2}, {2, 4}, {1, 8}, {1, 8}};
+  static const int order_mid[4][2] = {{2, 4}, {1, 8}, {4, 2}, {4, 2}};
+  static const int order_small[4][2] = {{1, 8}, {2, 4}, {4, 2}, {4, 2}};
+  const int(*order)[2] = tiles >= kGemvWideTiles ? order_wide
+                         : tiles >= 768 ? order_big : tiles >= 384 ? order_mid : order_small;
+  for (int i = 0; i < 4; ++i) {
     const int nt = order[i][0], nk = order[i][1];
     int64_t per = (S + nk - 1) / nk;
     if (sg4) per = (per + 3) / 4 * 4;
@@ -457,6 +465,7 @@ int launch_gemv_stream(hipStream_t s, const void* w, int64_t n, int64_t k, const
     }
   }
   const StreamLaunch L{(unsigned)wgs, (unsigned)slices, k * format_info(FMT).bits / 8, part_stride};
+  if (g.nt == 8) return launch_stream_shape<FMT, 8, 1>(g, sc, xv, L, lds, s, w, n, ks, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
   if (g.nt == 4) return launch_stream_shape<FMT, 4, 2>(g, sc, xv, L, lds, s, w, n, ks, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
   if (g.nt == 2) return launch_stream_shape<FMT, 2, 4>(g, sc, xv, L, lds, s, w, n, ks, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
   return launch_stream_shape<FMT, 1, 8>(g, sc, xv, L, lds, s, w, n, ks, scales, nblk, x, m, ldx, y, ydt, ldy, swiglu, rpw);
