@@ -387,8 +387,10 @@ F16_ROUNDING, BF16_ROUNDING = 2.0 ** -10, 2.0 ** -7
 
 
 @pytest.mark.parametrize("attention", ["fused", "gemm", "split"])
-@pytest.mark.parametrize("batch,prompt,ffn", [(8, 6, 512), (1, 9, 512), (3, 40, 512), (8, 6, 4096), (5, 7, 4096)])
-def test_decoder_layers_match_oracle_elementwise(dev, batch, prompt, ffn, attention):
+@pytest.mark.parametrize("batch,prompt,ffn,hidden", [(8, 6, 512, 256), (1, 9, 512, 256), (3, 40, 512, 256),
+                                                     (8, 6, 4096, 256), (5, 7, 4096, 256), (8, 6, 2048, 1024),
+                                                     (5, 7, 4096, 1024), (3, 9, 2048, 1024)])
+def test_decoder_layers_match_oracle_elementwise(dev, batch, prompt, ffn, hidden, attention):
     """Teacher-forced parity of every operation of every layer, elementwise.  Each operation is
     recomputed by the oracle from the device's own input to it (the device's residual, normed
     activations, KV cache, attention output and SwiGLU output of that layer), so an activation
@@ -398,13 +400,16 @@ def test_decoder_layers_match_oracle_elementwise(dev, batch, prompt, ffn, attent
       results: max relative error 1e-2, floor 1e-3 of the largest element;
     * values the device rounds (the f16 / bf16 normed activations, the bf16 k and v it stores):
       within one unit of the rounding (relative 2^-10 for f16, 2^-7 for bf16, same floor);
-    * the logits of the device's last residual: 1e-2.
+    * the final RMSNorm of the device's last residual within one bf16 unit, and the logits of
+      the device's normed rows: 1e-2.
 
     Prefill (GEMM path at 48 and 120 rows, GEMV path at 9), then three cached decode steps
     (batch 8: eight sequences per multi-row GEMV, SwiGLU GEMV and decode attention launch).  With
     a feed-forward width of 4096 the decode steps at 5 and 8 tokens run the down projection as
-    two K-slice parts that the next norm adds."""
-    cfg, max_seq = dataclasses.replace(SMALL, ffn=ffn), 64
+    two K-slice parts that the next norm adds.  Hidden 1024 (8 heads of 128) runs the INT4
+    projections on the register-activation GEMV (K = 1024) and the MFMA output head at K = 1024."""
+    cfg, max_seq = dataclasses.replace(SMALL, ffn=ffn, hidden=hidden, heads=hidden // 64 if hidden == 256 else 8,
+                                       head_dim=64 if hidden == 256 else 128), 64
     w = random_weights(cfg, dev, seed=batch + 20)
     prompts = np.random.default_rng(prompt).integers(0, cfg.vocab, (batch, prompt))
     dec = Decoder(w, cfg, batch, max_seq, prompt)
@@ -446,7 +451,10 @@ def test_decoder_layers_match_oracle_elementwise(dev, batch, prompt, ffn, attent
             close(act, oracle.swiglu(li, xb), 1e-2, f"{at}: gate|up + SwiGLU")
             close(delta, act @ oracle.w.layers[li].w_down.T, 1e-2, f"{at}: down projection")
             h = mid + delta
-        close(np64(dec.logits), oracle.head(h[:, -1]), 1e-2, f"{where}: logits")
+        # the final norm within one bf16 unit, then the head over the device's own normed rows
+        xf = np64(dec.xnb[[b * T + T - 1 for b in range(batch)]])
+        close(xf, D.bf16(D.rmsnorm(h[:, -1], oracle.w.final_norm, cfg.eps)), BF16_ROUNDING, f"{where}: final RMSNorm")
+        close(np64(dec.logits), xf @ oracle.w.lm_head.T, 1e-2, f"{where}: logits")
 
     dec.layer_trace = []
     first = dec.prefill(torch.from_numpy(prompts).to(dev))
