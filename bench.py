@@ -815,7 +815,8 @@ def summarize_decoder(folder: Path, workload: str, part: str) -> str:
     run = json.loads((folder / "bench.json").read_text())[workload]
     unit = "step" if part == "decode" else "prefill"
     lines = [f"# {workload}_{part}",
-             "# rocprofv3 kernel trace of the config-5 decoder bench on one MI355X (gfx950); commands, from the "
+             "# rocprofv3 kernel trace of the 8-layer decoder bench (hidden 4096, INT4 attention, FP4 feed-forward) on one "
+             "MI355X (gfx950); commands, from the "
              "repository root (OUT = any output folder):",
              f"#   rocprofv3 --kernel-trace --stats --output-format csv -d OUT -o run -- python3 bench.py --only {workload} "
              "> OUT/bench.json",

@@ -4,7 +4,7 @@ Rendered kernels are checked against numpy computing the same operations in the 
 (bit-exact for integer, bool, f16, f32, f64 and bf16 arithmetic, where bf16 is fp32 arithmetic
 rounded to bf16 after each operation; the device math library's EXP2 / LOG2 / SIN within 4 ulp
 of fp32).  Scheduled matrix products -- lowered to the GEMMs or left as rendered kernels -- are
-checked against the fp64 product of the same operands with the north-star tolerance (max
+checked against the fp64 product of the same operands with the packed-product tolerance (max
 relative error <= 1e-2; fp32 outputs within 1e-3).
 """
 
