@@ -382,7 +382,10 @@ struct StreamLaunch {
 template <int FMT, int NT, int NK, int SMAX, bool EXACT, int XV, int SC>
 int launch_stream(const StreamLaunch& L, size_t lds, hipStream_t s, const void* w, int64_t n, int64_t k, const void* scales,
                   int64_t nblk, const void* x, int64_t m, int64_t ldx, void* y, int ydt, int64_t ldy, int swiglu, int rpw) {
-  auto kernel = gemv_stream<FMT, NT, NK, (XV > 0 ? kGemvRing : kGemvRingX), SMAX, EXACT, XV, SC>;
+  // slices of 8 super-steps keep 6 in flight rather than all 8: 0.45-0.9 us less per launch on
+  // every shape (the decoder's K-slice down projection: batch-8 decode 0.583 -> 0.573 ms per step)
+  constexpr int RING = XV == 0 ? kGemvRingX : SMAX == 8 ? 6 : kGemvRing;
+  auto kernel = gemv_stream<FMT, NT, NK, RING, SMAX, EXACT, XV, SC>;
   if (lds > 64 * 1024) {
     static bool raised = false;  // per instantiation
     if (!raised) {
