@@ -848,8 +848,9 @@ __global__ void __launch_bounds__(256) dec_gemv_bf16(const uint16_t* __restrict_
 // flight), and MFMA s (v_mfma_f32_16x16x32_bf16, A = those weights, B = x) takes load s against
 // x at the same K, so lane l ends with Y[m = l & 15][n0 + 4 (l / 16) + i] (rows m >= M read x
 // row 0 and are not stored).
-// Products of bf16 values are exact in the fp32 accumulator, as in the dot2 form.
-constexpr int kHeadRing = 4;
+// Products of bf16 values are exact in the fp32 accumulator, as in the dot2 form.  Two steps in
+// flight per wave (8 KB; about 16 MB over the chip at 8 waves per CU) beat 3, 4, 6 and 8.
+constexpr int kHeadRing = 2;
 __global__ void __launch_bounds__(256) dec_gemv_bf16_mfma(const uint16_t* __restrict__ w, int N, int K,
                                                           const uint16_t* __restrict__ x, int64_t ldx, int M,
                                                           float* __restrict__ y, int64_t ldy) {
