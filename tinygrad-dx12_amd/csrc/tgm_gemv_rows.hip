@@ -504,7 +504,10 @@ static int launch_norm_rows(hipStream_t s, const void* w, int fmt, int64_t n, co
                          (const uint8_t*)w, n, (const uint8_t*)scales, (const __bf16*)nullptr, y, ydt, nm);
     return TGM_OK;
   }
-  constexpr int R = kRowsPerWaveInt4, D = R * IPR;
+  // at K = 4096, 4 of a wave's 8 loads in flight: the norm's operand loads go first, and fewer
+  // weight loads behind them measured faster in the batch-1 decode step (0.3946 -> 0.3878 ms),
+  // while the plain one-row INT4 GEMV keeps all 8 (4 there cost 0.2-0.45 us per launch)
+  constexpr int R = kRowsPerWaveInt4, D = IPR == 2 ? 4 : R * IPR;
   const unsigned grid = (unsigned)((n + 4 * R - 1) / (4 * R));
   const bool sgn = fmt == TGM_FMT_INT4;
 #define TGM_NORM_I4(SDT)                                                                                          \
